@@ -1,0 +1,233 @@
+#!/usr/bin/env python3
+"""Benchmark of the FP8 hot path on one MI355X.
+
+Step (timed): config 3 of the baseline -- block_scaled_matmul forward + FP8
+backward on x [8192, 2048], W [2048, 8192], dY [8192, 8192] (bf16, synthetic,
+seeded), i.e. quantize x / W.T -> GEMM Y; quantize dY, W along N -> GEMM dX;
+quantize X.T, dY.T along M -> GEMM dW.  Every kernel is a C-ABI call into
+libtg_fp8.so on torch's current stream; the step allocates nothing.
+
+value        = 3 * 2*8192*2048*8192 FLOP / step time (TFLOP/s, quantization included)
+roofline     = the GEMM kernel: 2*M*N*K FLOP per launch / its mean launch time
+               (HIP events around each GEMM launch in the timed region) vs
+               MI355X dense FP8 MFMA peak 5.0 PFLOP/s
+norm_quant   = config 2 fused RMSNorm -> FP8 quantize, bytes per launch
+               84,414,464 (x read + y/q/scales written + gamma) / mean launch
+               time vs 8 TB/s HBM; input/output sets rotate over > 256 MB so
+               the Infinity Cache cannot serve them
+cpu_baseline = the CPU oracle (numpy + C) on a row sample of the same step
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "train-gpt_amd"))
+sys.path.insert(0, ROOT)
+
+FP8_PEAK_TFLOPS = 5000.0       # MI355X dense FP8 MFMA
+HBM_PEAK_GBPS = 8000.0         # MI355X HBM3E
+M3, K3, N3 = 8192, 2048, 8192
+GEMM_FLOP = 2.0 * M3 * N3 * K3
+STEP_FLOP = 3 * GEMM_FLOP
+C2_ROWS, C2_D = 8 * 1024, 2048
+C2_BYTES = C2_ROWS * C2_D * (2 + 2 + 1) + C2_ROWS * (C2_D // 128) * 4 + C2_D * 2
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--norm-iters", type=int, default=200)
+    return p.parse_args()
+
+
+class Step:
+    """Config-3 forward + FP8 backward through the C ABI with preallocated buffers."""
+
+    def __init__(self, dev):
+        import torch
+        import _tglib as L
+        self.L, self.lib, self.torch = L, L.lib(), torch
+        g = torch.Generator(device=dev)
+        g.manual_seed(2)
+        bf = torch.bfloat16
+        self.x = torch.randn((M3, K3), generator=g, device=dev).to(bf)
+        self.w = (torch.randn((K3, N3), generator=g, device=dev) * 0.02).to(bf)
+        self.dy = (torch.randn((M3, N3), generator=g, device=dev) * 1e-3).to(bf)
+        u8, f32 = torch.uint8, torch.float32
+        e = lambda *s: torch.empty(s, dtype=u8, device=dev)
+        f = lambda *s: torch.empty(s, dtype=f32, device=dev)
+        self.qx, self.sx = e(M3, K3), f(M3, K3 // 128)          # x along K
+        self.qwt, self.swt = e(N3, K3), f(N3, K3 // 128)        # W.T along K
+        self.qdy, self.sdy = e(M3, N3), f(M3, N3 // 128)        # dY along N
+        self.qw, self.sw = e(K3, N3), f(K3, N3 // 128)          # W along N
+        self.qxt, self.sxt = e(K3, M3), f(K3, M3 // 128)        # X.T along M
+        self.qdyt, self.sdyt = e(N3, M3), f(N3, M3 // 128)      # dY.T along M
+        self.y = torch.empty((M3, N3), dtype=bf, device=dev)
+        self.dx = torch.empty((M3, K3), dtype=bf, device=dev)
+        self.dw = torch.empty((K3, N3), dtype=bf, device=dev)
+        self.stream = L.stream_of(self.x)
+        self.events = []
+
+    def _gemm(self, qa, sa, qb, sb, c, M, N, K, ev):
+        L = self.L
+        if ev is not None:
+            s, e = self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True)
+            s.record()
+        L.check(self.lib.tg_gemm_fp8_nt(L.ptr(qa), L.ptr(sa), L.ptr(qb), L.ptr(sb), 1, L.ptr(c),
+                                        L.TG_DTYPE_BF16, M, N, K, 128, self.stream))
+        if ev is not None:
+            e.record()
+            ev.append((s, e))
+
+    def run(self, ev=None):
+        L, lib, st, p = self.L, self.lib, self.stream, self.L.ptr
+        bf = L.TG_DTYPE_BF16
+        # forward (fp8.py:66,68,70-78)
+        L.check(lib.tg_quantize_rows(p(self.x), bf, M3, K3, 128, p(self.qx), p(self.sx), st))
+        L.check(lib.tg_quantize_cols(p(self.w), bf, K3, N3, 128, p(self.qwt), p(self.swt), st))
+        self._gemm(self.qx, self.sx, self.qwt, self.swt, self.y, M3, N3, K3, ev)
+        # dX = dY . W.T
+        L.check(lib.tg_quantize_rows(p(self.dy), bf, M3, N3, 128, p(self.qdy), p(self.sdy), st))
+        L.check(lib.tg_quantize_rows(p(self.w), bf, K3, N3, 128, p(self.qw), p(self.sw), st))
+        self._gemm(self.qdy, self.sdy, self.qw, self.sw, self.dx, M3, K3, N3, ev)
+        # dW = X.T . dY
+        L.check(lib.tg_quantize_cols(p(self.x), bf, M3, K3, 128, p(self.qxt), p(self.sxt), st))
+        L.check(lib.tg_quantize_cols(p(self.dy), bf, M3, N3, 128, p(self.qdyt), p(self.sdyt), st))
+        self._gemm(self.qxt, self.sxt, self.qdyt, self.sdyt, self.dw, K3, N3, M3, ev)
+
+
+def bench_norm(dev, iters):
+    """Config 2 fused RMSNorm -> quantize; mean kernel time over rotating buffer sets."""
+    import torch
+    import _tglib as L
+    lib = L.lib()
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    nsets = 5                                    # 5 x 84 MB > 256 MB Infinity Cache
+    xs, ys, qs, ss = [], [], [], []
+    for _ in range(nsets):
+        x = torch.randn((C2_ROWS, C2_D), generator=g, device=dev)
+        mask = torch.rand((C2_ROWS, C2_D), generator=g, device=dev) < 1e-3
+        xs.append(torch.where(mask, x * 50, x).to(torch.bfloat16))
+        ys.append(torch.empty((C2_ROWS, C2_D), dtype=torch.bfloat16, device=dev))
+        qs.append(torch.empty((C2_ROWS, C2_D), dtype=torch.uint8, device=dev))
+        ss.append(torch.empty((C2_ROWS, C2_D // 128), dtype=torch.float32, device=dev))
+    gamma = (1 + 0.1 * torch.randn((C2_D,), generator=g, device=dev)).to(torch.bfloat16)
+    st = L.stream_of(gamma)
+
+    def launch(i):
+        k = i % nsets
+        L.check(lib.tg_rms_norm_fp8(L.ptr(xs[k]), L.ptr(gamma), L.ptr(ys[k]), L.ptr(qs[k]), L.ptr(ss[k]),
+                                    C2_ROWS, C2_D, 1e-6, 128, st))
+
+    for i in range(10):
+        launch(i)
+    torch.cuda.synchronize()
+    evs = []
+    for i in range(iters):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        launch(i)
+        e.record()
+        evs.append((s, e))
+    torch.cuda.synchronize()
+    ms = sum(s.elapsed_time(e) for s, e in evs) / len(evs)
+    gbps = C2_BYTES / (ms * 1e-3) / 1e9
+    return {"workload": "C2 fused RMSNorm+FP8 quant, x bf16 [8,1024,2048], eps 1e-6",
+            "us_per_launch": round(ms * 1e3, 3), "bytes_per_launch": C2_BYTES,
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None}}
+
+
+def cpu_baseline(rows=4096):
+    """The CPU oracle on a row sample of the step: quantize (C oracle) and the
+    dequantized f32 GEMMs (numpy/BLAS) of fwd + FP8 bwd restricted to `rows`
+    of the 8192 token rows.  FLOP counted = 3 * 2 * rows * 2048 * 8192."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+    from oracle import bf16 as ob
+    from oracle import cbind, fp8_ref
+    rng = np.random.default_rng(2)
+    x = ob.randn_bf16(rng, (rows, K3))
+    w = ob.randn_bf16(rng, (K3, N3), std=0.02)
+    dy = ob.randn_bf16(rng, (rows, N3), std=1e-3)
+    dec = lambda q, s: (fp8_ref.E4M3FN_VALUES[q].reshape(q.shape[0], -1, 128)
+                        * s[:, :, None]).reshape(q.shape[0], -1)
+    t0 = time.perf_counter()
+    qx, sx = cbind.quantize_rows_bf16(x)
+    qwt, swt = cbind.quantize_cols_bf16(w)
+    y = dec(qx, sx) @ dec(qwt, swt).T
+    qdy, sdy = cbind.quantize_rows_bf16(dy)
+    qw, sw = cbind.quantize_rows_bf16(w)
+    dx = dec(qdy, sdy) @ dec(qw, sw).T
+    qxt, sxt = cbind.quantize_cols_bf16(x)
+    qdyt, sdyt = cbind.quantize_cols_bf16(dy)
+    dw = dec(qxt, sxt) @ dec(qdyt, sdyt).T
+    dt = time.perf_counter() - t0
+    assert y.shape == (rows, N3) and dx.shape == (rows, K3) and dw.shape == (K3, N3)
+    flop = 3 * 2.0 * rows * K3 * N3
+    threads = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    return {"value": round(flop / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"C3 fwd+FP8 bwd restricted to {rows} of 8192 token rows (C oracle quantize "
+                      f"single-thread, numpy f32 dequant GEMMs on {threads} BLAS threads), "
+                      f"{dt:.2f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    step = Step(dev)
+    for _ in range(args.warmup):
+        step.run()
+    torch.cuda.synchronize()
+    ev = []
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        step.run(ev)
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = max(wall * 1e3, start.elapsed_time(stop)) / args.steps
+    gemm_ms = sum(s.elapsed_time(e) for s, e in ev) / len(ev)
+    gemm_tflops = GEMM_FLOP / (gemm_ms * 1e-3) / 1e12
+    value = STEP_FLOP / (ms_step * 1e-3) / 1e12
+    norm = bench_norm(dev, args.norm_iters)
+    out = {
+        "metric": "FP8 block-scaled GEMM TFLOP/s (% fp8 MFMA peak); RMSNorm+quant HBM GB/s",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp8e4m3 (f32 accumulate, bf16 io)",
+        "data": "synthetic (torch GPU RNG, seeded)",
+        "config": {"workload": "C3 block_scaled_matmul fwd + FP8 bwd, x[8192,2048] W[2048,8192] "
+                               "dY[8192,8192] bf16, 1x128 scales (quantization included)",
+                   "M": M3, "K": K3, "N": N3, "block_k": 128},
+        "gemm_us_per_launch": round(gemm_ms * 1e3, 2),
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": FP8_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "norm_quant": norm,
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,125 @@
+/*
+ * tg_fp8.h -- C ABI of the MI355X (gfx950) FP8 hot path of train-gpt.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t
+ * passed as void*.  None allocates device memory, none synchronises the
+ * host, and all work is enqueued on `stream`, so each is usable from an XLA
+ * FFI handler (which receives its buffers and stream from XLA) or from a
+ * ctypes/torch caller.  Return value: 0 on success, TG_EINVAL for a bad
+ * argument (nothing is launched), TG_EHIP for a HIP launch failure;
+ * tg_last_error() returns the calling thread's last message.
+ *
+ * Layouts are row-major and contiguous.  bf16 is passed as uint16_t bits,
+ * e4m3fn bytes as uint8_t (OCP float8_e4m3fn, the gfx950 FP8 format).
+ * block_k must be 128 (the reference's DEFAULT_BLOCK_K, fp8.py:27, and the K
+ * depth of one gfx950 FP8 MFMA).
+ *
+ * Reference citations are /root/reference/<file>:<line>.
+ */
+#ifndef TG_FP8_H
+#define TG_FP8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { TG_OK = 0, TG_EINVAL = 1, TG_EHIP = 2 };
+enum { TG_DTYPE_BF16 = 0, TG_DTYPE_F32 = 1 };
+
+/* Message for the calling thread's last non-zero return. */
+const char* tg_last_error(void);
+
+/* _quantize_to_fp8 (fp8.py:39-47) along the last axis.
+ * x: (rows, cols) bf16 or f32; q: (rows, cols) e4m3fn; scales: (rows, cols/block_k) f32.
+ * scale = max(amax/448, 1e-30); q = e4m3fn(x / scale).  cols % block_k == 0. */
+int tg_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, int block_k,
+                     uint8_t* q, float* scales, void* stream);
+
+/* _quantize_to_fp8 of x.T (fp8.py:68 applies it to b.T): quantizes the columns
+ * of x (rows, cols) bf16 and writes them transposed:
+ * q_t: (cols, rows) e4m3fn; scales_t: (cols, rows/block_k) f32.  rows % block_k == 0,
+ * cols % 8 == 0. */
+int tg_quantize_cols(const void* x, int x_dtype, int64_t rows, int64_t cols, int block_k,
+                     uint8_t* q_t, float* scales_t, void* stream);
+
+/* jax.nn.scaled_matmul + bf16 cast as called at fp8.py:70-78 ("NT" layout):
+ * c[m, n] = sum_kb a_s[m, kb] * b_s[n / b_scale_bn, kb] * sum_{k in kb} a_q[m, k] * b_q[n, k]
+ * a_q: (M, K) e4m3fn, a_s: (M, K/128) f32; b_q: (N, K) e4m3fn;
+ * b_s: (N, K/128) f32 when b_scale_bn == 1 (fp8.py:68's per-column scales) or
+ *      (ceil(N/128), K/128) when b_scale_bn == 128 (128x128 weight tiles).
+ * c: (M, N) bf16 (RNE, fp8.py:78) or f32 (c_dtype).  f32 accumulation. */
+int tg_gemm_fp8_nt(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s,
+                   int b_scale_bn, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
+                   int block_k, void* stream);
+
+/* Device workspace (bytes) tg_block_scaled_matmul needs for its quantized operands. */
+size_t tg_block_scaled_matmul_workspace(int64_t M, int64_t N, int64_t K, int block_k);
+
+/* _fp8_forward (fp8.py:50-78) in one call: quantize a (M, K) and b.T (b is (K, N)),
+ * then the scaled GEMM into out (M, N) bf16.  a and b are bf16.
+ * workspace: >= tg_block_scaled_matmul_workspace(M, N, K, block_k) bytes, 256-B aligned. */
+int tg_block_scaled_matmul(const void* a, const void* b, void* out, int64_t M, int64_t N,
+                           int64_t K, int block_k, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* Device workspace (bytes) of tg_block_scaled_matmul_bwd_fp8. */
+size_t tg_block_scaled_matmul_bwd_workspace(int64_t M, int64_t N, int64_t K, int block_k);
+
+/* FP8 backward of block_scaled_matmul (the custom_vjp of fp8.py:81-101 with
+ * the forward's quantize -> scaled GEMM composition reused for both
+ * gradients; fp8.py:85-98 itself is the bf16 straight-through rule):
+ *   da (M, K) = fwd(g, b.T):  g row-quantized along N, b row-quantized along N
+ *   db (K, N) = fwd(a.T, g):  a.T and g.T quantized along M
+ * a: (M, K), b: (K, N), g: (M, N), all bf16; da, db bf16.  M % 128 == 0. */
+int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, const void* g, void* da,
+                                   void* db, int64_t M, int64_t N, int64_t K, int block_k,
+                                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* _rms_norm_pure (kernels.py:30-33) over the last axis of x (rows, dim) bf16,
+ * scale (dim,) bf16, y (rows, dim) bf16:
+ * r = bf16(rsqrt(mean(x^2) + eps)); y = bf16(bf16(x * r) * scale).
+ * Replaces the Pallas rms_norm_gpu forward (kernels.py:41-99) on ROCm. */
+int tg_rms_norm(const void* x, const void* scale, void* y, int64_t rows, int64_t dim, float eps,
+                void* stream);
+
+/* Fused RMSNorm -> FP8 quantize (the composition of kernels.py:30-33 and
+ * fp8.py:39-47 on the bf16 norm output, from one read of x):
+ * y (rows, dim) bf16, q (rows, dim) e4m3fn, s (rows, dim/block_k) f32. */
+int tg_rms_norm_fp8(const void* x, const void* scale, void* y, uint8_t* q, float* s,
+                    int64_t rows, int64_t dim, float eps, int block_k, void* stream);
+
+/* Decode-shape GEMM with a pre-quantized weight (no reference function; the
+ * reference re-quantizes W every call at fp8.py:68):
+ * out[m, n] = sum_kb x_s[m, kb] * w_s[n / w_scale_bn, kb] * sum_k x_q[m, k] * w_q[n, k]
+ * x_q (M, K), x_s (M, K/128); w_q (N, K), w_s as b_s of tg_gemm_fp8_nt;
+ * out (M, N) bf16.  Intended for M <= 64. */
+int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* w_q, const float* w_s,
+                int w_scale_bn, void* out, int64_t M, int64_t N, int64_t K, int block_k,
+                void* stream);
+
+/* Quantize W.T into the pre-quantized weight format with one scale per
+ * 128x128 tile (w_scale_bn == 128).  w: (K, N) bf16; w_q (N, K); w_s (ceil(N/128), K/128). */
+int tg_quantize_weight_128x128(const void* w, int64_t K, int64_t N, uint8_t* w_q, float* w_s,
+                               void* stream);
+
+/* Test support: compares the hardware e4m3fn convert with the integer
+ * encoder over every f32 bit pattern.  counts[0] = mismatches with
+ * |v| <= 448*(1+2^-12) (covering the range quantization produces), counts[1] =
+ * mismatches elsewhere (finite), counts[2] = mismatches for NaN/inf inputs.
+ * counts must point to 3 device uint64_t (zeroed by the call). */
+int tg_selftest_fp8_cvt(uint64_t* counts, void* stream);
+
+/* Test support: compares the quantizers' bf16 divide (reciprocal refinement)
+ * with the IEEE f32 divide for every bf16 amax and every bf16 x with
+ * |x| <= amax.  counts[0] = e4m3fn byte mismatches, counts[1] = f32 quotient
+ * mismatches with |x/s| > 2^-10, counts[2] = quotient mismatches at or below
+ * 2^-10 (which encode to +-0 either way).  3 device uint64_t, zeroed by the call. */
+int tg_selftest_divide(uint64_t* counts, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TG_FP8_H */

@@ -1,0 +1,171 @@
+"""GPU parity of the block-scaled FP8 GEMM (fp8.py:50-78) and its VJP.
+
+Bar (north star): bit-exact quantized operands; GEMM outputs within 1e-2
+max-abs-normalised error of the oracle (float64 dequant GEMM of the same
+quantized operands, fp8_ref.dequant_gemm_nt); the bf16 output is the RNE of
+the f32 accumulator.  The error against a plain bf16 matmul is printed.
+"""
+import numpy as np
+import pytest
+import torch
+
+import fp8
+from helpers import maxabs_rel, same_scales, to_dev, u8
+from oracle import bf16 as ob
+from oracle import fp8_ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _gemm(qa, sa, qb, sb, dev, bn=1, out=torch.bfloat16):
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return fp8.scaled_matmul(t(qa), t(sa), t(qb), t(sb), b_scale_bn=bn, out_dtype=out)
+
+
+def test_ones_known_answer(dev):
+    """debug_fp8.py:104-109: ones(4,128) @ ones(128,4) == 128."""
+    a = torch.ones((4, 128), dtype=torch.bfloat16, device=dev)
+    b = torch.ones((128, 4 * 2), dtype=torch.bfloat16, device=dev)
+    y = fp8.block_scaled_matmul(a, b)
+    assert torch.all(y.float() == 128.0)
+
+
+def test_layout_known_answer(dev):
+    """Asymmetric operands catch transposed fragments: c[m, n] = (m + 1) * (n + 1) * 128 / 448^2 * 448^2."""
+    M, N, K = 48, 40, 256
+    qa = np.full((M, K), 0x38, np.uint8)          # e4m3 1.0
+    qb = np.full((N, K), 0x38, np.uint8)
+    sa = np.repeat((np.arange(M, dtype=np.float32) + 1)[:, None], K // 128, axis=1)
+    sb = np.repeat((np.arange(N, dtype=np.float32) + 1)[:, None], K // 128, axis=1)
+    sb[:, 1] *= 2
+    c = _gemm(qa, sa, qb, sb, dev, out=torch.float32).cpu().numpy()
+    ref = fp8_ref.dequant_gemm_nt(qa, sa, qb, sb)
+    np.testing.assert_allclose(c, ref, rtol=1e-6)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 8, 128), (17, 40, 256), (130, 200, 384), (256, 256, 512),
+                                   (300, 136, 1024), (2048, 3072, 768)])
+def test_scaled_gemm_random(dev, M, N, K):
+    rng = np.random.default_rng(M * 7 + N)
+    a = ob.bf16_to_f32(ob.randn_bf16(rng, (M, K)))
+    b = ob.bf16_to_f32(ob.randn_bf16(rng, (N, K), std=0.02))
+    qa, sa = fp8_ref.quantize_fp8(a)
+    qb, sb = fp8_ref.quantize_fp8(b)
+    ref = fp8_ref.dequant_gemm_nt(qa, sa, qb, sb)
+    for out in (torch.bfloat16, torch.float32):
+        c = _gemm(qa, sa, qb, sb, dev, out=out)
+        assert maxabs_rel(c, ref) <= TOL
+    c32 = _gemm(qa, sa, qb, sb, dev, out=torch.float32).cpu().numpy()
+    # the bf16 output is the RNE of the f32 accumulator (fp8.py:78)
+    c16 = _gemm(qa, sa, qb, sb, dev).view(torch.int16).cpu().numpy().view(np.uint16)
+    np.testing.assert_array_equal(c16, ob.f32_to_bf16(c32))
+
+
+def test_scaled_gemm_weight_tiles_128x128(dev):
+    rng = np.random.default_rng(21)
+    M, N, K = 96, 300, 512
+    a = ob.bf16_to_f32(ob.randn_bf16(rng, (M, K)))
+    w_t = ob.bf16_to_f32(ob.randn_bf16(rng, (N, K), std=0.02))
+    qa, sa = fp8_ref.quantize_fp8(a)
+    qw, sw = fp8_ref.quantize_weight_128x128(w_t)
+    c = _gemm(qa, sa, qw, sw, dev, bn=128, out=torch.float32)
+    assert maxabs_rel(c, fp8_ref.gemv_prequant(qa, sa, qw, sw, bn=128)) <= TOL
+
+
+def test_block_scaled_matmul_c1(dev):
+    """Config 1: x [2048, 768] ~N(0,1), W [768, 3072] ~N(0, 0.02^2), seed 0."""
+    rng = np.random.default_rng(0)
+    x = ob.randn_bf16(rng, (2048, 768))
+    w = ob.randn_bf16(rng, (768, 3072), std=0.02)
+    y = fp8.block_scaled_matmul(to_dev(x, dev), to_dev(w, dev))
+    assert y.dtype == torch.bfloat16 and y.shape == (2048, 3072)
+    _, ref, (qa, sa), (qb, sb) = fp8_ref.fp8_forward(x, w)
+    err = maxabs_rel(y, ref)
+    assert err <= TOL
+    # the operands the forward quantizes are bit-exact (fp8.py:66,68)
+    qx, sx = fp8._quantize_to_fp8(to_dev(x, dev).float(), 128)
+    np.testing.assert_array_equal(u8(qx), qa)
+    assert same_scales(sx.cpu().numpy(), sa)
+    qw, sw = fp8.quantize_fp8(to_dev(w, dev), transpose=True)
+    np.testing.assert_array_equal(u8(qw), qb)
+    assert same_scales(sw.cpu().numpy(), sb)
+    bf = ob.bf16_to_f32(x).astype(np.float64) @ ob.bf16_to_f32(w).astype(np.float64)
+    print(f"C1 rel err vs oracle {err:.3e}, vs bf16 matmul {maxabs_rel(y, bf):.3e}")
+
+
+def test_block_scaled_matmul_leading_dims_and_errors(dev):
+    rng = np.random.default_rng(1)
+    x = ob.randn_bf16(rng, (2, 3, 256))
+    w = ob.randn_bf16(rng, (256, 64), std=0.02)
+    y = fp8.block_scaled_matmul(to_dev(x, dev), to_dev(w, dev))
+    assert y.shape == (2, 3, 64)
+    _, ref, _, _ = fp8_ref.fp8_forward(x, w)
+    assert maxabs_rel(y.reshape(6, 64), ref) <= TOL
+    with pytest.raises(ValueError, match="contracted-dim mismatch"):
+        fp8.block_scaled_matmul(to_dev(x, dev), to_dev(w[:128], dev))
+    with pytest.raises(ValueError, match="not divisible by block_k"):
+        fp8.block_scaled_matmul(to_dev(x[..., :200], dev), to_dev(w[:200], dev))
+
+
+def test_block_scaled_matmul_f32_inputs(dev):
+    rng = np.random.default_rng(8)
+    a = rng.standard_normal((64, 256)).astype(np.float32)
+    b = (0.02 * rng.standard_normal((256, 96))).astype(np.float32)
+    y = fp8.block_scaled_matmul(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev))
+    qa, sa = fp8_ref.quantize_fp8(a)
+    qb, sb = fp8_ref.quantize_fp8(np.ascontiguousarray(b.T))
+    assert maxabs_rel(y, fp8_ref.dequant_gemm_nt(qa, sa, qb, sb)) <= TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 128), (256, 384, 512), (512, 256, 768)])
+def test_fp8_backward(dev, M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    a_u = ob.randn_bf16(rng, (M, K))
+    b_u = ob.randn_bf16(rng, (K, N), std=0.02)
+    g_u = ob.randn_bf16(rng, (M, N), std=1e-3)
+    a = to_dev(a_u, dev).requires_grad_(True)
+    b = to_dev(b_u, dev).requires_grad_(True)
+    y = fp8.block_scaled_matmul(a, b)
+    y.backward(to_dev(g_u, dev))
+    dx_ref, dw_ref, ops = fp8_ref.fp8_backward_fp8(a_u, b_u, g_u)
+    assert a.grad.dtype == torch.bfloat16 and b.grad.dtype == torch.bfloat16
+    assert maxabs_rel(a.grad, dx_ref) <= TOL
+    assert maxabs_rel(b.grad, dw_ref) <= TOL
+    dx_bf, dw_bf = fp8_ref.fp8_backward_bf16(a_u, b_u, g_u)
+    print(f"bwd ({M},{N},{K}): dX err vs bf16 rule {maxabs_rel(a.grad, dx_bf):.3e}, "
+          f"dW {maxabs_rel(b.grad, dw_bf):.3e}")
+    # the gradient operands are quantized bit-exactly
+    qg, sg = fp8.quantize_fp8(to_dev(g_u, dev))
+    np.testing.assert_array_equal(u8(qg), ops["g_rows"][0])
+    qat, sat = fp8.quantize_fp8(to_dev(a_u, dev), transpose=True)
+    np.testing.assert_array_equal(u8(qat), ops["a_cols"][0])
+    assert same_scales(sat.cpu().numpy(), ops["a_cols"][1])
+
+
+def test_gemm_c3_full_size_sampled(dev):
+    """Config 3 forward+backward at full size; rows/columns sampled against the oracle."""
+    rng = np.random.default_rng(2)
+    M, K, N = 8192, 2048, 8192
+    a_u = ob.randn_bf16(rng, (M, K))
+    b_u = ob.randn_bf16(rng, (K, N), std=0.02)
+    g_u = ob.randn_bf16(rng, (M, N), std=1e-3)
+    a = to_dev(a_u, dev).requires_grad_(True)
+    b = to_dev(b_u, dev).requires_grad_(True)
+    y = fp8.block_scaled_matmul(a, b)
+    y.backward(to_dev(g_u, dev))
+    torch.cuda.synchronize()
+    rows = np.sort(rng.choice(M, 48, replace=False))
+    cols = np.sort(rng.choice(N, 48, replace=False))
+    a32, b32, g32 = (ob.bf16_to_f32(v) for v in (a_u, b_u, g_u))
+    qa, sa = fp8_ref.quantize_fp8(a32[rows])
+    qbt, sbt = fp8_ref.quantize_fp8(np.ascontiguousarray(b32.T))
+    assert maxabs_rel(y[torch.from_numpy(rows).to(dev)], fp8_ref.dequant_gemm_nt(qa, sa, qbt, sbt)) <= TOL
+    qg, sg = fp8_ref.quantize_fp8(g32[rows])
+    qb, sb = fp8_ref.quantize_fp8(b32)
+    assert maxabs_rel(a.grad[torch.from_numpy(rows).to(dev)], fp8_ref.dequant_gemm_nt(qg, sg, qb, sb)) <= TOL
+    qat, sat = fp8_ref.quantize_fp8(np.ascontiguousarray(a32.T))
+    qgt, sgt = fp8_ref.quantize_fp8(np.ascontiguousarray(g32[:, cols].T))
+    dw_ref = fp8_ref.dequant_gemm_nt(qat, sat, qgt, sgt)
+    assert maxabs_rel(b.grad[:, torch.from_numpy(cols).to(dev)], dw_ref) <= TOL

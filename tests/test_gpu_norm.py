@@ -1,0 +1,96 @@
+"""GPU parity of RMSNorm (kernels.py:30-33) and the fused norm -> FP8 quantize.
+
+Bar: y bf16 bit-exact against the oracle's _rms_norm_pure (f64 sum of f32
+squares, correctly rounded rsqrt, bf16 rounding after each op); q / scales
+bit-exact against quantizing that y (fp8.py:39-47).
+"""
+import numpy as np
+import pytest
+import torch
+
+import kernels
+from helpers import bf16_bits, f32_bits, maxabs_rel, same_scales, to_dev, u8
+from oracle import bf16 as ob
+from oracle import cbind, norm_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(rng, shape, outliers=True):
+    x = rng.standard_normal(shape)
+    if outliers:
+        mask = rng.random(shape) < 1e-3
+        x = np.where(mask, x * 50.0, x)
+    D = shape[-1]
+    g = 1.0 + 0.1 * rng.standard_normal(D)        # non-uniform gamma (debug_bf16_norm.py:499-503)
+    return ob.f32_to_bf16(x.astype(np.float32)), ob.f32_to_bf16(g.astype(np.float32))
+
+
+@pytest.mark.parametrize("shape", [(1, 128), (5, 768), (64, 2048), (3, 7, 2304), (33, 9216), (2, 16384)])
+def test_rms_norm_pure_bit_exact(dev, shape):
+    rng = np.random.default_rng(sum(shape))
+    x, g = _inputs(rng, shape)
+    y = kernels._rms_norm_pure(to_dev(x, dev), to_dev(g, dev), 1e-6)
+    assert y.shape == shape and y.dtype == torch.bfloat16
+    yo = norm_ref.rms_norm_pure(x, g, 1e-6)
+    np.testing.assert_array_equal(bf16_bits(y), yo)
+
+
+@pytest.mark.parametrize("D", [8, 200, 1000])
+def test_rms_norm_dims_not_multiple_of_128(dev, D):
+    rng = np.random.default_rng(D)
+    x, g = _inputs(rng, (6, D))
+    y = kernels.rms_norm(to_dev(x, dev), to_dev(g, dev), 1e-5)
+    np.testing.assert_array_equal(bf16_bits(y), norm_ref.rms_norm_pure(x, g, 1e-5))
+
+
+@pytest.mark.parametrize("shape", [(4, 128), (64, 2048), (2, 5, 2304), (17, 4096)])
+def test_rms_norm_fp8_bit_exact(dev, shape):
+    rng = np.random.default_rng(sum(shape) + 1)
+    x, g = _inputs(rng, shape)
+    y, q, s = kernels.rms_norm_fp8(to_dev(x, dev), to_dev(g, dev), 1e-6)
+    yo, qo, so = norm_ref.rms_norm_fp8(x, g, 1e-6)
+    np.testing.assert_array_equal(bf16_bits(y), yo)
+    np.testing.assert_array_equal(u8(q), qo)
+    assert same_scales(s.cpu().numpy(), so)
+
+
+def test_rms_norm_fp8_c2_full_size(dev):
+    """Config 2: x bf16 [8, 1024, 2048] with 0.1% x50 outliers, gamma 1+N(0,0.1^2), eps 1e-6, seed 1."""
+    rng = np.random.default_rng(1)
+    x, g = _inputs(rng, (8, 1024, 2048))
+    y, q, s = kernels.rms_norm_fp8(to_dev(x, dev), to_dev(g, dev), 1e-6)
+    yo, qo, so = cbind.rms_norm_quant_bf16(x, g, 1e-6)
+    np.testing.assert_array_equal(bf16_bits(y).reshape(-1, 2048), yo)
+    np.testing.assert_array_equal(u8(q).reshape(-1, 2048), qo)
+    np.testing.assert_array_equal(f32_bits(s).reshape(-1, 16), so.view(np.uint32))
+    # fp32 tolerance bar against the single-rounding arithmetic too (kernels.py:49-53)
+    y1 = norm_ref.rms_norm_single_rounding(x[0, :64], g, 1e-6)
+    assert maxabs_rel(ob.bf16_to_f32(bf16_bits(y)[0, :64]), ob.bf16_to_f32(y1)) <= 1e-2
+
+
+def test_rms_norm_special_rows(dev):
+    D = 256
+    rows = np.stack([
+        np.zeros(D), np.full(D, 3.0), -np.full(D, 1e-20), np.full(D, 1e30),
+        np.where(np.arange(D) == 3, 1e4, 1e-4),
+    ]).astype(np.float32)
+    x = ob.f32_to_bf16(rows)
+    g = ob.f32_to_bf16(np.linspace(0.5, 1.5, D).astype(np.float32))
+    y, q, s = kernels.rms_norm_fp8(to_dev(x, dev), to_dev(g, dev), 1e-6)
+    yo, qo, so = norm_ref.rms_norm_fp8(x, g, 1e-6)
+    np.testing.assert_array_equal(bf16_bits(y), yo)
+    np.testing.assert_array_equal(u8(q), qo)
+    assert same_scales(s.cpu().numpy(), so)
+
+
+def test_rms_norm_errors(dev):
+    x = torch.zeros((2, 100), dtype=torch.bfloat16, device=dev)
+    g = torch.ones(100, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError, match="multiple of 8"):
+        kernels.rms_norm(x, g, 1e-6)
+    with pytest.raises(ValueError, match="not divisible by block_k"):
+        kernels.rms_norm_fp8(torch.zeros((2, 200), dtype=torch.bfloat16, device=dev),
+                             torch.ones(200, dtype=torch.bfloat16, device=dev), 1e-6)
+    with pytest.raises(TypeError):
+        kernels.rms_norm(x.float(), g, 1e-6)

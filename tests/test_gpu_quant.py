@@ -1,0 +1,133 @@
+"""GPU parity of the quantizers (fp8.py:39-47, fp8.py:68) against the CPU oracle.
+
+Bar: e4m3fn bytes and fp32 scales bit-exact (NaN scales compare as NaN).
+"""
+import numpy as np
+import pytest
+import torch
+
+import fp8
+from helpers import bf16_bits, f32_bits, same_scales, to_dev, u8
+from oracle import bf16 as ob
+from oracle import cbind, fp8_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _special_rows(rng, K):
+    """Rows exercising the edge cases of fp8.py:42-46."""
+    rows = []
+    rows.append(np.zeros(K, np.float32))                                  # all zero -> s = 1e-30
+    r = np.zeros(K, np.float32); r[::2] = -0.0; rows.append(r)            # -0 -> 0x80
+    rows.append(np.ones(K, np.float32))                                   # ones KAT
+    r = rng.standard_normal(K).astype(np.float32); r[5] = np.nan; rows.append(r)      # NaN block
+    r = rng.standard_normal(K).astype(np.float32); r[7] = np.inf; rows.append(r)      # +inf block
+    r = rng.standard_normal(K).astype(np.float32); r[9] = -np.inf; r[10] = np.inf; rows.append(r)
+    r = (rng.standard_normal(K) * 1e-38).astype(np.float32); rows.append(r)           # subnormal-ish
+    r = (rng.standard_normal(K) * 1e-30).astype(np.float32); rows.append(r)           # scale floor
+    r = (rng.standard_normal(K) * 3e38).astype(np.float32); rows.append(r)            # near max
+    r = np.full(K, 2.0 ** -133, np.float32); r[0] = 1.0; rows.append(r)               # bf16 min subnormal
+    return ob.f32_to_bf16(np.stack(rows))
+
+
+def _check_rows(x_u16, dev):
+    q, s = fp8.quantize_fp8(to_dev(x_u16, dev))
+    qo, so = fp8_ref.quantize_fp8(ob.bf16_to_f32(x_u16))
+    np.testing.assert_array_equal(u8(q), qo)
+    assert same_scales(s.cpu().numpy(), so)
+
+
+@pytest.mark.parametrize("shape", [(1, 128), (3, 384), (17, 256), (2048, 768), (130, 2304)])
+def test_quantize_rows_random(dev, shape):
+    rng = np.random.default_rng(hash(shape) % 2**32)
+    x = ob.randn_bf16(rng, shape)
+    x[..., 3] = ob.f32_to_bf16(np.float32(60.0))            # outlier in the first block
+    _check_rows(x, dev)
+
+
+def test_quantize_rows_special_values(dev):
+    rng = np.random.default_rng(7)
+    _check_rows(_special_rows(rng, 256), dev)
+
+
+def test_quantize_rows_every_bf16_value(dev):
+    """All 65536 bf16 patterns, grouped 128 per block in several orders."""
+    allv = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    rng = np.random.default_rng(11)
+    for perm in (allv, rng.permutation(allv), np.sort(allv)[::-1].copy()):
+        _check_rows(perm.reshape(-1, 128), dev)
+
+
+def test_quantize_rows_f32_input(dev):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((64, 512)) * np.exp(rng.standard_normal((64, 512)))).astype(np.float32)
+    x[0, :128] = 0.0
+    q, s = fp8.quantize_fp8(torch.from_numpy(x).to(dev))
+    qo, so = fp8_ref.quantize_fp8(x)
+    np.testing.assert_array_equal(u8(q), qo)
+    assert same_scales(s.cpu().numpy(), so)
+
+
+@pytest.mark.parametrize("shape", [(128, 8), (256, 72), (768, 3072), (384, 200)])
+def test_quantize_cols_transposed(dev, shape):
+    """fp8.py:68: quantize b.T of b (K, N) along K."""
+    rng = np.random.default_rng(sum(shape))
+    b = ob.randn_bf16(rng, shape, std=0.02)
+    q, s = fp8.quantize_fp8(to_dev(b, dev), transpose=True)
+    qo, so = fp8_ref.quantize_fp8(np.ascontiguousarray(ob.bf16_to_f32(b).T))
+    np.testing.assert_array_equal(u8(q), qo)
+    assert same_scales(s.cpu().numpy(), so)
+
+
+def test_quantize_cols_special_values(dev):
+    rng = np.random.default_rng(5)
+    b = np.ascontiguousarray(_special_rows(rng, 128).T)           # (128, 10) -> pad cols to 16
+    b = np.concatenate([b, ob.randn_bf16(rng, (128, 6))], axis=1)
+    q, s = fp8.quantize_fp8(to_dev(b, dev), transpose=True)
+    qo, so = fp8_ref.quantize_fp8(np.ascontiguousarray(ob.bf16_to_f32(b).T))
+    np.testing.assert_array_equal(u8(q), qo)
+    assert same_scales(s.cpu().numpy(), so)
+
+
+def test_quantize_full_size_c3_operands(dev):
+    """C3 operands at full size, checked against the C oracle."""
+    rng = np.random.default_rng(2)
+    x = ob.randn_bf16(rng, (8192, 2048))
+    w = ob.randn_bf16(rng, (2048, 8192), std=0.02)
+    qx, sx = fp8.quantize_fp8(to_dev(x, dev))
+    qo, so = cbind.quantize_rows_bf16(x)
+    np.testing.assert_array_equal(u8(qx), qo)
+    np.testing.assert_array_equal(f32_bits(sx), so.view(np.uint32))
+    qw, sw = fp8.quantize_fp8(to_dev(w, dev), transpose=True)
+    qo, so = cbind.quantize_cols_bf16(w)
+    np.testing.assert_array_equal(u8(qw), qo)
+    np.testing.assert_array_equal(f32_bits(sw), so.view(np.uint32))
+
+
+def test_quantize_deterministic(dev):
+    rng = np.random.default_rng(9)
+    x = to_dev(ob.randn_bf16(rng, (512, 1024)), dev)
+    q1, s1 = fp8.quantize_fp8(x)
+    q2, s2 = fp8.quantize_fp8(x)
+    assert torch.equal(q1.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(s1, s2)
+
+
+def test_weight_128x128(dev):
+    rng = np.random.default_rng(4)
+    w = ob.randn_bf16(rng, (512, 300), std=0.02)
+    wq, ws, bn = fp8.quantize_weight(to_dev(w, dev), layout="128x128")
+    assert bn == 128
+    qo, so = fp8_ref.quantize_weight_128x128(np.ascontiguousarray(ob.bf16_to_f32(w).T))
+    np.testing.assert_array_equal(u8(wq), qo)
+    np.testing.assert_array_equal(f32_bits(ws), so.view(np.uint32))
+
+
+def test_errors(dev):
+    x = torch.zeros((4, 200), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError, match="not divisible by block_k"):
+        fp8.quantize_fp8(x)
+    with pytest.raises(NotImplementedError):
+        fp8.quantize_fp8(torch.zeros((4, 256), dtype=torch.bfloat16, device=dev), block_k=64)
+    q, s = fp8.quantize_fp8(torch.zeros((0, 256), dtype=torch.bfloat16, device=dev))
+    assert q.shape == (0, 256) and s.shape == (0, 2)
+    assert bf16_bits is not None

@@ -1,0 +1,58 @@
+"""Builds libtg_fp8.so (the C ABI of include/tg_fp8.h) for gfx950 with hipcc.
+
+Usage: ``python train-gpt_amd/build.py`` (or ``__graft_entry__.build()``).
+Each ``csrc/*.hip`` compiles to an object in ``csrc/_build`` in parallel; the
+objects link into ``train-gpt_amd/libtg_fp8.so``.  hipcc cross-compiles for
+gfx950 without a GPU.
+"""
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OBJDIR = os.path.join(CSRC, "_build")
+LIB = os.path.join(HERE, "libtg_fp8.so")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+SOURCES = ["quant.hip", "rmsnorm.hip", "gemm_fp8.hip"]
+
+# -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 (plain f32 VALU only).
+# -ffp-contract=off: every multiply/add in the numeric contract stays a single
+#   IEEE operation unless written as an explicit fma.
+# correctly rounded f32 divide/sqrt: the quantizer's x / s is an IEEE divide.
+FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",
+    "-fhip-fp32-correctly-rounded-divide-sqrt", "-Wall", "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _compile(src: str) -> str:
+    obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
+    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
+    return obj
+
+
+def build_library(verbose: bool = False) -> str:
+    os.makedirs(OBJDIR, exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+        objs = list(ex.map(_compile, SOURCES))
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+if __name__ == "__main__":
+    build_library(verbose=True)
+    sys.exit(0)

@@ -1,0 +1,442 @@
+// Block-scaled FP8 GEMM ("NT": both operands K-contiguous) for gfx950.
+//
+// Computes what jax.nn.scaled_matmul does at /root/reference/fp8.py:70-78:
+//   c[m, n] = bf16( sum_kb sa[m, kb] * sb[n, kb] * sum_{k in kb} qa[m, k] * qb[n, k] )
+// with e4m3fn operands and one fp32 scale per 128-wide K block.
+//
+// Design (gfx950, wave64):
+//   * v_mfma_f32_16x16x128_f8f6f4: one MFMA consumes exactly one 128-wide
+//     scale block, so its 16x16 fp32 result P is promoted immediately:
+//     acc = fma(P, sa[m] * sb[n], acc).  The promotion is VALU work that
+//     overlaps the MFMA pipe of the other wave on the SIMD.
+//   * Workgroup tile BM x BN x 128 (2 x 2 waves, each TM x TN MFMA tiles),
+//     staged through LDS with two buffers: while the waves run the MFMAs of
+//     K block kb from one buffer, the next block's bytes and scales travel
+//     HBM -> registers and are written to the other buffer; one barrier per
+//     K block.  16-byte chunks are XOR-swizzled by row so the fragment reads
+//     (16 rows x 32 B per 16 lanes) spread over all LDS banks.
+//   * Tile order: consecutive workgroup ids go to different XCDs, so ids are
+//     remapped to give each XCD a contiguous range of tiles, and within that
+//     range tiles are walked in groups of 8 tile-rows for L2 reuse of B.
+#include "tg_device.h"
+#include "tg_host.h"
+
+namespace tg {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4f mfma_f8_16x16x128(const v8i& a, const v8i& b, const v4f& c) {
+  // Format codes 0/0 = FP8 E4M3 for A and B; zero scale operands select the
+  // unscaled v_mfma_f32_16x16x128_f8f6f4.
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+__device__ __forceinline__ v8i as_v8i(const uint4& lo, const uint4& hi) {
+  v8i r;
+  r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+  r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+  return r;
+}
+
+// XCD-aware, grouped tile order.  Returns the (tile_m, tile_n) of workgroup bid.
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int ntiles = tiles_m * tiles_n;
+  const int xcd = bid & 7, slot = bid >> 3;
+  const int q = ntiles >> 3, rem = ntiles & 7;
+  const int t = xcd * q + min(xcd, rem) + slot;
+  constexpr int GROUP = 8;
+  const int per_group = GROUP * tiles_n;
+  const int g = t / per_group;
+  const int first_m = g * GROUP;
+  const int gsize = min(tiles_m - first_m, GROUP);
+  const int in_g = t - g * per_group;
+  tm = first_m + in_g % gsize;
+  tn = in_g / gsize;
+}
+
+template <int TM, int TN, int BNS, bool OUT_F32>
+__global__ __launch_bounds__(256, 2) void gemm_fp8_nt_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ SA, const uint8_t* __restrict__ B,
+    const float* __restrict__ SB, void* __restrict__ C, int M, int N, int K, int tiles_m,
+    int tiles_n) {
+  constexpr int BM = 2 * TM * 16, BN = 2 * TN * 16;
+  constexpr int LA = BM / 32, LB = BN / 32;          // 16-byte chunks per thread per K block
+  constexpr int STAGE = (BM + BN) * 8;               // uint4 per stage (128 B per row)
+  static_assert(BM + BN <= 256, "one scale per thread per K block");
+  extern __shared__ uint4 smem[];
+  float* sscale = reinterpret_cast<float*>(smem + 2 * STAGE);   // [2][BM + BN]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int tmi, tni;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tmi, tni);
+  const int m0 = tmi * BM, n0 = tni * BN;
+  const int nkb = K >> 7;
+
+  // ---- global -> register staging of one K block ----
+  uint4 ra[LA], rb[LB];
+  float rs = 0.0f;
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int u = 0; u < LA; ++u) {
+      const int id = tid + 256 * u, row = id >> 3, ch = id & 7;
+      const int m = m0 + row;
+      ra[u] = m < M ? *reinterpret_cast<const uint4*>(A + (int64_t)m * K + kb * 128 + ch * 16)
+                    : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < LB; ++u) {
+      const int id = tid + 256 * u, row = id >> 3, ch = id & 7;
+      const int n = n0 + row;
+      rb[u] = n < N ? *reinterpret_cast<const uint4*>(B + (int64_t)n * K + kb * 128 + ch * 16)
+                    : make_uint4(0, 0, 0, 0);
+    }
+    if (tid < BM) {
+      const int m = m0 + tid;
+      rs = m < M ? SA[(int64_t)m * nkb + kb] : 0.0f;
+    } else if (tid < BM + BN) {
+      const int n = n0 + tid - BM;
+      rs = n < N ? SB[(int64_t)(n / BNS) * nkb + kb] : 0.0f;
+    }
+  };
+  auto lstore = [&](int stage) {
+    uint4* sa = smem + stage * STAGE;
+    uint4* sb = sa + BM * 8;
+#pragma unroll
+    for (int u = 0; u < LA; ++u) {
+      const int id = tid + 256 * u, row = id >> 3, ch = id & 7;
+      sa[row * 8 + (ch ^ (row & 7))] = ra[u];
+    }
+#pragma unroll
+    for (int u = 0; u < LB; ++u) {
+      const int id = tid + 256 * u, row = id >> 3, ch = id & 7;
+      sb[row * 8 + (ch ^ (row & 7))] = rb[u];
+    }
+    if (tid < BM + BN) sscale[stage * (BM + BN) + tid] = rs;
+  };
+
+  v4f acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+
+  const int fr = lane & 15, fg = lane >> 4;     // fragment row, 32-byte K group
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int cur = kb & 1;
+    if (kb + 1 < nkb) gload(kb + 1);
+
+    const uint4* sa = smem + cur * STAGE;
+    const uint4* sb = sa + BM * 8;
+    const float* ssa = sscale + cur * (BM + BN);
+    const float* ssb = ssa + BM;
+
+    v8i bf[TN];
+    float sbv[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int r = wn * TN * 16 + j * 16 + fr;
+      bf[j] = as_v8i(sb[r * 8 + ((2 * fg) ^ (r & 7))], sb[r * 8 + ((2 * fg + 1) ^ (r & 7))]);
+      sbv[j] = ssb[r];
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = wm * TM * 16 + i * 16 + fr;
+      const v8i af = as_v8i(sa[r * 8 + ((2 * fg) ^ (r & 7))], sa[r * 8 + ((2 * fg + 1) ^ (r & 7))]);
+      const float4 sav = *reinterpret_cast<const float4*>(ssa + wm * TM * 16 + i * 16 + 4 * fg);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const v4f p = mfma_f8_16x16x128(af, bf[j], zero);
+        acc[i][j][0] = __builtin_fmaf(p[0], sav.x * sbv[j], acc[i][j][0]);
+        acc[i][j][1] = __builtin_fmaf(p[1], sav.y * sbv[j], acc[i][j][1]);
+        acc[i][j][2] = __builtin_fmaf(p[2], sav.z * sbv[j], acc[i][j][2]);
+        acc[i][j][3] = __builtin_fmaf(p[3], sav.w * sbv[j], acc[i][j][3]);
+      }
+    }
+    if (kb + 1 < nkb) lstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds rows 4*fg + r, column fr of each 16x16 tile ----
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn * TN * 16 + j * 16 + fr;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * TM * 16 + i * 16 + 4 * fg + r;
+        if (m < M && n < N) {
+          if (OUT_F32)
+            reinterpret_cast<float*>(C)[(int64_t)m * N + n] = acc[i][j][r];
+          else
+            reinterpret_cast<__bf16*>(C)[(int64_t)m * N + n] = (__bf16)acc[i][j][r];
+        }
+      }
+    }
+}
+
+template <int TM, int TN, int BNS, bool OUT_F32>
+static int launch_gemm_cfg(const uint8_t* a_q, const float* a_s, const uint8_t* b_q,
+                           const float* b_s, void* c, int M, int N, int K, hipStream_t st) {
+  constexpr int BM = 2 * TM * 16, BN = 2 * TN * 16;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const size_t lds = (size_t)2 * (BM + BN) * 128 + (size_t)2 * (BM + BN) * 4;
+  auto kern = gemm_fp8_nt_kernel<TM, TN, BNS, OUT_F32>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+      return check_launch("gemm_fp8 (set LDS size)");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), lds, st, a_q, a_s, b_q,
+                     b_s, c, M, N, K, tiles_m, tiles_n);
+  return check_launch("gemm_fp8_nt");
+}
+
+int launch_gemm_fp8(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s,
+                    int b_scale_bn, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
+                    hipStream_t st) {
+  if (M == 0 || N == 0) return TG_OK;
+  const int m = (int)M, n = (int)N, k = (int)K;
+  const bool f32 = c_dtype == TG_DTYPE_F32;
+  if (b_scale_bn == 1)
+    return f32 ? launch_gemm_cfg<4, 4, 1, true>(a_q, a_s, b_q, b_s, c, m, n, k, st)
+               : launch_gemm_cfg<4, 4, 1, false>(a_q, a_s, b_q, b_s, c, m, n, k, st);
+  return f32 ? launch_gemm_cfg<4, 4, 128, true>(a_q, a_s, b_q, b_s, c, m, n, k, st)
+             : launch_gemm_cfg<4, 4, 128, false>(a_q, a_s, b_q, b_s, c, m, n, k, st);
+}
+
+// ---------------------------------------------------------------------------
+// Decode-shape GEMM (M <= 16 * MT) with a pre-quantized weight.  HBM-bound on
+// W: each workgroup streams NT x 16 weight rows once; its 4 waves split the K
+// blocks and issue all of their weight loads before the first MFMA, then
+// reduce the four partial tiles through LDS.  The MFMA takes W as the A
+// operand (16 weight rows) and x as B (16 activation rows).
+// ---------------------------------------------------------------------------
+template <int NT, int MT, int KCH>
+__global__ __launch_bounds__(256) void gemv_fp8_kernel(const uint8_t* __restrict__ XQ,
+                                                       const float* __restrict__ XS,
+                                                       const uint8_t* __restrict__ WQ,
+                                                       const float* __restrict__ WS, int bns,
+                                                       __bf16* __restrict__ out, int M, int N,
+                                                       int K) {
+  __shared__ v4f red[3][NT][MT][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 15, fg = lane >> 4;
+  const int n0 = blockIdx.x * (NT * 16);
+  const int nkb = K >> 7;
+  const int kb_lo = (wave * nkb) >> 2, kb_hi = ((wave + 1) * nkb) >> 2;
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  v4f acc[NT][MT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = zero;
+
+  for (int kb0 = kb_lo; kb0 < kb_hi; kb0 += KCH) {
+    uint4 w[KCH][NT][2];
+#pragma unroll
+    for (int c = 0; c < KCH; ++c)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int n = n0 + t * 16 + fr, kb = kb0 + c;
+        if (kb < kb_hi && n < N) {
+          const uint4* p = reinterpret_cast<const uint4*>(WQ + (int64_t)n * K + kb * 128 + fg * 32);
+          w[c][t][0] = ldg_stream(p);
+          w[c][t][1] = ldg_stream(p + 1);
+        } else {
+          w[c][t][0] = w[c][t][1] = make_uint4(0, 0, 0, 0);
+        }
+      }
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const int kb = kb0 + c;
+      if (kb < kb_hi) {
+        float sw[NT][4];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int n = n0 + t * 16 + 4 * fg + r;
+            sw[t][r] = n < N ? WS[(int64_t)(n / bns) * nkb + kb] : 0.0f;
+          }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int m = mt * 16 + fr;
+          uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
+          float sx = 0.0f;
+          if (m < M) {
+            const uint4* p = reinterpret_cast<const uint4*>(XQ + (int64_t)m * K + kb * 128 + fg * 32);
+            x0 = p[0];
+            x1 = p[1];
+            sx = XS[(int64_t)m * nkb + kb];
+          }
+          // the x scale of activation row m sits in the lane whose column is m
+          const v8i xb = as_v8i(x0, x1);
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            const v4f p = mfma_f8_16x16x128(as_v8i(w[c][t][0], w[c][t][1]), xb, zero);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[t][mt][r] = __builtin_fmaf(p[r], sw[t][r] * sx, acc[t][mt][r]);
+          }
+        }
+      }
+    }
+  }
+
+  if (wave > 0) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) red[wave - 1][t][mt][lane] = acc[t][mt];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        v4f s = acc[t][mt];
+#pragma unroll
+        for (int w2 = 0; w2 < 3; ++w2) {
+          const v4f o = red[w2][t][mt][lane];
+          s[0] += o[0]; s[1] += o[1]; s[2] += o[2]; s[3] += o[3];
+        }
+        const int m = mt * 16 + fr;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int n = n0 + t * 16 + 4 * fg + r;
+          if (m < M && n < N) out[(int64_t)m * N + n] = (__bf16)s[r];
+        }
+      }
+  }
+}
+
+}  // namespace tg
+
+using namespace tg;
+
+static int check_gemm_args(const char* who, int64_t M, int64_t N, int64_t K, int block_k, int bns) {
+  if (block_k != 128) return einval("block_k must be 128");
+  if (M < 0 || N < 0 || K <= 0) return einval("bad GEMM shape");
+  if (K % block_k) return einval("K not divisible by block_k");
+  if (M > 0x7FFFFFFF || N > 0x7FFFFFFF || K > 0x7FFFFFFF) return einval("GEMM dimension too large");
+  if (bns != 1 && bns != 128) return einval("scale block along N must be 1 or 128");
+  (void)who;
+  return TG_OK;
+}
+
+extern "C" int tg_gemm_fp8_nt(const uint8_t* a_q, const float* a_s, const uint8_t* b_q,
+                              const float* b_s, int b_scale_bn, void* c, int c_dtype, int64_t M,
+                              int64_t N, int64_t K, int block_k, void* stream) {
+  TG_TRY(check_gemm_args("gemm_fp8_nt", M, N, K, block_k, b_scale_bn));
+  if (c_dtype != TG_DTYPE_BF16 && c_dtype != TG_DTYPE_F32) return einval("gemm_fp8_nt: bad c_dtype");
+  if (M == 0 || N == 0) return TG_OK;
+  if (!a_q || !a_s || !b_q || !b_s || !c) return einval("gemm_fp8_nt: null pointer");
+  if (!aligned(a_q, 16) || !aligned(b_q, 16)) return einval("gemm_fp8_nt: operands must be 16-byte aligned");
+  return launch_gemm_fp8(a_q, a_s, b_q, b_s, b_scale_bn, c, c_dtype, M, N, K, as_stream(stream));
+}
+
+static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+extern "C" size_t tg_block_scaled_matmul_workspace(int64_t M, int64_t N, int64_t K, int block_k) {
+  if (block_k <= 0 || M < 0 || N < 0 || K < 0) return 0;
+  const size_t nkb = (size_t)(K / block_k);
+  return align256((size_t)M * K) + align256((size_t)M * nkb * 4) + align256((size_t)N * K) +
+         align256((size_t)N * nkb * 4);
+}
+
+extern "C" int tg_block_scaled_matmul(const void* a, const void* b, void* out, int64_t M,
+                                      int64_t N, int64_t K, int block_k, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  TG_TRY(check_gemm_args("block_scaled_matmul", M, N, K, block_k, 1));
+  if (N % 8) return einval("block_scaled_matmul: N must be a multiple of 8");
+  if (M == 0 || N == 0) return TG_OK;
+  if (!a || !b || !out || !workspace) return einval("block_scaled_matmul: null pointer");
+  if (workspace_bytes < tg_block_scaled_matmul_workspace(M, N, K, block_k))
+    return einval("block_scaled_matmul: workspace too small");
+  if (!aligned(workspace, 256) || !aligned(a, 16) || !aligned(b, 16))
+    return einval("block_scaled_matmul: a, b must be 16-byte and workspace 256-byte aligned");
+  hipStream_t st = as_stream(stream);
+  const int64_t nkb = K / 128;
+  uint8_t* p = reinterpret_cast<uint8_t*>(workspace);
+  uint8_t* qa = p;                 p += align256((size_t)M * K);
+  float* sa = reinterpret_cast<float*>(p);   p += align256((size_t)M * nkb * 4);
+  uint8_t* qb = p;                 p += align256((size_t)N * K);
+  float* sb = reinterpret_cast<float*>(p);
+  TG_TRY(launch_quant_rows(a, TG_DTYPE_BF16, M, K, qa, sa, st));     // fp8.py:66
+  TG_TRY(launch_quant_cols(b, K, N, qb, sb, st));                     // fp8.py:68
+  return launch_gemm_fp8(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, K, st);   // fp8.py:70-78
+}
+
+extern "C" size_t tg_block_scaled_matmul_bwd_workspace(int64_t M, int64_t N, int64_t K, int block_k) {
+  if (block_k <= 0 || M < 0 || N < 0 || K < 0) return 0;
+  const size_t mkb = (size_t)(M / block_k), nkb = (size_t)(N / block_k);
+  return align256((size_t)M * N) + align256((size_t)M * nkb * 4) +   // g along N
+         align256((size_t)K * N) + align256((size_t)K * nkb * 4) +   // b along N
+         align256((size_t)K * M) + align256((size_t)K * mkb * 4) +   // a.T along M
+         align256((size_t)N * M) + align256((size_t)N * mkb * 4);    // g.T along M
+}
+
+extern "C" int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, const void* g,
+                                              void* da, void* db, int64_t M, int64_t N, int64_t K,
+                                              int block_k, void* workspace,
+                                              size_t workspace_bytes, void* stream) {
+  TG_TRY(check_gemm_args("block_scaled_matmul_bwd_fp8", M, N, K, block_k, 1));
+  if (M % 128 || N % 128) return einval("block_scaled_matmul_bwd_fp8: M and N must be multiples of 128");
+  if (M == 0 || N == 0) return TG_OK;
+  if (!a || !b || !g || !da || !db || !workspace) return einval("block_scaled_matmul_bwd_fp8: null pointer");
+  if (workspace_bytes < tg_block_scaled_matmul_bwd_workspace(M, N, K, block_k))
+    return einval("block_scaled_matmul_bwd_fp8: workspace too small");
+  if (!aligned(workspace, 256) || !aligned(a, 16) || !aligned(b, 16) || !aligned(g, 16))
+    return einval("block_scaled_matmul_bwd_fp8: inputs must be 16-byte and workspace 256-byte aligned");
+  hipStream_t st = as_stream(stream);
+  const int64_t mkb = M / 128, nkb = N / 128;
+  uint8_t* p = reinterpret_cast<uint8_t*>(workspace);
+  uint8_t* qg = p;    p += align256((size_t)M * N);
+  float* sg = reinterpret_cast<float*>(p);    p += align256((size_t)M * nkb * 4);
+  uint8_t* qb = p;    p += align256((size_t)K * N);
+  float* sb = reinterpret_cast<float*>(p);    p += align256((size_t)K * nkb * 4);
+  uint8_t* qat = p;   p += align256((size_t)K * M);
+  float* sat = reinterpret_cast<float*>(p);   p += align256((size_t)K * mkb * 4);
+  uint8_t* qgt = p;   p += align256((size_t)N * M);
+  float* sgt = reinterpret_cast<float*>(p);
+  TG_TRY(launch_quant_rows(g, TG_DTYPE_BF16, M, N, qg, sg, st));
+  TG_TRY(launch_quant_rows(b, TG_DTYPE_BF16, K, N, qb, sb, st));
+  TG_TRY(launch_gemm_fp8(qg, sg, qb, sb, 1, da, TG_DTYPE_BF16, M, K, N, st));    // dX = g . b.T
+  TG_TRY(launch_quant_cols(a, M, K, qat, sat, st));
+  TG_TRY(launch_quant_cols(g, M, N, qgt, sgt, st));
+  return launch_gemm_fp8(qat, sat, qgt, sgt, 1, db, TG_DTYPE_BF16, K, N, M, st);  // dW = a.T . g
+}
+
+extern "C" int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* w_q,
+                           const float* w_s, int w_scale_bn, void* out, int64_t M, int64_t N,
+                           int64_t K, int block_k, void* stream) {
+  TG_TRY(check_gemm_args("gemv_fp8", M, N, K, block_k, w_scale_bn));
+  if (M > 64) return einval("gemv_fp8: M must be <= 64 (use tg_gemm_fp8_nt)");
+  if (M == 0 || N == 0) return TG_OK;
+  if (!x_q || !x_s || !w_q || !w_s || !out) return einval("gemv_fp8: null pointer");
+  if (!aligned(x_q, 16) || !aligned(w_q, 16)) return einval("gemv_fp8: operands must be 16-byte aligned");
+  hipStream_t st = as_stream(stream);
+  const int m = (int)M, n = (int)N, k = (int)K;
+  auto o = reinterpret_cast<__bf16*>(out);
+  if (M <= 16) {
+    hipLaunchKernelGGL((gemv_fp8_kernel<2, 1, 8>), dim3((unsigned)((N + 31) / 32)), dim3(256), 0, st,
+                       x_q, x_s, w_q, w_s, w_scale_bn, o, m, n, k);
+  } else if (M <= 32) {
+    hipLaunchKernelGGL((gemv_fp8_kernel<2, 2, 8>), dim3((unsigned)((N + 31) / 32)), dim3(256), 0, st,
+                       x_q, x_s, w_q, w_s, w_scale_bn, o, m, n, k);
+  } else {
+    hipLaunchKernelGGL((gemv_fp8_kernel<2, 4, 4>), dim3((unsigned)((N + 31) / 32)), dim3(256), 0, st,
+                       x_q, x_s, w_q, w_s, w_scale_bn, o, m, n, k);
+  }
+  return check_launch("gemv_fp8");
+}

@@ -1,0 +1,376 @@
+// FP8 e4m3fn quantization kernels for gfx950 (HBM-bound byte work).
+//
+//   quant_rows_kernel   _quantize_to_fp8 along the last axis (fp8.py:39-47)
+//   quant_cols_kernel   _quantize_to_fp8 of x.T (fp8.py:68), transposed through LDS
+//   quant_w128_kernel   128x128-tile weight quantization for the GEMV format
+//   selftest_cvt_kernel hardware e4m3fn convert vs the integer encoder
+//
+// Layout: a 128-element scale block is 16 lanes x 8 elements (one 16-byte
+// load per lane), i.e. exactly one DPP row, so the block amax is four DPP
+// max steps with no LDS traffic.
+#include <stdarg.h>
+#include <string.h>
+
+#include "tg_device.h"
+#include "tg_host.h"
+
+namespace tg {
+
+static thread_local char g_err[512];
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+// ---------------------------------------------------------------------------
+// Row quantization.  A "chunk" is 8 consecutive elements; chunks 16c..16c+15
+// form scale block c.  Each thread handles UNROLL chunks spaced 256 apart so
+// that UNROLL independent 16-byte loads are in flight per lane.
+// ---------------------------------------------------------------------------
+template <bool F32_IN>
+__device__ __forceinline__ void load_chunk(const void* __restrict__ x, int64_t c, bool ok,
+                                           float (&v)[8]) {
+  if (F32_IN) {
+    const uint4* p = reinterpret_cast<const uint4*>(x) + 2 * c;
+    uint4 a = ok ? ldg_stream(p) : make_uint4(0, 0, 0, 0);
+    uint4 b = ok ? ldg_stream(p + 1) : make_uint4(0, 0, 0, 0);
+    v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
+    v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+    v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y);
+    v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
+  } else {
+    const uint4* p = reinterpret_cast<const uint4*>(x) + c;
+    uint4 a = ok ? ldg_stream(p) : make_uint4(0, 0, 0, 0);
+    v[0] = bf16lo(a.x); v[1] = bf16hi(a.x); v[2] = bf16lo(a.y); v[3] = bf16hi(a.y);
+    v[4] = bf16lo(a.z); v[5] = bf16hi(a.z); v[6] = bf16lo(a.w); v[7] = bf16hi(a.w);
+  }
+}
+
+// Quantize 8 values of one block with scale sc; bf16-valued inputs use the
+// exact reciprocal-refinement divide, f32 inputs the IEEE divide.
+template <bool BF16_VALUES>
+__device__ __forceinline__ uint2 quant8(const float (&v)[8], float sc) {
+  Divider d(sc);
+  uint2 out;
+  if (d.fast) {
+    float t[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) t[i] = BF16_VALUES ? d.div(v[i]) : v[i] / sc;
+    out.x = e4m3x4(t[0], t[1], t[2], t[3]);
+    out.y = e4m3x4(t[4], t[5], t[6], t[7]);
+  } else {
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = e4m3_nonfinite_scale(v[i], sc);
+    out.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+    out.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+  }
+  return out;
+}
+
+__device__ __forceinline__ uint32_t absmax8(const float (&v)[8]) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m = max(m, __float_as_uint(v[i]) & 0x7FFFFFFFu);
+  return m;
+}
+
+template <bool F32_IN, int UNROLL>
+__global__ __launch_bounds__(256) void quant_rows_kernel(const void* __restrict__ x,
+                                                         uint2* __restrict__ q,
+                                                         float* __restrict__ s,
+                                                         int64_t nchunks) {
+  const int64_t base = (int64_t)blockIdx.x * (256 * UNROLL) + threadIdx.x;
+  float v[UNROLL][8];
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    int64_t c = base + u * 256;
+    load_chunk<F32_IN>(x, c, c < nchunks, v[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    int64_t c = base + u * 256;
+    uint32_t m = row16_max_u32(absmax8(v[u]));   // uniform control flow for DPP
+    float sc = block_scale(m);
+    if (c < nchunks) {
+      q[c] = quant8<!F32_IN>(v[u], sc);
+      if ((threadIdx.x & 15) == 0) s[c >> 4] = sc;
+    }
+  }
+}
+
+int launch_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, uint8_t* q,
+                      float* s, hipStream_t st) {
+  const int64_t nchunks = rows * cols / 8;
+  if (nchunks == 0) return TG_OK;
+  constexpr int UNROLL = 4;
+  const int64_t grid = (nchunks + 256 * UNROLL - 1) / (256 * UNROLL);
+  if (x_dtype == TG_DTYPE_F32)
+    hipLaunchKernelGGL((quant_rows_kernel<true, UNROLL>), dim3((unsigned)grid), dim3(256), 0, st, x,
+                       reinterpret_cast<uint2*>(q), s, nchunks);
+  else
+    hipLaunchKernelGGL((quant_rows_kernel<false, UNROLL>), dim3((unsigned)grid), dim3(256), 0, st,
+                       x, reinterpret_cast<uint2*>(q), s, nchunks);
+  return check_launch("quant_rows");
+}
+
+// ---------------------------------------------------------------------------
+// Column quantization with transpose: tile = 128 rows (one scale block of the
+// output) x 64 columns.  Load coalesced rows into LDS (row pitch 136 B), let
+// 4 lanes share each column (rows 16i + 4j + r for lane j, so a DPP quad holds
+// the block), stage the e4m3 bytes in a second LDS tile (pitch 144 B) and
+// store 32 contiguous bytes per lane.  Both pitches keep the column reads and
+// the 16-byte reads bank-conflict free for 32- and 64-bank LDS.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quant_cols_kernel(const uint16_t* __restrict__ x,
+                                                         int64_t rows, int64_t cols,
+                                                         uint8_t* __restrict__ qt,
+                                                         float* __restrict__ st) {
+  __shared__ uint32_t tile[128 * 34];
+  __shared__ uint32_t tq[64 * 36];
+  const int tid = threadIdx.x;
+  const int64_t c0 = (int64_t)blockIdx.x * 64;
+  const int64_t r0 = (int64_t)blockIdx.y * 128;
+
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int id = tid + 256 * u;
+    const int row = id >> 3, ch = id & 7;
+    const int64_t col = c0 + ch * 8;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (col < cols)
+      v = ldg_stream(reinterpret_cast<const uint4*>(x + (r0 + row) * cols + col));
+    uint2* p = reinterpret_cast<uint2*>(&tile[row * 34 + ch * 4]);
+    p[0] = make_uint2(v.x, v.y);
+    p[1] = make_uint2(v.z, v.w);
+  }
+  __syncthreads();
+
+  const int n = tid >> 2, j = tid & 3;
+  const uint16_t* t16 = reinterpret_cast<const uint16_t*>(tile);
+  float f[32];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      f[i * 4 + r] = __uint_as_float(((uint32_t)t16[(16 * i + 4 * j + r) * 68 + n]) << 16);
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) m = max(m, __float_as_uint(f[i]) & 0x7FFFFFFFu);
+  m = quad_max_u32(m);
+  const float sc = block_scale(m);
+  Divider d(sc);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t w;
+    if (d.fast) {
+      w = e4m3x4(d.div(f[4 * i]), d.div(f[4 * i + 1]), d.div(f[4 * i + 2]), d.div(f[4 * i + 3]));
+    } else {
+      w = e4m3_nonfinite_scale(f[4 * i], sc) | (e4m3_nonfinite_scale(f[4 * i + 1], sc) << 8) |
+          (e4m3_nonfinite_scale(f[4 * i + 2], sc) << 16) |
+          (e4m3_nonfinite_scale(f[4 * i + 3], sc) << 24);
+    }
+    tq[n * 36 + 4 * i + j] = w;
+  }
+  const bool col_ok = (c0 + n) < cols;
+  if (j == 0 && col_ok) st[(c0 + n) * (rows >> 7) + blockIdx.y] = sc;
+  __syncthreads();
+  if (col_ok) {
+    const uint4* src = reinterpret_cast<const uint4*>(&tq[n * 36 + 8 * j]);
+    uint4* dst = reinterpret_cast<uint4*>(qt + (c0 + n) * rows + r0 + 32 * j);
+    dst[0] = src[0];
+    dst[1] = src[1];
+  }
+}
+
+int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, float* s_t,
+                      hipStream_t st) {
+  if (rows == 0 || cols == 0) return TG_OK;
+  if (rows / 128 > 65535) return einval("quantize_cols: rows / 128 must be <= 65535");
+  dim3 grid((unsigned)((cols + 63) / 64), (unsigned)(rows / 128));
+  hipLaunchKernelGGL(quant_cols_kernel, grid, dim3(256), 0, st,
+                     reinterpret_cast<const uint16_t*>(x), rows, cols, q_t, s_t);
+  return check_launch("quant_cols");
+}
+
+// ---------------------------------------------------------------------------
+// 128x128-tile weight quantization (offline weight preparation for the GEMV).
+// One workgroup per tile: pass 1 finds the tile amax, pass 2 writes w.T bytes.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quant_w128_kernel(const uint16_t* __restrict__ w, int64_t K,
+                                                         int64_t N, uint8_t* __restrict__ wq,
+                                                         float* __restrict__ ws) {
+  __shared__ uint32_t red[4];
+  const int tid = threadIdx.x;
+  const int64_t k0 = (int64_t)blockIdx.y * 128, n0 = (int64_t)blockIdx.x * 128;
+  uint32_t m = 0;
+  for (int e = tid; e < 128 * 128; e += 256) {
+    const int64_t k = k0 + (e >> 7), n = n0 + (e & 127);
+    if (n < N) m = max(m, ((uint32_t)w[k * N + n] << 16) & 0x7FFFFFFFu);
+  }
+  for (int o = 32; o >= 1; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  m = max(max(red[0], red[1]), max(red[2], red[3]));
+  const float sc = block_scale(m);
+  if (tid == 0) ws[blockIdx.x * (K >> 7) + blockIdx.y] = sc;
+  Divider d(sc);
+  const int nl = tid >> 1, half = tid & 1;
+  const int64_t n = n0 + nl;
+  if (n >= N) return;
+  uint32_t out[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float f[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      f[r] = __uint_as_float(((uint32_t)w[(k0 + half * 64 + 4 * i + r) * N + n]) << 16);
+    if (d.fast)
+      out[i] = e4m3x4(d.div(f[0]), d.div(f[1]), d.div(f[2]), d.div(f[3]));
+    else
+      out[i] = e4m3_nonfinite_scale(f[0], sc) | (e4m3_nonfinite_scale(f[1], sc) << 8) |
+               (e4m3_nonfinite_scale(f[2], sc) << 16) | (e4m3_nonfinite_scale(f[3], sc) << 24);
+  }
+  uint4* dst = reinterpret_cast<uint4*>(wq + n * K + k0 + half * 64);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    dst[i] = make_uint4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
+}
+
+// ---------------------------------------------------------------------------
+// Self-test of the hardware convert over all 2^32 f32 bit patterns.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void selftest_cvt_kernel(unsigned long long* counts) {
+  unsigned long long c0 = 0, c1 = 0, c2 = 0;
+  const uint64_t stride = (uint64_t)gridDim.x * 256 * 4;
+  for (uint64_t base = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4; base < (1ull << 32);
+       base += stride) {
+    float f[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float((uint32_t)(base + i));
+    int hw = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], 0, false);
+    hw = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], hw, true);
+    const uint32_t sw = e4m3x4_sw(f[0], f[1], f[2], f[3]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t hb = ((uint32_t)hw >> (8 * i)) & 0xFF, sb = (sw >> (8 * i)) & 0xFF;
+      if (hb != sb) {
+        const uint32_t a = __float_as_uint(f[i]) & 0x7FFFFFFFu;
+        if (a >= 0x7F800000u) ++c2;
+        else if (a <= 0x43E00E00u) ++c0;   // 448 * (1 + 2^-12)
+        else ++c1;
+      }
+    }
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    c0 += __shfl_xor(c0, o, 64);
+    c1 += __shfl_xor(c1, o, 64);
+    c2 += __shfl_xor(c2, o, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicAdd(&counts[0], c0);
+    atomicAdd(&counts[1], c1);
+    atomicAdd(&counts[2], c2);
+  }
+}
+
+// Self-test of Divider::div against the device's IEEE divide over every bf16
+// amax (one workgroup each) and every bf16 x with |x| <= amax, both signs.
+// counts[0]: e4m3fn byte mismatches; counts[1]: f32 quotient mismatches with
+// |x/s| > 2^-10; counts[2]: quotient mismatches at or below 2^-10.
+__global__ __launch_bounds__(256) void selftest_divide_kernel(unsigned long long* counts) {
+  const uint32_t ab = blockIdx.x;                       // bf16 pattern of amax
+  const float a = __uint_as_float(ab << 16);
+  const float sc = block_scale(__float_as_uint(a));
+  const Divider d(sc);
+  unsigned long long c0 = 0, c1 = 0, c2 = 0;
+  for (uint32_t i = threadIdx.x; i <= 2 * ab + 1; i += 256) {
+    const float x = __uint_as_float(((i >> 1) << 16) | ((i & 1u) << 31));
+    const float q = d.div(x);
+    const float ref = x / sc;
+    if (e4m3_sw(q) != e4m3_sw(ref)) ++c0;
+    if (__float_as_uint(q) != __float_as_uint(ref)) {
+      if (__builtin_fabsf(ref) > 0x1p-10f) ++c1; else ++c2;
+    }
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    c0 += __shfl_xor(c0, o, 64);
+    c1 += __shfl_xor(c1, o, 64);
+    c2 += __shfl_xor(c2, o, 64);
+  }
+  if ((threadIdx.x & 63) == 0 && (c0 | c1 | c2)) {
+    atomicAdd(&counts[0], c0);
+    atomicAdd(&counts[1], c1);
+    atomicAdd(&counts[2], c2);
+  }
+}
+
+__global__ void zero3_kernel(unsigned long long* c) {
+  if (threadIdx.x < 3) c[threadIdx.x] = 0;
+}
+
+}  // namespace tg
+
+using namespace tg;
+
+extern "C" const char* tg_last_error(void) { return g_err; }
+
+extern "C" int tg_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                                int block_k, uint8_t* q, float* scales, void* stream) {
+  if (block_k != 128) return einval("quantize_rows: block_k must be 128");
+  if (rows < 0 || cols < 0) return einval("quantize_rows: negative shape");
+  if (cols % block_k) return einval("quantize_rows: cols not divisible by block_k");
+  if (x_dtype != TG_DTYPE_BF16 && x_dtype != TG_DTYPE_F32)
+    return einval("quantize_rows: x_dtype must be TG_DTYPE_BF16 or TG_DTYPE_F32");
+  if (rows * cols == 0) return TG_OK;
+  if (!x || !q || !scales) return einval("quantize_rows: null pointer");
+  if (!aligned(x, 16) || !aligned(q, 8) || !aligned(scales, 4))
+    return einval("quantize_rows: x must be 16-byte and q 8-byte aligned");
+  return launch_quant_rows(x, x_dtype, rows, cols, q, scales, as_stream(stream));
+}
+
+extern "C" int tg_quantize_cols(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                                int block_k, uint8_t* q_t, float* scales_t, void* stream) {
+  if (block_k != 128) return einval("quantize_cols: block_k must be 128");
+  if (x_dtype != TG_DTYPE_BF16) return einval("quantize_cols: x_dtype must be TG_DTYPE_BF16");
+  if (rows < 0 || cols < 0) return einval("quantize_cols: negative shape");
+  if (rows % block_k) return einval("quantize_cols: rows not divisible by block_k");
+  if (cols % 8) return einval("quantize_cols: cols must be a multiple of 8");
+  if (rows * cols == 0) return TG_OK;
+  if (!x || !q_t || !scales_t) return einval("quantize_cols: null pointer");
+  if (!aligned(x, 16) || !aligned(q_t, 16)) return einval("quantize_cols: x and q_t must be 16-byte aligned");
+  return launch_quant_cols(x, rows, cols, q_t, scales_t, as_stream(stream));
+}
+
+extern "C" int tg_quantize_weight_128x128(const void* w, int64_t K, int64_t N, uint8_t* w_q,
+                                          float* w_s, void* stream) {
+  if (K <= 0 || N <= 0 || K % 128) return einval("quantize_weight_128x128: K must be a positive multiple of 128");
+  if (K / 128 > 65535) return einval("quantize_weight_128x128: K too large");
+  if (!w || !w_q || !w_s) return einval("quantize_weight_128x128: null pointer");
+  if (!aligned(w_q, 16)) return einval("quantize_weight_128x128: w_q must be 16-byte aligned");
+  dim3 grid((unsigned)((N + 127) / 128), (unsigned)(K / 128));
+  hipLaunchKernelGGL(quant_w128_kernel, grid, dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const uint16_t*>(w), K, N, w_q, w_s);
+  return check_launch("quant_w128");
+}
+
+extern "C" int tg_selftest_fp8_cvt(uint64_t* counts, void* stream) {
+  if (!counts) return einval("selftest_fp8_cvt: null pointer");
+  auto* c = reinterpret_cast<unsigned long long*>(counts);
+  hipLaunchKernelGGL(zero3_kernel, dim3(1), dim3(64), 0, as_stream(stream), c);
+  TG_TRY(check_launch("zero3"));
+  hipLaunchKernelGGL(selftest_cvt_kernel, dim3(4096), dim3(256), 0, as_stream(stream), c);
+  return check_launch("selftest_cvt");
+}
+
+extern "C" int tg_selftest_divide(uint64_t* counts, void* stream) {
+  if (!counts) return einval("selftest_divide: null pointer");
+  auto* c = reinterpret_cast<unsigned long long*>(counts);
+  hipLaunchKernelGGL(zero3_kernel, dim3(1), dim3(64), 0, as_stream(stream), c);
+  TG_TRY(check_launch("zero3"));
+  hipLaunchKernelGGL(selftest_divide_kernel, dim3(0x7F80), dim3(256), 0, as_stream(stream), c);
+  return check_launch("selftest_divide");
+}

@@ -1,0 +1,47 @@
+// Host-side helpers of the C ABI: argument checks and thread-local errors.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/tg_fp8.h"
+
+namespace tg {
+
+void set_error(const char* fmt, ...);
+
+inline int einval(const char* what) {
+  set_error("invalid argument: %s", what);
+  return TG_EINVAL;
+}
+
+inline int check_launch(const char* kernel) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s launch failed: %s", kernel, hipGetErrorString(e));
+    return TG_EHIP;
+  }
+  return TG_OK;
+}
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// Kernel launchers shared between translation units.
+int launch_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, uint8_t* q,
+                      float* s, hipStream_t st);
+int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, float* s_t,
+                      hipStream_t st);
+int launch_gemm_fp8(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s,
+                    int b_scale_bn, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
+                    hipStream_t st);
+
+}  // namespace tg
+
+#define TG_TRY(expr)              \
+  do {                            \
+    int _rc = (expr);             \
+    if (_rc != TG_OK) return _rc; \
+  } while (0)

@@ -1,0 +1,238 @@
+"""Per-block-scaled FP8 matmul on MI355X -- drop-in for the reference's fp8.py.
+
+Same names, arguments, dtypes and errors as /root/reference/fp8.py:
+  * E4M3_MAX, DEFAULT_BLOCK_K                       fp8.py:26-27
+  * block_scaled_matmul(a, b, block_k=128)          fp8.py:30-36 (custom_vjp -> autograd.Function)
+  * _quantize_to_fp8(x_f32, block_k)                fp8.py:39-47
+  * _fp8_forward(a, b, block_k)                     fp8.py:50-78
+  * _fp8_forward_with_residuals / _fp8_backward     fp8.py:81-98
+Arrays are torch device tensors (the reference's are jax.Arrays); the
+computation is the HIP kernels of libtg_fp8.so behind include/tg_fp8.h.
+
+Backward modes (``BACKWARD_MODE``):
+  * "fp8" (default): dX and dW run through the same quantize -> scaled GEMM
+    composition as the forward (g and W quantized along N; X.T and g.T along
+    M, all 1x128 blocks), on FP8 MFMA.
+  * "bf16": the reference's straight-through rule (fp8.py:85-98) needs bf16
+    GEMMs, which this library does not implement yet; it raises.
+
+Additive entry points (no reference counterpart): ``quantize_fp8`` (row or
+transposed), ``quantize_weight`` (pre-quantized weight format) and
+``fp8_gemv`` (decode-shape GEMM on a pre-quantized weight).
+"""
+import torch
+
+import _tglib as _L
+
+E4M3_MAX = 448.0          # fp8.py:26
+DEFAULT_BLOCK_K = 128     # fp8.py:27
+BACKWARD_MODE = "fp8"
+
+_SUPPORTED_BLOCK_K = (128,)
+
+
+def _check_block_k(block_k: int) -> None:
+    if block_k not in _SUPPORTED_BLOCK_K:
+        raise NotImplementedError(
+            f"block_k={block_k}: the gfx950 kernels implement block_k=128 "
+            "(one FP8 MFMA K step per scale block)")
+
+
+def block_scaled_matmul(a: torch.Tensor, b: torch.Tensor, block_k: int = DEFAULT_BLOCK_K) -> torch.Tensor:
+    """Per-K-tile block-scaled FP8 matmul (fp8.py:30-36).
+
+    a: (..., K), b: (K, N) -> (..., N) bf16.  Requires K % block_k == 0.
+    """
+    return _BlockScaledMatmul.apply(a, b, block_k)
+
+
+def _quantize_to_fp8(x_f32: torch.Tensor, block_k: int):
+    """fp8.py:39-47 along the last axis -> (x_f8 float8_e4m3fn, scales f32)."""
+    return quantize_fp8(x_f32, block_k)
+
+
+def quantize_fp8(x: torch.Tensor, block_k: int = DEFAULT_BLOCK_K, transpose: bool = False):
+    """_quantize_to_fp8 of x (..., K) along its last axis, or, with
+    transpose=True, of x.T for a 2-D x (R, C) (what fp8.py:68 does to b).
+
+    x may be bf16 or f32 (f32 is what the reference feeds; bf16 values
+    widen to f32 exactly).  Returns (q float8_e4m3fn, scales float32).
+    """
+    _L.require_gpu(x)
+    _check_block_k(block_k)
+    if transpose:
+        if x.dim() != 2:
+            raise ValueError("transpose=True needs a 2-D tensor")
+        R, C = x.shape
+        if R % block_k != 0:
+            raise ValueError(f"K={R} not divisible by block_k={block_k}")
+        if x.dtype != torch.bfloat16:
+            # the transposing kernel reads bf16; other dtypes go through a row quantize of x.T
+            return quantize_fp8(x.t().contiguous(), block_k)
+        x = x.contiguous()
+        q = torch.empty((C, R), dtype=torch.uint8, device=x.device)
+        s = torch.empty((C, R // block_k), dtype=torch.float32, device=x.device)
+        _L.check(_L.lib().tg_quantize_cols(_L.ptr(x), _L.TG_DTYPE_BF16, R, C, block_k,
+                                           _L.ptr(q), _L.ptr(s), _L.stream_of(x)))
+        return q.view(torch.float8_e4m3fn), s
+    *lead, K = x.shape
+    if K % block_k != 0:
+        raise ValueError(f"K={K} not divisible by block_k={block_k}")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        x = x.to(torch.float32)
+    x2 = x.reshape(-1, K).contiguous()
+    R = x2.shape[0]
+    q = torch.empty((R, K), dtype=torch.uint8, device=x.device)
+    s = torch.empty((R, K // block_k), dtype=torch.float32, device=x.device)
+    _L.check(_L.lib().tg_quantize_rows(_L.ptr(x2), _L.dtype_code(x2), R, K, block_k,
+                                       _L.ptr(q), _L.ptr(s), _L.stream_of(x2)))
+    return q.view(torch.float8_e4m3fn).reshape(*lead, K), s.reshape(*lead, K // block_k)
+
+
+def _validate(a: torch.Tensor, b: torch.Tensor, block_k: int):
+    *leading, K = a.shape
+    K_b, N = b.shape
+    if K != K_b:                                                   # fp8.py:53-54
+        raise ValueError(f"contracted-dim mismatch: a K={K}, b K={K_b}")
+    if K % block_k != 0:                                           # fp8.py:55-56
+        raise ValueError(f"K={K} not divisible by block_k={block_k}")
+    return leading, K, N
+
+
+def scaled_matmul(a_q, a_s, b_q, b_s, b_scale_bn: int = 1, out_dtype=torch.bfloat16):
+    """The scaled GEMM of fp8.py:70-76 on already-quantized operands ("NT"):
+    a_q (M, K), b_q (N, K) e4m3fn; a_s (M, K/128), b_s (N or ceil(N/128), K/128) f32.
+    Returns (M, N) in out_dtype (bf16 by RNE, or f32)."""
+    _L.require_gpu(a_q, b_q)
+    M, K = a_q.shape
+    N = b_q.shape[0]
+    if b_q.shape[1] != K:
+        raise ValueError(f"contracted-dim mismatch: a K={K}, b K={b_q.shape[1]}")
+    c = torch.empty((M, N), dtype=out_dtype, device=a_q.device)
+    code = _L.TG_DTYPE_F32 if out_dtype == torch.float32 else _L.TG_DTYPE_BF16
+    a_q, b_q = a_q.contiguous(), b_q.contiguous()
+    a_s, b_s = a_s.contiguous().float(), b_s.contiguous().float()
+    _L.check(_L.lib().tg_gemm_fp8_nt(_L.ptr(a_q), _L.ptr(a_s), _L.ptr(b_q), _L.ptr(b_s),
+                                     b_scale_bn, _L.ptr(c), code, M, N, K, DEFAULT_BLOCK_K,
+                                     _L.stream_of(a_q)))
+    return c
+
+
+def _fp8_forward(a: torch.Tensor, b: torch.Tensor, block_k: int) -> torch.Tensor:
+    """fp8.py:50-78: quantize a and b.T, scaled GEMM, bf16 output (..., N)."""
+    leading, K, N = _validate(a, b, block_k)
+    _L.require_gpu(a, b)
+    _check_block_k(block_k)
+    a_2d = a.reshape(-1, K)
+    M = a_2d.shape[0]
+    if a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16 and N % 8 == 0:
+        a_2d = a_2d.contiguous()
+        b_c = b.contiguous()
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+        ws_bytes = _L.lib().tg_block_scaled_matmul_workspace(M, N, K, block_k)
+        ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=a.device)
+        _L.check(_L.lib().tg_block_scaled_matmul(_L.ptr(a_2d), _L.ptr(b_c), _L.ptr(out), M, N, K,
+                                                 block_k, _L.ptr(ws), ws_bytes, _L.stream_of(a_2d)))
+        return out.reshape(*leading, N)
+    a_q, a_s = quantize_fp8(a_2d, block_k)                         # fp8.py:66
+    b_q, b_s = quantize_fp8(b, block_k, transpose=True)            # fp8.py:68
+    out = scaled_matmul(a_q.view(torch.uint8), a_s, b_q.view(torch.uint8), b_s)   # fp8.py:70-78
+    return out.reshape(*leading, N)
+
+
+def _fp8_forward_with_residuals(a, b, block_k):
+    """fp8.py:81-82: the residuals are the un-quantized operands."""
+    return _fp8_forward(a, b, block_k), (a, b)
+
+
+def _fp8_backward(block_k, residuals, g):
+    """Gradients of block_scaled_matmul: (da as a.dtype, db as b.dtype).
+
+    BACKWARD_MODE "fp8": da = fwd(g, b.T), db = fwd(a.T, g) through FP8 MFMA.
+    BACKWARD_MODE "bf16": fp8.py:85-98's straight-through bf16 rule (not built).
+    """
+    a, b = residuals
+    *leading, K = a.shape
+    _, N = b.shape
+    if BACKWARD_MODE == "bf16":
+        raise NotImplementedError("bf16 straight-through backward needs the bf16 GEMM (not built)")
+    _check_block_k(block_k)
+    a_2d = a.reshape(-1, K).to(torch.bfloat16).contiguous()
+    g_2d = g.reshape(-1, N).to(torch.bfloat16).contiguous()
+    b_bf = b.to(torch.bfloat16).contiguous()
+    M = a_2d.shape[0]
+    _L.require_gpu(a_2d, b_bf, g_2d)
+    if M % 128 or N % 128:
+        raise NotImplementedError("FP8 backward needs M and N to be multiples of 128")
+    da = torch.empty((M, K), dtype=torch.bfloat16, device=a.device)
+    db = torch.empty((K, N), dtype=torch.bfloat16, device=a.device)
+    ws_bytes = _L.lib().tg_block_scaled_matmul_bwd_workspace(M, N, K, block_k)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=a.device)
+    _L.check(_L.lib().tg_block_scaled_matmul_bwd_fp8(
+        _L.ptr(a_2d), _L.ptr(b_bf), _L.ptr(g_2d), _L.ptr(da), _L.ptr(db), M, N, K, block_k,
+        _L.ptr(ws), ws_bytes, _L.stream_of(a_2d)))
+    return da.reshape(*leading, K).to(a.dtype), db.to(b.dtype)
+
+
+class _BlockScaledMatmul(torch.autograd.Function):
+    """custom_vjp of fp8.py:30-36,101 as a torch autograd Function."""
+
+    @staticmethod
+    def forward(ctx, a, b, block_k):
+        out, (ra, rb) = _fp8_forward_with_residuals(a, b, block_k)
+        ctx.save_for_backward(ra, rb)
+        ctx.block_k = block_k
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        a, b = ctx.saved_tensors
+        da, db = _fp8_backward(ctx.block_k, (a, b), g)
+        return da, db, None
+
+
+# ---------------------------------------------------------------------------
+# Pre-quantized weights and decode-shape GEMM (no reference counterpart).
+# ---------------------------------------------------------------------------
+def quantize_weight(w: torch.Tensor, layout: str = "128x1"):
+    """Quantize W (K, N) once into (w_q (N, K) e4m3fn, w_s f32, bn).
+
+    layout "128x1": per (128-K block, column) scales, w_s (N, K/128) -- the
+    scales fp8.py:68 computes every call.  layout "128x128": one scale per
+    128x128 tile, w_s (ceil(N/128), K/128).
+    """
+    _L.require_gpu(w)
+    if layout == "128x1":
+        q, s = quantize_fp8(w, DEFAULT_BLOCK_K, transpose=True)
+        return q, s, 1
+    if layout != "128x128":
+        raise ValueError("layout must be '128x1' or '128x128'")
+    K, N = w.shape
+    if K % 128:
+        raise ValueError(f"K={K} not divisible by block_k=128")
+    w = w.to(torch.bfloat16).contiguous()
+    q = torch.empty((N, K), dtype=torch.uint8, device=w.device)
+    s = torch.empty(((N + 127) // 128, K // 128), dtype=torch.float32, device=w.device)
+    _L.check(_L.lib().tg_quantize_weight_128x128(_L.ptr(w), K, N, _L.ptr(q), _L.ptr(s),
+                                                 _L.stream_of(w)))
+    return q.view(torch.float8_e4m3fn), s, 128
+
+
+def fp8_gemv(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, w_scale_bn: int = 1,
+             block_k: int = DEFAULT_BLOCK_K) -> torch.Tensor:
+    """Decode-shape GEMM: x (..., K) bf16 (M = prod(...) <= 64 rows) times a
+    pre-quantized weight (w_q (N, K), w_s) -> (..., N) bf16."""
+    _L.require_gpu(x, w_q)
+    _check_block_k(block_k)
+    *lead, K = x.shape
+    N = w_q.shape[0]
+    if w_q.shape[1] != K:
+        raise ValueError(f"contracted-dim mismatch: x K={K}, w K={w_q.shape[1]}")
+    x_q, x_s = quantize_fp8(x.reshape(-1, K), block_k)
+    M = x_q.shape[0]
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    wq = w_q.view(torch.uint8).contiguous()
+    ws = w_s.contiguous()
+    _L.check(_L.lib().tg_gemv_fp8(_L.ptr(x_q), _L.ptr(x_s), _L.ptr(wq), _L.ptr(ws), w_scale_bn,
+                                  _L.ptr(out), M, N, K, block_k, _L.stream_of(x_q)))
+    return out.reshape(*lead, N)

@@ -1,0 +1,78 @@
+"""RMSNorm on MI355X -- drop-in for the reference's kernels.py.
+
+Same names and arguments as /root/reference/kernels.py:
+  * _rms_norm_pure(x, scale, eps)     kernels.py:30-33 (the canonical semantics)
+  * rms_norm(x, scale, eps)           kernels.py:55-127 (custom_vjp; backend-selected)
+Both run the gfx950 kernel tg_rms_norm with _rms_norm_pure's arithmetic:
+r = bf16(rsqrt(mean(x^2) + eps)), y = bf16(bf16(x * r) * scale).  The
+reference selects its Pallas kernel when jax.default_backend() == "gpu"
+(kernels.py:124-127), which would pick the CUDA-only Mosaic path on ROCm; here
+the HIP kernel is the only implementation.
+
+Additive (no single reference function): ``rms_norm_fp8(x, scale, eps,
+block_k)`` returns the bf16 norm output together with its e4m3fn bytes and
+1x128 fp32 scales from one read of x -- what ``_quantize_to_fp8`` of the norm
+output (fp8.py:66) would produce.
+
+The backward (kernels.py:104-118) is not yet a HIP kernel: calling
+``rms_norm(...).backward()`` raises.
+"""
+import torch
+
+import _tglib as _L
+
+
+def _prep(x: torch.Tensor, scale: torch.Tensor):
+    _L.require_gpu(x, scale)
+    if x.dtype != torch.bfloat16 or scale.dtype != torch.bfloat16:
+        raise TypeError("rms_norm: x and scale must be bfloat16 (the model's dtype)")
+    D = x.shape[-1]
+    if scale.shape != (D,):
+        raise ValueError(f"scale must have shape ({D},), got {tuple(scale.shape)}")
+    return x.reshape(-1, D).contiguous(), scale.contiguous(), D
+
+
+def _rms_norm_pure(x: torch.Tensor, scale: torch.Tensor, eps: float) -> torch.Tensor:
+    """kernels.py:30-33 on the GPU: x (..., D) bf16, scale (D,) bf16 -> bf16 (..., D)."""
+    x2, g, D = _prep(x, scale)
+    y = torch.empty_like(x2)
+    _L.check(_L.lib().tg_rms_norm(_L.ptr(x2), _L.ptr(g), _L.ptr(y), x2.shape[0], D, float(eps),
+                                  _L.stream_of(x2)))
+    return y.reshape(x.shape)
+
+
+def rms_norm_fp8(x: torch.Tensor, scale: torch.Tensor, eps: float, block_k: int = 128):
+    """Fused RMSNorm -> FP8 quantize.
+
+    Returns (y bf16 (..., D), y_f8 float8_e4m3fn (..., D), y_scales f32 (..., D/block_k)),
+    where (y_f8, y_scales) == _quantize_to_fp8(y.astype(f32), block_k) bit for bit.
+    """
+    x2, g, D = _prep(x, scale)
+    if D % block_k:
+        raise ValueError(f"K={D} not divisible by block_k={block_k}")
+    R = x2.shape[0]
+    y = torch.empty_like(x2)
+    q = torch.empty((R, D), dtype=torch.uint8, device=x.device)
+    s = torch.empty((R, D // block_k), dtype=torch.float32, device=x.device)
+    _L.check(_L.lib().tg_rms_norm_fp8(_L.ptr(x2), _L.ptr(g), _L.ptr(y), _L.ptr(q), _L.ptr(s), R, D,
+                                      float(eps), block_k, _L.stream_of(x2)))
+    lead = x.shape[:-1]
+    return (y.reshape(x.shape), q.view(torch.float8_e4m3fn).reshape(x.shape),
+            s.reshape(*lead, D // block_k))
+
+
+class _RMSNorm(torch.autograd.Function):
+    """custom_vjp of kernels.py:55,101-120 (forward only for now)."""
+
+    @staticmethod
+    def forward(ctx, x, scale, eps):
+        return _rms_norm_pure(x, scale, eps)
+
+    @staticmethod
+    def backward(ctx, g):
+        raise NotImplementedError("rms_norm backward (kernels.py:104-118) is not built as a HIP kernel yet")
+
+
+def rms_norm(x: torch.Tensor, scale: torch.Tensor, eps: float) -> torch.Tensor:
+    """kernels.py:124-127's rms_norm: the HIP kernel on every backend."""
+    return _RMSNorm.apply(x, scale, eps)
