@@ -40,8 +40,8 @@ int tg_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, int
 
 /* _quantize_to_fp8 of x.T (fp8.py:68 applies it to b.T): quantizes the columns
  * of x (rows, cols) bf16 and writes them transposed:
- * q_t: (cols, rows) e4m3fn; scales_t: (cols, rows/block_k) f32.  rows % block_k == 0,
- * cols % 8 == 0. */
+ * q_t: (cols, rows) e4m3fn; scales_t: (cols, rows/block_k) f32.  rows % block_k == 0;
+ * any cols (16-byte loads when cols % 8 == 0 and x is 16-byte aligned). */
 int tg_quantize_cols(const void* x, int x_dtype, int64_t rows, int64_t cols, int block_k,
                      uint8_t* q_t, float* scales_t, void* stream);
 

@@ -37,8 +37,9 @@ def e4m3fn_encode(v: np.ndarray) -> np.ndarray:
     code_n = rnd - (120 << 3)
     # subnormal range: the f32 adder rounds |v| to a multiple of 2**-9 (RNE)
     af = a.view(np.float32)
-    code_s = ((af + _MAGIC_SUB).view(np.uint32).astype(np.int64)
-              - int(_MAGIC_SUB.view(np.uint32)))
+    with np.errstate(invalid="ignore", over="ignore"):
+        code_s = ((af + _MAGIC_SUB).view(np.uint32).astype(np.int64)
+                  - int(_MAGIC_SUB.view(np.uint32)))
     code = np.where(a < _TWO_POW_M6_BITS, code_s, code_n)
     nan = (a > 0x7F800000) | (code > 0x7E) | (a == 0x7F800000)
     code = np.where(nan, 0x7F, code)

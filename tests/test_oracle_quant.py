@@ -1,0 +1,109 @@
+"""Pins the oracle's _quantize_to_fp8 (fp8.py:39-47).
+
+Closed forms and invariants, each chosen so that a plausible mistake fails:
+the scale is fl32(amax / 448) floored at fl32(1e-30) (computed here exactly
+with fractions, not by retyping the oracle's numpy expression); the amax
+element encodes to +-448 (a wrong divisor or a reciprocal-multiply off by an
+ulp breaks it at the 0x7E/0x7F boundary); dequantized values are within half
+an e4m3 step; NaN/inf propagate; the C and numpy restatements agree.
+"""
+from fractions import Fraction
+
+import numpy as np
+
+from oracle import bf16 as ob
+from oracle import cbind, fp8_ref
+
+
+def _round_f32(fr: Fraction) -> np.float32:
+    """Correctly rounded (RNE) f32 of an exact rational (normal range)."""
+    f = np.float32(float(fr))                       # within 1 ulp
+    cands = [np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))]
+    best = min(cands, key=lambda c: (abs(Fraction(float(c)) - fr),
+                                     int(np.array(c, np.float32).view(np.uint32)) & 1))
+    return np.float32(best)
+
+
+def test_scale_closed_form():
+    rng = np.random.default_rng(0)
+    x = ob.bf16_to_f32(ob.randn_bf16(rng, (64, 512), std=3.0))
+    x[0, :128] = 0.0
+    x[1, :128] = 1e-35
+    _, s = fp8_ref.quantize_fp8(x)
+    for r in range(x.shape[0]):
+        for b in range(4):
+            amax = float(np.max(np.abs(x[r, 128 * b:128 * (b + 1)])))
+            want = max(_round_f32(Fraction(amax) / 448), np.float32(1e-30))
+            assert s[r, b] == want, (r, b, s[r, b], want)
+    assert np.float32(1e-30).view(np.uint32) == 0x0DA24260
+
+
+def test_ones_known_answer():
+    """debug_fp8.py:104-109's operand: ones -> s = fl(1/448), x/s = 447.99997 -> 0x7E."""
+    q, s = fp8_ref.quantize_fp8(np.ones((4, 128), np.float32))
+    assert np.all(s == np.float32(1.0) / np.float32(448.0))
+    assert np.all(q == 0x7E)
+
+
+def test_amax_element_encodes_to_448():
+    rng = np.random.default_rng(1)
+    x = ob.bf16_to_f32(ob.randn_bf16(rng, (256, 1024)))
+    q, s = fp8_ref.quantize_fp8(x)
+    xb = x.reshape(256, 8, 128)
+    qb = q.reshape(256, 8, 128)
+    idx = np.argmax(np.abs(xb), axis=-1)
+    top = np.take_along_axis(qb, idx[..., None], -1)[..., 0]
+    assert np.all((top == 0x7E) | (top == 0xFE))
+
+
+def test_dequant_error_bound():
+    rng = np.random.default_rng(2)
+    x = ob.bf16_to_f32(ob.randn_bf16(rng, (128, 512)))
+    q, s = fp8_ref.quantize_fp8(x)
+    deq = fp8_ref.e4m3fn_decode(q).reshape(128, 4, 128) * s[..., None]
+    xb = x.reshape(128, 4, 128)
+    # half an e4m3 step: 2^-4 relative for normals, 2^-10 * s absolute for subnormals
+    bound = np.maximum(np.abs(xb) * 2.0 ** -4, s[..., None] * 2.0 ** -10) * (1 + 1e-6)
+    assert np.all(np.abs(deq - xb) <= bound)
+
+
+def test_special_blocks():
+    x = np.zeros((5, 128), np.float32)
+    x[1] = -0.0
+    x[2, :] = 1.0; x[2, 3] = np.nan
+    x[3, :] = 1.0; x[3, 4] = np.inf
+    x[4, :] = -2.0; x[4, 0] = -np.inf
+    q, s = fp8_ref.quantize_fp8(x)
+    assert s[0, 0] == np.float32(1e-30) and np.all(q[0] == 0)
+    assert np.all(q[1] == 0x80)
+    assert np.isnan(s[2, 0]) and np.all(q[2] & 0x7F == 0x7F)
+    assert s[3, 0] == np.inf and q[3, 4] in (0x7F, 0xFF) and np.all(q[3, :4] == 0)
+    assert s[4, 0] == np.inf and np.all(q[4, 1:] == 0x80)
+
+
+def test_c_and_numpy_restatements_agree():
+    rng = np.random.default_rng(3)
+    x = ob.randn_bf16(rng, (300, 768))
+    x[0, 5] = 0x7FC0          # NaN
+    x[1, 9] = 0x7F80          # inf
+    x[2, :128] = 0x8000       # -0 block
+    q1, s1 = fp8_ref.quantize_fp8(ob.bf16_to_f32(x))
+    q2, s2 = cbind.quantize_rows_bf16(x)
+    np.testing.assert_array_equal(q1, q2)
+    np.testing.assert_array_equal(np.isnan(s1), np.isnan(s2))
+    np.testing.assert_array_equal(s1[~np.isnan(s1)], s2[~np.isnan(s2)])
+    w = ob.randn_bf16(rng, (256, 200), std=0.02)
+    q3, s3 = cbind.quantize_cols_bf16(w)
+    q4, s4 = fp8_ref.quantize_fp8(np.ascontiguousarray(ob.bf16_to_f32(w).T))
+    np.testing.assert_array_equal(q3, q4)
+    np.testing.assert_array_equal(s3, s4)
+
+
+def test_weight_128x128_tiles():
+    rng = np.random.default_rng(4)
+    w_t = ob.bf16_to_f32(ob.randn_bf16(rng, (200, 256)))
+    q, s = fp8_ref.quantize_weight_128x128(w_t)
+    assert s.shape == (2, 2)
+    assert s[1, 1] == np.float32(np.max(np.abs(w_t[128:, 128:]))) / np.float32(448)
+    deq = fp8_ref.e4m3fn_decode(q) * np.repeat(np.repeat(s, 128, 0)[:200], 128, 1)
+    assert np.max(np.abs(deq - w_t)) <= np.max(np.abs(w_t)) * 2.0 ** -4

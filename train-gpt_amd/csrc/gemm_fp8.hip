@@ -358,7 +358,6 @@ extern "C" int tg_block_scaled_matmul(const void* a, const void* b, void* out, i
                                       int64_t N, int64_t K, int block_k, void* workspace,
                                       size_t workspace_bytes, void* stream) {
   TG_TRY(check_gemm_args("block_scaled_matmul", M, N, K, block_k, 1));
-  if (N % 8) return einval("block_scaled_matmul: N must be a multiple of 8");
   if (M == 0 || N == 0) return TG_OK;
   if (!a || !b || !out || !workspace) return einval("block_scaled_matmul: null pointer");
   if (workspace_bytes < tg_block_scaled_matmul_workspace(M, N, K, block_k))

@@ -125,6 +125,7 @@ int launch_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, ui
 // store 32 contiguous bytes per lane.  Both pitches keep the column reads and
 // the 16-byte reads bank-conflict free for 32- and 64-bank LDS.
 // ---------------------------------------------------------------------------
+template <bool VEC>
 __global__ __launch_bounds__(256) void quant_cols_kernel(const uint16_t* __restrict__ x,
                                                          int64_t rows, int64_t cols,
                                                          uint8_t* __restrict__ qt,
@@ -141,8 +142,15 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(const uint16_t* __restr
     const int row = id >> 3, ch = id & 7;
     const int64_t col = c0 + ch * 8;
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (col < cols)
-      v = ldg_stream(reinterpret_cast<const uint4*>(x + (r0 + row) * cols + col));
+    if (VEC) {
+      if (col < cols) v = ldg_stream(x + (r0 + row) * cols + col);
+    } else {
+      // rows are not 16-byte aligned when cols % 8 != 0: element loads
+      uint32_t e[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) e[k] = (col + k < cols) ? x[(r0 + row) * cols + col + k] : 0u;
+      v = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+    }
     uint2* p = reinterpret_cast<uint2*>(&tile[row * 34 + ch * 4]);
     p[0] = make_uint2(v.x, v.y);
     p[1] = make_uint2(v.z, v.w);
@@ -191,8 +199,12 @@ int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, f
   if (rows == 0 || cols == 0) return TG_OK;
   if (rows / 128 > 65535) return einval("quantize_cols: rows / 128 must be <= 65535");
   dim3 grid((unsigned)((cols + 63) / 64), (unsigned)(rows / 128));
-  hipLaunchKernelGGL(quant_cols_kernel, grid, dim3(256), 0, st,
-                     reinterpret_cast<const uint16_t*>(x), rows, cols, q_t, s_t);
+  if (cols % 8 == 0 && aligned(x, 16))
+    hipLaunchKernelGGL(quant_cols_kernel<true>, grid, dim3(256), 0, st,
+                       reinterpret_cast<const uint16_t*>(x), rows, cols, q_t, s_t);
+  else
+    hipLaunchKernelGGL(quant_cols_kernel<false>, grid, dim3(256), 0, st,
+                       reinterpret_cast<const uint16_t*>(x), rows, cols, q_t, s_t);
   return check_launch("quant_cols");
 }
 
@@ -338,10 +350,9 @@ extern "C" int tg_quantize_cols(const void* x, int x_dtype, int64_t rows, int64_
   if (x_dtype != TG_DTYPE_BF16) return einval("quantize_cols: x_dtype must be TG_DTYPE_BF16");
   if (rows < 0 || cols < 0) return einval("quantize_cols: negative shape");
   if (rows % block_k) return einval("quantize_cols: rows not divisible by block_k");
-  if (cols % 8) return einval("quantize_cols: cols must be a multiple of 8");
   if (rows * cols == 0) return TG_OK;
   if (!x || !q_t || !scales_t) return einval("quantize_cols: null pointer");
-  if (!aligned(x, 16) || !aligned(q_t, 16)) return einval("quantize_cols: x and q_t must be 16-byte aligned");
+  if (!aligned(x, 2) || !aligned(q_t, 16)) return einval("quantize_cols: q_t must be 16-byte aligned");
   return launch_quant_cols(x, rows, cols, q_t, scales_t, as_stream(stream));
 }
 

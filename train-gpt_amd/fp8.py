@@ -125,7 +125,7 @@ def _fp8_forward(a: torch.Tensor, b: torch.Tensor, block_k: int) -> torch.Tensor
     _check_block_k(block_k)
     a_2d = a.reshape(-1, K)
     M = a_2d.shape[0]
-    if a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16 and N % 8 == 0:
+    if a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16:
         a_2d = a_2d.contiguous()
         b_c = b.contiguous()
         out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
@@ -148,7 +148,9 @@ def _fp8_forward_with_residuals(a, b, block_k):
 def _fp8_backward(block_k, residuals, g):
     """Gradients of block_scaled_matmul: (da as a.dtype, db as b.dtype).
 
-    BACKWARD_MODE "fp8": da = fwd(g, b.T), db = fwd(a.T, g) through FP8 MFMA.
+    BACKWARD_MODE "fp8": da = fwd(g, b.T), db = fwd(a.T, g) through FP8 MFMA,
+    so N (da's contraction) and M (db's) must divide by block_k, with the
+    reference's ValueError text (fp8.py:55-56) otherwise.
     BACKWARD_MODE "bf16": fp8.py:85-98's straight-through bf16 rule (not built).
     """
     a, b = residuals
@@ -157,20 +159,32 @@ def _fp8_backward(block_k, residuals, g):
     if BACKWARD_MODE == "bf16":
         raise NotImplementedError("bf16 straight-through backward needs the bf16 GEMM (not built)")
     _check_block_k(block_k)
-    a_2d = a.reshape(-1, K).to(torch.bfloat16).contiguous()
-    g_2d = g.reshape(-1, N).to(torch.bfloat16).contiguous()
-    b_bf = b.to(torch.bfloat16).contiguous()
+    a_2d = a.reshape(-1, K)
+    g_2d = g.reshape(-1, N)
     M = a_2d.shape[0]
-    _L.require_gpu(a_2d, b_bf, g_2d)
-    if M % 128 or N % 128:
-        raise NotImplementedError("FP8 backward needs M and N to be multiples of 128")
-    da = torch.empty((M, K), dtype=torch.bfloat16, device=a.device)
-    db = torch.empty((K, N), dtype=torch.bfloat16, device=a.device)
-    ws_bytes = _L.lib().tg_block_scaled_matmul_bwd_workspace(M, N, K, block_k)
-    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=a.device)
-    _L.check(_L.lib().tg_block_scaled_matmul_bwd_fp8(
-        _L.ptr(a_2d), _L.ptr(b_bf), _L.ptr(g_2d), _L.ptr(da), _L.ptr(db), M, N, K, block_k,
-        _L.ptr(ws), ws_bytes, _L.stream_of(a_2d)))
+    _L.require_gpu(a_2d, b, g_2d)
+    if N % block_k:
+        raise ValueError(f"K={N} not divisible by block_k={block_k}")
+    if M % block_k:
+        raise ValueError(f"K={M} not divisible by block_k={block_k}")
+    bf = torch.bfloat16
+    if a.dtype == bf and b.dtype == bf and g.dtype == bf:
+        a_2d, g_2d, b_c = a_2d.contiguous(), g_2d.contiguous(), b.contiguous()
+        da = torch.empty((M, K), dtype=bf, device=a.device)
+        db = torch.empty((K, N), dtype=bf, device=a.device)
+        ws_bytes = _L.lib().tg_block_scaled_matmul_bwd_workspace(M, N, K, block_k)
+        ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=a.device)
+        _L.check(_L.lib().tg_block_scaled_matmul_bwd_fp8(
+            _L.ptr(a_2d), _L.ptr(b_c), _L.ptr(g_2d), _L.ptr(da), _L.ptr(db), M, N, K, block_k,
+            _L.ptr(ws), ws_bytes, _L.stream_of(a_2d)))
+    else:
+        u8 = torch.uint8
+        qg, sg = quantize_fp8(g_2d, block_k)                       # g along N
+        qb, sb = quantize_fp8(b, block_k)                          # b along N
+        da = scaled_matmul(qg.view(u8), sg, qb.view(u8), sb)
+        qat, sat = quantize_fp8(a_2d, block_k, transpose=True)     # a.T along M
+        qgt, sgt = quantize_fp8(g_2d, block_k, transpose=True)     # g.T along M
+        db = scaled_matmul(qat.view(u8), sat, qgt.view(u8), sgt)
     return da.reshape(*leading, K).to(a.dtype), db.to(b.dtype)
 
 
