@@ -46,7 +46,10 @@ def test_layout_known_answer(dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 8, 128), (17, 40, 256), (130, 200, 384), (256, 256, 512),
-                                   (300, 136, 1024), (2048, 3072, 768)])
+                                   (300, 136, 1024), (2048, 3072, 768),
+                                   # >= 128 tiles of 256 x 256: the large-tile kernel, with ragged
+                                   # M / N edges and odd / even numbers of K blocks
+                                   (2100, 4000, 384), (4096, 4096, 256), (3000, 2900, 640)])
 def test_scaled_gemm_random(dev, M, N, K):
     rng = np.random.default_rng(M * 7 + N)
     a = ob.bf16_to_f32(ob.randn_bf16(rng, (M, K)))

@@ -182,6 +182,214 @@ __global__ __launch_bounds__(256, 2) void gemm_fp8_nt_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Large-tile variant: workgroup tile 256 x 256 x 128, 8 waves (4 along M x 2
+// along N), wave tile 64 x 128 (4 x 8 MFMA tiles).  Operands travel HBM -> LDS
+// with buffer_load_dwordx4 ... lds (no VGPR staging): each lane's 16-byte
+// chunk lands at LDS offset lane * 16 of its wave's 1 KiB slot, so the XOR
+// swizzle is applied to the global offset a lane fetches.  Rows past M / N
+// fall outside the buffer's range and read as zero.  Per-lane state is one
+// 32-bit offset per operand; the row step and the K-block step ride in SGPR
+// offsets.  The two stages are distinct __shared__ objects and the K loop is
+// unrolled by two, so the compiler sees that the prefetch into one stage
+// does not alias the fragment reads from the other and puts no wait
+// between them.
+// ---------------------------------------------------------------------------
+__shared__ __attribute__((aligned(16))) uint8_t g256_a0[256 * 128];
+__shared__ __attribute__((aligned(16))) uint8_t g256_b0[256 * 128];
+__shared__ __attribute__((aligned(16))) float g256_s0[512];
+__shared__ __attribute__((aligned(16))) uint8_t g256_a1[256 * 128];
+__shared__ __attribute__((aligned(16))) uint8_t g256_b1[256 * 128];
+__shared__ __attribute__((aligned(16))) float g256_s1[512];
+
+template <int S> __device__ __forceinline__ uint8_t* g256_a() { return S ? g256_a1 : g256_a0; }
+template <int S> __device__ __forceinline__ uint8_t* g256_b() { return S ? g256_b1 : g256_b0; }
+template <int S> __device__ __forceinline__ float* g256_s() { return S ? g256_s1 : g256_s0; }
+
+constexpr int kBufferWord3 = 0x00020000;   // gfx9 raw buffer: 32-bit data format
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufferWord3);
+}
+
+struct G256Ctx {
+  __amdgpu_buffer_rsrc_t ra, rb, rs;
+  uint32_t voa, vob, vos;     // per-lane byte offsets (kb = 0, u = 0)
+  uint32_t row8;              // 8 rows of A / B in bytes (8 * K)
+  int wave, nkb;
+  uint32_t fa0, fa1, fb0, fb1;   // LDS byte offsets of this lane's fragment chunks
+  uint32_t fsa, fsb;             // LDS float offsets of this lane's scales
+};
+
+template <int S>
+__device__ __forceinline__ void g256_issue(const G256Ctx& c, int kb) {
+  uint8_t* la = g256_a<S>() + c.wave * 4096;
+  uint8_t* lb = g256_b<S>() + c.wave * 4096;
+  const uint32_t kofs = (uint32_t)kb * 128u;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.ra, la + u * 1024, 16, c.voa, kofs + u * c.row8, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rb, lb + u * 1024, 16, c.vob, kofs + u * c.row8, 0, 0);
+  }
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rs, g256_s<S>() + c.wave * 64, 4, c.vos,
+                                           (uint32_t)kb * 4u, 0, 0);
+}
+
+__device__ __forceinline__ void promote4(v4f& acc, const v4f& p, const float4& sa, float sb) {
+  acc[0] = __builtin_fmaf(p[0], sa.x * sb, acc[0]);
+  acc[1] = __builtin_fmaf(p[1], sa.y * sb, acc[1]);
+  acc[2] = __builtin_fmaf(p[2], sa.z * sb, acc[2]);
+  acc[3] = __builtin_fmaf(p[3], sa.w * sb, acc[3]);
+}
+
+// MFMAs of n-tile j are issued while the 16x16 results of n-tile j-1 are
+// promoted (8 VALU per MFMA), so at most two tiles of partial results are
+// live and the VALU work runs in the MFMA shadow.
+template <int S>
+__device__ __forceinline__ void g256_compute(const G256Ctx& c, v4f (&acc)[4][8]) {
+  const uint8_t* la = g256_a<S>();
+  const uint8_t* lb = g256_b<S>();
+  const float* ls = g256_s<S>();
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  v8i af[4];
+  float4 sav[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    af[i] = as_v8i(*reinterpret_cast<const uint4*>(la + c.fa0 + i * 2048),
+                   *reinterpret_cast<const uint4*>(la + c.fa1 + i * 2048));
+    sav[i] = *reinterpret_cast<const float4*>(ls + c.fsa + i * 16);
+  }
+  v4f pc[4];
+  float sbc = ls[c.fsb];
+  {
+    const v8i bf = as_v8i(*reinterpret_cast<const uint4*>(lb + c.fb0),
+                          *reinterpret_cast<const uint4*>(lb + c.fb1));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pc[i] = mfma_f8_16x16x128(af[i], bf, zero);
+  }
+#pragma unroll
+  for (int j = 1; j < 8; ++j) {
+    v8i bf = as_v8i(*reinterpret_cast<const uint4*>(lb + c.fb0 + j * 2048),
+                    *reinterpret_cast<const uint4*>(lb + c.fb1 + j * 2048));
+    const float sbn = ls[c.fsb + j * 16];
+    // register fences: the MFMAs of tile j may not rise above this point and
+    // the promotions of tile j-1 must be done at the fence below, so the
+    // compiler cannot batch all MFMAs of the K block (that keeps 32 partial
+    // tiles alive and spills).
+    asm volatile("" : "+v"(bf));
+    v4f pn[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pn[i] = mfma_f8_16x16x128(af[i], bf, zero);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) promote4(acc[i][j - 1], pc[i], sav[i], sbc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][j - 1]));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pc[i] = pn[i];
+    sbc = sbn;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) promote4(acc[i][7], pc[i], sav[i], sbc);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][7]));
+}
+
+// One K block: prefetch block kb+1 into the other stage, compute block kb
+// from stage S, then wait for this wave's prefetch and meet at the barrier.
+template <int S>
+__device__ __forceinline__ void g256_step(const G256Ctx& c, int kb, v4f (&acc)[4][8]) {
+  if (kb + 1 < c.nkb) g256_issue<S ^ 1>(c, kb + 1);
+  g256_compute<S>(c, acc);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
+template <int BNS, bool OUT_F32>
+__global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ SA, const uint8_t* __restrict__ B,
+    const float* __restrict__ SB, void* __restrict__ C, int M, int N, int K, int tiles_m,
+    int tiles_n) {
+  G256Ctx c;
+  const int tid = threadIdx.x, lane = tid & 63;
+  c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: keeps descriptors in SGPRs
+  c.nkb = K >> 7;
+  const int fr = lane & 15, fg = lane >> 4;
+  const int wm = c.wave >> 1, wn = c.wave & 1;
+  int tmi, tni;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tmi, tni);
+  const int m0 = tmi * 256, n0 = tni * 256;
+
+  const int nsb = BNS == 1 ? N : (N + 127) / 128;
+  c.ra = make_rsrc(A, (uint32_t)M * (uint32_t)K);
+  c.rb = make_rsrc(B, (uint32_t)N * (uint32_t)K);
+  c.row8 = 8u * (uint32_t)K;
+  // loader slot: LDS row wave*32 + u*8 + lane/8, physical chunk lane%8 holds
+  // logical chunk (lane%8) ^ (row%8); row%8 == (lane/8)%8.
+  const int lrow = c.wave * 32 + (lane >> 3);
+  const int lch = (lane & 7) ^ ((lane >> 3) & 7);
+  c.voa = (uint32_t)(m0 + lrow) * (uint32_t)K + lch * 16;
+  c.vob = (uint32_t)(n0 + lrow) * (uint32_t)K + lch * 16;
+  const int sidx = (c.wave & 3) * 64 + lane;
+  if (c.wave < 4) {
+    c.rs = make_rsrc(SA, (uint32_t)M * c.nkb * 4u);
+    c.vos = (uint32_t)(m0 + sidx) * c.nkb * 4u;
+  } else {
+    c.rs = make_rsrc(SB, (uint32_t)nsb * c.nkb * 4u);
+    c.vos = (uint32_t)((n0 + sidx) / BNS) * c.nkb * 4u;
+  }
+  // fragment chunks: row r = (w* tile row) + 16 * t + fr holds logical chunks
+  // 2fg, 2fg+1 at physical positions (2fg) ^ (r%8), (2fg+1) ^ (r%8); r%8 == fr%8.
+  const uint32_t ch0 = (uint32_t)((2 * fg) ^ (fr & 7)) * 16u;
+  c.fa0 = (uint32_t)(wm * 64 + fr) * 128u + ch0;
+  c.fa1 = c.fa0 ^ 16u;
+  c.fb0 = (uint32_t)(wn * 128 + fr) * 128u + ch0;
+  c.fb1 = c.fb0 ^ 16u;
+  c.fsa = wm * 64 + 4 * fg;
+  c.fsb = 256 + wn * 128 + fr;
+
+  v4f acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  g256_issue<0>(c, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  int kb = 0;
+  for (; kb + 1 < c.nkb; kb += 2) {
+    g256_step<0>(c, kb, acc);
+    g256_step<1>(c, kb + 1, acc);
+  }
+  if (kb < c.nkb) g256_step<0>(c, kb, acc);
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int n = n0 + wn * 128 + j * 16 + fr;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * 64 + i * 16 + 4 * fg + r;
+        if (m < M && n < N) {
+          if (OUT_F32)
+            reinterpret_cast<float*>(C)[(int64_t)m * N + n] = acc[i][j][r];
+          else
+            reinterpret_cast<__bf16*>(C)[(int64_t)m * N + n] = (__bf16)acc[i][j][r];
+        }
+      }
+    }
+}
+
+template <int BNS, bool OUT_F32>
+static int launch_gemm_256(const uint8_t* a_q, const float* a_s, const uint8_t* b_q,
+                           const float* b_s, void* c, int M, int N, int K, hipStream_t st) {
+  const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
+  hipLaunchKernelGGL((gemm_fp8_nt_256_kernel<BNS, OUT_F32>), dim3((unsigned)(tiles_m * tiles_n)),
+                     dim3(512), 0, st, a_q, a_s, b_q, b_s, c, M, N, K, tiles_m, tiles_n);
+  return check_launch("gemm_fp8_nt_256");
+}
+
 template <int TM, int TN, int BNS, bool OUT_F32>
 static int launch_gemm_cfg(const uint8_t* a_q, const float* a_s, const uint8_t* b_q,
                            const float* b_s, void* c, int M, int N, int K, hipStream_t st) {
@@ -207,6 +415,15 @@ int launch_gemm_fp8(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, co
   if (M == 0 || N == 0) return TG_OK;
   const int m = (int)M, n = (int)N, k = (int)K;
   const bool f32 = c_dtype == TG_DTYPE_F32;
+  // 256 x 256 tiles once they fill the chip (>= 128 workgroups), else 128 x 128
+  const bool fits32 = (uint64_t)M * (uint64_t)K < (1ull << 31) && (uint64_t)N * (uint64_t)K < (1ull << 31);
+  if (fits32 && ((M + 255) / 256) * ((N + 255) / 256) >= 128) {
+    if (b_scale_bn == 1)
+      return f32 ? launch_gemm_256<1, true>(a_q, a_s, b_q, b_s, c, m, n, k, st)
+                 : launch_gemm_256<1, false>(a_q, a_s, b_q, b_s, c, m, n, k, st);
+    return f32 ? launch_gemm_256<128, true>(a_q, a_s, b_q, b_s, c, m, n, k, st)
+               : launch_gemm_256<128, false>(a_q, a_s, b_q, b_s, c, m, n, k, st);
+  }
   if (b_scale_bn == 1)
     return f32 ? launch_gemm_cfg<4, 4, 1, true>(a_q, a_s, b_q, b_s, c, m, n, k, st)
                : launch_gemm_cfg<4, 4, 1, false>(a_q, a_s, b_q, b_s, c, m, n, k, st);
