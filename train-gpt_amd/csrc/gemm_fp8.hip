@@ -208,13 +208,23 @@ template <int S> __device__ __forceinline__ float* g256_s() { return S ? g256_s1
 
 constexpr int kBufferWord3 = 0x00020000;   // gfx9 raw buffer: 32-bit data format
 
+// LDS row swizzle of the 256-tile kernel: 16-byte chunk c of row r is stored
+// at chunk position c ^ swz(r).  (r >> 1) & 7 spreads the 16 rows one
+// fragment read touches over all 64 banks (two rows per 256-byte bank line);
+// r & 7 is the 32-bank arrangement.
+#ifndef TG_G256_SWZ_SHIFT
+#define TG_G256_SWZ_SHIFT 1
+#endif
+__host__ __device__ constexpr int g256_swz(int r) { return (r >> TG_G256_SWZ_SHIFT) & 7; }
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufferWord3);
 }
 
 struct G256Ctx {
   __amdgpu_buffer_rsrc_t ra, rb, rs;
-  uint32_t voa, vob, vos;     // per-lane byte offsets (kb = 0, u = 0)
+  uint32_t voa[2], vob[2];    // per-lane byte offsets (kb = 0) for even / odd u
+  uint32_t vos;
   uint32_t row8;              // 8 rows of A / B in bytes (8 * K)
   int wave, nkb;
   uint32_t fa0, fa1, fb0, fb1;   // LDS byte offsets of this lane's fragment chunks
@@ -228,8 +238,8 @@ __device__ __forceinline__ void g256_issue(const G256Ctx& c, int kb) {
   const uint32_t kofs = (uint32_t)kb * 128u;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.ra, la + u * 1024, 16, c.voa, kofs + u * c.row8, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rb, lb + u * 1024, 16, c.vob, kofs + u * c.row8, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.ra, la + u * 1024, 16, c.voa[u & 1], kofs + u * c.row8, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rb, lb + u * 1024, 16, c.vob[u & 1], kofs + u * c.row8, 0, 0);
   }
   __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rs, g256_s<S>() + c.wave * 64, 4, c.vos,
                                            (uint32_t)kb * 4u, 0, 0);
@@ -272,18 +282,31 @@ __device__ __forceinline__ void g256_compute(const G256Ctx& c, v4f (&acc)[4][8])
     v8i bf = as_v8i(*reinterpret_cast<const uint4*>(lb + c.fb0 + j * 2048),
                     *reinterpret_cast<const uint4*>(lb + c.fb1 + j * 2048));
     const float sbn = ls[c.fsb + j * 16];
-    // register fences: the MFMAs of tile j may not rise above this point and
-    // the promotions of tile j-1 must be done at the fence below, so the
-    // compiler cannot batch all MFMAs of the K block (that keeps 32 partial
-    // tiles alive and spills).
+    // register fences: the MFMAs of tile j and the promotions of tile j-1 may
+    // not rise above this point and must be done at the fence below.  Left
+    // free, the compiler either batches all MFMAs of the K block (32 partial
+    // tiles alive: spills) or places each promotion right behind its own
+    // MFMA (MFMA and VALU serialize).
     asm volatile("" : "+v"(bf));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][j - 1]));
     v4f pn[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) pn[i] = mfma_f8_16x16x128(af[i], bf, zero);
 #pragma unroll
     for (int i = 0; i < 4; ++i) promote4(acc[i][j - 1], pc[i], sav[i], sbc);
+    // issue order MFMA / 8 VALU x 4: the promotion of tile j-1 co-executes
+    // with the MFMAs of tile j
 #pragma unroll
-    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][j - 1]));
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);   // 8 VALU
+    }
+    // the fence also takes tile j's MFMA results as inputs: without it the
+    // compiler sinks each MFMA down to the promotion that reads it and the
+    // MFMA / VALU pairs serialize
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][j - 1]) : "v"(pn[i]));
 #pragma unroll
     for (int i = 0; i < 4; ++i) pc[i] = pn[i];
     sbc = sbn;
@@ -324,11 +347,15 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
   c.rb = make_rsrc(B, (uint32_t)N * (uint32_t)K);
   c.row8 = 8u * (uint32_t)K;
   // loader slot: LDS row wave*32 + u*8 + lane/8, physical chunk lane%8 holds
-  // logical chunk (lane%8) ^ (row%8); row%8 == (lane/8)%8.
+  // logical chunk (lane%8) ^ swz(row); swz(row) only depends on lane/8 and
+  // on the parity of u (wave*32 + u*8 with u even / odd).
   const int lrow = c.wave * 32 + (lane >> 3);
-  const int lch = (lane & 7) ^ ((lane >> 3) & 7);
-  c.voa = (uint32_t)(m0 + lrow) * (uint32_t)K + lch * 16;
-  c.vob = (uint32_t)(n0 + lrow) * (uint32_t)K + lch * 16;
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int lch = (lane & 7) ^ g256_swz(lrow + par * 8);
+    c.voa[par] = (uint32_t)(m0 + lrow) * (uint32_t)K + lch * 16;
+    c.vob[par] = (uint32_t)(n0 + lrow) * (uint32_t)K + lch * 16;
+  }
   const int sidx = (c.wave & 3) * 64 + lane;
   if (c.wave < 4) {
     c.rs = make_rsrc(SA, (uint32_t)M * c.nkb * 4u);
@@ -337,9 +364,10 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
     c.rs = make_rsrc(SB, (uint32_t)nsb * c.nkb * 4u);
     c.vos = (uint32_t)((n0 + sidx) / BNS) * c.nkb * 4u;
   }
-  // fragment chunks: row r = (w* tile row) + 16 * t + fr holds logical chunks
-  // 2fg, 2fg+1 at physical positions (2fg) ^ (r%8), (2fg+1) ^ (r%8); r%8 == fr%8.
-  const uint32_t ch0 = (uint32_t)((2 * fg) ^ (fr & 7)) * 16u;
+  // fragment chunks: row r = (wave tile row) + 16 * t + fr holds logical
+  // chunks 2fg, 2fg+1 at physical positions (2fg) ^ swz(r), (2fg+1) ^ swz(r);
+  // swz(r) == swz(fr) because the other terms are multiples of 16.
+  const uint32_t ch0 = (uint32_t)((2 * fg) ^ g256_swz(fr)) * 16u;
   c.fa0 = (uint32_t)(wm * 64 + fr) * 128u + ch0;
   c.fa1 = c.fa0 ^ 16u;
   c.fb0 = (uint32_t)(wn * 128 + fr) * 128u + ch0;
@@ -363,22 +391,57 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
   }
   if (kb < c.nkb) g256_step<0>(c, kb, acc);
 
+  if (OUT_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int n = n0 + wn * 128 + j * 16 + fr;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm * 64 + i * 16 + 4 * fg + r;
+          if (m < M && n < N) reinterpret_cast<float*>(C)[(int64_t)m * N + n] = acc[i][j][r];
+        }
+      }
+    return;
+  }
+  // bf16 epilogue through LDS (the stage buffers are free after the last
+  // barrier): each wave writes its 64 x 128 tile (16 KiB as two 8 KiB halves
+  // of 32 rows x 256 B) and stores it back 16 bytes per lane, 4 rows x 256
+  // contiguous bytes per instruction.
+  uint8_t* ep = (c.wave < 4 ? g256_a0 + c.wave * 8192 : g256_b0 + (c.wave - 4) * 8192);
+  uint8_t* ep2 = (c.wave < 4 ? g256_a1 + c.wave * 8192 : g256_b1 + (c.wave - 4) * 8192);
+  // rows 0..31 of the wave tile go to ep, rows 32..63 to ep2
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int n = n0 + wn * 128 + j * 16 + fr;
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 64 + i * 16 + 4 * fg + r;
-        if (m < M && n < N) {
-          if (OUT_F32)
-            reinterpret_cast<float*>(C)[(int64_t)m * N + n] = acc[i][j][r];
-          else
-            reinterpret_cast<__bf16*>(C)[(int64_t)m * N + n] = (__bf16)acc[i][j][r];
-        }
+        const int row = i * 16 + 4 * fg + r, col = j * 16 + fr;
+        uint8_t* base = row < 32 ? ep : ep2;
+        *reinterpret_cast<__bf16*>(base + (row & 31) * 256 + col * 2) = (__bf16)acc[i][j][r];
+      }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's tile is in LDS
+  const bool vec_ok = (N % 8) == 0;
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    const int row = t * 4 + (lane >> 4), chunk = lane & 15;      // 16 lanes x 16 B per row
+    const uint8_t* base = row < 32 ? ep : ep2;
+    const uint4 v = *reinterpret_cast<const uint4*>(base + (row & 31) * 256 + chunk * 16);
+    const int m = m0 + wm * 64 + row, n = n0 + wn * 128 + chunk * 8;
+    if (m < M) {
+      __bf16* dst = reinterpret_cast<__bf16*>(C) + (int64_t)m * N + n;
+      if (vec_ok && n + 8 <= N) {
+        *reinterpret_cast<uint4*>(dst) = v;
+      } else {
+        const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (n + k < N) reinterpret_cast<uint16_t*>(dst)[k] = e[k];
       }
     }
+  }
 }
 
 template <int BNS, bool OUT_F32>
