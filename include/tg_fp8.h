@@ -112,11 +112,13 @@ int tg_quantize_weight_128x128(const void* w, int64_t K, int64_t N, uint8_t* w_q
  * counts must point to 3 device uint64_t (zeroed by the call). */
 int tg_selftest_fp8_cvt(uint64_t* counts, void* stream);
 
-/* Test support: compares the quantizers' bf16 divide (reciprocal refinement)
- * with the IEEE f32 divide for every bf16 amax and every bf16 x with
- * |x| <= amax.  counts[0] = e4m3fn byte mismatches, counts[1] = f32 quotient
- * mismatches with |x/s| > 2^-10, counts[2] = quotient mismatches at or below
- * 2^-10 (which encode to +-0 either way).  3 device uint64_t, zeroed by the call. */
+/* Test support: compares the quantizers' bf16 arithmetic with IEEE f32
+ * operations for every bf16 amax and every bf16 x with |x| <= amax.
+ * counts[0] = e4m3fn byte mismatches of the refined divide, counts[1] = f32
+ * quotient mismatches with |x/s| > 2^-10, counts[2] = quotient mismatches at
+ * or below 2^-10 (which encode to +-0 either way), counts[3] = refined scale
+ * amax/448 != IEEE, counts[4] = refined reciprocal != IEEE 1/s.
+ * 5 device uint64_t, zeroed by the call. */
 int tg_selftest_divide(uint64_t* counts, void* stream);
 
 #ifdef __cplusplus

@@ -1,17 +1,25 @@
 /*
- * Exhaustive host check of the divide the gfx950 quantizers use for
- * bf16-valued inputs (train-gpt_amd/csrc/tg_device.h, Divider::div):
- *   y = 1/s;  q0 = |x|*y;  nr = fma(q0, s, -|x|);  q = copysign(fma(-nr, y, q0), x)
- * against the IEEE quotient x / s, for every bf16 amax a,
- * s = max(a/448, 1e-30), and every bf16 x (both signs) with |x| <= a -- the
- * only (x, s) pairs the row/column/norm quantizers form.
+ * Exhaustive host check of the arithmetic the gfx950 quantizers use for
+ * bf16-valued inputs (train-gpt_amd/csrc/tg_device.h):
+ *   scale:  q0 = a*c (c = fl(1/448)); r = fma(-q0, 448, a); s = fma(r, c, q0),
+ *           floored at 1e-30                              (block_scale_bf16)
+ *   divide: y = fl(1/s); q0 = x*y; nr = fma(q0, s, -x); q = fma(-nr, y, q0)
+ *                                                         (Divider::div)
+ * against IEEE a/448 and x/s, for every bf16 amax a and every bf16 x (both
+ * signs) with |x| <= a -- the only (x, s) pairs the row/column/norm
+ * quantizers form.  (The device's reciprocal is checked against IEEE 1/s by
+ * tg_selftest_divide.)
  *
- * Counts (printed "pairs enc_mismatch q_mismatch_above q_mismatch_below"):
+ * Printed "pairs enc_mismatch q_mismatch_above q_mismatch_below scale_mismatch":
  *   enc_mismatch        e4m3fn bytes of q and x/s differ       (must be 0)
  *   q_mismatch_above    f32 q != x/s with |x/s| >  2^-10        (must be 0)
  *   q_mismatch_below    f32 q != x/s with |x/s| <= 2^-10        (reported;
  *                       both encode to +-0 there)
- * Compile with -O2 -mfma -ffp-contract=off.
+ *   scale_mismatch      refined scale != IEEE scale            (must be 0)
+ * Compile with -O2 -mfma -ffp-contract=off.  The operands pass through
+ * volatile so that the compiler keeps each fma exactly as written: gcc
+ * otherwise rewrites -fma(a, b, c) as fnmsub -(a*b) - c, which differs in
+ * the sign of a zero result.
  */
 #include <math.h>
 #include <stdint.h>
@@ -37,22 +45,36 @@ static uint8_t enc(float v) {
     return (uint8_t)(sign | (uint32_t)code);
 }
 
+static float scale_refined(float a) {
+    volatile float c = 1.0f / 448.0f, m = 448.0f;
+    const float q0 = a * c;
+    const float r = __builtin_fmaf(-q0, m, a);
+    float s = __builtin_fmaf(r, c, q0);
+    if (isinf(a)) s = a;
+    return s < 1e-30f ? 1e-30f : s;
+}
+
 int main(int argc, char** argv) {
     uint32_t a_lo = 0, a_hi = 0x7F7F;      /* positive finite bf16 patterns */
     if (argc == 3) { a_lo = (uint32_t)strtoul(argv[1], 0, 0); a_hi = (uint32_t)strtoul(argv[2], 0, 0); }
-    unsigned long long pairs = 0, bad_enc = 0, bad_hi = 0, bad_lo = 0;
+    unsigned long long pairs = 0, bad_enc = 0, bad_hi = 0, bad_lo = 0, bad_scale = 0;
     for (uint32_t ab = a_lo; ab <= a_hi; ++ab) {
         const float a = u2f(ab << 16);
-        float s = a / 448.0f;
-        if (s < 1e-30f) s = 1e-30f;
+        float s_ieee = a / 448.0f;
+        if (s_ieee < 1e-30f) s_ieee = 1e-30f;
+        const float s = scale_refined(a);
+        if (f2u(s) != f2u(s_ieee)) ++bad_scale;
         const float y = 1.0f / s;
         for (uint32_t xb = 0; xb <= ab; ++xb) {
             for (uint32_t sign = 0; sign < 2; ++sign) {
-                const float x = u2f((xb << 16) | (sign << 31));
-                const float ax = fabsf(x);
-                const float q0 = ax * y;
-                const float nr = __builtin_fmaf(q0, s, -ax);
-                const float q = copysignf(__builtin_fmaf(-nr, y, q0), x);
+                volatile float xv = u2f((xb << 16) | (sign << 31));
+                const float x = xv;
+                const float q0 = x * y;
+                volatile float nx = -x, vs = s;
+                volatile float nr = __builtin_fmaf(q0, vs, nx);   /* stored: not fused into its negation */
+                const float nnr = -nr;
+                volatile float vy = y;
+                const float q = __builtin_fmaf(nnr, vy, q0);
                 const float ref = x / s;
                 ++pairs;
                 if (enc(q) != enc(ref)) {
@@ -66,6 +88,6 @@ int main(int argc, char** argv) {
             }
         }
     }
-    printf("%llu %llu %llu %llu\n", pairs, bad_enc, bad_hi, bad_lo);
+    printf("%llu %llu %llu %llu %llu\n", pairs, bad_enc, bad_hi, bad_lo, bad_scale);
     return 0;
 }

@@ -1,9 +1,9 @@
-"""Exhaustive host check of the quantizers' bf16 divide (tests/csrc/div_identity.c).
+"""Exhaustive host check of the quantizers' bf16 arithmetic (tests/csrc/div_identity.c).
 
-For every bf16 amax and every bf16 x with |x| <= amax, the reciprocal
-refinement used on the GPU must give the same e4m3fn byte as the IEEE
-quotient, and the same f32 quotient wherever |x/s| > 2^-10.  The sweep is
-split over 8 processes.
+For every bf16 amax the refined scale must equal IEEE amax/448, and for
+every bf16 x with |x| <= amax the refined divide must give the same e4m3fn
+byte as the IEEE quotient, and the same f32 quotient wherever
+|x/s| > 2^-10.  The sweep is split over 8 processes.
 """
 import os
 import subprocess
@@ -23,12 +23,13 @@ def test_divide_identity_all_bf16_pairs():
     for k in range(8):
         lo, up = edges[k] + (1 if k else 0), edges[k + 1]
         procs.append(subprocess.Popen([exe, hex(lo), hex(up)], stdout=subprocess.PIPE, text=True))
-    pairs = enc = above = 0
+    pairs = enc = above = scale = 0
     for p in procs:
         out, _ = p.communicate()
         assert p.returncode == 0
-        a, b, c, _ = (int(v) for v in out.split())
-        pairs, enc, above = pairs + a, enc + b, above + c
+        a, b, c, _, e = (int(v) for v in out.split())
+        pairs, enc, above, scale = pairs + a, enc + b, above + c, scale + e
     assert pairs == sum(2 * (ab + 1) for ab in range(hi + 1))
+    assert scale == 0
     assert enc == 0
     assert above == 0

@@ -17,8 +17,8 @@ import _tglib as L
 pytestmark = pytest.mark.gpu
 
 
-def _run(fn_name, dev):
-    counts = torch.zeros(3, dtype=torch.int64, device=dev)
+def _run(fn_name, dev, n=3):
+    counts = torch.zeros(n, dtype=torch.int64, device=dev)
     L.check(getattr(L.lib(), fn_name)(L.ptr(counts), L.stream_of(counts)))
     torch.cuda.synchronize()
     return [int(v) for v in counts.cpu()]
@@ -33,8 +33,10 @@ def test_hw_fp8_convert_matches_integer_encoder(dev):
 
 
 def test_divide_refinement_matches_ieee(dev):
-    byte_mm, q_above, q_below = _run("tg_selftest_divide", dev)
+    byte_mm, q_above, q_below, scale_mm, rcp_mm = _run("tg_selftest_divide", dev, 5)
     print(f"divide: byte mismatches {byte_mm}, quotient mismatches above 2^-10 {q_above}, "
-          f"at/below 2^-10 {q_below}")
+          f"at/below 2^-10 {q_below}; scale mismatches {scale_mm}, reciprocal mismatches {rcp_mm}")
+    assert scale_mm == 0
+    assert rcp_mm == 0
     assert byte_mm == 0
     assert q_above == 0

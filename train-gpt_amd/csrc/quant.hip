@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const void* __restrict_
   for (int u = 0; u < UNROLL; ++u) {
     int64_t c = base + u * 256;
     uint32_t m = row16_max_u32(absmax8(v[u]));   // uniform control flow for DPP
-    float sc = block_scale(m);
+    float sc = F32_IN ? block_scale(m) : block_scale_bf16(m);
     if (c < nchunks) {
       q[c] = quant8<!F32_IN>(v[u], sc);
       if ((threadIdx.x & 15) == 0) s[c >> 4] = sc;
@@ -169,7 +169,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(const uint16_t* __restr
 #pragma unroll
   for (int i = 0; i < 32; ++i) m = max(m, __float_as_uint(f[i]) & 0x7FFFFFFFu);
   m = quad_max_u32(m);
-  const float sc = block_scale(m);
+  const float sc = block_scale_bf16(m);
   Divider d(sc);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(256) void quant_w128_kernel(const uint16_t* __restr
   if ((tid & 63) == 0) red[tid >> 6] = m;
   __syncthreads();
   m = max(max(red[0], red[1]), max(red[2], red[3]));
-  const float sc = block_scale(m);
+  const float sc = block_scale_bf16(m);
   if (tid == 0) ws[blockIdx.x * (K >> 7) + blockIdx.y] = sc;
   Divider d(sc);
   const int nl = tid >> 1, half = tid & 1;
@@ -289,15 +289,22 @@ __global__ __launch_bounds__(256) void selftest_cvt_kernel(unsigned long long* c
   }
 }
 
-// Self-test of Divider::div against the device's IEEE divide over every bf16
-// amax (one workgroup each) and every bf16 x with |x| <= amax, both signs.
-// counts[0]: e4m3fn byte mismatches; counts[1]: f32 quotient mismatches with
-// |x/s| > 2^-10; counts[2]: quotient mismatches at or below 2^-10.
+// Self-test of the bf16 quantizer arithmetic against the device's IEEE
+// operations, over every bf16 amax (one workgroup each) and every bf16 x
+// with |x| <= amax, both signs.  counts[0]: e4m3fn byte mismatches of
+// Divider::div; counts[1]: f32 quotient mismatches with |x/s| > 2^-10;
+// counts[2]: quotient mismatches at or below 2^-10; counts[3]:
+// block_scale_bf16 != IEEE scale; counts[4]: Divider's reciprocal != IEEE 1/s.
 __global__ __launch_bounds__(256) void selftest_divide_kernel(unsigned long long* counts) {
   const uint32_t ab = blockIdx.x;                       // bf16 pattern of amax
   const float a = __uint_as_float(ab << 16);
-  const float sc = block_scale(__float_as_uint(a));
+  const float sc = block_scale_bf16(__float_as_uint(a));
+  const float sc_ieee = block_scale(__float_as_uint(a));
   const Divider d(sc);
+  if (threadIdx.x == 0) {
+    if (__float_as_uint(sc) != __float_as_uint(sc_ieee)) atomicAdd(&counts[3], 1ull);
+    if (d.fast && __float_as_uint(d.y) != __float_as_uint(1.0f / sc)) atomicAdd(&counts[4], 1ull);
+  }
   unsigned long long c0 = 0, c1 = 0, c2 = 0;
   for (uint32_t i = threadIdx.x; i <= 2 * ab + 1; i += 256) {
     const float x = __uint_as_float(((i >> 1) << 16) | ((i & 1u) << 31));
@@ -320,8 +327,8 @@ __global__ __launch_bounds__(256) void selftest_divide_kernel(unsigned long long
   }
 }
 
-__global__ void zero3_kernel(unsigned long long* c) {
-  if (threadIdx.x < 3) c[threadIdx.x] = 0;
+__global__ void zero_kernel(unsigned long long* c, int n) {
+  if ((int)threadIdx.x < n) c[threadIdx.x] = 0;
 }
 
 }  // namespace tg
@@ -371,8 +378,8 @@ extern "C" int tg_quantize_weight_128x128(const void* w, int64_t K, int64_t N, u
 extern "C" int tg_selftest_fp8_cvt(uint64_t* counts, void* stream) {
   if (!counts) return einval("selftest_fp8_cvt: null pointer");
   auto* c = reinterpret_cast<unsigned long long*>(counts);
-  hipLaunchKernelGGL(zero3_kernel, dim3(1), dim3(64), 0, as_stream(stream), c);
-  TG_TRY(check_launch("zero3"));
+  hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(64), 0, as_stream(stream), c, 3);
+  TG_TRY(check_launch("zero"));
   hipLaunchKernelGGL(selftest_cvt_kernel, dim3(4096), dim3(256), 0, as_stream(stream), c);
   return check_launch("selftest_cvt");
 }
@@ -380,8 +387,8 @@ extern "C" int tg_selftest_fp8_cvt(uint64_t* counts, void* stream) {
 extern "C" int tg_selftest_divide(uint64_t* counts, void* stream) {
   if (!counts) return einval("selftest_divide: null pointer");
   auto* c = reinterpret_cast<unsigned long long*>(counts);
-  hipLaunchKernelGGL(zero3_kernel, dim3(1), dim3(64), 0, as_stream(stream), c);
-  TG_TRY(check_launch("zero3"));
+  hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(64), 0, as_stream(stream), c, 5);
+  TG_TRY(check_launch("zero"));
   hipLaunchKernelGGL(selftest_divide_kernel, dim3(0x7F80), dim3(256), 0, as_stream(stream), c);
   return check_launch("selftest_divide");
 }

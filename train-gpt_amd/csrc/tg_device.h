@@ -5,8 +5,8 @@
 //   * e4m3fn: OCP E4M3 (bias 7, max 448 = 0x7E, 0x7F/0xFF NaN, no inf),
 //     round-to-nearest-even, non-saturating.
 //   * x / s is an IEEE f32 divide.  For bf16 inputs it is evaluated as
-//     y = 1/s (IEEE), q0 = |x|*y, nr = fma(q0, s, -|x|), q = fma(-nr, y, q0)
-//     with x's sign copied on.  Over every bf16 amax a (s = max(a/448, 1e-30))
+//     y = 1/s, q0 = x*y, nr = fma(q0, s, -x), q = fma(-nr, y, q0).
+//     Over every bf16 amax a (s = max(a/448, 1e-30))
 //     and every bf16 x with |x| <= a this gives the same e4m3fn byte as the
 //     IEEE quotient, and the same f32 quotient whenever |x/s| > 2^-10 (below
 //     that both encode to +-0); the residual only underflows when s is the
@@ -31,14 +31,28 @@ __device__ __forceinline__ uint4 ldg_stream(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+// Streaming stores (written once, not re-read by this kernel).
+__device__ __forceinline__ void stg_stream(uint4* p, const uint4& v) {
+  const u32x4_t w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(p));
+}
+__device__ __forceinline__ void stg_stream(uint2* p, const uint2& v) {
+  const u32x2_t w = {v.x, v.y};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x2_t*>(p));
+}
+
 __device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
-// Two f32 -> packed bf16 (lo in bits 0..15), round-to-nearest-even.
+// Two f32 -> packed bf16 (lo in bits 0..15), round-to-nearest-even: one
+// v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  bf16x2_t v = {(__bf16)lo, (__bf16)hi};
-  return __builtin_bit_cast(uint32_t, v);
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 // f32 -> bf16 -> f32 (the value a bf16 tensor would hold).
@@ -87,21 +101,39 @@ __device__ __forceinline__ float block_scale(uint32_t amax_bits) {
   return (s < kScaleFloor) ? kScaleFloor : s;      // jnp.maximum; NaN stays NaN
 }
 
+// The same scale for a bf16-valued amax: fl32(amax / 448) by one refinement
+// of amax * fl32(1/448) (three VALU instead of the IEEE divide sequence; equal
+// to the IEEE quotient for every bf16 amax, checked by tg_selftest_divide and
+// tests/csrc/div_identity.c).  The refinement turns +inf into NaN, so +inf is
+// restored explicitly; NaN propagates.
+__device__ __forceinline__ float block_scale_bf16(uint32_t amax_bits) {
+  const float amax = __uint_as_float(amax_bits);
+  constexpr float c = 1.0f / 448.0f;
+  const float q0 = amax * c;
+  const float r = __builtin_fmaf(-q0, kE4M3Max, amax);
+  float s = __builtin_fmaf(r, c, q0);
+  if (amax_bits == 0x7F800000u) s = __builtin_inff();
+  return (s < kScaleFloor) ? kScaleFloor : s;
+}
+
 struct Divider {
   float s, y;
   bool fast;
+  // y = fl32(1/s): v_rcp_f32 plus one Newton step (equal to the IEEE
+  // reciprocal for every scale a bf16 amax can produce, checked by
+  // tg_selftest_divide).  A finite scale is >= 1e-30, so s and 1/s are normal.
   __device__ __forceinline__ explicit Divider(float scale) : s(scale) {
-    y = 1.0f / scale;                              // IEEE reciprocal
-    // finite scale: s >= 1e-30 is always normal, 1/s normal
+    const float y0 = __builtin_amdgcn_rcpf(scale);
+    y = __builtin_fmaf(__builtin_fmaf(-scale, y0, 1.0f), y0, y0);
     fast = (__float_as_uint(scale) & 0x7F800000u) != 0x7F800000u;
   }
-  // x / s for bf16-valued x and finite s (see header comment).  Works on |x|
-  // and restores the sign last, so +-0 (and underflow to +-0) keep x's sign.
+  // x / s for bf16-valued x and finite s (see header comment):
+  // q0 = x*y, nr = q0*s - x (exact), q = q0 - nr*y.  The residual is formed
+  // negated so that x = -0 yields -0.
   __device__ __forceinline__ float div(float x) const {
-    const float ax = __builtin_fabsf(x);
-    const float q0 = ax * y;
-    const float nr = __builtin_fmaf(q0, s, -ax);
-    return __builtin_copysignf(__builtin_fmaf(-nr, y, q0), x);
+    const float q0 = x * y;
+    const float nr = __builtin_fmaf(q0, s, -x);
+    return __builtin_fmaf(-nr, y, q0);
   }
 };
 
