@@ -45,7 +45,22 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--norm-iters", type=int, default=200)
+    p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                   help="only run a plain device copy of MIB MiB (calibrates the FETCH_SIZE / "
+                        "WRITE_SIZE counters for the roofline traffic figure) and exit")
     return p.parse_args()
+
+
+def copy_probe(mib: int) -> None:
+    """A plain copy of known size: FETCH_SIZE / WRITE_SIZE of this dispatch
+    divided by mib MiB is the counter's scale factor on this GPU."""
+    import torch
+    src = torch.ones(mib * (1 << 20) // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": mib * (1 << 20)}))
 
 
 class Step:
@@ -183,6 +198,9 @@ def cpu_baseline(rows=4096):
 
 def main():
     args = parse()
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
                           "n_gpus": args.gpus}))
