@@ -222,27 +222,46 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
 }
 
 struct G256Ctx {
-  __amdgpu_buffer_rsrc_t ra, rb, rs;
+  __amdgpu_buffer_rsrc_t ra, rb, rsa, rsb;
   uint32_t voa[2], vob[2];    // per-lane byte offsets (kb = 0) for even / odd u
-  uint32_t vos;
+  uint32_t vosa, vosb;
   uint32_t row8;              // 8 rows of A / B in bytes (8 * K)
   int wave, nkb;
   uint32_t fa0, fa1, fb0, fb1;   // LDS byte offsets of this lane's fragment chunks
   uint32_t fsa, fsb;             // LDS float offsets of this lane's scales
 };
 
+// Loads of one K block into a stage, in 16 parts issued by the four loader
+// waves (waves 0-3; each covers its own LDS slot w and slot w + 4):
+// parts 0-7 are A rows (slot w, then w + 4; four 1 KiB row groups each),
+// parts 8-15 B rows; part 0 also loads this wave's 64 A-row scales and 64
+// B-row scales.  A DMA instruction stalls its wave for a while at issue, so
+// the loads ride on half of the waves and two parts per compute region: on
+// every SIMD one wave keeps issuing MFMAs while the other feeds LDS.
+__device__ __forceinline__ void g256_issue_part(const G256Ctx& c, uint8_t* la, uint8_t* lb,
+                                                float* ls, int kb, int part) {
+  const uint32_t kofs = (uint32_t)kb * 128u;
+  const int slot = c.wave + ((part >> 2) & 1) * 4;
+  const int u = part & 3;
+  const uint32_t sofs = kofs + u * c.row8 + ((part >> 2) & 1) * 16u * c.row8;   // slot w+4: +128 rows
+  if (part < 8)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.ra, la + slot * 4096 + u * 1024, 16, c.voa[u & 1],
+                                             sofs, 0, 0);
+  else
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rb, lb + slot * 4096 + u * 1024, 16, c.vob[u & 1],
+                                             sofs, 0, 0);
+  if (part == 0) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rsa, ls + c.wave * 64, 4, c.vosa, (uint32_t)kb * 4u, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rsb, ls + 256 + c.wave * 64, 4, c.vosb, (uint32_t)kb * 4u, 0, 0);
+  }
+}
+
 template <int S>
 __device__ __forceinline__ void g256_issue(const G256Ctx& c, int kb) {
-  uint8_t* la = g256_a<S>() + c.wave * 4096;
-  uint8_t* lb = g256_b<S>() + c.wave * 4096;
-  const uint32_t kofs = (uint32_t)kb * 128u;
+  if (c.wave < 4) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.ra, la + u * 1024, 16, c.voa[u & 1], kofs + u * c.row8, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rb, lb + u * 1024, 16, c.vob[u & 1], kofs + u * c.row8, 0, 0);
+    for (int p = 0; p < 16; ++p) g256_issue_part(c, g256_a<S>(), g256_b<S>(), g256_s<S>(), kb, p);
   }
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rs, g256_s<S>() + c.wave * 64, 4, c.vos,
-                                           (uint32_t)kb * 4u, 0, 0);
 }
 
 __device__ __forceinline__ void promote4(v4f& acc, const v4f& p, const float4& sa, float sb) {
@@ -254,13 +273,19 @@ __device__ __forceinline__ void promote4(v4f& acc, const v4f& p, const float4& s
 
 // MFMAs of n-tile j are issued while the 16x16 results of n-tile j-1 are
 // promoted (8 VALU per MFMA), so at most two tiles of partial results are
-// live and the VALU work runs in the MFMA shadow.
+// live and the VALU work runs in the MFMA shadow.  The B fragment and column
+// scale of n-tile j+1 are read from LDS one region ahead, so no region waits
+// on LDS latency.
 template <int S>
-__device__ __forceinline__ void g256_compute(const G256Ctx& c, v4f (&acc)[4][8]) {
+__device__ __forceinline__ void g256_compute(const G256Ctx& c, v4f (&acc)[4][8], int kb_next) {
   const uint8_t* la = g256_a<S>();
   const uint8_t* lb = g256_b<S>();
   const float* ls = g256_s<S>();
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  auto read_b = [&](int j) {
+    return as_v8i(*reinterpret_cast<const uint4*>(lb + c.fb0 + j * 2048),
+                  *reinterpret_cast<const uint4*>(lb + c.fb1 + j * 2048));
+  };
   v8i af[4];
   float4 sav[4];
 #pragma unroll
@@ -269,19 +294,28 @@ __device__ __forceinline__ void g256_compute(const G256Ctx& c, v4f (&acc)[4][8])
                    *reinterpret_cast<const uint4*>(la + c.fa1 + i * 2048));
     sav[i] = *reinterpret_cast<const float4*>(ls + c.fsa + i * 16);
   }
+  v8i bn = read_b(1);
+  float sbn = ls[c.fsb + 16];
   v4f pc[4];
   float sbc = ls[c.fsb];
+  const bool pf = kb_next < c.nkb && c.wave < 4;   // loader waves, wave-uniform
+  if (pf) {
+    g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, 0);
+    g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, 1);
+  }
   {
-    const v8i bf = as_v8i(*reinterpret_cast<const uint4*>(lb + c.fb0),
-                          *reinterpret_cast<const uint4*>(lb + c.fb1));
+    const v8i bf = read_b(0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) pc[i] = mfma_f8_16x16x128(af[i], bf, zero);
   }
 #pragma unroll
   for (int j = 1; j < 8; ++j) {
-    v8i bf = as_v8i(*reinterpret_cast<const uint4*>(lb + c.fb0 + j * 2048),
-                    *reinterpret_cast<const uint4*>(lb + c.fb1 + j * 2048));
-    const float sbn = ls[c.fsb + j * 16];
+    v8i bf = bn;
+    const float sbj = sbn;
+    if (j + 1 < 8) {
+      bn = read_b(j + 1);
+      sbn = ls[c.fsb + (j + 1) * 16];
+    }
     // register fences: the MFMAs of tile j and the promotions of tile j-1 may
     // not rise above this point and must be done at the fence below.  Left
     // free, the compiler either batches all MFMAs of the K block (32 partial
@@ -290,6 +324,10 @@ __device__ __forceinline__ void g256_compute(const G256Ctx& c, v4f (&acc)[4][8])
     asm volatile("" : "+v"(bf));
 #pragma unroll
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][j - 1]));
+    if (pf) {
+      g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, 2 * j);
+      g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, 2 * j + 1);
+    }
     v4f pn[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) pn[i] = mfma_f8_16x16x128(af[i], bf, zero);
@@ -309,7 +347,7 @@ __device__ __forceinline__ void g256_compute(const G256Ctx& c, v4f (&acc)[4][8])
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][j - 1]) : "v"(pn[i]));
 #pragma unroll
     for (int i = 0; i < 4; ++i) pc[i] = pn[i];
-    sbc = sbn;
+    sbc = sbj;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) promote4(acc[i][7], pc[i], sav[i], sbc);
@@ -317,12 +355,12 @@ __device__ __forceinline__ void g256_compute(const G256Ctx& c, v4f (&acc)[4][8])
   for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][7]));
 }
 
-// One K block: prefetch block kb+1 into the other stage, compute block kb
-// from stage S, then wait for this wave's prefetch and meet at the barrier.
+// One K block: compute block kb from stage S while prefetching block kb+1
+// into the other stage (issued part by part inside the compute regions), then
+// wait for this wave's prefetch and meet at the barrier.
 template <int S>
 __device__ __forceinline__ void g256_step(const G256Ctx& c, int kb, v4f (&acc)[4][8]) {
-  if (kb + 1 < c.nkb) g256_issue<S ^ 1>(c, kb + 1);
-  g256_compute<S>(c, acc);
+  g256_compute<S>(c, acc, kb + 1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 }
@@ -357,13 +395,10 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
     c.vob[par] = (uint32_t)(n0 + lrow) * (uint32_t)K + lch * 16;
   }
   const int sidx = (c.wave & 3) * 64 + lane;
-  if (c.wave < 4) {
-    c.rs = make_rsrc(SA, (uint32_t)M * c.nkb * 4u);
-    c.vos = (uint32_t)(m0 + sidx) * c.nkb * 4u;
-  } else {
-    c.rs = make_rsrc(SB, (uint32_t)nsb * c.nkb * 4u);
-    c.vos = (uint32_t)((n0 + sidx) / BNS) * c.nkb * 4u;
-  }
+  c.rsa = make_rsrc(SA, (uint32_t)M * c.nkb * 4u);
+  c.vosa = (uint32_t)(m0 + sidx) * c.nkb * 4u;
+  c.rsb = make_rsrc(SB, (uint32_t)nsb * c.nkb * 4u);
+  c.vosb = (uint32_t)((n0 + sidx) / BNS) * c.nkb * 4u;
   // fragment chunks: row r = (wave tile row) + 16 * t + fr holds logical
   // chunks 2fg, 2fg+1 at physical positions (2fg) ^ swz(r), (2fg+1) ^ swz(r);
   // swz(r) == swz(fr) because the other terms are multiples of 16.
