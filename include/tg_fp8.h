@@ -78,6 +78,35 @@ int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, const void* g, 
                                    void* db, int64_t M, int64_t N, int64_t K, int block_k,
                                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* The bf16 dot of the straight-through backward (fp8.py:95-96, `x @ y` on bf16
+ * operands): c (M, N) = bf16(sum_k a[m, k] * b[n, k]) with fp32 accumulation.
+ * a (M, K), b (N, K), c (M, N), all bf16 row-major; K % 64 == 0; a and b
+ * 16-byte aligned and each below 2 GiB. */
+int tg_gemm_bf16_nt(const void* a, const void* b, void* c, int64_t M, int64_t N, int64_t K,
+                    void* stream);
+
+/* The `.astype(jnp.bfloat16)` operand casts of fp8.py:92-94 (RNE for f32),
+ * optionally transposed (the `a_2d.T` of fp8.py:96), into rows padded with
+ * zeros to `pitch` elements:
+ *   transpose = 0: x (rows, cols) -> y (rows, pitch), pitch >= cols
+ *   transpose = 1: x (rows, cols) -> y (cols, pitch), pitch >= rows
+ * x_dtype: TG_DTYPE_BF16 or TG_DTYPE_F32; y bf16. */
+int tg_pack_bf16(const void* x, int x_dtype, int64_t rows, int64_t cols, int transpose, void* y,
+                 int64_t pitch, void* stream);
+
+/* Device workspace (bytes) of tg_block_scaled_matmul_bwd_bf16. */
+size_t tg_block_scaled_matmul_bwd_bf16_workspace(int64_t M, int64_t N, int64_t K);
+
+/* _fp8_backward (fp8.py:85-98), the reference's straight-through rule:
+ *   da (M, K) = bf16(g) @ bf16(b).T      db (K, N) = bf16(a).T @ bf16(g)
+ * a (M, K), b (K, N), g (M, N), each bf16 or f32 (its *_dtype); da, db bf16
+ * (the caller widens to a.dtype / b.dtype as fp8.py:95-96 does).  Any M, N, K;
+ * an empty contraction writes zero gradients. */
+int tg_block_scaled_matmul_bwd_bf16(const void* a, int a_dtype, const void* b, int b_dtype,
+                                    const void* g, int g_dtype, void* da, void* db, int64_t M,
+                                    int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
+                                    void* stream);
+
 /* _rms_norm_pure (kernels.py:30-33) over the last axis of x (rows, dim) bf16,
  * scale (dim,) bf16, y (rows, dim) bf16:
  * r = bf16(rsqrt(mean(x^2) + eps)); y = bf16(bf16(x * r) * scale).

@@ -34,6 +34,11 @@ SIGNATURES = {
     "tg_rms_norm_fp8": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _int, _vp]),
     "tg_gemv_fp8": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _i64, _i64, _i64, _int, _vp]),
     "tg_quantize_weight_128x128": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "tg_gemm_bf16_nt": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "tg_pack_bf16": (_int, [_vp, _int, _i64, _i64, _int, _vp, _i64, _vp]),
+    "tg_block_scaled_matmul_bwd_bf16_workspace": (_sz, [_i64, _i64, _i64]),
+    "tg_block_scaled_matmul_bwd_bf16": (_int, [_vp, _int, _vp, _int, _vp, _int, _vp, _vp, _i64,
+                                               _i64, _i64, _vp, _sz, _vp]),
     "tg_selftest_fp8_cvt": (_int, [_vp, _vp]),
     "tg_selftest_divide": (_int, [_vp, _vp]),
 }

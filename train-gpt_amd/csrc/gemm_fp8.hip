@@ -20,11 +20,11 @@
 //     range tiles are walked in groups of 8 tile-rows for L2 reuse of B.
 #include "tg_device.h"
 #include "tg_host.h"
+#include "gemm_tile.h"
 
 namespace tg {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
-typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ v4f mfma_f8_16x16x128(const v8i& a, const v8i& b, const v4f& c) {
   // Format codes 0/0 = FP8 E4M3 for A and B; zero scale operands select the
@@ -37,22 +37,6 @@ __device__ __forceinline__ v8i as_v8i(const uint4& lo, const uint4& hi) {
   r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
   r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
   return r;
-}
-
-// XCD-aware, grouped tile order.  Returns the (tile_m, tile_n) of workgroup bid.
-__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int ntiles = tiles_m * tiles_n;
-  const int xcd = bid & 7, slot = bid >> 3;
-  const int q = ntiles >> 3, rem = ntiles & 7;
-  const int t = xcd * q + min(xcd, rem) + slot;
-  constexpr int GROUP = 8;
-  const int per_group = GROUP * tiles_n;
-  const int g = t / per_group;
-  const int first_m = g * GROUP;
-  const int gsize = min(tiles_m - first_m, GROUP);
-  const int in_g = t - g * per_group;
-  tm = first_m + in_g % gsize;
-  tn = in_g / gsize;
 }
 
 template <int TM, int TN, int BNS, bool OUT_F32>
@@ -205,21 +189,6 @@ __shared__ __attribute__((aligned(16))) float g256_s1[512];
 template <int S> __device__ __forceinline__ uint8_t* g256_a() { return S ? g256_a1 : g256_a0; }
 template <int S> __device__ __forceinline__ uint8_t* g256_b() { return S ? g256_b1 : g256_b0; }
 template <int S> __device__ __forceinline__ float* g256_s() { return S ? g256_s1 : g256_s0; }
-
-constexpr int kBufferWord3 = 0x00020000;   // gfx9 raw buffer: 32-bit data format
-
-// LDS row swizzle of the 256-tile kernel: 16-byte chunk c of row r is stored
-// at chunk position c ^ swz(r).  (r >> 1) & 7 spreads the 16 rows one
-// fragment read touches over all 64 banks (two rows per 256-byte bank line);
-// r & 7 is the 32-bank arrangement.
-#ifndef TG_G256_SWZ_SHIFT
-#define TG_G256_SWZ_SHIFT 1
-#endif
-__host__ __device__ constexpr int g256_swz(int r) { return (r >> TG_G256_SWZ_SHIFT) & 7; }
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufferWord3);
-}
 
 struct G256Ctx {
   __amdgpu_buffer_rsrc_t ra, rb, rsa, rsb;

@@ -151,13 +151,17 @@ def _fp8_backward(block_k, residuals, g):
     BACKWARD_MODE "fp8": da = fwd(g, b.T), db = fwd(a.T, g) through FP8 MFMA,
     so N (da's contraction) and M (db's) must divide by block_k, with the
     reference's ValueError text (fp8.py:55-56) otherwise.
-    BACKWARD_MODE "bf16": fp8.py:85-98's straight-through bf16 rule (not built).
+    BACKWARD_MODE "bf16": fp8.py:85-98's straight-through rule, da = bf16(g) @
+    bf16(b).T and db = bf16(a).T @ bf16(g), each a bf16 MFMA GEMM with fp32
+    accumulation rounded once to bf16; block_k is unused, as in the reference.
     """
     a, b = residuals
     *leading, K = a.shape
     _, N = b.shape
     if BACKWARD_MODE == "bf16":
-        raise NotImplementedError("bf16 straight-through backward needs the bf16 GEMM (not built)")
+        return _bf16_backward(a, b, g)
+    if BACKWARD_MODE != "fp8":
+        raise ValueError(f"unknown BACKWARD_MODE {BACKWARD_MODE!r} (expected 'fp8' or 'bf16')")
     _check_block_k(block_k)
     a_2d = a.reshape(-1, K)
     g_2d = g.reshape(-1, N)
@@ -185,6 +189,28 @@ def _fp8_backward(block_k, residuals, g):
         qat, sat = quantize_fp8(a_2d, block_k, transpose=True)     # a.T along M
         qgt, sgt = quantize_fp8(g_2d, block_k, transpose=True)     # g.T along M
         db = scaled_matmul(qat.view(u8), sat, qgt.view(u8), sgt)
+    return da.reshape(*leading, K).to(a.dtype), db.to(b.dtype)
+
+
+def _bf16_backward(a, b, g):
+    """fp8.py:85-98: straight-through bf16 gradients (da as a.dtype, db as b.dtype)."""
+    *leading, K = a.shape
+    _, N = b.shape
+    a_2d = a.reshape(-1, K).contiguous()
+    g_2d = g.reshape(-1, N).contiguous()
+    b_c = b.contiguous()
+    M = a_2d.shape[0]
+    _L.require_gpu(a_2d, b_c, g_2d)
+    bf = torch.bfloat16
+    da = torch.empty((M, K), dtype=bf, device=a.device)
+    db = torch.empty((K, N), dtype=bf, device=a.device)
+    ws_bytes = _L.lib().tg_block_scaled_matmul_bwd_bf16_workspace(M, N, K)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=a.device)
+    _L.check(_L.lib().tg_block_scaled_matmul_bwd_bf16(
+        _L.ptr(a_2d), _L.dtype_code(a_2d), _L.ptr(b_c), _L.dtype_code(b_c), _L.ptr(g_2d),
+        _L.dtype_code(g_2d), _L.ptr(da), _L.ptr(db), M, N, K, _L.ptr(ws), ws_bytes,
+        _L.stream_of(a_2d)))
+    # fp8.py:95-96: .astype(a.dtype) / .astype(b.dtype) of the bf16 results (exact widening)
     return da.reshape(*leading, K).to(a.dtype), db.to(b.dtype)
 
 
