@@ -127,13 +127,15 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_nt_256_kernel(const __bf16* 
     c.voa[par] = (uint32_t)(m0 + lrow) * rowb + lch * 16;
     c.vob[par] = (uint32_t)(n0 + lrow) * rowb + lch * 16;
   }
-  // fragments: lane (fr, fg) reads logical chunks 2fg, 2fg+1 of row
-  // (wave tile row) + 16t + fr, i.e. k elements 16fg .. 16fg+15 of the step
-  const uint32_t ch0 = (uint32_t)((2 * fg) ^ g256_swz(fr)) * 16u;
+  // fragments: lane (fr, fg) reads logical chunks fg and fg + 4 of row
+  // (wave tile row) + 16t + fr (k elements 8fg .. 8fg+7 and 32+8fg ..
+  // 32+8fg+7 of the step; A and B lanes agree).  Chunk pairs {2fg, 2fg + 1}
+  // make the four lane groups of a read collide in LDS (~30% slower reads).
+  const uint32_t ch0 = (uint32_t)(fg ^ g256_swz(fr)) * 16u;
   c.fa0 = (uint32_t)(wm * 64 + fr) * 128u + ch0;
-  c.fa1 = c.fa0 ^ 16u;
+  c.fa1 = c.fa0 ^ 64u;
   c.fb0 = (uint32_t)(wn * 128 + fr) * 128u + ch0;
-  c.fb1 = c.fb0 ^ 16u;
+  c.fb1 = c.fb0 ^ 64u;
 
   v4f acc[4][8];
 #pragma unroll
