@@ -120,6 +120,20 @@ int tg_rms_norm(const void* x, const void* scale, void* y, int64_t rows, int64_t
 int tg_rms_norm_fp8(const void* x, const void* scale, void* y, uint8_t* q, float* s,
                     int64_t rows, int64_t dim, float eps, int block_k, void* stream);
 
+/* Device workspace (bytes) of tg_rms_norm_bwd. */
+size_t tg_rms_norm_bwd_workspace(int64_t rows, int64_t dim);
+
+/* rms_norm's backward, the custom VJP _bwd of kernels.py:104-118:
+ *   rnorm = rsqrt(mean(x^2) + eps), normed = x * rnorm, gs = dy * scale
+ *   dx = bf16(rnorm * (gs - normed * mean(gs * normed)))   (rows, dim)
+ *   dscale = bf16(sum over rows of dy * normed)            (dim,)
+ * x, dy, dx bf16 (rows, dim); scale, dscale bf16 (dim,); dim % 8 == 0 and
+ * dim <= 4096.  dscale is summed in a fixed order (identical on every call);
+ * rows == 0 gives dscale = 0. */
+int tg_rms_norm_bwd(const void* x, const void* scale, const void* dy, void* dx, void* dscale,
+                    int64_t rows, int64_t dim, float eps, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 /* Decode-shape GEMM with a pre-quantized weight (no reference function; the
  * reference re-quantizes W every call at fp8.py:68):
  * out[m, n] = sum_kb x_s[m, kb] * w_s[n / w_scale_bn, kb] * sum_k x_q[m, k] * w_q[n, k]

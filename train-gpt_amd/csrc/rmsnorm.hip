@@ -163,6 +163,206 @@ static int launch_rmsnorm(const void* x, const void* gamma, void* y, uint8_t* q,
   return einval("rms_norm: dim must be <= 16384");
 }
 
+// ---------------------------------------------------------------------------
+// Backward of rms_norm: the custom VJP of /root/reference/kernels.py:104-118.
+//   rnorm  = rsqrt(mean(x^2) + eps)            (f32, recomputed from x)
+//   normed = x * rnorm,  gs = dy * scale
+//   dx     = bf16(rnorm * (gs - normed * mean(gs * normed)))
+//   dscale = bf16(sum over rows of dy * normed)
+// One pass over a row's registers gives both sums (sum x^2 accumulated in
+// f64 as in the forward, and sum gs * x, since mean(gs * normed) = rnorm *
+// mean(gs * x)); a second pass writes dx.  Same row walk as the forward (one
+// wave per row, lane l owns 16-byte chunks l + 64j): x and dy are read once,
+// dx written once.  The dscale column sums stay in registers across all rows
+// a wave visits; the four waves of a workgroup add theirs into LDS in wave
+// order and the workgroup writes one partial row, which rmsnorm_bwd_reduce
+// adds up in workgroup order.  Both orders are fixed, so dscale is the same
+// on every run.
+// GREG: gamma in registers (J <= 4); PF: prefetch the next row (J <= 4).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void unpack_bf16x8(const uint4& v, float (&f)[8]) {
+  f[0] = bf16lo(v.x); f[1] = bf16hi(v.x); f[2] = bf16lo(v.y); f[3] = bf16hi(v.y);
+  f[4] = bf16lo(v.z); f[5] = bf16hi(v.z); f[6] = bf16lo(v.w); f[7] = bf16hi(v.w);
+}
+
+constexpr int kNormBwdMaxGrid = 512;
+
+template <int J, bool FULL>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint4* __restrict__ x,
+                                                          const uint4* __restrict__ gamma,
+                                                          const uint4* __restrict__ dy,
+                                                          uint4* __restrict__ dx,
+                                                          float* __restrict__ partial,
+                                                          int64_t rows, int nch, float dimf,
+                                                          float eps) {
+  constexpr bool GREG = J <= 4, PF = J <= 4;
+  extern __shared__ float colsum[];   // nch * 8 floats
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t wave0 = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t wstride = (int64_t)gridDim.x * 4;
+
+  auto gamma_chunk = [&](int j, float (&f)[8]) {
+    const int c = lane + 64 * j;
+    unpack_bf16x8((FULL || c < nch) ? gamma[c] : make_uint4(0, 0, 0, 0), f);
+  };
+  float greg[GREG ? J : 1][8];
+  if (GREG) {
+#pragma unroll
+    for (int j = 0; j < (GREG ? J : 1); ++j) gamma_chunk(j, greg[j]);
+  }
+  float dg[J][8];
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dg[j][e] = 0.0f;
+
+  uint4 nx[J], nd[J];
+  auto load_row = [&](int64_t row) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int c = lane + 64 * j;
+      nx[j] = (FULL || c < nch) ? ldg_stream(x + row * nch + c) : make_uint4(0, 0, 0, 0);
+      nd[j] = (FULL || c < nch) ? ldg_stream(dy + row * nch + c) : make_uint4(0, 0, 0, 0);
+    }
+  };
+
+  if (PF && wave0 < rows) load_row(wave0);
+  for (int64_t row = wave0; row < rows; row += wstride) {
+    if (!PF) load_row(row);
+    float xf[J][8], d[J][8];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      unpack_bf16x8(nx[j], xf[j]);
+      unpack_bf16x8(nd[j], d[j]);
+    }
+    if (PF && row + wstride < rows) load_row(row + wstride);
+
+    double sq = 0.0;
+    float gx = 0.0f;   // this lane's part of sum(gs * x)
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      float gl[8];
+      if (!GREG) gamma_chunk(j, gl);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float gm = GREG ? greg[GREG ? j : 0][e] : gl[e];
+        sq += (double)(xf[j][e] * xf[j][e]);
+        gx = __builtin_fmaf(d[j][e] * gm, xf[j][e], gx);   // dy * scale is exact in f32
+      }
+    }
+    sq = wave_sum_f64(sq);
+    const double gxs = wave_sum_f64((double)gx);
+    const float var = (float)sq / dimf;
+    const float rn = (float)(1.0 / __builtin_sqrt((double)(var + eps)));
+    const float dot = rn * ((float)gxs / dimf);
+
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int c = lane + 64 * j;
+      float gl[8];
+      if (!GREG) gamma_chunk(j, gl);
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float gm = GREG ? greg[GREG ? j : 0][e] : gl[e];
+        const float nrm = xf[j][e] * rn;
+        o[e] = rn * (d[j][e] * gm - nrm * dot);
+        dg[j][e] = __builtin_fmaf(d[j][e], nrm, dg[j][e]);
+      }
+      uint4 ov;
+      ov.x = pack_bf16x2(o[0], o[1]); ov.y = pack_bf16x2(o[2], o[3]);
+      ov.z = pack_bf16x2(o[4], o[5]); ov.w = pack_bf16x2(o[6], o[7]);
+      if (FULL || c < nch) stg_stream(dx + row * nch + c, ov);
+    }
+  }
+
+  // workgroup column sums in wave order, then one partial row per workgroup
+  for (int w = 0; w < 4; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int c = lane + 64 * j;
+        if (FULL || c < nch) {
+          float4* p = reinterpret_cast<float4*>(colsum + c * 8);
+          float4 a = w ? p[0] : make_float4(0.f, 0.f, 0.f, 0.f);
+          float4 b = w ? p[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+          a.x += dg[j][0]; a.y += dg[j][1]; a.z += dg[j][2]; a.w += dg[j][3];
+          b.x += dg[j][4]; b.y += dg[j][5]; b.z += dg[j][6]; b.w += dg[j][7];
+          p[0] = a;
+          p[1] = b;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  const int dim = nch * 8;
+  for (int i = threadIdx.x; i < dim; i += 256) partial[(int64_t)blockIdx.x * dim + i] = colsum[i];
+}
+
+// dscale[c] = bf16(sum over b of partial[b][c]), b in order (f64 accumulation).
+// Workgroup: 64 columns; its four waves take interleaved quarters of the
+// partial rows and are combined in wave order.
+__global__ __launch_bounds__(256) void rmsnorm_bwd_reduce(const float* __restrict__ partial,
+                                                          int nparts, int dim,
+                                                          uint16_t* __restrict__ dscale) {
+  __shared__ double wsum[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
+  double acc = 0.0;
+  if (c < dim)
+    for (int b = wave; b < nparts; b += 4) acc += (double)partial[(int64_t)b * dim + c];
+  wsum[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && c < dim) {
+    const double t = ((wsum[0][lane] + wsum[1][lane]) + wsum[2][lane]) + wsum[3][lane];
+    dscale[c] = __builtin_bit_cast(uint16_t, (__bf16)(float)t);
+  }
+}
+
+static int64_t norm_bwd_grid(int64_t rows) {
+  // about four rows per wave, at most two workgroups per CU
+  int64_t g = (rows + 15) / 16;
+  if (g > kNormBwdMaxGrid) g = kNormBwdMaxGrid;
+  return g;
+}
+
+static int launch_rmsnorm_bwd(const void* x, const void* gamma, const void* dy, void* dx,
+                              void* dscale, float* partial, int64_t rows, int64_t dim, float eps,
+                              hipStream_t st) {
+  const int nch = (int)(dim / 8);
+  const int jneed = (nch + 63) / 64;
+  const int64_t grid = norm_bwd_grid(rows);
+  auto X = reinterpret_cast<const uint4*>(x);
+  auto G = reinterpret_cast<const uint4*>(gamma);
+  auto DY = reinterpret_cast<const uint4*>(dy);
+  auto DX = reinterpret_cast<uint4*>(dx);
+  const float dimf = (float)dim;
+  const size_t lds = (size_t)dim * 4;
+  if (grid > 0) {
+    bool launched = false;
+#define TG_NORM_BWD_CASE(JJ)                                                                       \
+    if (!launched && jneed <= JJ) {                                                                \
+      if (nch == JJ * 64)                                                                          \
+        hipLaunchKernelGGL((rmsnorm_bwd_kernel<JJ, true>), dim3((unsigned)grid), dim3(256), lds, st, \
+                           X, G, DY, DX, partial, rows, nch, dimf, eps);                           \
+      else                                                                                         \
+        hipLaunchKernelGGL((rmsnorm_bwd_kernel<JJ, false>), dim3((unsigned)grid), dim3(256), lds,  \
+                           st, X, G, DY, DX, partial, rows, nch, dimf, eps);                       \
+      launched = true;                                                                             \
+    }
+    TG_NORM_BWD_CASE(1)
+    TG_NORM_BWD_CASE(2)
+    TG_NORM_BWD_CASE(4)
+    TG_NORM_BWD_CASE(8)
+#undef TG_NORM_BWD_CASE
+    if (!launched) return einval("rms_norm_bwd: dim must be <= 4096");
+    TG_TRY(check_launch("rmsnorm_bwd"));
+  }
+  hipLaunchKernelGGL(rmsnorm_bwd_reduce, dim3((unsigned)((dim + 63) / 64)), dim3(256), 0, st,
+                     partial, (int)grid, (int)dim, reinterpret_cast<uint16_t*>(dscale));
+  return check_launch("rmsnorm_bwd_reduce");
+}
+
 }  // namespace tg
 
 using namespace tg;
@@ -188,4 +388,24 @@ extern "C" int tg_rms_norm_fp8(const void* x, const void* scale, void* y, uint8_
   if (!aligned(x, 16) || !aligned(scale, 16) || !aligned(y, 16) || !aligned(q, 8))
     return einval("rms_norm_fp8: x, scale, y must be 16-byte and q 8-byte aligned");
   return launch_rmsnorm<true>(x, scale, y, q, s, rows, dim, eps, as_stream(stream));
+}
+
+extern "C" size_t tg_rms_norm_bwd_workspace(int64_t rows, int64_t dim) {
+  if (rows < 0 || dim <= 0) return 0;
+  return (size_t)norm_bwd_grid(rows) * (size_t)dim * 4;
+}
+
+extern "C" int tg_rms_norm_bwd(const void* x, const void* scale, const void* dy, void* dx,
+                               void* dscale, int64_t rows, int64_t dim, float eps,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  if (rows < 0 || dim <= 0) return einval("rms_norm_bwd: bad shape");
+  if (dim % 8) return einval("rms_norm_bwd: dim must be a multiple of 8");
+  if (dim > 4096) return einval("rms_norm_bwd: dim must be <= 4096");
+  if (!scale || !dscale) return einval("rms_norm_bwd: null pointer");
+  if (rows > 0 && (!x || !dy || !dx || !workspace)) return einval("rms_norm_bwd: null pointer");
+  if (workspace_bytes < tg_rms_norm_bwd_workspace(rows, dim)) return einval("rms_norm_bwd: workspace too small");
+  if (!aligned(x, 16) || !aligned(scale, 16) || !aligned(dy, 16) || !aligned(dx, 16) || !aligned(workspace, 16))
+    return einval("rms_norm_bwd: x, scale, dy, dx and workspace must be 16-byte aligned");
+  return launch_rmsnorm_bwd(x, scale, dy, dx, dscale, reinterpret_cast<float*>(workspace), rows, dim,
+                            eps, as_stream(stream));
 }

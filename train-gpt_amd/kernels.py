@@ -14,8 +14,10 @@ block_k)`` returns the bf16 norm output together with its e4m3fn bytes and
 1x128 fp32 scales from one read of x -- what ``_quantize_to_fp8`` of the norm
 output (fp8.py:66) would produce.
 
-The backward (kernels.py:104-118) is not yet a HIP kernel: calling
-``rms_norm(...).backward()`` raises.
+The backward is the reference's custom VJP (kernels.py:104-118) as the HIP
+kernel tg_rms_norm_bwd: dx = bf16(rnorm * (gs - normed * mean(gs * normed)))
+and dscale = bf16(sum over rows of dy * normed), with gs = dy * scale; the
+dscale sum runs in a fixed order, so it is the same on every call.
 """
 import torch
 
@@ -61,16 +63,37 @@ def rms_norm_fp8(x: torch.Tensor, scale: torch.Tensor, eps: float, block_k: int 
             s.reshape(*lead, D // block_k))
 
 
+def _rms_norm_bwd(x: torch.Tensor, scale: torch.Tensor, eps: float, g: torch.Tensor):
+    """kernels.py:104-118: (grad_x as x.dtype, grad_scale as scale.dtype)."""
+    x2, sc, D = _prep(x, scale)
+    if g.dtype != torch.bfloat16:
+        g = g.to(torch.bfloat16)
+    g2 = g.reshape(-1, D).contiguous()
+    R = x2.shape[0]
+    dx = torch.empty_like(x2)
+    dscale = torch.empty((D,), dtype=torch.bfloat16, device=x.device)
+    ws_bytes = _L.lib().tg_rms_norm_bwd_workspace(R, D)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=x.device)
+    _L.check(_L.lib().tg_rms_norm_bwd(_L.ptr(x2), _L.ptr(sc), _L.ptr(g2), _L.ptr(dx), _L.ptr(dscale),
+                                      R, D, float(eps), _L.ptr(ws), ws_bytes, _L.stream_of(x2)))
+    return dx.reshape(x.shape), dscale
+
+
 class _RMSNorm(torch.autograd.Function):
-    """custom_vjp of kernels.py:55,101-120 (forward only for now)."""
+    """custom_vjp of kernels.py:55,101-120: the saved residuals are (x, scale),
+    and the backward recomputes normed from x (kernels.py:102-106)."""
 
     @staticmethod
     def forward(ctx, x, scale, eps):
+        ctx.save_for_backward(x, scale)
+        ctx.eps = eps
         return _rms_norm_pure(x, scale, eps)
 
     @staticmethod
     def backward(ctx, g):
-        raise NotImplementedError("rms_norm backward (kernels.py:104-118) is not built as a HIP kernel yet")
+        x, scale = ctx.saved_tensors
+        dx, dscale = _rms_norm_bwd(x, scale, ctx.eps, g)
+        return dx, dscale, None
 
 
 def rms_norm(x: torch.Tensor, scale: torch.Tensor, eps: float) -> torch.Tensor:
