@@ -299,22 +299,35 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint4* __restric
   for (int i = threadIdx.x; i < dim; i += 256) partial[(int64_t)blockIdx.x * dim + i] = colsum[i];
 }
 
-// dscale[c] = bf16(sum over b of partial[b][c]), b in order (f64 accumulation).
-// Workgroup: 64 columns; its four waves take interleaved quarters of the
-// partial rows and are combined in wave order.
-__global__ __launch_bounds__(256) void rmsnorm_bwd_reduce(const float* __restrict__ partial,
-                                                          int nparts, int dim,
-                                                          uint16_t* __restrict__ dscale) {
-  __shared__ double wsum[4][64];
+// dscale[c] = bf16(sum over b of partial[b][c]) with f64 accumulation in a
+// fixed order: workgroup = 64 columns x 16 waves; wave w adds partial rows
+// w, w + 16, w + 32, ... in that order (eight loads in flight per lane), and
+// the 16 wave sums are added in wave order.
+__global__ __launch_bounds__(1024) void rmsnorm_bwd_reduce(const float* __restrict__ partial,
+                                                           int nparts, int dim,
+                                                           uint16_t* __restrict__ dscale) {
+  constexpr int W = 16, U = 8;
+  __shared__ double wsum[W][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + lane;
   double acc = 0.0;
-  if (c < dim)
-    for (int b = wave; b < nparts; b += 4) acc += (double)partial[(int64_t)b * dim + c];
+  if (c < dim) {
+    int b = wave;
+    for (; b + (U - 1) * W < nparts; b += U * W) {
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = partial[(int64_t)(b + u * W) * dim + c];
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc += (double)v[u];
+    }
+    for (; b < nparts; b += W) acc += (double)partial[(int64_t)b * dim + c];
+  }
   wsum[wave][lane] = acc;
   __syncthreads();
   if (wave == 0 && c < dim) {
-    const double t = ((wsum[0][lane] + wsum[1][lane]) + wsum[2][lane]) + wsum[3][lane];
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < W; ++w) t += wsum[w][lane];
     dscale[c] = __builtin_bit_cast(uint16_t, (__bf16)(float)t);
   }
 }
@@ -358,7 +371,7 @@ static int launch_rmsnorm_bwd(const void* x, const void* gamma, const void* dy, 
     if (!launched) return einval("rms_norm_bwd: dim must be <= 4096");
     TG_TRY(check_launch("rmsnorm_bwd"));
   }
-  hipLaunchKernelGGL(rmsnorm_bwd_reduce, dim3((unsigned)((dim + 63) / 64)), dim3(256), 0, st,
+  hipLaunchKernelGGL(rmsnorm_bwd_reduce, dim3((unsigned)((dim + 63) / 64)), dim3(1024), 0, st,
                      partial, (int)grid, (int)dim, reinterpret_cast<uint16_t*>(dscale));
   return check_launch("rmsnorm_bwd_reduce");
 }
