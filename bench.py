@@ -15,6 +15,16 @@ norm_quant   = config 2 fused RMSNorm -> FP8 quantize, bytes per launch
                84,414,464 (x read + y/q/scales written + gamma) / mean launch
                time vs 8 TB/s HBM; input/output sets rotate over > 256 MB so
                the Infinity Cache cannot serve them
+norm_bwd     = rms_norm's backward (kernels.py:104-118) at config 2's shape:
+               x, dy read + dx written + gamma / dgamma = 100,671,488 B per call
+               (row kernel + column reduce) vs 8 TB/s HBM
+gemv         = config 5 decode GEMV on a pre-quantized W [4096, 14336] (e4m3,
+               128x128 scales) for M in {1, 8, 32}: algorithmic bytes of the
+               GEMV launch (W bytes + W scales + x bytes + x scales + bf16 out)
+               / mean launch time vs 8 TB/s; 5 weight copies rotate (> 256 MB)
+bwd_bf16     = the reference's straight-through bf16 backward (fp8.py:85-98)
+               at config 3: 2 bf16 GEMMs (+ operand packing) per call vs the
+               2.5 PFLOP/s dense bf16 MFMA peak
 cpu_baseline = the CPU oracle (numpy + C) on a row sample of the same step
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
@@ -30,12 +40,15 @@ sys.path.insert(0, os.path.join(ROOT, "train-gpt_amd"))
 sys.path.insert(0, ROOT)
 
 FP8_PEAK_TFLOPS = 5000.0       # MI355X dense FP8 MFMA
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 HBM_PEAK_GBPS = 8000.0         # MI355X HBM3E
 M3, K3, N3 = 8192, 2048, 8192
 GEMM_FLOP = 2.0 * M3 * N3 * K3
 STEP_FLOP = 3 * GEMM_FLOP
 C2_ROWS, C2_D = 8 * 1024, 2048
 C2_BYTES = C2_ROWS * C2_D * (2 + 2 + 1) + C2_ROWS * (C2_D // 128) * 4 + C2_D * 2
+C2_BWD_BYTES = C2_ROWS * C2_D * (2 + 2 + 2) + 2 * C2_D * 2
+C5_K, C5_N = 4096, 14336
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "bench_c3_c2_hbm_traffic_counters.md")
@@ -178,6 +191,130 @@ def bench_norm(dev, iters):
                          "traffic": measured_traffic().get("rmsnorm_fp8")}}
 
 
+def _mean_launch_us(launch, iters, warm=5):
+    """Mean duration of back-to-back launches between one pair of events on
+    the launch stream (what the rocprofv3 kernel trace averages)."""
+    import torch
+    for i in range(warm):
+        launch(i)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(iters):
+        launch(i)
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters * 1e3
+
+
+def bench_norm_bwd(dev, iters):
+    """rms_norm backward at config 2's shape (row kernel + column reduce)."""
+    import torch
+    import _tglib as L
+    lib = L.lib()
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    nsets = 3                                    # 3 x 100 MB > 256 MB Infinity Cache
+    bf = torch.bfloat16
+    xs = [torch.randn((C2_ROWS, C2_D), generator=g, device=dev).to(bf) for _ in range(nsets)]
+    dys = [(torch.randn((C2_ROWS, C2_D), generator=g, device=dev) * 1e-2).to(bf) for _ in range(nsets)]
+    dxs = [torch.empty((C2_ROWS, C2_D), dtype=bf, device=dev) for _ in range(nsets)]
+    gamma = (1 + 0.1 * torch.randn((C2_D,), generator=g, device=dev)).to(bf)
+    dgamma = torch.empty((C2_D,), dtype=bf, device=dev)
+    wsb = lib.tg_rms_norm_bwd_workspace(C2_ROWS, C2_D)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    st = L.stream_of(gamma)
+
+    def launch(i):
+        k = i % nsets
+        L.check(lib.tg_rms_norm_bwd(L.ptr(xs[k]), L.ptr(gamma), L.ptr(dys[k]), L.ptr(dxs[k]),
+                                    L.ptr(dgamma), C2_ROWS, C2_D, 1e-6, L.ptr(ws), wsb, st))
+    us = _mean_launch_us(launch, iters)
+    gbps = C2_BWD_BYTES / (us * 1e-6) / 1e9
+    return {"workload": "rms_norm backward (kernels.py:104-118), x/dy bf16 [8,1024,2048]",
+            "us_per_call": round(us, 3), "bytes_per_call": C2_BWD_BYTES,
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None}}
+
+
+def bench_gemv(dev, iters):
+    """Config 5: decode GEMV on a pre-quantized W (128x128 scales), M in {1, 8, 32}."""
+    import torch
+    import _tglib as L
+    lib = L.lib()
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    nsets = 5                                    # 5 x 58.7 MB > 256 MB Infinity Cache
+    wq, ws = [], []
+    for _ in range(nsets):
+        w = (torch.randn((C5_K, C5_N), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        q = torch.empty((C5_N, C5_K), dtype=torch.uint8, device=dev)
+        s = torch.empty(((C5_N + 127) // 128, C5_K // 128), dtype=torch.float32, device=dev)
+        L.check(lib.tg_quantize_weight_128x128(L.ptr(w), C5_K, C5_N, L.ptr(q), L.ptr(s), L.stream_of(w)))
+        wq.append(q)
+        ws.append(s)
+        del w
+    out = []
+    for M in (1, 8, 32):
+        x = torch.randn((M, C5_K), generator=g, device=dev).to(torch.bfloat16)
+        xq = torch.empty((M, C5_K), dtype=torch.uint8, device=dev)
+        xs = torch.empty((M, C5_K // 128), dtype=torch.float32, device=dev)
+        y = torch.empty((M, C5_N), dtype=torch.bfloat16, device=dev)
+        st = L.stream_of(x)
+        L.check(lib.tg_quantize_rows(L.ptr(x), L.TG_DTYPE_BF16, M, C5_K, 128, L.ptr(xq), L.ptr(xs), st))
+
+        def launch(i):
+            k = i % nsets
+            L.check(lib.tg_gemv_fp8(L.ptr(xq), L.ptr(xs), L.ptr(wq[k]), L.ptr(ws[k]), 128, L.ptr(y),
+                                    M, C5_N, C5_K, 128, st))
+        us = _mean_launch_us(launch, iters)
+
+        def step(i):          # x quantization + GEMV, the decode step's FP8 matmul
+            k = i % nsets
+            L.check(lib.tg_quantize_rows(L.ptr(x), L.TG_DTYPE_BF16, M, C5_K, 128, L.ptr(xq), L.ptr(xs), st))
+            L.check(lib.tg_gemv_fp8(L.ptr(xq), L.ptr(xs), L.ptr(wq[k]), L.ptr(ws[k]), 128, L.ptr(y),
+                                    M, C5_N, C5_K, 128, st))
+        us_step = _mean_launch_us(step, iters)
+        byts = C5_N * C5_K + ws[0].numel() * 4 + M * C5_K + M * (C5_K // 128) * 4 + 2 * M * C5_N
+        gbps = byts / (us * 1e-6) / 1e9
+        out.append({"M": M, "us_per_launch": round(us, 3), "us_quant_plus_gemv": round(us_step, 3),
+                    "bytes_per_launch": byts,
+                    "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                                 "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                                 "traffic": None}})
+    return {"workload": "C5 decode GEMV, W e4m3 [14336, 4096] + 128x128 scales (pre-quantized), "
+                        "x quantized 1x128", "by_M": out}
+
+
+def bench_bwd_bf16(dev, iters):
+    """The reference's straight-through bf16 backward at config 3 (2 GEMMs per call)."""
+    import torch
+    import _tglib as L
+    lib = L.lib()
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    bf = torch.bfloat16
+    x = torch.randn((M3, K3), generator=g, device=dev).to(bf)
+    w = (torch.randn((K3, N3), generator=g, device=dev) * 0.02).to(bf)
+    dy = (torch.randn((M3, N3), generator=g, device=dev) * 1e-3).to(bf)
+    dx = torch.empty((M3, K3), dtype=bf, device=dev)
+    dw = torch.empty((K3, N3), dtype=bf, device=dev)
+    wsb = lib.tg_block_scaled_matmul_bwd_bf16_workspace(M3, N3, K3)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    st = L.stream_of(x)
+    B = L.TG_DTYPE_BF16
+
+    def launch(i):
+        L.check(lib.tg_block_scaled_matmul_bwd_bf16(L.ptr(x), B, L.ptr(w), B, L.ptr(dy), B, L.ptr(dx),
+                                                     L.ptr(dw), M3, N3, K3, L.ptr(ws), wsb, st))
+    us = _mean_launch_us(launch, iters, warm=3)
+    tf = 2 * GEMM_FLOP / (us * 1e-6) / 1e12
+    return {"workload": "C3 straight-through bf16 backward (fp8.py:85-98): dX = dY . W.T, "
+                        "dW = X.T . dY, incl. the X.T / dY.T packing",
+            "us_per_call": round(us, 2), "tflops": round(tf, 1),
+            "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+
+
 def cpu_baseline(rows=8192, repeats=5):
     """The CPU oracle on the step: quantize (C oracle) and the dequantized f32
     GEMMs (numpy/BLAS) of fwd + FP8 bwd over `rows` of the 8192 token rows,
@@ -253,6 +390,9 @@ def main():
     gemm_tflops = GEMM_FLOP / (gemm_ms * 1e-3) / 1e12
     value = STEP_FLOP / (ms_step * 1e-3) / 1e12
     norm = bench_norm(dev, args.norm_iters)
+    norm_bwd = bench_norm_bwd(dev, args.norm_iters)
+    gemv = bench_gemv(dev, args.norm_iters)
+    bwd_bf16 = bench_bwd_bf16(dev, 10)
     out = {
         "metric": "FP8 block-scaled GEMM TFLOP/s (% fp8 MFMA peak); RMSNorm+quant HBM GB/s",
         "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -267,6 +407,9 @@ def main():
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic().get("gemm_fp8_nt_256")},
         "norm_quant": norm,
+        "norm_bwd": norm_bwd,
+        "gemv": gemv,
+        "bwd_bf16": bwd_bf16,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
