@@ -45,6 +45,15 @@ int tg_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, int
 int tg_quantize_cols(const void* x, int x_dtype, int64_t rows, int64_t cols, int block_k,
                      uint8_t* q_t, float* scales_t, void* stream);
 
+/* Both of the above from one read of x: _quantize_to_fp8 (fp8.py:39-47) of x
+ * along its rows and of x.T, the two forms of dY that the FP8 backward feeds to
+ * its dX and dW GEMMs.  x (rows, cols) bf16, 16-byte aligned; rows and cols
+ * multiples of block_k.  q (rows, cols) + scales (rows, cols/block_k) are
+ * bit-identical to tg_quantize_rows, q_t (cols, rows) + scales_t
+ * (cols, rows/block_k) to tg_quantize_cols. */
+int tg_quantize_dual(const void* x, int64_t rows, int64_t cols, int block_k, uint8_t* q,
+                     float* scales, uint8_t* q_t, float* scales_t, void* stream);
+
 /* jax.nn.scaled_matmul + bf16 cast as called at fp8.py:70-78 ("NT" layout):
  * c[m, n] = sum_kb a_s[m, kb] * b_s[n / b_scale_bn, kb] * sum_{k in kb} a_q[m, k] * b_q[n, k]
  * a_q: (M, K) e4m3fn, a_s: (M, K/128) f32; b_q: (N, K) e4m3fn;

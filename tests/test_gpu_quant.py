@@ -104,6 +104,36 @@ def test_quantize_full_size_c3_operands(dev):
     np.testing.assert_array_equal(f32_bits(sw), so.view(np.uint32))
 
 
+@pytest.mark.parametrize("shape", [(128, 128), (256, 384), (1024, 640), (8192, 8192)])
+def test_quantize_dual_equals_separate(dev, shape):
+    """tg_quantize_dual = tg_quantize_rows + tg_quantize_cols, bit for bit (C3's dY at full size)."""
+    rng = np.random.default_rng(sum(shape) + 3)
+    x = to_dev(ob.randn_bf16(rng, shape, std=1e-3), dev)
+    q, s, qt, st = fp8.quantize_fp8_dual(x)
+    q1, s1 = fp8.quantize_fp8(x)
+    q2, s2 = fp8.quantize_fp8(x, transpose=True)
+    assert torch.equal(q.view(torch.uint8), q1.view(torch.uint8))
+    assert torch.equal(qt.view(torch.uint8), q2.view(torch.uint8))
+    assert np.array_equal(f32_bits(s), f32_bits(s1)) and np.array_equal(f32_bits(st), f32_bits(s2))
+
+
+def test_quantize_dual_special_values(dev):
+    """Edge-case blocks in both directions against the oracle."""
+    rng = np.random.default_rng(6)
+    rows = _special_rows(rng, 256)                                 # (10, 256)
+    x = np.concatenate([rows, ob.randn_bf16(rng, (118, 256))], axis=0)
+    x[20:30, :128] = _special_rows(rng, 128)                      # special row blocks mid-tile
+    cols = np.ascontiguousarray(_special_rows(rng, 128).T)         # (128, 10): special columns
+    x[:, 200:210] = cols
+    q, s, qt, st = fp8.quantize_fp8_dual(to_dev(x, dev))
+    qo, so = fp8_ref.quantize_fp8(ob.bf16_to_f32(x))
+    np.testing.assert_array_equal(u8(q), qo)
+    assert same_scales(s.cpu().numpy(), so)
+    qo, so = fp8_ref.quantize_fp8(np.ascontiguousarray(ob.bf16_to_f32(x).T))
+    np.testing.assert_array_equal(u8(qt), qo)
+    assert same_scales(st.cpu().numpy(), so)
+
+
 def test_quantize_deterministic(dev):
     rng = np.random.default_rng(9)
     x = to_dev(ob.randn_bf16(rng, (512, 1024)), dev)

@@ -504,24 +504,26 @@ int launch_gemm_fp8(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, co
 
 // ---------------------------------------------------------------------------
 // Decode-shape GEMM (M <= 16 * MT) with a pre-quantized weight.  HBM-bound on
-// W: each workgroup streams NT x 16 weight rows once; its 4 waves split the K
-// blocks and issue all of their weight loads before the first MFMA, then
-// reduce the four partial tiles through LDS.  The MFMA takes W as the A
+// W: each workgroup owns NT x 16 weight rows and its NW waves split the K
+// blocks, KPW blocks per wave at a time.  A wave issues every load of its
+// blocks (W bytes, x bytes, both scales) before it waits on any of them, so
+// each wave keeps KPW * NT * 16 * 128 bytes of W in flight; the NW partial
+// tiles are then added in wave order through LDS.  The MFMA takes W as the A
 // operand (16 weight rows) and x as B (16 activation rows).
 // ---------------------------------------------------------------------------
-template <int NT, int MT, int KCH>
-__global__ __launch_bounds__(256) void gemv_fp8_kernel(const uint8_t* __restrict__ XQ,
-                                                       const float* __restrict__ XS,
-                                                       const uint8_t* __restrict__ WQ,
-                                                       const float* __restrict__ WS, int bns,
-                                                       __bf16* __restrict__ out, int M, int N,
-                                                       int K) {
-  __shared__ v4f red[3][NT][MT][64];
+template <int NT, int MT, int NW, int KPW, int BNS>
+__global__ __launch_bounds__(NW * 64) void gemv_fp8_kernel(const uint8_t* __restrict__ XQ,
+                                                           const float* __restrict__ XS,
+                                                           const uint8_t* __restrict__ WQ,
+                                                           const float* __restrict__ WS,
+                                                           __bf16* __restrict__ out, int M, int N,
+                                                           int K) {
+  static_assert(BNS == 1 || (BNS % (NT * 16) == 0), "a workgroup's rows share one scale row");
+  __shared__ v4f red[NW - 1][NT][MT][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, fg = lane >> 4;
   const int n0 = blockIdx.x * (NT * 16);
   const int nkb = K >> 7;
-  const int kb_lo = (wave * nkb) >> 2, kb_hi = ((wave + 1) * nkb) >> 2;
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
   v4f acc[NT][MT];
 #pragma unroll
@@ -529,55 +531,66 @@ __global__ __launch_bounds__(256) void gemv_fp8_kernel(const uint8_t* __restrict
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = zero;
 
-  for (int kb0 = kb_lo; kb0 < kb_hi; kb0 += KCH) {
-    uint4 w[KCH][NT][2];
+  for (int kb0 = wave * KPW; kb0 < nkb; kb0 += NW * KPW) {
+    uint4 w[KPW][NT][2], xv[KPW][MT][2];
+    float sw[KPW][NT][4], sx[KPW][MT];
 #pragma unroll
-    for (int c = 0; c < KCH; ++c)
+    for (int c = 0; c < KPW; ++c) {
+      const int kb = kb0 + c;
+      const bool kv = kb < nkb;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const int n = n0 + t * 16 + fr, kb = kb0 + c;
-        if (kb < kb_hi && n < N) {
-          const uint4* p = reinterpret_cast<const uint4*>(WQ + (int64_t)n * K + kb * 128 + fg * 32);
+        const int n = n0 + t * 16 + fr;
+        if (kv && n < N) {
+          // chunks fg and fg + 4 of the 128-byte block (x uses the same
+          // pairing): each load instruction reads 64 contiguous bytes per row
+          const uint4* p = reinterpret_cast<const uint4*>(WQ + (int64_t)n * K + kb * 128 + fg * 16);
           w[c][t][0] = ldg_stream(p);
-          w[c][t][1] = ldg_stream(p + 1);
+          w[c][t][1] = ldg_stream(p + 4);
         } else {
           w[c][t][0] = w[c][t][1] = make_uint4(0, 0, 0, 0);
         }
-      }
-#pragma unroll
-    for (int c = 0; c < KCH; ++c) {
-      const int kb = kb0 + c;
-      if (kb < kb_hi) {
-        float sw[NT][4];
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
+        if (BNS == 1) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int n = n0 + t * 16 + 4 * fg + r;
-            sw[t][r] = n < N ? WS[(int64_t)(n / bns) * nkb + kb] : 0.0f;
+            const int nr = n0 + t * 16 + 4 * fg + r;
+            sw[c][t][r] = (kv && nr < N) ? WS[(int64_t)nr * nkb + kb] : 0.0f;
           }
+        } else {
+          // one scale for every row of the workgroup (wave-uniform load)
+          const float v = kv ? WS[(int64_t)(n0 / BNS) * nkb + kb] : 0.0f;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int m = mt * 16 + fr;
-          uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
-          float sx = 0.0f;
-          if (m < M) {
-            const uint4* p = reinterpret_cast<const uint4*>(XQ + (int64_t)m * K + kb * 128 + fg * 32);
-            x0 = p[0];
-            x1 = p[1];
-            sx = XS[(int64_t)m * nkb + kb];
-          }
-          // the x scale of activation row m sits in the lane whose column is m
-          const v8i xb = as_v8i(x0, x1);
+          for (int r = 0; r < 4; ++r) sw[c][t][r] = v;
+        }
+      }
 #pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            const v4f p = mfma_f8_16x16x128(as_v8i(w[c][t][0], w[c][t][1]), xb, zero);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[t][mt][r] = __builtin_fmaf(p[r], sw[t][r] * sx, acc[t][mt][r]);
-          }
+      for (int mt = 0; mt < MT; ++mt) {
+        // the x scale of activation row m sits in the lane whose column is m
+        const int m = mt * 16 + fr;
+        if (kv && m < M) {
+          const uint4* p = reinterpret_cast<const uint4*>(XQ + (int64_t)m * K + kb * 128 + fg * 16);
+          xv[c][mt][0] = p[0];
+          xv[c][mt][1] = p[4];
+          sx[c][mt] = XS[(int64_t)m * nkb + kb];
+        } else {
+          xv[c][mt][0] = xv[c][mt][1] = make_uint4(0, 0, 0, 0);
+          sx[c][mt] = 0.0f;
         }
       }
     }
+#pragma unroll
+    for (int c = 0; c < KPW; ++c)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const v8i xb = as_v8i(xv[c][mt][0], xv[c][mt][1]);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const v4f p = mfma_f8_16x16x128(as_v8i(w[c][t][0], w[c][t][1]), xb, zero);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[t][mt][r] = __builtin_fmaf(p[r], sw[c][t][r] * sx[c][mt], acc[t][mt][r]);
+        }
+      }
   }
 
   if (wave > 0) {
@@ -594,7 +607,7 @@ __global__ __launch_bounds__(256) void gemv_fp8_kernel(const uint8_t* __restrict
       for (int mt = 0; mt < MT; ++mt) {
         v4f s = acc[t][mt];
 #pragma unroll
-        for (int w2 = 0; w2 < 3; ++w2) {
+        for (int w2 = 0; w2 < NW - 1; ++w2) {
           const v4f o = red[w2][t][mt][lane];
           s[0] += o[0]; s[1] += o[1]; s[2] += o[2]; s[3] += o[3];
         }
@@ -696,11 +709,11 @@ extern "C" int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, cons
   float* sat = reinterpret_cast<float*>(p);   p += align256((size_t)K * mkb * 4);
   uint8_t* qgt = p;   p += align256((size_t)N * M);
   float* sgt = reinterpret_cast<float*>(p);
-  TG_TRY(launch_quant_rows(g, TG_DTYPE_BF16, M, N, qg, sg, st));
+  // g along N and g.T along M from one read of g
+  TG_TRY(launch_quant_dual(g, M, N, qg, sg, qgt, sgt, st));
   TG_TRY(launch_quant_rows(b, TG_DTYPE_BF16, K, N, qb, sb, st));
   TG_TRY(launch_gemm_fp8(qg, sg, qb, sb, 1, da, TG_DTYPE_BF16, M, K, N, st));    // dX = g . b.T
   TG_TRY(launch_quant_cols(a, M, K, qat, sat, st));
-  TG_TRY(launch_quant_cols(g, M, N, qgt, sgt, st));
   return launch_gemm_fp8(qat, sat, qgt, sgt, 1, db, TG_DTYPE_BF16, K, N, M, st);  // dW = a.T . g
 }
 
@@ -715,15 +728,21 @@ extern "C" int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* 
   hipStream_t st = as_stream(stream);
   const int m = (int)M, n = (int)N, k = (int)K;
   auto o = reinterpret_cast<__bf16*>(out);
+  const dim3 grid((unsigned)((N + 31) / 32));
+#define TG_GEMV(MT, KPW)                                                                          \
+  if (w_scale_bn == 1)                                                                            \
+    hipLaunchKernelGGL((gemv_fp8_kernel<2, MT, 8, KPW, 1>), grid, dim3(512), 0, st, x_q, x_s, w_q, \
+                       w_s, o, m, n, k);                                                          \
+  else                                                                                            \
+    hipLaunchKernelGGL((gemv_fp8_kernel<2, MT, 8, KPW, 128>), grid, dim3(512), 0, st, x_q, x_s,   \
+                       w_q, w_s, o, m, n, k);
   if (M <= 16) {
-    hipLaunchKernelGGL((gemv_fp8_kernel<2, 1, 8>), dim3((unsigned)((N + 31) / 32)), dim3(256), 0, st,
-                       x_q, x_s, w_q, w_s, w_scale_bn, o, m, n, k);
+    TG_GEMV(1, 2)
   } else if (M <= 32) {
-    hipLaunchKernelGGL((gemv_fp8_kernel<2, 2, 8>), dim3((unsigned)((N + 31) / 32)), dim3(256), 0, st,
-                       x_q, x_s, w_q, w_s, w_scale_bn, o, m, n, k);
+    TG_GEMV(2, 2)
   } else {
-    hipLaunchKernelGGL((gemv_fp8_kernel<2, 4, 4>), dim3((unsigned)((N + 31) / 32)), dim3(256), 0, st,
-                       x_q, x_s, w_q, w_s, w_scale_bn, o, m, n, k);
+    TG_GEMV(4, 1)
   }
+#undef TG_GEMV
   return check_launch("gemv_fp8");
 }

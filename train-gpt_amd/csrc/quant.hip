@@ -209,6 +209,94 @@ int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, f
 }
 
 // ---------------------------------------------------------------------------
+// Dual quantization: _quantize_to_fp8 of x along its rows AND of x.T (the two
+// operands the FP8 backward needs from dY, fp8.py:39-47) from one read of x.
+// Tile = 128 x 128 bf16.  Lanes 16r .. 16r+15 of a wave hold one 128-element
+// row block (as in quant_rows_kernel), quantize it and keep the raw tile in
+// LDS (row pitch 272 B); then quads of lanes own whole columns (as in
+// quant_cols_kernel), quantize them and store 128 contiguous bytes per
+// column.  The bytes and scales equal those of the two separate kernels.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quant_dual_kernel(const uint4* __restrict__ x, int64_t rows,
+                                                         int64_t cols, uint2* __restrict__ q,
+                                                         float* __restrict__ s,
+                                                         uint8_t* __restrict__ qt,
+                                                         float* __restrict__ st) {
+  __shared__ uint32_t tile[128 * 68];
+  __shared__ uint32_t tq[128 * 36];
+  const int tid = threadIdx.x;
+  const int64_t c0 = (int64_t)blockIdx.x * 128, r0 = (int64_t)blockIdx.y * 128;
+  const int ch = tid & 15, rr = tid >> 4;
+  const int64_t cchunks = cols >> 3;
+  uint4 v[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) v[u] = ldg_stream(x + (r0 + rr + 16 * u) * cchunks + (c0 >> 3) + ch);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int row = rr + 16 * u;
+    float f[8];
+    f[0] = bf16lo(v[u].x); f[1] = bf16hi(v[u].x); f[2] = bf16lo(v[u].y); f[3] = bf16hi(v[u].y);
+    f[4] = bf16lo(v[u].z); f[5] = bf16hi(v[u].z); f[6] = bf16lo(v[u].w); f[7] = bf16hi(v[u].w);
+    const float sc = block_scale_bf16(row16_max_u32(absmax8(f)));
+    q[(r0 + row) * cchunks + (c0 >> 3) + ch] = quant8<true>(f, sc);
+    if (ch == 0) s[(r0 + row) * (cols >> 7) + blockIdx.x] = sc;
+    *reinterpret_cast<uint4*>(&tile[row * 68 + ch * 4]) = v[u];
+  }
+  __syncthreads();
+
+  const uint16_t* t16 = reinterpret_cast<const uint16_t*>(tile);
+  const int j = tid & 3;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int n = (tid >> 2) + 64 * p;
+    float f[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        f[i * 4 + r] = __uint_as_float(((uint32_t)t16[(16 * i + 4 * j + r) * 136 + n]) << 16);
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) m = max(m, __float_as_uint(f[i]) & 0x7FFFFFFFu);
+    const float sc = block_scale_bf16(quad_max_u32(m));
+    Divider d(sc);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t w;
+      if (d.fast) {
+        w = e4m3x4(d.div(f[4 * i]), d.div(f[4 * i + 1]), d.div(f[4 * i + 2]), d.div(f[4 * i + 3]));
+      } else {
+        w = e4m3_nonfinite_scale(f[4 * i], sc) | (e4m3_nonfinite_scale(f[4 * i + 1], sc) << 8) |
+            (e4m3_nonfinite_scale(f[4 * i + 2], sc) << 16) |
+            (e4m3_nonfinite_scale(f[4 * i + 3], sc) << 24);
+      }
+      tq[n * 36 + 4 * i + j] = w;
+    }
+    if (j == 0) st[(c0 + n) * (rows >> 7) + blockIdx.y] = sc;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int n = (tid >> 2) + 64 * p;
+    const uint4* src = reinterpret_cast<const uint4*>(&tq[n * 36 + 8 * j]);
+    uint4* dst = reinterpret_cast<uint4*>(qt + (c0 + n) * rows + r0 + 32 * j);
+    stg_stream(dst, src[0]);
+    stg_stream(dst + 1, src[1]);
+  }
+}
+
+int launch_quant_dual(const void* x, int64_t rows, int64_t cols, uint8_t* q, float* s, uint8_t* q_t,
+                      float* s_t, hipStream_t st) {
+  if (rows == 0 || cols == 0) return TG_OK;
+  if (rows % 128 || cols % 128) return einval("quantize_dual: rows and cols must be multiples of 128");
+  if (rows / 128 > 65535) return einval("quantize_dual: rows / 128 must be <= 65535");
+  const dim3 grid((unsigned)(cols / 128), (unsigned)(rows / 128));
+  hipLaunchKernelGGL(quant_dual_kernel, grid, dim3(256), 0, st, reinterpret_cast<const uint4*>(x), rows,
+                     cols, reinterpret_cast<uint2*>(q), s, q_t, s_t);
+  return check_launch("quant_dual");
+}
+
+// ---------------------------------------------------------------------------
 // 128x128-tile weight quantization (offline weight preparation for the GEMV).
 // One workgroup per tile: pass 1 finds the tile amax, pass 2 writes w.T bytes.
 // ---------------------------------------------------------------------------
@@ -391,4 +479,15 @@ extern "C" int tg_selftest_divide(uint64_t* counts, void* stream) {
   TG_TRY(check_launch("zero"));
   hipLaunchKernelGGL(selftest_divide_kernel, dim3(0x7F80), dim3(256), 0, as_stream(stream), c);
   return check_launch("selftest_divide");
+}
+
+extern "C" int tg_quantize_dual(const void* x, int64_t rows, int64_t cols, int block_k, uint8_t* q,
+                                float* s, uint8_t* q_t, float* s_t, void* stream) {
+  if (block_k != 128) return einval("quantize_dual: block_k must be 128");
+  if (rows < 0 || cols < 0) return einval("quantize_dual: bad shape");
+  if (rows == 0 || cols == 0) return TG_OK;
+  if (!x || !q || !s || !q_t || !s_t) return einval("quantize_dual: null pointer");
+  if (!aligned(x, 16) || !aligned(q, 8) || !aligned(q_t, 16))
+    return einval("quantize_dual: x and q_t must be 16-byte, q 8-byte aligned");
+  return launch_quant_dual(x, rows, cols, q, s, q_t, s_t, as_stream(stream));
 }

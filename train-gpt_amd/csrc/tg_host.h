@@ -34,6 +34,8 @@ int launch_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, ui
                       float* s, hipStream_t st);
 int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, float* s_t,
                       hipStream_t st);
+int launch_quant_dual(const void* x, int64_t rows, int64_t cols, uint8_t* q, float* s, uint8_t* q_t,
+                      float* s_t, hipStream_t st);
 int launch_gemm_fp8(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s,
                     int b_scale_bn, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
                     hipStream_t st);

@@ -99,6 +99,30 @@ def _validate(a: torch.Tensor, b: torch.Tensor, block_k: int):
     return leading, K, N
 
 
+def quantize_fp8_dual(x: torch.Tensor, block_k: int = DEFAULT_BLOCK_K):
+    """_quantize_to_fp8 (fp8.py:39-47) of a 2-D bf16 x (R, C) along its rows and
+    of x.T, from one read of x: returns (q, scales, q_t, scales_t), equal bit for
+    bit to quantize_fp8(x) and quantize_fp8(x, transpose=True).  R and C must
+    be multiples of block_k (the FP8 backward's dY)."""
+    _L.require_gpu(x)
+    _check_block_k(block_k)
+    if x.dim() != 2 or x.dtype != torch.bfloat16:
+        raise ValueError("quantize_fp8_dual needs a 2-D bfloat16 tensor")
+    R, C = x.shape
+    if R % block_k or C % block_k:
+        raise ValueError(f"K={R if R % block_k else C} not divisible by block_k={block_k}")
+    x = x.contiguous()
+    u8, f32 = torch.uint8, torch.float32
+    q = torch.empty((R, C), dtype=u8, device=x.device)
+    s = torch.empty((R, C // block_k), dtype=f32, device=x.device)
+    qt = torch.empty((C, R), dtype=u8, device=x.device)
+    st = torch.empty((C, R // block_k), dtype=f32, device=x.device)
+    _L.check(_L.lib().tg_quantize_dual(_L.ptr(x), R, C, block_k, _L.ptr(q), _L.ptr(s), _L.ptr(qt),
+                                       _L.ptr(st), _L.stream_of(x)))
+    e4 = torch.float8_e4m3fn
+    return q.view(e4), s, qt.view(e4), st
+
+
 def scaled_matmul(a_q, a_s, b_q, b_s, b_scale_bn: int = 1, out_dtype=torch.bfloat16):
     """The scaled GEMM of fp8.py:70-76 on already-quantized operands ("NT"):
     a_q (M, K), b_q (N, K) e4m3fn; a_s (M, K/128), b_s (N or ceil(N/128), K/128) f32.
@@ -183,11 +207,14 @@ def _fp8_backward(block_k, residuals, g):
             _L.ptr(ws), ws_bytes, _L.stream_of(a_2d)))
     else:
         u8 = torch.uint8
-        qg, sg = quantize_fp8(g_2d, block_k)                       # g along N
+        if g_2d.dtype == bf:
+            qg, sg, qgt, sgt = quantize_fp8_dual(g_2d, block_k)    # g along N and g.T along M
+        else:
+            qg, sg = quantize_fp8(g_2d, block_k)                   # g along N
+            qgt, sgt = quantize_fp8(g_2d, block_k, transpose=True)  # g.T along M
         qb, sb = quantize_fp8(b, block_k)                          # b along N
         da = scaled_matmul(qg.view(u8), sg, qb.view(u8), sb)
         qat, sat = quantize_fp8(a_2d, block_k, transpose=True)     # a.T along M
-        qgt, sgt = quantize_fp8(g_2d, block_k, transpose=True)     # g.T along M
         db = scaled_matmul(qat.view(u8), sat, qgt.view(u8), sgt)
     return da.reshape(*leading, K).to(a.dtype), db.to(b.dtype)
 
