@@ -222,8 +222,10 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(const uint4* __restrict
                                                          float* __restrict__ s,
                                                          uint8_t* __restrict__ qt,
                                                          float* __restrict__ st) {
+  // the raw tile (row pitch 272 B); once every column is in registers the
+  // same memory stages the transposed bytes (column pitch 144 B)
   __shared__ uint32_t tile[128 * 68];
-  __shared__ uint32_t tq[128 * 36];
+  uint32_t* tq = tile;
   const int tid = threadIdx.x;
   const int64_t c0 = (int64_t)blockIdx.x * 128, r0 = (int64_t)blockIdx.y * 128;
   const int ch = tid & 15, rr = tid >> 4;
@@ -244,21 +246,28 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(const uint4* __restrict
   }
   __syncthreads();
 
-  const uint16_t* t16 = reinterpret_cast<const uint16_t*>(tile);
-  const int j = tid & 3;
+  // columns: quad (tid >> 2) owns the column pair 2c, 2c + 1 (one 32-bit LDS
+  // word per row); lane j of the quad holds rows 16i + 4j + r
+  const int j = tid & 3, cp = tid >> 2;
+  float f0[32], f1[32];
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const int n = (tid >> 2) + 64 * p;
-    float f[32];
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t w = tile[(16 * i + 4 * j + r) * 68 + cp];
+      f0[i * 4 + r] = __uint_as_float(w << 16);
+      f1[i * 4 + r] = __uint_as_float(w & 0xFFFF0000u);
+    }
+  uint32_t m0 = 0, m1 = 0;
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        f[i * 4 + r] = __uint_as_float(((uint32_t)t16[(16 * i + 4 * j + r) * 136 + n]) << 16);
-    uint32_t m = 0;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) m = max(m, __float_as_uint(f[i]) & 0x7FFFFFFFu);
-    const float sc = block_scale_bf16(quad_max_u32(m));
+  for (int i = 0; i < 32; ++i) {
+    m0 = max(m0, __float_as_uint(f0[i]) & 0x7FFFFFFFu);
+    m1 = max(m1, __float_as_uint(f1[i]) & 0x7FFFFFFFu);
+  }
+  const float sc0 = block_scale_bf16(quad_max_u32(m0));
+  const float sc1 = block_scale_bf16(quad_max_u32(m1));
+  __syncthreads();   // every lane has read its columns: the tile becomes tq
+  auto col_words = [&](const float (&f)[32], float sc, int n) {
     Divider d(sc);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -273,7 +282,9 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(const uint4* __restrict
       tq[n * 36 + 4 * i + j] = w;
     }
     if (j == 0) st[(c0 + n) * (rows >> 7) + blockIdx.y] = sc;
-  }
+  };
+  col_words(f0, sc0, 2 * cp);
+  col_words(f1, sc1, 2 * cp + 1);
   __syncthreads();
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
