@@ -285,6 +285,96 @@ def quantize_weight(w: torch.Tensor, layout: str = "128x1"):
     return q.view(torch.float8_e4m3fn), s, 128
 
 
+class QuantizedWeight:
+    """A weight W (K, N) quantized once and kept across calls and in checkpoints.
+
+    fp8.py:68 re-quantizes W on every forward; this keeps the e4m3fn bytes of
+    W.T (N, K) and their fp32 scales in the layout the scaled GEMM and the
+    decode GEMV consume, so a frozen or inference weight is quantized once:
+      layout "128x1":   scales (N, K/128), bn = 1 -- bit-identical to what
+                        fp8.py:68 computes on every call;
+      layout "128x128": scales (ceil(N/128), K/128), bn = 128.
+    Checkpoints are safetensors files (tensors "q" as float8_e4m3fn and
+    "scales" as float32, metadata format/bn/block_k/K/N): the reference's
+    pickled checkpoints (train_modal.py:403-410) would execute code on load,
+    safetensors does not.
+    """
+
+    FORMAT = "tg-fp8-weight-v1"
+
+    def __init__(self, q: torch.Tensor, scales: torch.Tensor, bn: int,
+                 block_k: int = DEFAULT_BLOCK_K):
+        if bn not in (1, 128):
+            raise ValueError("bn must be 1 or 128")
+        _check_block_k(block_k)
+        if q.dim() != 2 or scales.dim() != 2:
+            raise ValueError("q and scales must be 2-D")
+        N, K = q.shape
+        want = (N if bn == 1 else (N + 127) // 128, K // block_k)
+        if K % block_k or tuple(scales.shape) != want:
+            raise ValueError(f"scales shape {tuple(scales.shape)} does not match q {tuple(q.shape)} "
+                             f"with bn={bn} (expected {want})")
+        self.q = q.view(torch.float8_e4m3fn) if q.dtype == torch.uint8 else q
+        self.scales = scales.to(torch.float32)
+        self.bn = bn
+        self.block_k = block_k
+
+    @classmethod
+    def from_weight(cls, w: torch.Tensor, layout: str = "128x1") -> "QuantizedWeight":
+        q, s, bn = quantize_weight(w, layout)
+        return cls(q, s, bn)
+
+    @property
+    def shape(self):
+        """(K, N) of the weight this was quantized from."""
+        return (self.q.shape[1], self.q.shape[0])
+
+    def to(self, device) -> "QuantizedWeight":
+        return QuantizedWeight(self.q.to(device), self.scales.to(device), self.bn, self.block_k)
+
+    def matmul(self, x: torch.Tensor) -> torch.Tensor:
+        """x (..., K) -> bf16 (..., N): fp8.py:66's quantization of x, then the
+        scaled GEMM (or, for at most 64 rows, the decode GEMV) on the kept W."""
+        *lead, K = x.shape
+        if K != self.shape[0]:
+            raise ValueError(f"contracted-dim mismatch: a K={K}, b K={self.shape[0]}")
+        M = 1
+        for d in lead:
+            M *= d
+        if 0 < M <= 64:
+            return fp8_gemv(x, self.q, self.scales, self.bn, self.block_k)
+        a_q, a_s = quantize_fp8(x.reshape(-1, K), self.block_k)
+        out = scaled_matmul(a_q.view(torch.uint8), a_s, self.q.view(torch.uint8), self.scales,
+                            b_scale_bn=self.bn)
+        return out.reshape(*lead, self.shape[1])
+
+    def state_dict(self):
+        return {"q": self.q, "scales": self.scales}
+
+    def metadata(self):
+        K, N = self.shape
+        return {"format": self.FORMAT, "bn": str(self.bn), "block_k": str(self.block_k),
+                "K": str(K), "N": str(N)}
+
+    def save(self, path: str) -> None:
+        from safetensors.torch import save_file
+        save_file({k: v.detach().contiguous().cpu() for k, v in self.state_dict().items()}, path,
+                  metadata=self.metadata())
+
+    @classmethod
+    def load(cls, path: str, device="cpu") -> "QuantizedWeight":
+        from safetensors import safe_open
+        with safe_open(path, framework="pt", device="cpu") as f:
+            meta = f.metadata() or {}
+            if meta.get("format") != cls.FORMAT:
+                raise ValueError(f"{path}: not a {cls.FORMAT} file (format={meta.get('format')!r})")
+            q, s = f.get_tensor("q"), f.get_tensor("scales")
+        w = cls(q, s, int(meta["bn"]), int(meta["block_k"]))
+        if w.shape != (int(meta["K"]), int(meta["N"])):
+            raise ValueError(f"{path}: shape metadata {meta['K']}x{meta['N']} does not match the tensors")
+        return w.to(device)
+
+
 def fp8_gemv(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, w_scale_bn: int = 1,
              block_k: int = DEFAULT_BLOCK_K) -> torch.Tensor:
     """Decode-shape GEMM: x (..., K) bf16 (M = prod(...) <= 64 rows) times a
