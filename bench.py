@@ -51,7 +51,7 @@ C2_BWD_BYTES = C2_ROWS * C2_D * (2 + 2 + 2) + 2 * C2_D * 2
 C5_K, C5_N = 4096, 14336
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "bench_c3_c2_hbm_traffic_counters.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "bench_hbm_traffic_counters.md")
 
 
 def measured_traffic():
@@ -235,7 +235,8 @@ def bench_norm_bwd(dev, iters):
     return {"workload": "rms_norm backward (kernels.py:104-118), x/dy bf16 [8,1024,2048]",
             "us_per_call": round(us, 3), "bytes_per_call": C2_BWD_BYTES,
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
-                         "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None}}
+                         "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                         "traffic": measured_traffic().get("rmsnorm_bwd")}}
 
 
 def bench_gemv(dev, iters):
@@ -282,7 +283,8 @@ def bench_gemv(dev, iters):
                     "bytes_per_launch": byts,
                     "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
                                  "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                                 "traffic": None}})
+                                 "traffic": measured_traffic().get("gemv_fp8_m16" if M <= 16
+                                                                   else "gemv_fp8_m32")}})
     return {"workload": "C5 decode GEMV, W e4m3 [14336, 4096] + 128x128 scales (pre-quantized), "
                         "x quantized 1x128", "by_M": out}
 

@@ -1,7 +1,8 @@
 // FP8 e4m3fn quantization kernels for gfx950 (HBM-bound byte work).
 //
 //   quant_rows_kernel   _quantize_to_fp8 along the last axis (fp8.py:39-47)
-//   quant_cols_kernel   _quantize_to_fp8 of x.T (fp8.py:68), transposed through LDS
+//   quant_cols_kernel   _quantize_to_fp8 of x.T (fp8.py:68) for unaligned rows
+//   quant_dual_kernel   rows and / or x.T from one read, transposed through LDS
 //   quant_w128_kernel   128x128-tile weight quantization for the GEMV format
 //   selftest_cvt_kernel hardware e4m3fn convert vs the integer encoder
 //
@@ -118,7 +119,9 @@ int launch_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, ui
 }
 
 // ---------------------------------------------------------------------------
-// Column quantization with transpose: tile = 128 rows (one scale block of the
+// Column quantization with transpose for rows that are not 16-byte aligned
+// (cols % 8 != 0; element loads, VEC = false).  Aligned rows take
+// quant_dual_kernel<false, ...> below.  Tile = 128 rows (one scale block of the
 // output) x 64 columns.  Load coalesced rows into LDS (row pitch 136 B), let
 // 4 lanes share each column (rows 16i + 4j + r for lane j, so a DPP quad holds
 // the block), stage the e4m3 bytes in a second LDS tile (pitch 144 B) and
@@ -194,19 +197,6 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(const uint16_t* __restr
   }
 }
 
-int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, float* s_t,
-                      hipStream_t st) {
-  if (rows == 0 || cols == 0) return TG_OK;
-  if (rows / 128 > 65535) return einval("quantize_cols: rows / 128 must be <= 65535");
-  dim3 grid((unsigned)((cols + 63) / 64), (unsigned)(rows / 128));
-  if (cols % 8 == 0 && aligned(x, 16))
-    hipLaunchKernelGGL(quant_cols_kernel<true>, grid, dim3(256), 0, st,
-                       reinterpret_cast<const uint16_t*>(x), rows, cols, q_t, s_t);
-  else
-    hipLaunchKernelGGL(quant_cols_kernel<false>, grid, dim3(256), 0, st,
-                       reinterpret_cast<const uint16_t*>(x), rows, cols, q_t, s_t);
-  return check_launch("quant_cols");
-}
 
 // ---------------------------------------------------------------------------
 // Dual quantization: _quantize_to_fp8 of x along its rows AND of x.T (the two
@@ -217,6 +207,9 @@ int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, f
 // quant_cols_kernel), quantize them and store 128 contiguous bytes per
 // column.  The bytes and scales equal those of the two separate kernels.
 // ---------------------------------------------------------------------------
+// ROWS = false gives the column quantization alone (tg_quantize_cols for
+// 16-byte-aligned rows); GUARD handles a last tile narrower than 128 columns.
+template <bool ROWS, bool GUARD>
 __global__ __launch_bounds__(256) void quant_dual_kernel(const uint4* __restrict__ x, int64_t rows,
                                                          int64_t cols, uint2* __restrict__ q,
                                                          float* __restrict__ s,
@@ -230,18 +223,22 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(const uint4* __restrict
   const int64_t c0 = (int64_t)blockIdx.x * 128, r0 = (int64_t)blockIdx.y * 128;
   const int ch = tid & 15, rr = tid >> 4;
   const int64_t cchunks = cols >> 3;
+  const bool ch_ok = !GUARD || (c0 >> 3) + ch < cchunks;
   uint4 v[8];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) v[u] = ldg_stream(x + (r0 + rr + 16 * u) * cchunks + (c0 >> 3) + ch);
+  for (int u = 0; u < 8; ++u)
+    v[u] = ch_ok ? ldg_stream(x + (r0 + rr + 16 * u) * cchunks + (c0 >> 3) + ch) : make_uint4(0, 0, 0, 0);
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int row = rr + 16 * u;
-    float f[8];
-    f[0] = bf16lo(v[u].x); f[1] = bf16hi(v[u].x); f[2] = bf16lo(v[u].y); f[3] = bf16hi(v[u].y);
-    f[4] = bf16lo(v[u].z); f[5] = bf16hi(v[u].z); f[6] = bf16lo(v[u].w); f[7] = bf16hi(v[u].w);
-    const float sc = block_scale_bf16(row16_max_u32(absmax8(f)));
-    q[(r0 + row) * cchunks + (c0 >> 3) + ch] = quant8<true>(f, sc);
-    if (ch == 0) s[(r0 + row) * (cols >> 7) + blockIdx.x] = sc;
+    if (ROWS) {
+      float f[8];
+      f[0] = bf16lo(v[u].x); f[1] = bf16hi(v[u].x); f[2] = bf16lo(v[u].y); f[3] = bf16hi(v[u].y);
+      f[4] = bf16lo(v[u].z); f[5] = bf16hi(v[u].z); f[6] = bf16lo(v[u].w); f[7] = bf16hi(v[u].w);
+      const float sc = block_scale_bf16(row16_max_u32(absmax8(f)));
+      q[(r0 + row) * cchunks + (c0 >> 3) + ch] = quant8<true>(f, sc);
+      if (ch == 0) s[(r0 + row) * (cols >> 7) + blockIdx.x] = sc;
+    }
     *reinterpret_cast<uint4*>(&tile[row * 68 + ch * 4]) = v[u];
   }
   __syncthreads();
@@ -281,19 +278,45 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(const uint4* __restrict
       }
       tq[n * 36 + 4 * i + j] = w;
     }
-    if (j == 0) st[(c0 + n) * (rows >> 7) + blockIdx.y] = sc;
+    if (j == 0 && (!GUARD || c0 + n < cols)) st[(c0 + n) * (rows >> 7) + blockIdx.y] = sc;
   };
   col_words(f0, sc0, 2 * cp);
   col_words(f1, sc1, 2 * cp + 1);
   __syncthreads();
+  // each store instruction writes 64 contiguous bytes of a column (lane j of
+  // the quad: bytes 16j.. and 64 + 16j..), so no partial 32-byte sectors
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     const int n = (tid >> 2) + 64 * p;
-    const uint4* src = reinterpret_cast<const uint4*>(&tq[n * 36 + 8 * j]);
-    uint4* dst = reinterpret_cast<uint4*>(qt + (c0 + n) * rows + r0 + 32 * j);
-    stg_stream(dst, src[0]);
-    stg_stream(dst + 1, src[1]);
+    if (GUARD && c0 + n >= cols) continue;
+    const uint4* src = reinterpret_cast<const uint4*>(&tq[n * 36]);
+    uint4* dst = reinterpret_cast<uint4*>(qt + (c0 + n) * rows + r0);
+    stg_stream(dst + j, src[j]);
+    stg_stream(dst + 4 + j, src[4 + j]);
   }
+}
+
+int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, float* s_t,
+                      hipStream_t st) {
+  if (rows == 0 || cols == 0) return TG_OK;
+  if (rows / 128 > 65535) return einval("quantize_cols: rows / 128 must be <= 65535");
+  if (cols % 8 == 0 && aligned(x, 16)) {
+    // 128 x 128 tiles: column pairs per LDS read, 64-byte contiguous stores
+    const dim3 g128((unsigned)((cols + 127) / 128), (unsigned)(rows / 128));
+    auto X = reinterpret_cast<const uint4*>(x);
+    if (cols % 128 == 0)
+      hipLaunchKernelGGL((quant_dual_kernel<false, false>), g128, dim3(256), 0, st, X, rows, cols,
+                         nullptr, nullptr, q_t, s_t);
+    else
+      hipLaunchKernelGGL((quant_dual_kernel<false, true>), g128, dim3(256), 0, st, X, rows, cols,
+                         nullptr, nullptr, q_t, s_t);
+    return check_launch("quant_cols");
+  }
+  // rows not 16-byte aligned: the element-load kernel
+  const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)(rows / 128));
+  hipLaunchKernelGGL(quant_cols_kernel<false>, grid, dim3(256), 0, st,
+                     reinterpret_cast<const uint16_t*>(x), rows, cols, q_t, s_t);
+  return check_launch("quant_cols");
 }
 
 int launch_quant_dual(const void* x, int64_t rows, int64_t cols, uint8_t* q, float* s, uint8_t* q_t,
@@ -302,8 +325,9 @@ int launch_quant_dual(const void* x, int64_t rows, int64_t cols, uint8_t* q, flo
   if (rows % 128 || cols % 128) return einval("quantize_dual: rows and cols must be multiples of 128");
   if (rows / 128 > 65535) return einval("quantize_dual: rows / 128 must be <= 65535");
   const dim3 grid((unsigned)(cols / 128), (unsigned)(rows / 128));
-  hipLaunchKernelGGL(quant_dual_kernel, grid, dim3(256), 0, st, reinterpret_cast<const uint4*>(x), rows,
-                     cols, reinterpret_cast<uint2*>(q), s, q_t, s_t);
+  hipLaunchKernelGGL((quant_dual_kernel<true, false>), grid, dim3(256), 0, st,
+                     reinterpret_cast<const uint4*>(x), rows, cols, reinterpret_cast<uint2*>(q), s, q_t,
+                     s_t);
   return check_launch("quant_dual");
 }
 
