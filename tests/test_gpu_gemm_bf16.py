@@ -91,7 +91,9 @@ def test_gemm_bf16_rejects_bad_k(dev):
 
 @pytest.mark.parametrize("transpose", [0, 1])
 @pytest.mark.parametrize("src", ["bf16", "f32"])
-@pytest.mark.parametrize("rows,cols,pad", [(1, 1, 63), (65, 130, 0), (100, 64, 28), (333, 77, 51)])
+@pytest.mark.parametrize("rows,cols,pad", [(1, 1, 63), (65, 130, 0), (100, 64, 28), (333, 77, 51),
+                                           # 16-byte rows: the 128 x 128 tile kernel when transposing
+                                           (200, 264, 56), (1000, 8, 0), (384, 1024, 0), (129, 136, 7)])
 def test_pack_bf16(dev, transpose, src, rows, cols, pad):
     rng = np.random.default_rng(rows * 7 + cols)
     x32 = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)

@@ -236,6 +236,49 @@ __global__ __launch_bounds__(256) void pack_bf16_kernel(const void* __restrict__
   }
 }
 
+// Transposing pack of 16-byte-aligned bf16 rows (cols % 8 == 0, pitch % 8 ==
+// 0): a 128 x 128 tile is loaded with 16-byte row loads into LDS (pitch
+// 272 B); lane p of a wave then reads the column pair 2p, 2p + 1 one 32-bit
+// word per row and writes 8 rows of both columns as two 16-byte stores.
+__global__ __launch_bounds__(256) void pack_bf16_t128_kernel(const uint4* __restrict__ x,
+                                                             uint16_t* __restrict__ y, int rows,
+                                                             int cols, int pitch) {
+  __shared__ uint32_t tile[128 * 68];
+  const int tid = threadIdx.x;
+  const int r0 = blockIdx.y * 128, c0 = blockIdx.x * 128;
+  const int ch = tid & 15, rr = tid >> 4;
+  const int cchunks = cols >> 3;
+  const bool ch_ok = (c0 >> 3) + ch < cchunks;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int r = r0 + rr + 16 * u;
+    const uint4 v = (ch_ok && r < rows) ? ldg_stream(x + (int64_t)r * cchunks + (c0 >> 3) + ch)
+                                        : make_uint4(0, 0, 0, 0);
+    *reinterpret_cast<uint4*>(&tile[(rr + 16 * u) * 68 + ch * 4]) = v;
+  }
+  __syncthreads();
+  const int p = tid & 63, g = tid >> 6;
+  const int oc0 = c0 + 2 * p;   // output rows oc0, oc0 + 1 (input columns)
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int rb = 32 * g + 8 * c;
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t w0 = tile[(rb + 2 * e) * 68 + p], w1 = tile[(rb + 2 * e + 1) * 68 + p];
+      lo[e] = (w0 & 0xFFFFu) | (w1 << 16);
+      hi[e] = (w0 >> 16) | (w1 & 0xFFFF0000u);
+    }
+    const int oc = r0 + rb;        // output column of the first of the 8 elements
+    if (oc < pitch) {
+      if (oc0 < cols)
+        *reinterpret_cast<uint4*>(y + (int64_t)oc0 * pitch + oc) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+      if (oc0 + 1 < cols)
+        *reinterpret_cast<uint4*>(y + (int64_t)(oc0 + 1) * pitch + oc) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    }
+  }
+}
+
 int launch_pack_bf16(const void* x, int x_dtype, int64_t rows, int64_t cols, int transpose,
                      __bf16* y, int64_t pitch, hipStream_t st) {
   if (rows == 0 || cols == 0) return TG_OK;
@@ -243,6 +286,13 @@ int launch_pack_bf16(const void* x, int x_dtype, int64_t rows, int64_t cols, int
   const int64_t ext_r = transpose ? pitch : rows, ext_c = transpose ? cols : pitch;
   const dim3 grid((unsigned)((ext_c + 63) / 64), (unsigned)((ext_r + 63) / 64));
   const int r = (int)rows, c = (int)cols, p = (int)pitch;
+  if (transpose && x_dtype == TG_DTYPE_BF16 && cols % 8 == 0 && pitch % 8 == 0 &&
+      (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0) {
+    const dim3 g128((unsigned)((cols + 127) / 128), (unsigned)((pitch + 127) / 128));
+    hipLaunchKernelGGL(pack_bf16_t128_kernel, g128, dim3(256), 0, st, reinterpret_cast<const uint4*>(x),
+                       reinterpret_cast<uint16_t*>(y), r, c, p);
+    return check_launch("pack_bf16_t128");
+  }
   if (x_dtype == TG_DTYPE_F32) {
     if (transpose) hipLaunchKernelGGL((pack_bf16_kernel<true, true>), grid, dim3(256), 0, st, x, y, r, c, p);
     else hipLaunchKernelGGL((pack_bf16_kernel<true, false>), grid, dim3(256), 0, st, x, y, r, c, p);
