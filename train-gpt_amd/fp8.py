@@ -258,6 +258,76 @@ class _BlockScaledMatmul(torch.autograd.Function):
         return da, db, None
 
 
+class _BlockScaledMatmulPrequant(torch.autograd.Function):
+    """block_scaled_matmul whose left operand arrives already quantized.
+
+    a_q / a_s must be _quantize_to_fp8(a) (for example the bytes and scales
+    kernels.rms_norm_fp8 writes together with its bf16 output a), so the
+    forward skips fp8.py:66's quantization of a; the residuals and the
+    backward are block_scaled_matmul's (fp8.py:81-98), on the un-quantized a.
+    """
+
+    @staticmethod
+    def forward(ctx, a, a_q, a_s, b, block_k):
+        leading, K, N = _validate(a, b, block_k)
+        _L.require_gpu(a, b)
+        _check_block_k(block_k)
+        b_q, b_s = quantize_fp8(b, block_k, transpose=True)                 # fp8.py:68
+        out = scaled_matmul(a_q.reshape(-1, K).view(torch.uint8), a_s.reshape(-1, K // block_k),
+                            b_q.view(torch.uint8), b_s)                        # fp8.py:70-78
+        ctx.save_for_backward(a, b)
+        ctx.block_k = block_k
+        return out.reshape(*leading, N)
+
+    @staticmethod
+    def backward(ctx, g):
+        a, b = ctx.saved_tensors
+        da, db = _fp8_backward(ctx.block_k, (a, b), g)
+        return da, None, None, db, None
+
+
+def block_scaled_matmul_prequant(a, a_q, a_s, b, block_k: int = DEFAULT_BLOCK_K):
+    """a @ b through FP8 with a's quantization (a_q, a_s) supplied by the caller."""
+    return _BlockScaledMatmulPrequant.apply(a, a_q, a_s, b, block_k)
+
+
+class _Bf16Matmul(torch.autograd.Function):
+    """A bf16 matmul on the bf16 MFMA GEMM: out = bf16(a @ b) with fp32
+    accumulation (the `x @ w_out` logits projection that model.py:95-96 and
+    bench_fp8_norm.py:117-118 keep in bf16); the backward is the
+    straight-through rule of fp8.py:85-98."""
+
+    @staticmethod
+    def forward(ctx, a, b):
+        *lead, K = a.shape
+        K_b, N = b.shape
+        if K != K_b:
+            raise ValueError(f"contracted-dim mismatch: a K={K}, b K={K_b}")
+        if K % 64:
+            raise ValueError(f"K={K} must be a multiple of 64 for the bf16 GEMM")
+        _L.require_gpu(a, b)
+        a2 = a.reshape(-1, K).to(torch.bfloat16).contiguous()
+        M = a2.shape[0]
+        bt = torch.empty((N, K), dtype=torch.bfloat16, device=a.device)         # b.T, packed
+        _L.check(_L.lib().tg_pack_bf16(_L.ptr(b.contiguous()), _L.dtype_code(b), K, N, 1, _L.ptr(bt), K,
+                                       _L.stream_of(a2)))
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+        _L.check(_L.lib().tg_gemm_bf16_nt(_L.ptr(a2), _L.ptr(bt), _L.ptr(out), M, N, K,
+                                          _L.stream_of(a2)))
+        ctx.save_for_backward(a, b)
+        return out.reshape(*lead, N)
+
+    @staticmethod
+    def backward(ctx, g):
+        a, b = ctx.saved_tensors
+        return _bf16_backward(a, b, g)
+
+
+def bf16_matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """bf16 a (..., K) @ b (K, N) -> bf16 (..., N) on the bf16 MFMA GEMM (autograd-aware)."""
+    return _Bf16Matmul.apply(a, b)
+
+
 # ---------------------------------------------------------------------------
 # Pre-quantized weights and decode-shape GEMM (no reference counterpart).
 # ---------------------------------------------------------------------------

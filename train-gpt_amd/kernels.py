@@ -48,7 +48,13 @@ def rms_norm_fp8(x: torch.Tensor, scale: torch.Tensor, eps: float, block_k: int 
 
     Returns (y bf16 (..., D), y_f8 float8_e4m3fn (..., D), y_scales f32 (..., D/block_k)),
     where (y_f8, y_scales) == _quantize_to_fp8(y.astype(f32), block_k) bit for bit.
+    Differentiable in y (the backward is rms_norm's, kernels.py:104-118); the
+    bytes and scales carry no gradient.
     """
+    return _RMSNormFP8.apply(x, scale, eps, block_k)
+
+
+def _rms_norm_fp8_fwd(x: torch.Tensor, scale: torch.Tensor, eps: float, block_k: int):
     x2, g, D = _prep(x, scale)
     if D % block_k:
         raise ValueError(f"K={D} not divisible by block_k={block_k}")
@@ -77,6 +83,22 @@ def _rms_norm_bwd(x: torch.Tensor, scale: torch.Tensor, eps: float, g: torch.Ten
     _L.check(_L.lib().tg_rms_norm_bwd(_L.ptr(x2), _L.ptr(sc), _L.ptr(g2), _L.ptr(dx), _L.ptr(dscale),
                                       R, D, float(eps), _L.ptr(ws), ws_bytes, _L.stream_of(x2)))
     return dx.reshape(x.shape), dscale
+
+
+class _RMSNormFP8(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, scale, eps, block_k):
+        y, q, s = _rms_norm_fp8_fwd(x, scale, eps, block_k)
+        ctx.save_for_backward(x, scale)
+        ctx.eps = eps
+        ctx.mark_non_differentiable(q, s)
+        return y, q, s
+
+    @staticmethod
+    def backward(ctx, gy, gq, gs):
+        x, scale = ctx.saved_tensors
+        dx, dscale = _rms_norm_bwd(x, scale, ctx.eps, gy)
+        return dx, dscale, None, None
 
 
 class _RMSNorm(torch.autograd.Function):
