@@ -25,6 +25,8 @@ gemv         = config 5 decode GEMV on a pre-quantized W [4096, 14336] (e4m3,
 bwd_bf16     = the reference's straight-through bf16 backward (fp8.py:85-98)
                at config 3: 2 bf16 GEMMs (+ operand packing) per call vs the
                2.5 PFLOP/s dense bf16 MFMA peak
+block_step   = config 4: one decoder block training step (block.py), FP8 linears
+               vs bf16 linears, wall time per step
 cpu_baseline = the CPU oracle (numpy + C) on a row sample of the same step
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
@@ -318,6 +320,32 @@ def bench_bwd_bf16(dev, iters):
             "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
 
 
+def bench_block(dev, steps=5, warm=3):
+    """Config 4: one decoder block training step (block.py), FP8 path vs the
+    same block with bf16 linears; wall time per step after a synchronize."""
+    import torch
+    import block
+    cfg = block.C4
+    params = block.init_params(cfg, dev)
+    ids, tgt = block.random_batch(cfg, dev)
+    out = {"workload": "C4 decoder block fwd+bwd: d 2048, 16x128 heads, MLP 8192 GELU, 4 x 2048 tokens, "
+                       "vocab 50304 (bf16 logits), CE loss; FP8 linears + HIP norms",
+           "flop_per_step": block.flops_per_step(cfg)}
+    for impl in ("fp8", "bf16"):
+        for _ in range(warm):
+            block.step_grads(params, ids, tgt, cfg, impl)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss, _ = block.step_grads(params, ids, tgt, cfg, impl)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        out[impl] = {"ms_per_step": round(dt * 1e3, 3),
+                     "tokens_per_s": round(cfg.batch * cfg.seq_len / dt, 1),
+                     "loss": round(float(loss), 6)}
+    return out
+
+
 def cpu_baseline(rows=8192, repeats=5):
     """The CPU oracle on the step: quantize (C oracle) and the dequantized f32
     GEMMs (numpy/BLAS) of fwd + FP8 bwd over `rows` of the 8192 token rows,
@@ -396,6 +424,7 @@ def main():
     norm_bwd = bench_norm_bwd(dev, args.norm_iters)
     gemv = bench_gemv(dev, args.norm_iters)
     bwd_bf16 = bench_bwd_bf16(dev, 10)
+    block_step = bench_block(dev)
     out = {
         "metric": "FP8 block-scaled GEMM TFLOP/s (% fp8 MFMA peak); RMSNorm+quant HBM GB/s",
         "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -413,6 +442,7 @@ def main():
         "norm_bwd": norm_bwd,
         "gemv": gemv,
         "bwd_bf16": bwd_bf16,
+        "block_step": block_step,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
