@@ -177,10 +177,36 @@ __device__ __forceinline__ double shfl_xor_f64(double v, int m) {
   return __hiloint2double(hi, lo);
 }
 
-// Sum over the 64 lanes (xor butterfly: every lane gets the same value).
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const int lo = __builtin_amdgcn_mov_dpp(__double2loint(v), CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_mov_dpp(__double2hiint(v), CTRL, 0xF, 0xF, false);
+  return __hiloint2double(hi, lo);
+}
+
+// Sum over the 64 lanes, every lane getting the same value, in VALU only:
+// four DPP steps inside each 16-lane row (pairs, quads, half rows, rows),
+// then the gfx950 row swaps (v_permlane16_swap: rows 0<->1 and 2<->3,
+// v_permlane32_swap: the two halves).  Each step adds a lane's value to its
+// partner's, and both partners form the same sum (IEEE addition commutes),
+// so the result is identical in all lanes.
 __device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_f64(v, m);
+  v += dpp_f64<0xB1>(v);     // quad_perm [1,0,3,2]
+  v += dpp_f64<0x4E>(v);     // quad_perm [2,3,0,1]
+  v += dpp_f64<0x141>(v);    // row_half_mirror
+  v += dpp_f64<0x140>(v);    // row_mirror
+  {
+    const int lo = __double2loint(v), hi = __double2hiint(v);
+    const auto l = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto h = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    v = __hiloint2double((int)h[0], (int)l[0]) + __hiloint2double((int)h[1], (int)l[1]);
+  }
+  {
+    const int lo = __double2loint(v), hi = __double2hiint(v);
+    const auto l = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto h = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    v = __hiloint2double((int)h[0], (int)l[0]) + __hiloint2double((int)h[1], (int)l[1]);
+  }
   return v;
 }
 
