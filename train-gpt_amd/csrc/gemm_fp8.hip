@@ -240,14 +240,19 @@ __device__ __forceinline__ void promote4(v4f& acc, const v4f& p, const float4& s
   acc[3] = __builtin_fmaf(p[3], sa.w * sb, acc[3]);
 }
 
-// MFMAs of n-tile j are issued while the 16x16 results of n-tile j-1 are
-// promoted (8 VALU per MFMA), so at most two tiles of partial results are
-// live and the VALU work runs in the MFMA shadow.  The B fragment and column
-// scale of n-tile j+1 are read from LDS one region ahead, so no region waits
-// on LDS latency.
+// One K block kb from stage S.  MFMAs of n-tile j are issued while the 16x16
+// results of n-tile j-1 are promoted (8 VALU per MFMA), so at most two tiles
+// of partial results are live and the VALU work runs in the MFMA shadow; the
+// B fragment and column scale of n-tile j+1 are read from LDS one region
+// ahead.  The A fragments of block kb arrive in af (read during the previous
+// block's last region).  All copies of block kb+1 into the other stage are
+// issued by region 6; the wave then waits for its copies and meets the others
+// at the barrier, and region 7 (MFMAs of n-tile 7, promotions of tiles 6 and
+// 7) overlaps the LDS reads of block kb+1's A fragments.  Region 7 reads no
+// LDS of stage S, so after the barrier stage S is free for block kb+2.
 template <int S>
-__device__ __forceinline__ void g256_compute(const G256Ctx& c, v4f (&acc)[4][8], int kb_next) {
-  const uint8_t* la = g256_a<S>();
+__device__ __forceinline__ void g256_compute_tail(const G256Ctx& c, v4f (&acc)[4][8], v8i (&af)[4],
+                                                  int kb_next) {
   const uint8_t* lb = g256_b<S>();
   const float* ls = g256_s<S>();
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
@@ -255,22 +260,18 @@ __device__ __forceinline__ void g256_compute(const G256Ctx& c, v4f (&acc)[4][8],
     return as_v8i(*reinterpret_cast<const uint4*>(lb + c.fb0 + j * 2048),
                   *reinterpret_cast<const uint4*>(lb + c.fb1 + j * 2048));
   };
-  v8i af[4];
   float4 sav[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    af[i] = as_v8i(*reinterpret_cast<const uint4*>(la + c.fa0 + i * 2048),
-                   *reinterpret_cast<const uint4*>(la + c.fa1 + i * 2048));
-    sav[i] = *reinterpret_cast<const float4*>(ls + c.fsa + i * 16);
-  }
+  for (int i = 0; i < 4; ++i) sav[i] = *reinterpret_cast<const float4*>(ls + c.fsa + i * 16);
   v8i bn = read_b(1);
   float sbn = ls[c.fsb + 16];
   v4f pc[4];
   float sbc = ls[c.fsb];
-  const bool pf = kb_next < c.nkb && c.wave < 4;   // loader waves, wave-uniform
+  const bool more = kb_next < c.nkb;                 // wave-uniform
+  const bool pf = more && c.wave < 4;                // loader waves
   if (pf) {
-    g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, 0);
-    g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, 1);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, p);
   }
   {
     const v8i bf = read_b(0);
@@ -285,6 +286,13 @@ __device__ __forceinline__ void g256_compute(const G256Ctx& c, v4f (&acc)[4][8],
       bn = read_b(j + 1);
       sbn = ls[c.fsb + (j + 1) * 16];
     }
+    if (j == 7) {
+      // every copy of block kb+1 was issued by region 6: wait for this
+      // wave's, then for everybody's (and for every wave to be done with the
+      // LDS reads of stage S)
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
     // register fences: the MFMAs of tile j and the promotions of tile j-1 may
     // not rise above this point and must be done at the fence below.  Left
     // free, the compiler either batches all MFMAs of the K block (32 partial
@@ -293,9 +301,9 @@ __device__ __forceinline__ void g256_compute(const G256Ctx& c, v4f (&acc)[4][8],
     asm volatile("" : "+v"(bf));
 #pragma unroll
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][j - 1]));
-    if (pf) {
-      g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, 2 * j);
-      g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, 2 * j + 1);
+    if (pf && j < 7) {
+      g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, 2 * j + 2);
+      g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, 2 * j + 3);
     }
     v4f pn[4];
 #pragma unroll
@@ -314,6 +322,13 @@ __device__ __forceinline__ void g256_compute(const G256Ctx& c, v4f (&acc)[4][8],
     // MFMA / VALU pairs serialize
 #pragma unroll
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][j - 1]) : "v"(pn[i]));
+    if (j == 7 && more) {
+      const uint8_t* la = g256_a<S ^ 1>();
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        af[i] = as_v8i(*reinterpret_cast<const uint4*>(la + c.fa0 + i * 2048),
+                       *reinterpret_cast<const uint4*>(la + c.fa1 + i * 2048));
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) pc[i] = pn[i];
     sbc = sbj;
@@ -322,16 +337,6 @@ __device__ __forceinline__ void g256_compute(const G256Ctx& c, v4f (&acc)[4][8],
   for (int i = 0; i < 4; ++i) promote4(acc[i][7], pc[i], sav[i], sbc);
 #pragma unroll
   for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][7]));
-}
-
-// One K block: compute block kb from stage S while prefetching block kb+1
-// into the other stage (issued part by part inside the compute regions), then
-// wait for this wave's prefetch and meet at the barrier.
-template <int S>
-__device__ __forceinline__ void g256_step(const G256Ctx& c, int kb, v4f (&acc)[4][8]) {
-  g256_compute<S>(c, acc, kb + 1);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
 }
 
 template <int BNS, bool OUT_F32>
@@ -393,11 +398,16 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   int kb = 0;
+  v8i af[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    af[i] = as_v8i(*reinterpret_cast<const uint4*>(g256_a0 + c.fa0 + i * 2048),
+                   *reinterpret_cast<const uint4*>(g256_a0 + c.fa1 + i * 2048));
   for (; kb + 1 < c.nkb; kb += 2) {
-    g256_step<0>(c, kb, acc);
-    g256_step<1>(c, kb + 1, acc);
+    g256_compute_tail<0>(c, acc, af, kb + 1);
+    g256_compute_tail<1>(c, acc, af, kb + 2);
   }
-  if (kb < c.nkb) g256_step<0>(c, kb, acc);
+  if (kb < c.nkb) g256_compute_tail<0>(c, acc, af, kb + 1);
 
   if (OUT_F32) {
 #pragma unroll
