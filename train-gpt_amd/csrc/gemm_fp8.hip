@@ -233,11 +233,14 @@ __device__ __forceinline__ void g256_issue(const G256Ctx& c, int kb) {
   }
 }
 
-__device__ __forceinline__ void promote4(v4f& acc, const v4f& p, const float4& sa, float sb) {
-  acc[0] = __builtin_fmaf(p[0], sa.x * sb, acc[0]);
-  acc[1] = __builtin_fmaf(p[1], sa.y * sb, acc[1]);
-  acc[2] = __builtin_fmaf(p[2], sa.z * sb, acc[2]);
-  acc[3] = __builtin_fmaf(p[3], sa.w * sb, acc[3]);
+// The 256 kernel computes each 16x16 tile as B.A^T (B fragment in the MFMA's
+// A slot), so lane (fr, fg) holds output row m = fr and the four consecutive
+// columns n = 4fg .. 4fg+3: one A-row scale and four B-column scales.
+__device__ __forceinline__ void promote4(v4f& acc, const v4f& p, float sa, const float4& sb) {
+  acc[0] = __builtin_fmaf(p[0], sa * sb.x, acc[0]);
+  acc[1] = __builtin_fmaf(p[1], sa * sb.y, acc[1]);
+  acc[2] = __builtin_fmaf(p[2], sa * sb.z, acc[2]);
+  acc[3] = __builtin_fmaf(p[3], sa * sb.w, acc[3]);
 }
 
 // One K block kb from stage S.  MFMAs of n-tile j are issued while the 16x16
@@ -260,13 +263,14 @@ __device__ __forceinline__ void g256_compute_tail(const G256Ctx& c, v4f (&acc)[4
     return as_v8i(*reinterpret_cast<const uint4*>(lb + c.fb0 + j * 2048),
                   *reinterpret_cast<const uint4*>(lb + c.fb1 + j * 2048));
   };
-  float4 sav[4];
+  float sav[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sav[i] = *reinterpret_cast<const float4*>(ls + c.fsa + i * 16);
+  for (int i = 0; i < 4; ++i) sav[i] = ls[c.fsa + i * 16];
+  auto read_sb = [&](int j) { return *reinterpret_cast<const float4*>(ls + c.fsb + j * 16); };
   v8i bn = read_b(1);
-  float sbn = ls[c.fsb + 16];
+  float4 sbn = read_sb(1);
   v4f pc[4];
-  float sbc = ls[c.fsb];
+  float4 sbc = read_sb(0);
   const bool more = kb_next < c.nkb;                 // wave-uniform
   const bool pf = more && c.wave < 4;                // loader waves
   if (pf) {
@@ -276,15 +280,15 @@ __device__ __forceinline__ void g256_compute_tail(const G256Ctx& c, v4f (&acc)[4
   {
     const v8i bf = read_b(0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pc[i] = mfma_f8_16x16x128(af[i], bf, zero);
+    for (int i = 0; i < 4; ++i) pc[i] = mfma_f8_16x16x128(bf, af[i], zero);
   }
 #pragma unroll
   for (int j = 1; j < 8; ++j) {
     v8i bf = bn;
-    const float sbj = sbn;
+    const float4 sbj = sbn;
     if (j + 1 < 8) {
       bn = read_b(j + 1);
-      sbn = ls[c.fsb + (j + 1) * 16];
+      sbn = read_sb(j + 1);
     }
     if (j == 7) {
       // every copy of block kb+1 was issued by region 6: wait for this
@@ -307,7 +311,7 @@ __device__ __forceinline__ void g256_compute_tail(const G256Ctx& c, v4f (&acc)[4
     }
     v4f pn[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pn[i] = mfma_f8_16x16x128(af[i], bf, zero);
+    for (int i = 0; i < 4; ++i) pn[i] = mfma_f8_16x16x128(bf, af[i], zero);
 #pragma unroll
     for (int i = 0; i < 4; ++i) promote4(acc[i][j - 1], pc[i], sav[i], sbc);
     // issue order MFMA / 8 VALU x 4: the promotion of tile j-1 co-executes
@@ -385,8 +389,8 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
   c.fa1 = c.fa0 ^ 64u;
   c.fb0 = (uint32_t)(wn * 128 + fr) * 128u + ch0;
   c.fb1 = c.fb0 ^ 64u;
-  c.fsa = wm * 64 + 4 * fg;
-  c.fsb = 256 + wn * 128 + fr;
+  c.fsa = wm * 64 + fr;                 // A-row scale of output row fr
+  c.fsb = 256 + wn * 128 + 4 * fg;      // B-column scales of columns 4fg .. 4fg+3
 
   v4f acc[4][8];
 #pragma unroll
@@ -409,54 +413,37 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
   }
   if (kb < c.nkb) g256_compute_tail<0>(c, acc, af, kb + 1);
 
-  if (OUT_F32) {
+  // Epilogue straight from registers: lane (fr, fg) holds row m = .. + fr and
+  // the four consecutive columns n = .. + 4fg .. 4fg+3 of every 16x16 tile,
+  // i.e. 8 contiguous bf16 bytes (16 f32 bytes).  Per store instruction the
+  // wave writes 16 rows x 32 (64) contiguous bytes; L2 merges the n-tiles.
+  const bool vec_ok = (N % 4) == 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + wm * 64 + i * 16 + fr;
+    if (m >= M) continue;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int n = n0 + wn * 128 + j * 16 + fr;
+    for (int j = 0; j < 8; ++j) {
+      const int n = n0 + wn * 128 + j * 16 + 4 * fg;
+      const v4f v = acc[i][j];
+      if (OUT_F32) {
+        float* dst = reinterpret_cast<float*>(C) + (int64_t)m * N + n;
+        if (vec_ok && n + 4 <= N) {
+          *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = m0 + wm * 64 + i * 16 + 4 * fg + r;
-          if (m < M && n < N) reinterpret_cast<float*>(C)[(int64_t)m * N + n] = acc[i][j][r];
+          for (int r = 0; r < 4; ++r)
+            if (n + r < N) dst[r] = v[r];
         }
-      }
-    return;
-  }
-  // bf16 epilogue through LDS (the stage buffers are free after the last
-  // barrier): each wave writes its 64 x 128 tile (16 KiB as two 8 KiB halves
-  // of 32 rows x 256 B) and stores it back 16 bytes per lane, 4 rows x 256
-  // contiguous bytes per instruction.
-  uint8_t* ep = (c.wave < 4 ? g256_a0 + c.wave * 8192 : g256_b0 + (c.wave - 4) * 8192);
-  uint8_t* ep2 = (c.wave < 4 ? g256_a1 + c.wave * 8192 : g256_b1 + (c.wave - 4) * 8192);
-  // rows 0..31 of the wave tile go to ep, rows 32..63 to ep2
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = i * 16 + 4 * fg + r, col = j * 16 + fr;
-        uint8_t* base = row < 32 ? ep : ep2;
-        *reinterpret_cast<__bf16*>(base + (row & 31) * 256 + col * 2) = (__bf16)acc[i][j][r];
-      }
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's tile is in LDS
-  const bool vec_ok = (N % 8) == 0;
-#pragma unroll
-  for (int t = 0; t < 16; ++t) {
-    const int row = t * 4 + (lane >> 4), chunk = lane & 15;      // 16 lanes x 16 B per row
-    const uint8_t* base = row < 32 ? ep : ep2;
-    const uint4 v = *reinterpret_cast<const uint4*>(base + (row & 31) * 256 + chunk * 16);
-    const int m = m0 + wm * 64 + row, n = n0 + wn * 128 + chunk * 8;
-    if (m < M) {
-      __bf16* dst = reinterpret_cast<__bf16*>(C) + (int64_t)m * N + n;
-      if (vec_ok && n + 8 <= N) {
-        *reinterpret_cast<uint4*>(dst) = v;
       } else {
-        const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+        __bf16* dst = reinterpret_cast<__bf16*>(C) + (int64_t)m * N + n;
+        if (vec_ok && n + 4 <= N) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        } else {
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-          if (n + k < N) reinterpret_cast<uint16_t*>(dst)[k] = e[k];
+          for (int r = 0; r < 4; ++r)
+            if (n + r < N) dst[r] = (__bf16)v[r];
+        }
       }
     }
   }
