@@ -30,6 +30,7 @@ block_step   = config 4: one decoder block training step (block.py), FP8 linears
 cpu_baseline = the CPU oracle (numpy + C) on a row sample of the same step
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                      [--only norm_quant|norm_bwd|gemv|bwd_bf16|block_step]
 """
 import argparse
 import json
@@ -75,6 +76,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--norm-iters", type=int, default=200)
+    p.add_argument("--only", choices=["norm_quant", "norm_bwd", "gemv", "bwd_bf16", "block_step"],
+                   help="run one secondary workload alone and print its JSON object")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (calibrates the FETCH_SIZE / "
                         "WRITE_SIZE counters for the roofline traffic figure) and exit")
@@ -401,6 +404,12 @@ def main():
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
+    if args.only:
+        fn = {"norm_quant": bench_norm, "norm_bwd": bench_norm_bwd, "gemv": bench_gemv,
+              "bwd_bf16": lambda d, _: bench_bwd_bf16(d, 10),
+              "block_step": lambda d, _: bench_block(d)}[args.only]
+        print(json.dumps({args.only: fn(dev, args.norm_iters)}))
+        return
     step = Step(dev)
     for _ in range(args.warmup):
         step.run()

@@ -18,6 +18,8 @@
 //   * Tile order: consecutive workgroup ids go to different XCDs, so ids are
 //     remapped to give each XCD a contiguous range of tiles, and within that
 //     range tiles are walked in groups of 8 tile-rows for L2 reuse of B.
+#include <type_traits>
+
 #include "tg_device.h"
 #include "tg_host.h"
 #include "gemm_tile.h"
@@ -38,6 +40,15 @@ __device__ __forceinline__ v8i as_v8i(const uint4& lo, const uint4& hi) {
   r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
   return r;
 }
+__device__ __forceinline__ v8i as_v8i(const u32x4_t& lo, const u32x4_t& hi) {
+  v8i r;
+  r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+  r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+  return r;
+}
+
+// Cache-policy operand of the raw buffer loads: nt (streaming, read once).
+constexpr int kAuxNT = 2;
 
 template <int TM, int TN, int BNS, bool OUT_F32>
 __global__ __launch_bounds__(256, 2) void gemm_fp8_nt_kernel(
@@ -500,121 +511,198 @@ int launch_gemm_fp8(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, co
 }
 
 // ---------------------------------------------------------------------------
-// Decode-shape GEMM (M <= 16 * MT) with a pre-quantized weight.  HBM-bound on
-// W: each workgroup owns NT x 16 weight rows and its NW waves split the K
-// blocks, KPW blocks per wave at a time.  A wave issues every load of its
-// blocks (W bytes, x bytes, both scales) before it waits on any of them, so
-// each wave keeps KPW * NT * 16 * 128 bytes of W in flight; the NW partial
-// tiles are then added in wave order through LDS.  The MFMA takes W as the A
-// operand (16 weight rows) and x as B (16 activation rows).
-// ---------------------------------------------------------------------------
-template <int NT, int MT, int NW, int KPW, int BNS>
-__global__ __launch_bounds__(NW * 64) void gemv_fp8_kernel(const uint8_t* __restrict__ XQ,
-                                                           const float* __restrict__ XS,
-                                                           const uint8_t* __restrict__ WQ,
-                                                           const float* __restrict__ WS,
-                                                           __bf16* __restrict__ out, int M, int N,
-                                                           int K) {
-  static_assert(BNS == 1 || (BNS % (NT * 16) == 0), "a workgroup's rows share one scale row");
-  __shared__ v4f red[NW - 1][NT][MT][64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int fr = lane & 15, fg = lane >> 4;
-  const int n0 = blockIdx.x * (NT * 16);
-  const int nkb = K >> 7;
-  const v4f zero = {0.f, 0.f, 0.f, 0.f};
-  v4f acc[NT][MT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = zero;
+// Decode-shape GEMM (M <= 16 * MT) on a pre-quantized weight; HBM-bound on W.
+//
+// Every workgroup owns R <= 64 consecutive weight rows (chosen on the host so
+// that each CU streams the same number of W bytes: 56 rows of the 14336-row C5
+// weight on 256 CUs).  K is walked in chunks of 32 blocks (4 KiB of a row);
+// within a chunk the rows are walked in stages of 8, and wave w loads row w of
+// a stage as four contiguous 1 KiB pieces.  Reading the workgroup's rows in
+// address order keeps each DRAM page to one visit: stages of 1 KiB from every
+// row (K-major) measured ~30% slower on the C5 weight.  Stages travel through
+// registers into LDS (row pitch 4112 B, so the 8 rows of a fragment read
+// spread over the banks) together with their W scales; three stages are in
+// flight, so the loads of stage G + 3 start as soon as stage G has landed,
+// whatever the compute of stage G costs.  Wave w computes blocks 4w .. 4w+3 of each stage: the MFMA takes the 8 rows
+// as its A operand (rows 8..15 repeat them and are discarded) and 16 x rows as
+// B; x fragments of the chunk stay in registers.  Every load is issued
+// unconditionally (masked lanes read zero through the buffer range check), so
+// the compiler counts the loads of each stage exactly.  The partial sums of
+// the 8 waves are added in wave order through LDS (deterministic).
+constexpr int kGemvPitch = 4112;                 // LDS bytes per W row of a stage
+constexpr int kGemvGroups = 8;                   // stages of 8 rows per chunk, at most
+constexpr int kGemvStage = 8 * kGemvPitch + 8 * 64 * 4;   // W rows + scales (64 per row)
+__shared__ __attribute__((aligned(16))) uint8_t gemv_lds0[kGemvStage];
+__shared__ __attribute__((aligned(16))) uint8_t gemv_lds1[kGemvStage];
+__shared__ __attribute__((aligned(16))) uint8_t gemv_lds2[kGemvStage];
+template <int S> __device__ __forceinline__ uint8_t* gemv_stage() {
+  return S == 0 ? gemv_lds0 : S == 1 ? gemv_lds1 : gemv_lds2;
+}
 
-  for (int kb0 = wave * KPW; kb0 < nkb; kb0 += NW * KPW) {
-    uint4 w[KPW][NT][2], xv[KPW][MT][2];
-    float sw[KPW][NT][4], sx[KPW][MT];
+template <int V> using IntC = std::integral_constant<int, V>;
+
+template <int MT, int BNS>
+__global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict__ XQ,
+                                                       const float* __restrict__ XS,
+                                                       const uint8_t* __restrict__ WQ,
+                                                       const float* __restrict__ WS,
+                                                       __bf16* __restrict__ out, int M, int N,
+                                                       int K, int R) {
+  constexpr int NW = 8;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 15, fg = lane >> 4;
+  const int nkb = K >> 7;
+  const int nchunk = (nkb + 31) >> 5;
+  const int n0 = blockIdx.x * R;
+  const int rows = min(R, N - n0);
+  const int ngroups = (rows + 7) >> 3;
+
+  const uint32_t wbytes = (uint32_t)rows * (uint32_t)K;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(WQ + (int64_t)n0 * K, wbytes);
+  const int srows = BNS == 1 ? N : (N + BNS - 1) / BNS;
+  const uint32_t sbytes = (uint32_t)srows * (uint32_t)nkb * 4u;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(WS, sbytes);
+  const uint32_t xbytes = (uint32_t)M * (uint32_t)K;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(XQ, xbytes);
+  const uint32_t xsbytes = (uint32_t)M * (uint32_t)nkb * 4u;
+  const __amdgpu_buffer_rsrc_t rxs = make_rsrc(XS, xsbytes);
+
+  u32x4_t wr[3][4];               // this wave's row of three stages in flight (4 x 1 KiB)
+  float wsr[3];                   // its 32 scales (lanes 0..31; lanes 32..63 read zero)
+  u32x4_t xr[4][MT][2];           // x fragments of blocks 4w .. 4w+3 of the chunk
+  float sxr[4][MT];
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  v4f acc[kGemvGroups][MT];
 #pragma unroll
-    for (int c = 0; c < KPW; ++c) {
-      const int kb = kb0 + c;
-      const bool kv = kb < nkb;
+  for (int g = 0; g < kGemvGroups; ++g)
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int n = n0 + t * 16 + fr;
-        if (kv && n < N) {
-          // chunks fg and fg + 4 of the 128-byte block (x uses the same
-          // pairing): each load instruction reads 64 contiguous bytes per row
-          const uint4* p = reinterpret_cast<const uint4*>(WQ + (int64_t)n * K + kb * 128 + fg * 16);
-          w[c][t][0] = ldg_stream(p);
-          w[c][t][1] = ldg_stream(p + 4);
-        } else {
-          w[c][t][0] = w[c][t][1] = make_uint4(0, 0, 0, 0);
-        }
-        if (BNS == 1) {
+    for (int mt = 0; mt < MT; ++mt) acc[g][mt] = zero;
+
+  // row 8g + w of chunk c (and its 32 scales) into register slot SL
+  auto load_w = [&](auto slot, int c, int g) {
+    constexpr int SL = decltype(slot)::value;
+    const int r = 8 * g + wave;
+    const bool rv = g < ngroups && r < rows;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int nr = n0 + t * 16 + 4 * fg + r;
-            sw[c][t][r] = (kv && nr < N) ? WS[(int64_t)nr * nkb + kb] : 0.0f;
-          }
-        } else {
-          // one scale for every row of the workgroup (wave-uniform load)
-          const float v = kv ? WS[(int64_t)(n0 / BNS) * nkb + kb] : 0.0f;
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t k = (uint32_t)c * 4096u + p * 1024u + lane * 16u;
+      const uint32_t off = (rv && k < (uint32_t)K) ? (uint32_t)r * (uint32_t)K + k : wbytes;
+      wr[SL][p] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kAuxNT);
+    }
+    const int b = c * 32 + lane;
+    const int srow = BNS == 1 ? n0 + r : (n0 + r) / BNS;
+    const uint32_t soff = (rv && lane < 32 && b < nkb) ? ((uint32_t)srow * (uint32_t)nkb + (uint32_t)b) * 4u
+                                                       : sbytes;
+    wsr[SL] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, soff, 0, 0));
+  };
+
+  // stage (c, G): registers -> LDS buffer SL = G % 3, start the loads of stage
+  // G + 3 into the same registers, barrier, then blocks 4w .. 4w+3 of the 8 rows
+  auto stage = [&](auto slot, auto grp, int c) {
+    constexpr int SL = decltype(slot)::value;
+    constexpr int G = decltype(grp)::value;
+    uint8_t* buf = gemv_stage<SL>();
+    float* ssw = reinterpret_cast<float*>(buf + 8 * kGemvPitch);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sw[c][t][r] = v;
-        }
-      }
+    for (int p = 0; p < 4; ++p)
+      *reinterpret_cast<u32x4_t*>(buf + wave * kGemvPitch + p * 1024 + lane * 16) = wr[SL][p];
+    ssw[wave * 64 + lane] = wsr[SL];      // every lane stores: no load sunk into a branch
+    load_w(slot, c, G + 3);
+    __syncthreads();
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        // the x scale of activation row m sits in the lane whose column is m
-        const int m = mt * 16 + fr;
-        if (kv && m < M) {
-          const uint4* p = reinterpret_cast<const uint4*>(XQ + (int64_t)m * K + kb * 128 + fg * 16);
-          xv[c][mt][0] = p[0];
-          xv[c][mt][1] = p[4];
-          sx[c][mt] = XS[(int64_t)m * nkb + kb];
-        } else {
-          xv[c][mt][0] = xv[c][mt][1] = make_uint4(0, 0, 0, 0);
-          sx[c][mt] = 0.0f;
+    for (int i = 0; i < 4; ++i) {
+      const int kb = c * 32 + 4 * wave + i;
+      if (kb < nkb) {
+        const uint8_t* pa = buf + (fr & 7) * kGemvPitch + (4 * wave + i) * 128 + fg * 16;
+        const v8i wa = as_v8i(*reinterpret_cast<const uint4*>(pa),
+                              *reinterpret_cast<const uint4*>(pa + 64));
+        float sw[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sw[r] = ssw[((4 * fg + r) & 7) * 64 + 4 * wave + i];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const v4f pr = mfma_f8_16x16x128(wa, as_v8i(xr[i][mt][0], xr[i][mt][1]), zero);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[G][mt][r] = __builtin_fmaf(pr[r], sw[r] * sxr[i][mt], acc[G][mt][r]);
         }
       }
     }
+  };
+
+  for (int c = 0; c < nchunk; ++c) {
 #pragma unroll
-    for (int c = 0; c < KPW; ++c)
+    for (int i = 0; i < 4; ++i) {
+      const int kb = c * 32 + 4 * wave + i;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const v8i xb = as_v8i(xv[c][mt][0], xv[c][mt][1]);
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          const v4f p = mfma_f8_16x16x128(as_v8i(w[c][t][0], w[c][t][1]), xb, zero);
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            acc[t][mt][r] = __builtin_fmaf(p[r], sw[c][t][r] * sx[c][mt], acc[t][mt][r]);
-        }
+        const int m = mt * 16 + fr;
+        const bool ok = m < M && kb < nkb;
+        const uint32_t xo = ok ? (uint32_t)m * (uint32_t)K + (uint32_t)kb * 128u + fg * 16u : xbytes;
+        xr[i][mt][0] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+        xr[i][mt][1] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? xo + 64u : xbytes, 0, 0);
+        const uint32_t so = ok ? ((uint32_t)m * (uint32_t)nkb + (uint32_t)kb) * 4u : xsbytes;
+        sxr[i][mt] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxs, so, 0, 0));
       }
+    }
+    load_w(IntC<0>{}, c, 0);
+    load_w(IntC<1>{}, c, 1);
+    load_w(IntC<2>{}, c, 2);
+    // every path to stage G runs stages 0 .. G-1 first (early exits only), so
+    // the compiler's count of the loads in flight at stage G is exact
+    do {
+      stage(IntC<0>{}, IntC<0>{}, c);
+      if (ngroups <= 1) break;
+      stage(IntC<1>{}, IntC<1>{}, c);
+      if (ngroups <= 2) break;
+      stage(IntC<2>{}, IntC<2>{}, c);
+      if (ngroups <= 3) break;
+      stage(IntC<0>{}, IntC<3>{}, c);
+      if (ngroups <= 4) break;
+      stage(IntC<1>{}, IntC<4>{}, c);
+      if (ngroups <= 5) break;
+      stage(IntC<2>{}, IntC<5>{}, c);
+      if (ngroups <= 6) break;
+      stage(IntC<0>{}, IntC<6>{}, c);
+      if (ngroups <= 7) break;
+      stage(IntC<1>{}, IntC<7>{}, c);
+    } while (false);
+    __syncthreads();                      // the next chunk rewrites the stage buffers
   }
 
-  if (wave > 0) {
+  // wave-ordered sum of the partial tiles through LDS (stage memory reused), one
+  // pass per x-row tile: lanes fg < 2 hold rows 8g + 4fg .. +3, so each wave
+  // stores those 32 lanes of its 8 group tiles (32 KiB for the workgroup), and
+  // wave g then adds group g's partials of the 8 waves in wave order
+  v4f* red = reinterpret_cast<v4f*>(gemv_lds0);   // [NW][8][32]
+  const bool vec = (N & 3) == 0 && (R & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0;
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+  for (int mt = 0; mt < MT; ++mt) {
+    if (mt > 0) __syncthreads();          // the previous pass has read red
+    if (fg < 2) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) red[wave - 1][t][mt][lane] = acc[t][mt];
-  }
-  __syncthreads();
-  if (wave == 0) {
+      for (int g = 0; g < kGemvGroups; ++g) red[(wave * kGemvGroups + g) * 32 + lane] = acc[g][mt];
+    }
+    __syncthreads();
+    const int g = wave;
+    const int m = mt * 16 + fr, lr = 8 * g + 4 * fg;
+    if (fg < 2 && g < ngroups && m < M && lr < rows) {
+      v4f s = red[g * 32 + lane];
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        v4f s = acc[t][mt];
-#pragma unroll
-        for (int w2 = 0; w2 < NW - 1; ++w2) {
-          const v4f o = red[w2][t][mt][lane];
-          s[0] += o[0]; s[1] += o[1]; s[2] += o[2]; s[3] += o[3];
-        }
-        const int m = mt * 16 + fr;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int n = n0 + t * 16 + 4 * fg + r;
-          if (m < M && n < N) out[(int64_t)m * N + n] = (__bf16)s[r];
-        }
+      for (int w2 = 1; w2 < NW; ++w2) {
+        const v4f o = red[(w2 * kGemvGroups + g) * 32 + lane];
+        s[0] += o[0]; s[1] += o[1]; s[2] += o[2]; s[3] += o[3];
       }
+      __bf16* o = out + (int64_t)m * N + n0 + lr;
+      if (vec && lr + 3 < rows) {
+        *reinterpret_cast<uint2*>(o) = make_uint2(pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3]));
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (lr + r < rows) o[r] = (__bf16)s[r];
+      }
+    }
   }
 }
 
@@ -714,6 +802,38 @@ extern "C" int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, cons
   return launch_gemm_fp8(qat, sat, qgt, sgt, 1, db, TG_DTYPE_BF16, K, N, M, st);  // dW = a.T . g
 }
 
+// Compute units of the current device (cached per device id).
+static int device_cus() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] <= 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cached[dev] = v;
+  }
+  return cached[dev];
+}
+
+// Rows per workgroup: equal rows per CU, a multiple of 8, at most 64.
+template <int MT>
+static int launch_gemv(const uint8_t* x_q, const float* x_s, const uint8_t* w_q, const float* w_s,
+                       int bn, __bf16* out, int M, int N, int K, hipStream_t st) {
+  const int cus = device_cus();
+  int R = (int)(((int64_t)N + cus - 1) / cus);
+  R = (R + 7) & ~7;
+  if (R > 8 * kGemvGroups) R = 8 * kGemvGroups;
+  const dim3 grid((unsigned)((N + R - 1) / R));
+  if (bn == 1)
+    hipLaunchKernelGGL((gemv_fp8_kernel<MT, 1>), grid, dim3(512), 0, st, x_q, x_s, w_q, w_s, out, M,
+                       N, K, R);
+  else
+    hipLaunchKernelGGL((gemv_fp8_kernel<MT, 128>), grid, dim3(512), 0, st, x_q, x_s, w_q, w_s, out,
+                       M, N, K, R);
+  return check_launch("gemv_fp8");
+}
+
 extern "C" int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* w_q,
                            const float* w_s, int w_scale_bn, void* out, int64_t M, int64_t N,
                            int64_t K, int block_k, void* stream) {
@@ -722,24 +842,16 @@ extern "C" int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* 
   if (M == 0 || N == 0) return TG_OK;
   if (!x_q || !x_s || !w_q || !w_s || !out) return einval("gemv_fp8: null pointer");
   if (!aligned(x_q, 16) || !aligned(w_q, 16)) return einval("gemv_fp8: operands must be 16-byte aligned");
+  if ((uint64_t)N * (uint64_t)(K / 128) * 4u >= (1ull << 32) || (uint64_t)M * (uint64_t)K >= (1ull << 32) ||
+      (uint64_t)64 * (uint64_t)K >= (1ull << 32))
+    return einval("gemv_fp8: operand too large for 32-bit buffer offsets");
   hipStream_t st = as_stream(stream);
   const int m = (int)M, n = (int)N, k = (int)K;
   auto o = reinterpret_cast<__bf16*>(out);
-  const dim3 grid((unsigned)((N + 31) / 32));
-#define TG_GEMV(MT, KPW)                                                                          \
-  if (w_scale_bn == 1)                                                                            \
-    hipLaunchKernelGGL((gemv_fp8_kernel<2, MT, 8, KPW, 1>), grid, dim3(512), 0, st, x_q, x_s, w_q, \
-                       w_s, o, m, n, k);                                                          \
-  else                                                                                            \
-    hipLaunchKernelGGL((gemv_fp8_kernel<2, MT, 8, KPW, 128>), grid, dim3(512), 0, st, x_q, x_s,   \
-                       w_q, w_s, o, m, n, k);
-  if (M <= 16) {
-    TG_GEMV(1, 2)
-  } else if (M <= 32) {
-    TG_GEMV(2, 2)
-  } else {
-    TG_GEMV(4, 1)
-  }
-#undef TG_GEMV
-  return check_launch("gemv_fp8");
+  if (M <= 16) return launch_gemv<1>(x_q, x_s, w_q, w_s, w_scale_bn, o, m, n, k, st);
+  if (M <= 32) return launch_gemv<2>(x_q, x_s, w_q, w_s, w_scale_bn, o, m, n, k, st);
+  // 33 <= M <= 64: activation rows 0..31 and 32..M-1 in two passes over W
+  TG_TRY(launch_gemv<2>(x_q, x_s, w_q, w_s, w_scale_bn, o, 32, n, k, st));
+  return launch_gemv<2>(x_q + 32 * K, x_s + 32 * (K / 128), w_q, w_s, w_scale_bn, o + 32 * N, m - 32,
+                        n, k, st);
 }
