@@ -27,10 +27,13 @@ bwd_bf16     = the reference's straight-through bf16 backward (fp8.py:85-98)
                2.5 PFLOP/s dense bf16 MFMA peak
 block_step   = config 4: one decoder block training step (block.py), FP8 linears
                vs bf16 linears, wall time per step
+decode       = KV-cached decode (decode.py) of the reference model config:
+               ms per decode step at batch 1 and 8, and the kept FP8 weights +
+               KV cache read per step against 8 TB/s
 cpu_baseline = the CPU oracle (numpy + C) on a row sample of the same step
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                      [--only norm_quant|norm_bwd|gemv|bwd_bf16|block_step]
+                      [--only norm_quant|norm_bwd|gemv|bwd_bf16|block_step|decode]
 """
 import argparse
 import json
@@ -76,7 +79,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--norm-iters", type=int, default=200)
-    p.add_argument("--only", choices=["norm_quant", "norm_bwd", "gemv", "bwd_bf16", "block_step"],
+    p.add_argument("--only", choices=["norm_quant", "norm_bwd", "gemv", "bwd_bf16", "block_step",
+                                      "decode"],
                    help="run one secondary workload alone and print its JSON object")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (calibrates the FETCH_SIZE / "
@@ -349,6 +353,56 @@ def bench_block(dev, steps=5, warm=3):
     return out
 
 
+def decode_weight_bytes(cfg):
+    """HBM bytes of the kept FP8 weights one decode step reads: e4m3 bytes plus
+    128x128 fp32 scales of the six linears per layer and of the unembedding."""
+    d, h, f, V, L = cfg.d_model, cfg.n_heads * cfg.head_dim, cfg.d_ff, cfg.vocab_size, cfg.n_layers
+    wb = lambda K, N: K * N + ((N + 127) // 128) * (K // 128) * 4
+    return L * (3 * wb(d, h) + wb(h, d) + wb(d, f) + wb(f, d)) + wb(d, V)
+
+
+def bench_decode(dev, steps=32, prompt=128):
+    """KV-cached decode (decode.py) of the reference Config (d 2304, 24 layers,
+    18 x 128 heads, d_ff 9216, vocab 50257): prefill `prompt` tokens, then
+    `steps` decode steps, each one replay of the captured step graph; ms per
+    step and the weight-read rate per step (kept FP8 weights + scales + the KV
+    cache positions <= t; the captured attention reads the whole cache under a
+    mask, which the figure does not count)."""
+    import torch
+    import decode
+    cfg = decode.Config()
+    params = decode.init_params(cfg, dev, seed=0)
+    out = {"workload": "KV-cached decode, reference Config (24 layers, d 2304, 18x128 heads, d_ff 9216, "
+                       f"vocab 50257), FP8 weights 128x128 scales, prompt {prompt}, {steps} steps"}
+    for B in (1, 8):
+        model = decode.FP8Decoder(params, cfg, max_batch=B)
+        model.capture_step(B)
+        g = torch.Generator(device=dev).manual_seed(1)
+        ids = torch.randint(0, cfg.vocab_size, (B, prompt), generator=g, device=dev)
+        toks = torch.randint(0, cfg.vocab_size, (steps + 4, B), generator=g, device=dev)
+        model.prefill(ids)
+        for i in range(4):
+            model.step(toks[i])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            model.step(toks[4 + i])
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        ctx = prompt + 4 + steps / 2
+        kv = 2 * cfg.n_layers * B * cfg.n_heads * ctx * cfg.head_dim * 2
+        byts = decode_weight_bytes(cfg) + kv
+        gbps = byts / dt / 1e9
+        out[f"batch_{B}"] = {"ms_per_step": round(dt * 1e3, 3), "tokens_per_s": round(B / dt, 1),
+                             "bytes_per_step": int(byts),
+                             "roofline": {"bound": "hbm", "achieved": round(gbps, 1),
+                                          "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                                          "frac": round(gbps / HBM_PEAK_GBPS, 4)}}
+        del model
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(rows=8192, repeats=5):
     """The CPU oracle on the step: quantize (C oracle) and the dequantized f32
     GEMMs (numpy/BLAS) of fwd + FP8 bwd over `rows` of the 8192 token rows,
@@ -407,7 +461,8 @@ def main():
     if args.only:
         fn = {"norm_quant": bench_norm, "norm_bwd": bench_norm_bwd, "gemv": bench_gemv,
               "bwd_bf16": lambda d, _: bench_bwd_bf16(d, 10),
-              "block_step": lambda d, _: bench_block(d)}[args.only]
+              "block_step": lambda d, _: bench_block(d),
+              "decode": lambda d, _: bench_decode(d)}[args.only]
         print(json.dumps({args.only: fn(dev, args.norm_iters)}))
         return
     step = Step(dev)
@@ -434,6 +489,7 @@ def main():
     gemv = bench_gemv(dev, args.norm_iters)
     bwd_bf16 = bench_bwd_bf16(dev, 10)
     block_step = bench_block(dev)
+    dec = bench_decode(dev)
     out = {
         "metric": "FP8 block-scaled GEMM TFLOP/s (% fp8 MFMA peak); RMSNorm+quant HBM GB/s",
         "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -452,6 +508,7 @@ def main():
         "gemv": gemv,
         "bwd_bf16": bwd_bf16,
         "block_step": block_step,
+        "decode": dec,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()

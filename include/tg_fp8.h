@@ -173,6 +173,23 @@ int tg_selftest_fp8_cvt(uint64_t* counts, void* stream);
  * 5 device uint64_t, zeroed by the call. */
 int tg_selftest_divide(uint64_t* counts, void* stream);
 
+/* One decode step of the attention of model.py:59-68 over a KV cache, for one
+ * new token per sequence at position t = *t_pos (device memory, 0 <= t < S; so a
+ * captured graph serves every position), fused with the cache append and the
+ * FP8 quantization of the output (the input of the output projection):
+ *   k_cache[b, h, t] = k[b, h];  v_cache[b, h, t] = v[b, h]
+ *   o[b, h] = softmax(q[b, h] . k_cache[b, h, 0..t]^T * scale) v_cache[b, h, 0..t]
+ *   (o_q, o_s) = _quantize_to_fp8(bf16(o))  (fp8.py:39-47; one scale per head)
+ * qkv: (B, 3 * H * head_dim) bf16, row b = [q | k | v] (the fused projection);
+ * k_cache, v_cache: (B, H, S, head_dim) bf16; o_q: (B, H * head_dim) e4m3fn;
+ * o_s: (B, H) f32; o: (B, H * head_dim) bf16 or NULL.  head_dim must be 128.
+ * Replaces the per-token full-context recompute of generate.py:166-171 (with
+ * cuDNN attention inside model.forward, model.py:67).  A t outside [0, S)
+ * touches no memory and writes NaN scales. */
+int tg_decode_attention(const void* qkv, void* k_cache, void* v_cache, const int64_t* t_pos,
+                        uint8_t* o_q, float* o_s, void* o, int64_t B, int64_t H, int64_t S,
+                        int64_t head_dim, float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

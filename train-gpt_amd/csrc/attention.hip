@@ -1,0 +1,190 @@
+// Decode attention over a KV cache, fused with the cache append and with the
+// FP8 quantization of its output (the input of the output projection).
+//
+// One decode step of /root/reference/model.py:59-68 for one new token per
+// sequence at position t (read from device memory, so a captured HIP graph
+// replays the step for every position):
+//   K[b, h, t] = k, V[b, h, t] = v                      (cache append)
+//   o[b, h]    = softmax(q . K[b, h, 0..t]^T / sqrt(Dh)) V[b, h, 0..t]
+//   o_bf16     = bf16(o);  (o_q, o_s) = _quantize_to_fp8(o_bf16)   fp8.py:39-47
+// Dh is 128: one head is exactly one 128-wide scale block, so the quantization
+// of o is local to the workgroup that computes the head.
+//
+// One workgroup per (sequence, head), 4 waves.  Lane l works on dims
+// 8 (l % 16) .. +7 of key (l / 16) of a group of four keys per wave, so a
+// K or V row slice is one 16-byte load and the dot product is reduced over a
+// 16-lane DPP row.  Each lane row keeps an online softmax (running max, sum
+// and 8 weighted-V accumulators, f32) over its keys; the 16 partial states
+// are merged through LDS.  The new key is taken from the projection output,
+// not read back from the cache.
+#include "tg_device.h"
+#include "tg_host.h"
+
+namespace tg {
+
+constexpr int kAttnDh = 128;
+constexpr int kAttnWaves = 4;
+constexpr int kAttnUnroll = 4;        // key groups in flight per wave
+
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // [2,3,0,1]
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // half mirror
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));  // mirror
+  return v;
+}
+
+__global__ __launch_bounds__(kAttnWaves * 64) void decode_attention_kernel(
+    const uint16_t* __restrict__ qkv, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+    const int64_t* __restrict__ tpos, uint8_t* __restrict__ oq, float* __restrict__ os,
+    uint16_t* __restrict__ ob, int H, int S, float scale) {
+  const int bh = blockIdx.x;
+  const int b = bh / H, h = bh - b * H;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int dl = lane & 15, kr = lane >> 4;            // dims 8 dl .. +7 of key row kr
+  const int64_t t = *tpos;
+  const int hd = H * kAttnDh;
+  if (t < 0 || t >= S) {                   // position outside the cache: touch nothing
+    if (threadIdx.x == 0) os[(int64_t)b * H + h] = __builtin_nanf("");
+    return;
+  }
+  const uint16_t* row = qkv + (int64_t)b * 3 * hd;
+  const int64_t cbase = ((int64_t)b * H + h) * S * kAttnDh;   // (b, h, 0, 0) of the caches
+
+  float qf[8];
+  {
+    const uint4 w = *reinterpret_cast<const uint4*>(row + h * kAttnDh + dl * 8);
+    qf[0] = bf16lo(w.x); qf[1] = bf16hi(w.x); qf[2] = bf16lo(w.y); qf[3] = bf16hi(w.y);
+    qf[4] = bf16lo(w.z); qf[5] = bf16hi(w.z); qf[6] = bf16lo(w.w); qf[7] = bf16hi(w.w);
+  }
+  const uint4 knew = *reinterpret_cast<const uint4*>(row + hd + h * kAttnDh + dl * 8);
+  const uint4 vnew = *reinterpret_cast<const uint4*>(row + 2 * hd + h * kAttnDh + dl * 8);
+  if (wave == 0 && kr == 0) {                           // append k, v at position t
+    *reinterpret_cast<uint4*>(kc + cbase + t * kAttnDh + dl * 8) = knew;
+    *reinterpret_cast<uint4*>(vc + cbase + t * kAttnDh + dl * 8) = vnew;
+  }
+
+  // online softmax over keys j = 16 i + 4 wave + kr (i = 0, 1, ...), j <= t
+  float m = -__builtin_inff(), l = 0.0f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  const int64_t nk = t + 1;
+  const int64_t ngroups = (nk + 4 * kAttnWaves - 1) / (4 * kAttnWaves);
+  for (int64_t i0 = 0; i0 < ngroups; i0 += kAttnUnroll) {
+    uint4 kv[kAttnUnroll], vv[kAttnUnroll];
+    int64_t js[kAttnUnroll];
+#pragma unroll
+    for (int u = 0; u < kAttnUnroll; ++u) {
+      const int64_t j = (i0 + u) * (4 * kAttnWaves) + 4 * wave + kr;
+      js[u] = j;
+      if (j < t) {
+        kv[u] = *reinterpret_cast<const uint4*>(kc + cbase + j * kAttnDh + dl * 8);
+        vv[u] = *reinterpret_cast<const uint4*>(vc + cbase + j * kAttnDh + dl * 8);
+      } else {
+        kv[u] = knew;
+        vv[u] = vnew;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kAttnUnroll; ++u) {
+      const uint4 k = kv[u], v = vv[u];
+      float d = qf[0] * bf16lo(k.x);
+      d = __builtin_fmaf(qf[1], bf16hi(k.x), d);
+      d = __builtin_fmaf(qf[2], bf16lo(k.y), d);
+      d = __builtin_fmaf(qf[3], bf16hi(k.y), d);
+      d = __builtin_fmaf(qf[4], bf16lo(k.z), d);
+      d = __builtin_fmaf(qf[5], bf16hi(k.z), d);
+      d = __builtin_fmaf(qf[6], bf16lo(k.w), d);
+      d = __builtin_fmaf(qf[7], bf16hi(k.w), d);
+      const float s = row16_sum(d) * scale;
+      if (js[u] <= t) {                                  // uniform over the 16-lane row
+        const float mn = s > m ? s : m;
+        const float corr = __expf(m - mn), p = __expf(s - mn);
+        l = l * corr + p;
+        acc[0] = __builtin_fmaf(p, bf16lo(v.x), acc[0] * corr);
+        acc[1] = __builtin_fmaf(p, bf16hi(v.x), acc[1] * corr);
+        acc[2] = __builtin_fmaf(p, bf16lo(v.y), acc[2] * corr);
+        acc[3] = __builtin_fmaf(p, bf16hi(v.y), acc[3] * corr);
+        acc[4] = __builtin_fmaf(p, bf16lo(v.z), acc[4] * corr);
+        acc[5] = __builtin_fmaf(p, bf16hi(v.z), acc[5] * corr);
+        acc[6] = __builtin_fmaf(p, bf16lo(v.w), acc[6] * corr);
+        acc[7] = __builtin_fmaf(p, bf16hi(v.w), acc[7] * corr);
+        m = mn;
+      }
+    }
+  }
+
+  // merge the 16 partial states (4 key rows x 4 waves) in a fixed order
+  __shared__ float sm[16], sl[16];
+  __shared__ float sacc[16][kAttnDh];
+  const int part = wave * 4 + kr;
+  if (dl == 0) { sm[part] = m; sl[part] = l; }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sacc[part][dl * 8 + e] = acc[e];
+  __syncthreads();
+  if (wave != 0 || kr != 0) return;
+  float M = sm[0];
+  for (int p = 1; p < 16; ++p) M = sm[p] > M ? sm[p] : M;
+  float L = 0.0f, o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+  for (int p = 0; p < 16; ++p) {
+    const float w = sl[p] > 0.0f ? __expf(sm[p] - M) : 0.0f;   // empty parts carry nothing
+    L = __builtin_fmaf(sl[p], w, L);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(sacc[p][dl * 8 + e], w, o[e]);
+  }
+  const float inv = 1.0f / L;
+  uint32_t ow[4];
+  float yv[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    ow[e] = pack_bf16x2(o[2 * e] * inv, o[2 * e + 1] * inv);
+    yv[2 * e] = bf16lo(ow[e]);
+    yv[2 * e + 1] = bf16hi(ow[e]);
+  }
+  const int64_t oi = (int64_t)b * hd + h * kAttnDh + dl * 8;
+  if (ob) *reinterpret_cast<uint4*>(ob + oi) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+  // quantize the bf16 head (one 128-wide block over the 16 lanes of this row)
+  uint32_t amb = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) amb = max(amb, __float_as_uint(yv[e]) & 0x7FFFFFFFu);
+  amb = row16_max_u32(amb);
+  const float sc = block_scale_bf16(amb);
+  uint2 qo;
+  Divider dv(sc);
+  if (dv.fast) {
+    qo.x = e4m3x4(dv.div(yv[0]), dv.div(yv[1]), dv.div(yv[2]), dv.div(yv[3]));
+    qo.y = e4m3x4(dv.div(yv[4]), dv.div(yv[5]), dv.div(yv[6]), dv.div(yv[7]));
+  } else {
+    uint32_t bq[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bq[e] = e4m3_nonfinite_scale(yv[e], sc);
+    qo.x = bq[0] | (bq[1] << 8) | (bq[2] << 16) | (bq[3] << 24);
+    qo.y = bq[4] | (bq[5] << 8) | (bq[6] << 16) | (bq[7] << 24);
+  }
+  *reinterpret_cast<uint2*>(oq + oi) = qo;
+  if (dl == 0) os[(int64_t)b * H + h] = sc;
+}
+
+}  // namespace tg
+
+using namespace tg;
+
+extern "C" int tg_decode_attention(const void* qkv, void* k_cache, void* v_cache, const int64_t* t,
+                                   uint8_t* o_q, float* o_s, void* o, int64_t B, int64_t H,
+                                   int64_t S, int64_t head_dim, float scale, void* stream) {
+  if (head_dim != kAttnDh) return einval("decode_attention: head_dim must be 128 (one scale block)");
+  if (B < 0 || H <= 0 || S <= 0) return einval("decode_attention: bad shape");
+  if (B == 0) return TG_OK;
+  if (B * H > 0x7FFFFFFF || S > 0x7FFFFFFF) return einval("decode_attention: shape too large");
+  if (!qkv || !k_cache || !v_cache || !t || !o_q || !o_s) return einval("decode_attention: null pointer");
+  if (!aligned(qkv, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(o_q, 8) ||
+      (o && !aligned(o, 16)))
+    return einval("decode_attention: qkv and caches must be 16-byte aligned, o_q 8-byte");
+  hipLaunchKernelGGL(decode_attention_kernel, dim3((unsigned)(B * H)), dim3(kAttnWaves * 64), 0,
+                     as_stream(stream), reinterpret_cast<const uint16_t*>(qkv),
+                     reinterpret_cast<uint16_t*>(k_cache), reinterpret_cast<uint16_t*>(v_cache), t,
+                     o_q, o_s, reinterpret_cast<uint16_t*>(o), (int)H, (int)S, scale);
+  return check_launch("decode_attention");
+}

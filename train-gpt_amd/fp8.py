@@ -418,6 +418,24 @@ class QuantizedWeight:
                             b_scale_bn=self.bn)
         return out.reshape(*lead, self.shape[1])
 
+    def matmul_prequant(self, x_q: torch.Tensor, x_s: torch.Tensor) -> torch.Tensor:
+        """Already-quantized rows (x_q (M, K) e4m3fn, x_s (M, K/128) f32, e.g. from
+        kernels.rms_norm_fp8) times the kept W -> bf16 (M, N): the decode GEMV for
+        at most 64 rows, the scaled GEMM above."""
+        M, K = x_q.shape
+        if K != self.shape[0]:
+            raise ValueError(f"contracted-dim mismatch: a K={K}, b K={self.shape[0]}")
+        xq = x_q.view(torch.uint8).contiguous()
+        xs = x_s.contiguous().float()
+        if 0 < M <= 64:
+            N = self.shape[1]
+            out = torch.empty((M, N), dtype=torch.bfloat16, device=x_q.device)
+            _L.check(_L.lib().tg_gemv_fp8(_L.ptr(xq), _L.ptr(xs), _L.ptr(self.q.view(torch.uint8)),
+                                          _L.ptr(self.scales), self.bn, _L.ptr(out), M, N, K,
+                                          self.block_k, _L.stream_of(xq)))
+            return out
+        return scaled_matmul(xq, xs, self.q.view(torch.uint8), self.scales, b_scale_bn=self.bn)
+
     def state_dict(self):
         return {"q": self.q, "scales": self.scales}
 
