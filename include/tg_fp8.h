@@ -38,6 +38,13 @@ const char* tg_last_error(void);
 int tg_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, int block_k,
                      uint8_t* q, float* scales, void* stream);
 
+/* _quantize_to_fp8 (fp8.py:39-47) of bf16(relu(x)^2) along the last axis: the
+ * MLP activation of model.py:72 (jax.nn.relu(x @ w_up) ** 2 on bf16, the
+ * square rounded once to bf16) fused with the quantization that feeds w_down.
+ * x: (rows, cols) bf16; q, scales as tg_quantize_rows.  relu keeps NaN. */
+int tg_quantize_rows_relu2(const void* x, int64_t rows, int64_t cols, int block_k, uint8_t* q,
+                           float* scales, void* stream);
+
 /* _quantize_to_fp8 of x.T (fp8.py:68 applies it to b.T): quantizes the columns
  * of x (rows, cols) bf16 and writes them transposed:
  * q_t: (cols, rows) e4m3fn; scales_t: (cols, rows/block_k) f32.  rows % block_k == 0;
@@ -128,6 +135,15 @@ int tg_rms_norm(const void* x, const void* scale, void* y, int64_t rows, int64_t
  * y (rows, dim) bf16, q (rows, dim) e4m3fn, s (rows, dim/block_k) f32. */
 int tg_rms_norm_fp8(const void* x, const void* scale, void* y, uint8_t* q, float* s,
                     int64_t rows, int64_t dim, float eps, int block_k, void* stream);
+
+/* The residual add of model.py:75-76 fused with the next norm -> FP8 quantize:
+ * x_out = bf16(x + delta) (the bf16 tensor add), then y = _rms_norm_pure(x_out,
+ * scale, eps) (kernels.py:30-33) and (q, s) = _quantize_to_fp8(f32(y))
+ * (fp8.py:39-47), exactly as tg_rms_norm_fp8 on x_out.  x_out may be x (in
+ * place); y may be NULL.  Shapes and alignment as tg_rms_norm_fp8. */
+int tg_add_rms_norm_fp8(const void* x, const void* delta, const void* scale, void* x_out, void* y,
+                        uint8_t* q, float* s, int64_t rows, int64_t dim, float eps, int block_k,
+                        void* stream);
 
 /* Device workspace (bytes) of tg_rms_norm_bwd. */
 size_t tg_rms_norm_bwd_workspace(int64_t rows, int64_t dim);

@@ -94,3 +94,37 @@ def test_rms_norm_errors(dev):
                              torch.ones(200, dtype=torch.bfloat16, device=dev), 1e-6)
     with pytest.raises(TypeError):
         kernels.rms_norm(x.float(), g, 1e-6)
+
+
+@pytest.mark.parametrize("shape", [(1, 2304), (8, 2048), (5, 768), (3, 16384)])
+@pytest.mark.parametrize("inplace", [False, True])
+def test_add_rms_norm_fp8_bit_exact(dev, shape, inplace):
+    """Residual add fused with norm -> FP8 (tg_add_rms_norm_fp8): x_out is the
+    bf16 tensor sum (f32 add, one RNE rounding), y / q / scales are the oracle's
+    rms_norm_fp8 of x_out, bit for bit."""
+    rng = np.random.default_rng(sum(shape) + inplace)
+    x, g = _inputs(rng, shape)
+    d = ob.randn_bf16(rng, shape, std=0.5)
+    xd = to_dev(x, dev)
+    xo, q, s, y = kernels.add_rms_norm_fp8(xd, to_dev(d, dev), to_dev(g, dev), 1e-5,
+                                            inplace=inplace, want_y=True)
+    xs = ob.f32_to_bf16(ob.bf16_to_f32(x) + ob.bf16_to_f32(d))
+    np.testing.assert_array_equal(bf16_bits(xo), xs)
+    if inplace:
+        assert xo.data_ptr() == xd.data_ptr()
+    y_o, q_o, s_o = norm_ref.rms_norm_fp8(xs, g, 1e-5)
+    np.testing.assert_array_equal(bf16_bits(y), y_o)
+    np.testing.assert_array_equal(u8(q).reshape(q_o.shape), q_o)
+    assert same_scales(s.cpu().numpy().reshape(s_o.shape), s_o)
+
+
+def test_add_rms_norm_fp8_without_y(dev):
+    rng = np.random.default_rng(11)
+    x, g = _inputs(rng, (4, 2304))
+    d = ob.randn_bf16(rng, (4, 2304))
+    xo, q, s, y = kernels.add_rms_norm_fp8(to_dev(x, dev), to_dev(d, dev), to_dev(g, dev), 1e-5)
+    assert y is None
+    xs = ob.f32_to_bf16(ob.bf16_to_f32(x) + ob.bf16_to_f32(d))
+    _, q_o, s_o = norm_ref.rms_norm_fp8(xs, g, 1e-5)
+    np.testing.assert_array_equal(u8(q), q_o)
+    assert same_scales(s.cpu().numpy(), s_o)

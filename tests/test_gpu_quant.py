@@ -161,3 +161,21 @@ def test_errors(dev):
     q, s = fp8.quantize_fp8(torch.zeros((0, 256), dtype=torch.bfloat16, device=dev))
     assert q.shape == (0, 256) and s.shape == (0, 2)
     assert bf16_bits is not None
+
+
+@pytest.mark.parametrize("shape", [(1, 9216), (8, 9216), (3, 256), (64, 1024)])
+def test_quantize_relu2_bit_exact(dev, shape):
+    """tg_quantize_rows_relu2: the oracle's _quantize_to_fp8 of bf16(relu(x)^2)
+    (model.py:72 on bf16 values: relu exact, the square rounded once)."""
+    import fp8
+    rng = np.random.default_rng(sum(shape))
+    x = ob.randn_bf16(rng, shape, std=3.0)
+    x[0, :3] = [0x7FC0, 0x8000, 0xFF80]        # NaN, -0, -inf
+    q, s = fp8.quantize_relu2(to_dev(x, dev))
+    xf = ob.bf16_to_f32(x)
+    with np.errstate(invalid="ignore"):
+        r = np.where(np.isnan(xf), xf, np.maximum(xf, np.float32(0)))
+    u = ob.round_bf16((r * r).astype(np.float32))
+    q_o, s_o = fp8_ref.quantize_fp8(u)
+    np.testing.assert_array_equal(u8(q), q_o)
+    assert same_scales(s.cpu().numpy(), s_o)

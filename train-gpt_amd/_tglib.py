@@ -44,6 +44,9 @@ SIGNATURES = {
     "tg_block_scaled_matmul_bwd_bf16_workspace": (_sz, [_i64, _i64, _i64]),
     "tg_block_scaled_matmul_bwd_bf16": (_int, [_vp, _int, _vp, _int, _vp, _int, _vp, _vp, _i64,
                                                _i64, _i64, _vp, _sz, _vp]),
+    "tg_quantize_rows_relu2": (_int, [_vp, _i64, _i64, _int, _vp, _vp, _vp]),
+    "tg_add_rms_norm_fp8": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float,
+                                   _int, _vp]),
     "tg_decode_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                    ctypes.c_float, _vp]),
     "tg_selftest_fp8_cvt": (_int, [_vp, _vp]),

@@ -79,7 +79,9 @@ __device__ __forceinline__ uint32_t absmax8(const float (&v)[8]) {
   return m;
 }
 
-template <bool F32_IN, int UNROLL>
+// RELU2: the values quantized are bf16(relu(x)^2) (model.py:72's activation
+// as bf16 tensor ops: relu exact, the square rounded once), for bf16 x.
+template <bool F32_IN, int UNROLL, bool RELU2 = false>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const void* __restrict__ x,
                                                          uint2* __restrict__ q,
                                                          float* __restrict__ s,
@@ -90,6 +92,17 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const void* __restrict_
   for (int u = 0; u < UNROLL; ++u) {
     int64_t c = base + u * 256;
     load_chunk<F32_IN>(x, c, c < nchunks, v[u]);
+    if (RELU2) {
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        // IEEE maximum keeps NaN (jnp.maximum / torch relu propagate it)
+        const float a = __builtin_elementwise_maximum(v[u][i], 0.0f);
+        const float b = __builtin_elementwise_maximum(v[u][i + 1], 0.0f);
+        const uint32_t w = pack_bf16x2(a * a, b * b);
+        v[u][i] = bf16lo(w);
+        v[u][i + 1] = bf16hi(w);
+      }
+    }
   }
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
@@ -116,6 +129,17 @@ int launch_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, ui
     hipLaunchKernelGGL((quant_rows_kernel<false, UNROLL>), dim3((unsigned)grid), dim3(256), 0, st,
                        x, reinterpret_cast<uint2*>(q), s, nchunks);
   return check_launch("quant_rows");
+}
+
+int launch_quant_rows_relu2(const void* x, int64_t rows, int64_t cols, uint8_t* q, float* s,
+                            hipStream_t st) {
+  const int64_t nchunks = rows * cols / 8;
+  if (nchunks == 0) return TG_OK;
+  constexpr int UNROLL = 4;
+  const int64_t grid = (nchunks + 256 * UNROLL - 1) / (256 * UNROLL);
+  hipLaunchKernelGGL((quant_rows_kernel<false, UNROLL, true>), dim3((unsigned)grid), dim3(256), 0,
+                     st, x, reinterpret_cast<uint2*>(q), s, nchunks);
+  return check_launch("quant_rows_relu2");
 }
 
 // ---------------------------------------------------------------------------
@@ -472,6 +496,17 @@ extern "C" int tg_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_
   if (!aligned(x, 16) || !aligned(q, 8) || !aligned(scales, 4))
     return einval("quantize_rows: x must be 16-byte and q 8-byte aligned");
   return launch_quant_rows(x, x_dtype, rows, cols, q, scales, as_stream(stream));
+}
+
+extern "C" int tg_quantize_rows_relu2(const void* x, int64_t rows, int64_t cols, int block_k,
+                                      uint8_t* q, float* scales, void* stream) {
+  if (block_k != 128) return einval("quantize_rows_relu2: block_k must be 128");
+  if (rows < 0 || cols < 0) return einval("quantize_rows_relu2: bad shape");
+  if (cols % block_k) return einval("quantize_rows_relu2: cols not divisible by block_k");
+  if (rows == 0 || cols == 0) return TG_OK;
+  if (!x || !q || !scales) return einval("quantize_rows_relu2: null pointer");
+  if (!aligned(x, 16) || !aligned(q, 8)) return einval("quantize_rows_relu2: x must be 16-byte and q 8-byte aligned");
+  return launch_quant_rows_relu2(x, rows, cols, q, scales, as_stream(stream));
 }
 
 extern "C" int tg_quantize_cols(const void* x, int x_dtype, int64_t rows, int64_t cols,

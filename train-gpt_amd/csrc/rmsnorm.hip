@@ -29,13 +29,18 @@ __device__ __forceinline__ float amax3(float a, float b, float c) {
 // no per-chunk guards are emitted.  Each wave walks rows with a stride of the
 // grid's wave count and prefetches the next row's x while it computes the
 // current one.
-template <int J, bool QUANT, bool FULL>
+// ADD: the input row is the residual sum x + delta, rounded to bf16 (a bf16
+// tensor add) and written to xout (which may be x itself) before the norm.
+// y may be null when only the FP8 rows are wanted.
+template <int J, bool QUANT, bool FULL, bool ADD = false>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint4* __restrict__ x,
                                                       const uint4* __restrict__ gamma,
                                                       uint4* __restrict__ y,
                                                       uint2* __restrict__ q,
                                                       float* __restrict__ s, int64_t rows,
-                                                      int nch, float dimf, float eps) {
+                                                      int nch, float dimf, float eps,
+                                                      const uint4* __restrict__ delta = nullptr,
+                                                      uint4* xout = nullptr) {
   const int lane = threadIdx.x & 63;
   const int64_t wave0 = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int64_t wstride = (int64_t)gridDim.x * 4;
@@ -49,8 +54,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint4* __restrict__ 
     g[j][4] = bf16lo(w.z); g[j][5] = bf16hi(w.z); g[j][6] = bf16lo(w.w); g[j][7] = bf16hi(w.w);
   }
 
-  auto load_row = [&](int64_t row, uint4 (&xv)[J]) {
-    const uint4* xr = x + row * nch;
+  auto load_row = [&](const uint4* src, int64_t row, uint4 (&xv)[J]) {
+    const uint4* xr = src + row * nch;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const int c = lane + 64 * j;
@@ -58,8 +63,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint4* __restrict__ 
     }
   };
 
-  uint4 nxt[J];
-  if (wave0 < rows) load_row(wave0, nxt);
+  uint4 nxt[J], nd[J];
+  if (wave0 < rows) {
+    load_row(x, wave0, nxt);
+    if (ADD) load_row(delta, wave0, nd);
+  }
   for (int64_t row = wave0; row < rows; row += wstride) {
     float xf[J][8];
 #pragma unroll
@@ -69,7 +77,26 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint4* __restrict__ 
       xf[j][4] = bf16lo(nxt[j].z); xf[j][5] = bf16hi(nxt[j].z);
       xf[j][6] = bf16lo(nxt[j].w); xf[j][7] = bf16hi(nxt[j].w);
     }
-    if (row + wstride < rows) load_row(row + wstride, nxt);   // prefetch the next row
+    if (ADD) {
+      // residual sum in bf16: each sum rounded once (RNE), stored, then normed
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const uint32_t dw[4] = {nd[j].x, nd[j].y, nd[j].z, nd[j].w};
+        uint32_t sw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sw[e] = pack_bf16x2(xf[j][2 * e] + bf16lo(dw[e]), xf[j][2 * e + 1] + bf16hi(dw[e]));
+          xf[j][2 * e] = bf16lo(sw[e]);
+          xf[j][2 * e + 1] = bf16hi(sw[e]);
+        }
+        const int c = lane + 64 * j;
+        if (FULL || c < nch) xout[row * nch + c] = make_uint4(sw[0], sw[1], sw[2], sw[3]);
+      }
+    }
+    if (row + wstride < rows) {                                // prefetch the next row
+      load_row(x, row + wstride, nxt);
+      if (ADD) load_row(delta, row + wstride, nd);
+    }
 
     double acc = 0.0;
 #pragma unroll
@@ -95,7 +122,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint4* __restrict__ 
         yv[2 * e] = bf16lo(yp);
         yv[2 * e + 1] = bf16hi(yp);
       }
-      if (FULL || c < nch) stg_stream(&y[row * nch + c], o);
+      if ((FULL || c < nch) && y) stg_stream(&y[row * nch + c], o);
       if (QUANT) {
         const float m = amax3(amax3(yv[0], yv[1], yv[2]), amax3(yv[3], yv[4], yv[5]),
                               __builtin_elementwise_maximum(__builtin_fabsf(yv[6]), __builtin_fabsf(yv[7])));
@@ -123,9 +150,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint4* __restrict__ 
   }
 }
 
-template <bool QUANT>
+template <bool QUANT, bool ADD = false>
 static int launch_rmsnorm(const void* x, const void* gamma, void* y, uint8_t* q, float* s,
-                          int64_t rows, int64_t dim, float eps, hipStream_t st) {
+                          int64_t rows, int64_t dim, float eps, hipStream_t st,
+                          const void* delta = nullptr, void* xout = nullptr) {
   const int nch = (int)(dim / 8);
   const int jneed = (nch + 63) / 64;
 #ifndef TG_NORM_ROWS_PER_WAVE
@@ -143,14 +171,16 @@ static int launch_rmsnorm(const void* x, const void* gamma, void* y, uint8_t* q,
   auto Y = reinterpret_cast<uint4*>(y);
   auto Q = reinterpret_cast<uint2*>(q);
   const float dimf = (float)dim;
+  auto D = reinterpret_cast<const uint4*>(delta);
+  auto XO = reinterpret_cast<uint4*>(xout);
 #define TG_NORM_CASE(JJ)                                                                        \
   if (jneed <= JJ) {                                                                             \
     if (nch == JJ * 64)                                                                          \
-      hipLaunchKernelGGL((rmsnorm_kernel<JJ, QUANT, true>), gdim, b, 0, st, X, G, Y, Q, s, rows, \
-                         nch, dimf, eps);                                                        \
+      hipLaunchKernelGGL((rmsnorm_kernel<JJ, QUANT, true, ADD>), gdim, b, 0, st, X, G, Y, Q, s,  \
+                         rows, nch, dimf, eps, D, XO);                                           \
     else                                                                                         \
-      hipLaunchKernelGGL((rmsnorm_kernel<JJ, QUANT, false>), gdim, b, 0, st, X, G, Y, Q, s,      \
-                         rows, nch, dimf, eps);                                                  \
+      hipLaunchKernelGGL((rmsnorm_kernel<JJ, QUANT, false, ADD>), gdim, b, 0, st, X, G, Y, Q, s, \
+                         rows, nch, dimf, eps, D, XO);                                           \
     return check_launch("rmsnorm");                                                              \
   }
   TG_NORM_CASE(1)
@@ -401,6 +431,20 @@ extern "C" int tg_rms_norm_fp8(const void* x, const void* scale, void* y, uint8_
   if (!aligned(x, 16) || !aligned(scale, 16) || !aligned(y, 16) || !aligned(q, 8))
     return einval("rms_norm_fp8: x, scale, y must be 16-byte and q 8-byte aligned");
   return launch_rmsnorm<true>(x, scale, y, q, s, rows, dim, eps, as_stream(stream));
+}
+
+extern "C" int tg_add_rms_norm_fp8(const void* x, const void* delta, const void* scale,
+                                   void* x_out, void* y, uint8_t* q, float* s, int64_t rows,
+                                   int64_t dim, float eps, int block_k, void* stream) {
+  if (block_k != 128) return einval("add_rms_norm_fp8: block_k must be 128");
+  if (rows < 0 || dim <= 0) return einval("add_rms_norm_fp8: bad shape");
+  if (dim % block_k) return einval("add_rms_norm_fp8: dim not divisible by block_k");
+  if (rows == 0) return TG_OK;
+  if (!x || !delta || !scale || !x_out || !q || !s) return einval("add_rms_norm_fp8: null pointer");
+  if (!aligned(x, 16) || !aligned(delta, 16) || !aligned(scale, 16) || !aligned(x_out, 16) ||
+      (y && !aligned(y, 16)) || !aligned(q, 8))
+    return einval("add_rms_norm_fp8: x, delta, scale, x_out, y must be 16-byte and q 8-byte aligned");
+  return launch_rmsnorm<true, true>(x, scale, y, q, s, rows, dim, eps, as_stream(stream), delta, x_out);
 }
 
 extern "C" size_t tg_rms_norm_bwd_workspace(int64_t rows, int64_t dim) {

@@ -32,6 +32,8 @@ inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintp
 // Kernel launchers shared between translation units.
 int launch_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, uint8_t* q,
                       float* s, hipStream_t st);
+int launch_quant_rows_relu2(const void* x, int64_t rows, int64_t cols, uint8_t* q, float* s,
+                            hipStream_t st);
 int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, float* s_t,
                       hipStream_t st);
 int launch_quant_dual(const void* x, int64_t rows, int64_t cols, uint8_t* q, float* s, uint8_t* q_t,

@@ -7,13 +7,14 @@ step over one row per sequence:
 
     x   = embed[tok] + pos[t]                                 model.py:83
     per layer (model.py:74-77):
-      h, h_q, h_s = rms_norm_fp8(x, norm1)                    fused norm -> FP8 rows
+      h_q, h_s    = rms_norm_fp8(x, norm1) (for layers > 0 fused with the
+                    residual add of the previous layer's MLP)
       q | k | v   = one decode GEMV on the kept [wq|wk|wv]    model.py:59-65
       K[:, t], V[:, t] = k, v ; o = attention(q, K[:t+1], V[:t+1]) -> FP8 rows
                     (one HIP kernel, tg_decode_attention)     model.py:67
-      x = x + GEMV(o, wo)                                     model.py:68, 75
-      h2, h2_q, h2_s = rms_norm_fp8(x, norm2)
-      x = x + GEMV(relu(GEMV(h2, w_up))^2, w_down)            model.py:71-72, 76
+      x = x + GEMV(o, wo); h2_q, h2_s = rms_norm_fp8(x, norm2)    (one kernel)  model.py:68, 75
+      u_q, u_s = quantize(relu(GEMV(h2, w_up))^2)                (one kernel)  model.py:71-72
+      x = x + GEMV(u, w_down)                                                 model.py:76
     logits = cap * tanh(GEMV(rms_norm_fp8(x, final_norm), unembed) / cap)   model.py:93-97
 
 Every linear runs on a weight quantized once (fp8.QuantizedWeight): the decode
@@ -247,18 +248,23 @@ class FP8Decoder:
         cfg = self.cfg
         H = cfg.n_heads
         x = self.embed[tok] + self.pos.index_select(0, t)                 # (B, d)
+        _, h_q, h_s = kernels.rms_norm_fp8(x, self.layers[0]["norm1"], cfg.rms_eps)
         for li, lp in enumerate(self.layers):
-            _, h_q, h_s = kernels.rms_norm_fp8(x, lp["norm1"], cfg.rms_eps)
             qkv = lp["wqkv"].matmul_prequant(h_q, h_s)                      # (B, 3 H Dh)
             if self.decode_attn == "hip":
                 o_q, o_s, _ = decode_attention(qkv, self.k_cache[li], self.v_cache[li], t, H)
-                x = x + lp["wo"].matmul_prequant(o_q, o_s)                  # model.py:68, 75
+                a = lp["wo"].matmul_prequant(o_q, o_s)                      # model.py:68
             else:
-                x = x + lp["wo"].matmul(self._sdpa_step(li, qkv, int(t.item())))
-            _, h2_q, h2_s = kernels.rms_norm_fp8(x, lp["norm2"], cfg.rms_eps)
-            u = F.relu(lp["w_up"].matmul_prequant(h2_q, h2_s)).square()     # model.py:72
-            x = x + lp["w_down"].matmul(u)                                  # model.py:76
-        return self._head(x)
+                a = lp["wo"].matmul(self._sdpa_step(li, qkv, int(t.item())))
+            # x = x + a (model.py:75) fused with norm2 -> FP8 rows
+            x, h2_q, h2_s, _ = kernels.add_rms_norm_fp8(x, a, lp["norm2"], cfg.rms_eps, inplace=True)
+            u_q, u_s = fp8.quantize_relu2(lp["w_up"].matmul_prequant(h2_q, h2_s))   # model.py:72
+            m = lp["w_down"].matmul_prequant(u_q, u_s)
+            # x = x + m (model.py:76) fused with the next norm (norm1 or final_norm)
+            nxt = self.layers[li + 1]["norm1"] if li + 1 < len(self.layers) else self.final_norm
+            x, h_q, h_s, _ = kernels.add_rms_norm_fp8(x, m, nxt, cfg.rms_eps, inplace=True)
+        logits = self.unembed.matmul_prequant(h_q, h_s).float()            # model.py:96
+        return cfg.logit_cap * torch.tanh(logits / cfg.logit_cap)           # model.py:97
 
     def _sdpa_step(self, li: int, qkv: torch.Tensor, t: int) -> torch.Tensor:
         """decode_attn="sdpa": append k, v at t, torch attention over 0 .. t."""

@@ -89,6 +89,25 @@ def quantize_fp8(x: torch.Tensor, block_k: int = DEFAULT_BLOCK_K, transpose: boo
     return q.view(torch.float8_e4m3fn).reshape(*lead, K), s.reshape(*lead, K // block_k)
 
 
+def quantize_relu2(x: torch.Tensor, block_k: int = DEFAULT_BLOCK_K):
+    """_quantize_to_fp8 of bf16(relu(x)^2) along the last axis (model.py:72's
+    activation fused with the quantization feeding the next matmul); x bf16."""
+    _L.require_gpu(x)
+    _check_block_k(block_k)
+    if x.dtype != torch.bfloat16:
+        raise TypeError("quantize_relu2: x must be bfloat16")
+    K = x.shape[-1]
+    if K % block_k:
+        raise ValueError(f"K={K} not divisible by block_k={block_k}")
+    x2 = x.reshape(-1, K).contiguous()
+    R = x2.shape[0]
+    q = torch.empty((R, K), dtype=torch.uint8, device=x.device)
+    s = torch.empty((R, K // block_k), dtype=torch.float32, device=x.device)
+    _L.check(_L.lib().tg_quantize_rows_relu2(_L.ptr(x2), R, K, block_k, _L.ptr(q), _L.ptr(s),
+                                             _L.stream_of(x2)))
+    return q.view(torch.float8_e4m3fn).reshape(x.shape), s.reshape(*x.shape[:-1], K // block_k)
+
+
 def _validate(a: torch.Tensor, b: torch.Tensor, block_k: int):
     *leading, K = a.shape
     K_b, N = b.shape

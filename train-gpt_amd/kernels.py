@@ -54,6 +54,33 @@ def rms_norm_fp8(x: torch.Tensor, scale: torch.Tensor, eps: float, block_k: int 
     return _RMSNormFP8.apply(x, scale, eps, block_k)
 
 
+def add_rms_norm_fp8(x: torch.Tensor, delta: torch.Tensor, scale: torch.Tensor, eps: float,
+                     block_k: int = 128, inplace: bool = False, want_y: bool = False):
+    """Residual add fused with the next norm -> FP8 quantize (model.py:75-76 then
+    74/76's norm): x_out = bf16(x + delta), y = rms_norm(x_out), (y_f8, y_s) =
+    _quantize_to_fp8(y).  Returns (x_out, y_f8, y_s, y or None); with
+    inplace=True x_out is x itself.  Inference only (no autograd)."""
+    x2, g, D = _prep(x, scale)
+    if D % block_k:
+        raise ValueError(f"K={D} not divisible by block_k={block_k}")
+    if delta.shape != x.shape or delta.dtype != torch.bfloat16:
+        raise ValueError("add_rms_norm_fp8: delta must be bf16 with x's shape")
+    if inplace and not x.is_contiguous():
+        raise ValueError("add_rms_norm_fp8: inplace needs a contiguous x")
+    d2 = delta.reshape(-1, D).contiguous()
+    R = x2.shape[0]
+    xo = x2 if inplace else torch.empty_like(x2)
+    y = torch.empty_like(x2) if want_y else None
+    q = torch.empty((R, D), dtype=torch.uint8, device=x.device)
+    s = torch.empty((R, D // block_k), dtype=torch.float32, device=x.device)
+    _L.check(_L.lib().tg_add_rms_norm_fp8(_L.ptr(x2), _L.ptr(d2), _L.ptr(g), _L.ptr(xo),
+                                          _L.ptr(y) if y is not None else None, _L.ptr(q), _L.ptr(s),
+                                          R, D, float(eps), block_k, _L.stream_of(x2)))
+    lead = x.shape[:-1]
+    return (xo.reshape(x.shape), q.view(torch.float8_e4m3fn).reshape(x.shape),
+            s.reshape(*lead, D // block_k), y.reshape(x.shape) if y is not None else None)
+
+
 def _rms_norm_fp8_fwd(x: torch.Tensor, scale: torch.Tensor, eps: float, block_k: int):
     x2, g, D = _prep(x, scale)
     if D % block_k:
