@@ -33,7 +33,7 @@ decode       = KV-cached decode (decode.py) of the reference model config:
 cpu_baseline = the CPU oracle (numpy + C) on a row sample of the same step
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                      [--only norm_quant|norm_bwd|gemv|bwd_bf16|block_step|decode]
+                      [--only step|norm_quant|norm_bwd|gemv|bwd_bf16|block_step|decode]
 """
 import argparse
 import json
@@ -79,8 +79,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--norm-iters", type=int, default=200)
-    p.add_argument("--only", choices=["norm_quant", "norm_bwd", "gemv", "bwd_bf16", "block_step",
-                                      "decode"],
+    p.add_argument("--only", choices=["step", "norm_quant", "norm_bwd", "gemv", "bwd_bf16",
+                                      "block_step", "decode"],
                    help="run one secondary workload alone and print its JSON object")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (calibrates the FETCH_SIZE / "
@@ -458,7 +458,7 @@ def main():
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
-    if args.only:
+    if args.only and args.only != "step":
         fn = {"norm_quant": bench_norm, "norm_bwd": bench_norm_bwd, "gemv": bench_gemv,
               "bwd_bf16": lambda d, _: bench_bwd_bf16(d, 10),
               "block_step": lambda d, _: bench_block(d),
@@ -484,12 +484,15 @@ def main():
     gemm_ms = sum(s.elapsed_time(e) for s, e in ev) / len(ev)
     gemm_tflops = GEMM_FLOP / (gemm_ms * 1e-3) / 1e12
     value = STEP_FLOP / (ms_step * 1e-3) / 1e12
-    norm = bench_norm(dev, args.norm_iters)
-    norm_bwd = bench_norm_bwd(dev, args.norm_iters)
-    gemv = bench_gemv(dev, args.norm_iters)
-    bwd_bf16 = bench_bwd_bf16(dev, 10)
-    block_step = bench_block(dev)
-    dec = bench_decode(dev)
+    if args.only == "step":
+        norm = norm_bwd = gemv = bwd_bf16 = block_step = dec = None
+    else:
+        norm = bench_norm(dev, args.norm_iters)
+        norm_bwd = bench_norm_bwd(dev, args.norm_iters)
+        gemv = bench_gemv(dev, args.norm_iters)
+        bwd_bf16 = bench_bwd_bf16(dev, 10)
+        block_step = bench_block(dev)
+        dec = bench_decode(dev)
     out = {
         "metric": "FP8 block-scaled GEMM TFLOP/s (% fp8 MFMA peak); RMSNorm+quant HBM GB/s",
         "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -510,6 +513,9 @@ def main():
         "block_step": block_step,
         "decode": dec,
     }
+    if args.only == "step":                      # the headline step alone (no secondary workloads)
+        out = {k: out[k] for k in ("metric", "value", "unit", "ms_per_step", "gemm_us_per_launch",
+                                   "roofline")}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))
