@@ -27,13 +27,17 @@ bwd_bf16     = the reference's straight-through bf16 backward (fp8.py:85-98)
                2.5 PFLOP/s dense bf16 MFMA peak
 block_step   = config 4: one decoder block training step (block.py), FP8 linears
                vs bf16 linears, wall time per step
+xent         = config 4's head: fused logit cap + cross entropy (losses.py) on
+               bf16 logits [8192, 50304]; forward reads the logits once
+               (+ targets, per-row loss / lse), backward reads them again and
+               writes bf16 dlogits; bytes / mean launch time vs 8 TB/s
 decode       = KV-cached decode (decode.py) of the reference model config:
                ms per decode step at batch 1 and 8, and the kept FP8 weights +
                KV cache read per step against 8 TB/s
 cpu_baseline = the CPU oracle (numpy + C) on a row sample of the same step
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                      [--only step|norm_quant|norm_bwd|gemv|bwd_bf16|block_step|decode]
+                      [--only step|norm_quant|norm_bwd|gemv|bwd_bf16|block_step|xent|decode]
 """
 import argparse
 import json
@@ -80,7 +84,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--norm-iters", type=int, default=200)
     p.add_argument("--only", choices=["step", "norm_quant", "norm_bwd", "gemv", "bwd_bf16",
-                                      "block_step", "decode"],
+                                      "block_step", "xent", "decode"],
                    help="run one secondary workload alone and print its JSON object")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (calibrates the FETCH_SIZE / "
@@ -353,6 +357,42 @@ def bench_block(dev, steps=5, warm=3):
     return out
 
 
+def bench_xent(dev, iters):
+    """Config 4's head: tg_logit_cap_xent_fwd / _bwd on bf16 logits [8192, 50304]
+    (824 MB, larger than the Infinity Cache, so one buffer set)."""
+    import torch
+    import _tglib as L
+    lib = L.lib()
+    R, V, cap = 4 * 2048, 50304, 15.0
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    logits = (torch.randn((R, V), generator=g, device=dev) * 3).to(torch.bfloat16)
+    tgt = torch.randint(0, V, (R,), generator=g, device=dev)
+    loss = torch.empty(R, dtype=torch.float32, device=dev)
+    lse = torch.empty(R, dtype=torch.float32, device=dev)
+    one = torch.ones(1, dtype=torch.float32, device=dev)
+    dl = torch.empty_like(logits)
+    st = L.stream_of(logits)
+
+    def fwd(i):
+        L.check(lib.tg_logit_cap_xent_fwd(L.ptr(logits), L.ptr(tgt), R, V, cap, L.ptr(loss), L.ptr(lse), st))
+
+    def bwd(i):
+        L.check(lib.tg_logit_cap_xent_bwd(L.ptr(logits), L.ptr(tgt), L.ptr(lse), L.ptr(one), 1.0 / R,
+                                          None, R, V, cap, L.ptr(dl), st))
+    n = max(iters // 10, 5)
+    out = {"workload": "C4 head: logit cap 15 + cross entropy, bf16 logits [8192, 50304], f32 loss, "
+                       "bf16 dlogits"}
+    for name, fn, byts in (("fwd", fwd, R * V * 2 + R * 16), ("bwd", bwd, 2 * R * V * 2 + R * 12)):
+        us = _mean_launch_us(fn, n, warm=2)
+        gbps = byts / (us * 1e-6) / 1e9
+        out[name] = {"us_per_launch": round(us, 2), "bytes_per_launch": byts,
+                     "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                                  "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                                  "traffic": measured_traffic().get("xent_" + name)}}
+    return out
+
+
 def decode_weight_bytes(cfg):
     """HBM bytes of the kept FP8 weights one decode step reads: e4m3 bytes plus
     128x128 fp32 scales of the six linears per layer and of the unembedding."""
@@ -461,7 +501,7 @@ def main():
     if args.only and args.only != "step":
         fn = {"norm_quant": bench_norm, "norm_bwd": bench_norm_bwd, "gemv": bench_gemv,
               "bwd_bf16": lambda d, _: bench_bwd_bf16(d, 10),
-              "block_step": lambda d, _: bench_block(d),
+              "block_step": lambda d, _: bench_block(d), "xent": bench_xent,
               "decode": lambda d, _: bench_decode(d)}[args.only]
         print(json.dumps({args.only: fn(dev, args.norm_iters)}))
         return
@@ -485,13 +525,14 @@ def main():
     gemm_tflops = GEMM_FLOP / (gemm_ms * 1e-3) / 1e12
     value = STEP_FLOP / (ms_step * 1e-3) / 1e12
     if args.only == "step":
-        norm = norm_bwd = gemv = bwd_bf16 = block_step = dec = None
+        norm = norm_bwd = gemv = bwd_bf16 = block_step = xent = dec = None
     else:
         norm = bench_norm(dev, args.norm_iters)
         norm_bwd = bench_norm_bwd(dev, args.norm_iters)
         gemv = bench_gemv(dev, args.norm_iters)
         bwd_bf16 = bench_bwd_bf16(dev, 10)
         block_step = bench_block(dev)
+        xent = bench_xent(dev, args.norm_iters)
         dec = bench_decode(dev)
     out = {
         "metric": "FP8 block-scaled GEMM TFLOP/s (% fp8 MFMA peak); RMSNorm+quant HBM GB/s",
@@ -511,6 +552,7 @@ def main():
         "gemv": gemv,
         "bwd_bf16": bwd_bf16,
         "block_step": block_step,
+        "xent": xent,
         "decode": dec,
     }
     if args.only == "step":                      # the headline step alone (no secondary workloads)

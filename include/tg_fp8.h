@@ -206,6 +206,28 @@ int tg_decode_attention(const void* qkv, void* k_cache, void* v_cache, const int
                         uint8_t* o_q, float* o_s, void* o, int64_t B, int64_t H, int64_t S,
                         int64_t head_dim, float scale, void* stream);
 
+/* Logit cap + cross entropy, forward: for each row r of the bf16 logits
+ * (rows, vocab) and target t = targets[r],
+ *   z = cap * tanh(l / cap)   (f32; model.py:96-97 with config.logit_cap)
+ *   row_lse[r]  = log sum_v exp(z_v)
+ *   row_loss[r] = row_lse[r] - z_t      (losses.py:8-12 before the mean)
+ * Replaces the f32 cast, tanh, log_softmax and take_along_axis passes of
+ * losses.py:8-12 over the model output.  A target outside [0, vocab) gives
+ * a NaN row loss.  row_loss, row_lse: (rows,) f32. */
+int tg_logit_cap_xent_fwd(const void* logits, const int64_t* targets, int64_t rows, int64_t vocab,
+                          float cap, float* row_loss, float* row_lse, void* stream);
+
+/* Logit cap + cross entropy, backward (the autodiff of losses.py:8-12, or of
+ * the masked mean of losses.py:15-34, through model.py:97): with
+ * g_r = *g * g_scale * row_weight[r] (g in device memory, so the upstream
+ * gradient needs no host read; row_weight NULL means 1; g_scale = 1 / rows
+ * for the mean; row_weight = mask / max(sum mask, 1) for the masked mean),
+ *   dlogits = bf16(g_r * (exp(z - row_lse) - onehot(t)) * (1 - (z / cap)^2))
+ * dlogits: (rows, vocab) bf16; it may not alias logits. */
+int tg_logit_cap_xent_bwd(const void* logits, const int64_t* targets, const float* row_lse,
+                          const float* g, float g_scale, const float* row_weight, int64_t rows,
+                          int64_t vocab, float cap, void* dlogits, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,7 +14,9 @@ rather than model.py:71-72's squared ReLU, a one-line swap (MLP_ACT).  The
 rest follows model.py: learned positional embedding (model.py:83), logit cap
 15 tanh (model.py:97, config.py:24), rms eps 1e-5 (config.py:17), untied
 unembedding kept in bf16 as bench_fp8_norm.py:117-118 does -- here on the
-bf16 MFMA GEMM (fp8.bf16_matmul).
+bf16 MFMA GEMM (fp8.bf16_matmul) -- and the cap fused with the loss
+(losses.capped_cross_entropy: f32 cap of the bf16 logits, one HIP kernel
+forward and one backward).
 
 Attention is not on the hot path (it stays bf16 in the reference too): it is
 torch's scaled_dot_product_attention restricted to its flash / memory-
@@ -34,6 +36,7 @@ import torch.nn.functional as F
 
 import fp8
 import kernels
+import losses
 
 
 @dataclass(frozen=True)
@@ -126,11 +129,10 @@ def loss(params, ids, tgt, cfg: BlockConfig, impl: str = "fp8"):
     # MLP half (model.py:71-72, 76)
     h2 = kernels.rms_norm(x, p["norm2"], cfg.rms_eps)
     x = x + mm(_act(mm(h2, p["w_up"])), p["w_down"])
-    # head (model.py:93-97), logits in bf16 on the bf16 GEMM
+    # head (model.py:93-97), logits in bf16 on the bf16 GEMM; the cap and the
+    # loss (losses.py:8-12) are one fused HIP pass each way
     xf = kernels.rms_norm(x, p["final_norm"], cfg.rms_eps)
-    logits = fp8.bf16_matmul(xf, p["unembed"]).float()
-    logits = cfg.logit_cap * torch.tanh(logits / cfg.logit_cap)
-    return F.cross_entropy(logits.reshape(B * T, -1), tgt.reshape(-1))
+    return losses.capped_cross_entropy(fp8.bf16_matmul(xf, p["unembed"]), tgt, cfg.logit_cap)
 
 
 def _norm_f32(x, w, eps):
