@@ -3,9 +3,11 @@
 
 Step (timed): config 3 of the baseline -- block_scaled_matmul forward + FP8
 backward on x [8192, 2048], W [2048, 8192], dY [8192, 8192] (bf16, synthetic,
-seeded), i.e. quantize x / W.T -> GEMM Y; quantize dY along N and dY.T along M
-(one read of dY), W along N -> GEMM dX; quantize X.T along M -> GEMM dW.  Every kernel is a C-ABI call into
-libtg_fp8.so on torch's current stream; the step allocates nothing.
+seeded), the kernel sequence of fp8.block_scaled_matmul's autograd path:
+quantize x along K and x.T along M (one read of x), W.T along K and W along N
+(one read of W) -> GEMM Y; quantize dY along N and dY.T along M (one read of
+dY) -> GEMM dX, GEMM dW.  Every kernel is a C-ABI call into libtg_fp8.so on
+torch's current stream; the step allocates nothing.
 
 value        = 3 * 2*8192*2048*8192 FLOP / step time (TFLOP/s, quantization included)
 roofline     = the GEMM kernel: 2*M*N*K FLOP per launch / its mean launch time
@@ -145,19 +147,19 @@ class Step:
 
     def run(self, ev=None):
         L, lib, st, p = self.L, self.lib, self.stream, self.L.ptr
-        bf = L.TG_DTYPE_BF16
-        # forward (fp8.py:66,68,70-78)
-        L.check(lib.tg_quantize_rows(p(self.x), bf, M3, K3, 128, p(self.qx), p(self.sx), st))
-        L.check(lib.tg_quantize_cols(p(self.w), bf, K3, N3, 128, p(self.qwt), p(self.swt), st))
+        # forward (fp8.py:66,68,70-78); x.T along M and W along N are the
+        # backward's operands, kept from the same reads
+        L.check(lib.tg_quantize_dual(p(self.x), M3, K3, 128, p(self.qx), p(self.sx), p(self.qxt),
+                                     p(self.sxt), st))
+        L.check(lib.tg_quantize_dual(p(self.w), K3, N3, 128, p(self.qw), p(self.sw), p(self.qwt),
+                                     p(self.swt), st))
         self._gemm(self.qx, self.sx, self.qwt, self.swt, self.y, M3, N3, K3, ev)
         # dY along N (for dX) and dY.T along M (for dW) from one read of dY
         L.check(lib.tg_quantize_dual(p(self.dy), M3, N3, 128, p(self.qdy), p(self.sdy), p(self.qdyt),
                                      p(self.sdyt), st))
         # dX = dY . W.T
-        L.check(lib.tg_quantize_rows(p(self.w), bf, K3, N3, 128, p(self.qw), p(self.sw), st))
         self._gemm(self.qdy, self.sdy, self.qw, self.sw, self.dx, M3, K3, N3, ev)
         # dW = X.T . dY
-        L.check(lib.tg_quantize_cols(p(self.x), bf, M3, K3, 128, p(self.qxt), p(self.sxt), st))
         self._gemm(self.qxt, self.sxt, self.qdyt, self.sdyt, self.dw, K3, N3, M3, ev)
 
 

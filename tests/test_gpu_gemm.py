@@ -172,3 +172,44 @@ def test_gemm_c3_full_size_sampled(dev):
     qgt, sgt = fp8_ref.quantize_fp8(np.ascontiguousarray(g32[:, cols].T))
     dw_ref = fp8_ref.dequant_gemm_nt(qat, sat, qgt, sgt)
     assert maxabs_rel(b.grad[:, torch.from_numpy(cols).to(dev)], dw_ref) <= TOL
+
+
+@pytest.mark.parametrize("need", ["both", "a", "b"])
+@pytest.mark.parametrize("shape", [(2, 128, 256, 384), (1, 1024, 640, 512)])
+def test_fp8_backward_kept_residuals_same_bits(dev, need, shape):
+    """The autograd path keeps FP8 forms of a.T and b from the forward; its
+    output and gradients equal _fp8_forward / _fp8_backward on the bf16
+    operands bit for bit, whichever operands need a gradient."""
+    B, T, K, N = shape
+    rng = np.random.default_rng(B + T + K + N)
+    a_u = ob.randn_bf16(rng, (B, T, K))
+    b_u = ob.randn_bf16(rng, (K, N), std=0.02)
+    g = to_dev(ob.randn_bf16(rng, (B, T, N), std=1e-3), dev)
+    a = to_dev(a_u, dev).requires_grad_(need in ("both", "a"))
+    b = to_dev(b_u, dev).requires_grad_(need in ("both", "b"))
+    y = fp8.block_scaled_matmul(a, b)
+    y.backward(g)
+    y_ref = fp8._fp8_forward(a.detach(), b.detach(), 128)
+    da_ref, db_ref = fp8._fp8_backward(128, (a.detach(), b.detach()), g)
+    assert torch.equal(y, y_ref)
+    if need in ("both", "a"):
+        assert a.grad.shape == a.shape and torch.equal(a.grad, da_ref)
+    else:
+        assert a.grad is None
+    if need in ("both", "b"):
+        assert torch.equal(b.grad, db_ref)
+    else:
+        assert b.grad is None
+
+
+def test_fp8_backward_mode_switch_after_forward_raises(dev):
+    a = torch.randn((128, 128), device=dev).to(torch.bfloat16).requires_grad_(True)
+    b = torch.randn((128, 128), device=dev).to(torch.bfloat16).requires_grad_(True)
+    y = fp8.block_scaled_matmul(a, b)
+    old = fp8.BACKWARD_MODE
+    try:
+        fp8.BACKWARD_MODE = "bf16"
+        with pytest.raises(RuntimeError, match="BACKWARD_MODE changed"):
+            y.sum().backward()
+    finally:
+        fp8.BACKWARD_MODE = old

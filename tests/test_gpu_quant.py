@@ -104,9 +104,11 @@ def test_quantize_full_size_c3_operands(dev):
     np.testing.assert_array_equal(f32_bits(sw), so.view(np.uint32))
 
 
-@pytest.mark.parametrize("shape", [(128, 128), (256, 384), (1024, 640), (8192, 8192)])
+@pytest.mark.parametrize("shape", [(128, 128), (256, 384), (1024, 640), (4096, 4096), (8192, 8192),
+                                   (16384, 4096), (2048, 32768)])
 def test_quantize_dual_equals_separate(dev, shape):
-    """tg_quantize_dual = tg_quantize_rows + tg_quantize_cols, bit for bit (C3's dY at full size)."""
+    """tg_quantize_dual = tg_quantize_rows + tg_quantize_cols, bit for bit (C3's dY at full size;
+    8192^2, 16384 x 4096 and 2048 x 32768 take the XCD-blocked tile order)."""
     rng = np.random.default_rng(sum(shape) + 3)
     x = to_dev(ob.randn_bf16(rng, shape, std=1e-3), dev)
     q, s, qt, st = fp8.quantize_fp8_dual(x)

@@ -233,18 +233,39 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(const uint16_t* __restr
 // ---------------------------------------------------------------------------
 // ROWS = false gives the column quantization alone (tg_quantize_cols for
 // 16-byte-aligned rows); GUARD handles a last tile narrower than 128 columns.
+//
+// Tile order.  Launch slots go round-robin to the 8 XCDs (slot % 8), each
+// with its own L2.  A line of row scales (32 tiles along x) and a line of
+// column scales (32 tiles along y) are each written 4 bytes at a time by 32
+// workgroups; on one XCD the pieces merge in its L2, spread over eight they
+// leave as partial-line writes.  The identity order keeps the column-scale
+// lines on one XCD (the XCD of a slot is tx % 8 when gridDim.x % 8 == 0) and
+// spreads the row-scale lines over all eight.  With xcd_blocks the tiles are
+// dealt to XCDs in blocks of 32 x 16 (each XCD a contiguous run of whole
+// blocks), which keeps a row-scale line on one XCD and a column-scale line on
+// two.  The host sets it when gridDim.x % 32 == 0, gridDim.y % 16 == 0 and
+// each XCD's share is a multiple of 512 tiles.
 template <bool ROWS, bool GUARD>
 __global__ __launch_bounds__(256) void quant_dual_kernel(const uint4* __restrict__ x, int64_t rows,
                                                          int64_t cols, uint2* __restrict__ q,
                                                          float* __restrict__ s,
                                                          uint8_t* __restrict__ qt,
-                                                         float* __restrict__ st) {
+                                                         float* __restrict__ st, int xcd_blocks) {
   // the raw tile (row pitch 272 B); once every column is in registers the
   // same memory stages the transposed bytes (column pitch 144 B)
   __shared__ uint32_t tile[128 * 68];
   uint32_t* tq = tile;
   const int tid = threadIdx.x;
-  const int64_t c0 = (int64_t)blockIdx.x * 128, r0 = (int64_t)blockIdx.y * 128;
+  int tx = blockIdx.x, ty = blockIdx.y;
+  if (xcd_blocks) {
+    const int slot = blockIdx.x + gridDim.x * blockIdx.y;
+    const int per_xcd = gridDim.x * gridDim.y / 8;
+    const int t = (slot & 7) * per_xcd + (slot >> 3);     // position in XCD-contiguous order
+    const int blk = t >> 9, w = t & 511;
+    tx = (blk % (gridDim.x / 32)) * 32 + (w & 31);
+    ty = (blk / (gridDim.x / 32)) * 16 + (w >> 5);
+  }
+  const int64_t c0 = (int64_t)tx * 128, r0 = (int64_t)ty * 128;
   const int ch = tid & 15, rr = tid >> 4;
   const int64_t cchunks = cols >> 3;
   const bool ch_ok = !GUARD || (c0 >> 3) + ch < cchunks;
@@ -261,7 +282,7 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(const uint4* __restrict
       f[4] = bf16lo(v[u].z); f[5] = bf16hi(v[u].z); f[6] = bf16lo(v[u].w); f[7] = bf16hi(v[u].w);
       const float sc = block_scale_bf16(row16_max_u32(absmax8(f)));
       q[(r0 + row) * cchunks + (c0 >> 3) + ch] = quant8<true>(f, sc);
-      if (ch == 0) s[(r0 + row) * (cols >> 7) + blockIdx.x] = sc;
+      if (ch == 0) s[(r0 + row) * (cols >> 7) + tx] = sc;
     }
     *reinterpret_cast<uint4*>(&tile[row * 68 + ch * 4]) = v[u];
   }
@@ -302,21 +323,19 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(const uint4* __restrict
       }
       tq[n * 36 + 4 * i + j] = w;
     }
-    if (j == 0 && (!GUARD || c0 + n < cols)) st[(c0 + n) * (rows >> 7) + blockIdx.y] = sc;
+    if (j == 0 && (!GUARD || c0 + n < cols)) st[(c0 + n) * (rows >> 7) + ty] = sc;
   };
   col_words(f0, sc0, 2 * cp);
   col_words(f1, sc1, 2 * cp + 1);
   __syncthreads();
-  // each store instruction writes 64 contiguous bytes of a column (lane j of
-  // the quad: bytes 16j.. and 64 + 16j..), so no partial 32-byte sectors
+  // eight lanes per column, lane k writing bytes 16k .. 16k + 15: each store
+  // instruction writes eight whole 128-byte columns (full lines)
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const int n = (tid >> 2) + 64 * p;
+  for (int p = 0; p < 4; ++p) {
+    const int n = (tid >> 3) + 32 * p, k = tid & 7;
     if (GUARD && c0 + n >= cols) continue;
-    const uint4* src = reinterpret_cast<const uint4*>(&tq[n * 36]);
-    uint4* dst = reinterpret_cast<uint4*>(qt + (c0 + n) * rows + r0);
-    stg_stream(dst + j, src[j]);
-    stg_stream(dst + 4 + j, src[4 + j]);
+    const uint4 val = *reinterpret_cast<const uint4*>(&tq[n * 36 + 4 * k]);
+    stg_stream(reinterpret_cast<uint4*>(qt + (c0 + n) * rows + r0) + k, val);
   }
 }
 
@@ -330,10 +349,10 @@ int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, f
     auto X = reinterpret_cast<const uint4*>(x);
     if (cols % 128 == 0)
       hipLaunchKernelGGL((quant_dual_kernel<false, false>), g128, dim3(256), 0, st, X, rows, cols,
-                         nullptr, nullptr, q_t, s_t);
+                         nullptr, nullptr, q_t, s_t, 0);
     else
       hipLaunchKernelGGL((quant_dual_kernel<false, true>), g128, dim3(256), 0, st, X, rows, cols,
-                         nullptr, nullptr, q_t, s_t);
+                         nullptr, nullptr, q_t, s_t, 0);
     return check_launch("quant_cols");
   }
   // rows not 16-byte aligned: the element-load kernel
@@ -348,10 +367,12 @@ int launch_quant_dual(const void* x, int64_t rows, int64_t cols, uint8_t* q, flo
   if (rows == 0 || cols == 0) return TG_OK;
   if (rows % 128 || cols % 128) return einval("quantize_dual: rows and cols must be multiples of 128");
   if (rows / 128 > 65535) return einval("quantize_dual: rows / 128 must be <= 65535");
-  const dim3 grid((unsigned)(cols / 128), (unsigned)(rows / 128));
-  hipLaunchKernelGGL((quant_dual_kernel<true, false>), grid, dim3(256), 0, st,
-                     reinterpret_cast<const uint4*>(x), rows, cols, reinterpret_cast<uint2*>(q), s, q_t,
-                     s_t);
+  const int64_t gx = cols / 128, gy = rows / 128;
+  const int xcd_blocks =
+      gx % 32 == 0 && gy % 16 == 0 && (gx * gy / 8) % 512 == 0 && gx * gy < (int64_t(1) << 31);
+  hipLaunchKernelGGL((quant_dual_kernel<true, false>), dim3((unsigned)gx, (unsigned)gy), dim3(256), 0,
+                     st, reinterpret_cast<const uint4*>(x), rows, cols, reinterpret_cast<uint2*>(q), s,
+                     q_t, s_t, xcd_blocks);
   return check_launch("quant_dual");
 }
 

@@ -13,8 +13,16 @@ Backward modes (``BACKWARD_MODE``):
   * "fp8" (default): dX and dW run through the same quantize -> scaled GEMM
     composition as the forward (g and W quantized along N; X.T and g.T along
     M, all 1x128 blocks), on FP8 MFMA.
-  * "bf16": the reference's straight-through rule (fp8.py:85-98) needs bf16
-    GEMMs, which this library does not implement yet; it raises.
+  * "bf16": the reference's straight-through rule (fp8.py:85-98): bf16 MFMA
+    GEMMs of the un-quantized operands.
+
+Residuals.  In "fp8" mode with bf16 operands whose M and N divide by
+block_k, the forward quantizes a and b once each in both directions
+(tg_quantize_dual: a along K and a.T along M; b.T along K and b along N) and
+keeps the FP8 forms the backward needs (a.T, b) instead of a and b.  The
+bytes are those the backward would compute from a and b, so the gradients
+are the same bits; each operand is read once instead of twice and the saved
+residuals take ~half the memory.
 
 Additive entry points (no reference counterpart): ``quantize_fp8`` (row or
 transposed), ``quantize_weight`` (pre-quantized weight format) and
@@ -260,18 +268,89 @@ def _bf16_backward(a, b, g):
     return da.reshape(*leading, K).to(a.dtype), db.to(b.dtype)
 
 
+def _fp8_forward_quantized_residuals(a, b, block_k, need_da, need_db):
+    """_fp8_forward with the FP8 operands of the backward kept as residuals.
+
+    a (..., K), b (K, N) bf16, M and N multiples of block_k.  Returns (out,
+    (a.T bytes, a.T scales) or None, (b bytes, b scales) or None): a.T along M
+    for db = fwd(a.T, g), b along N for da = fwd(g, b.T) -- the operands
+    _fp8_backward would quantize from a and b (fp8.py:66,68 on those inputs).
+    """
+    leading, K, N = _validate(a, b, block_k)
+    a_2d = a.reshape(-1, K)
+    if need_db:
+        qa, sa, qat, sat = quantize_fp8_dual(a_2d, block_k)    # a along K, a.T along M
+        res_a = (qat, sat)
+    else:
+        (qa, sa), res_a = quantize_fp8(a_2d, block_k), None
+    if need_da:
+        qb, sb, qbt, sbt = quantize_fp8_dual(b, block_k)       # b along N, b.T along K
+        res_b = (qb, sb)
+    else:
+        (qbt, sbt), res_b = quantize_fp8(b, block_k, transpose=True), None
+    u8 = torch.uint8
+    out = scaled_matmul(qa.view(u8), sa, qbt.view(u8), sbt)     # fp8.py:70-78
+    return out.reshape(*leading, N), res_a, res_b
+
+
+def _fp8_backward_quantized(block_k, res_a, res_b, g, a_shape, a_dtype, b_dtype):
+    """BACKWARD_MODE "fp8" gradients from the kept FP8 residuals (same bits as
+    _fp8_backward on the bf16 operands)."""
+    N = g.shape[-1]
+    g_2d = g.reshape(-1, N)
+    u8 = torch.uint8
+    if g_2d.dtype == torch.bfloat16 and res_a is not None and res_b is not None:
+        qg, sg, qgt, sgt = quantize_fp8_dual(g_2d, block_k)      # g along N and g.T along M
+    else:
+        qg, sg = quantize_fp8(g_2d, block_k) if res_b is not None else (None, None)
+        qgt, sgt = quantize_fp8(g_2d, block_k, transpose=True) if res_a is not None else (None, None)
+    da = db = None
+    if res_b is not None:
+        qb, sb = res_b
+        da = scaled_matmul(qg.view(u8), sg, qb.view(u8), sb).reshape(a_shape).to(a_dtype)
+    if res_a is not None:
+        qat, sat = res_a
+        db = scaled_matmul(qat.view(u8), sat, qgt.view(u8), sgt).to(b_dtype)
+    return da, db
+
+
 class _BlockScaledMatmul(torch.autograd.Function):
     """custom_vjp of fp8.py:30-36,101 as a torch autograd Function."""
 
     @staticmethod
     def forward(ctx, a, b, block_k):
+        ctx.block_k = block_k
+        ctx.quantized = False
+        need_da, need_db = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if (BACKWARD_MODE == "fp8" and a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16
+                and a.is_cuda and b.is_cuda and b.dim() == 2 and (need_da or need_db)):
+            leading, K, N = _validate(a, b, block_k)
+            _check_block_k(block_k)
+            M = a.numel() // K if K else 0
+            if M > 0 and N > 0 and M % block_k == 0 and N % block_k == 0:
+                out, res_a, res_b = _fp8_forward_quantized_residuals(a, b, block_k, need_da,
+                                                                     need_db)
+                ctx.quantized = True
+                ctx.has_a, ctx.has_b = res_a is not None, res_b is not None
+                ctx.save_for_backward(*(res_a or ()), *(res_b or ()))
+                ctx.a_shape, ctx.a_dtype, ctx.b_dtype = a.shape, a.dtype, b.dtype
+                return out
         out, (ra, rb) = _fp8_forward_with_residuals(a, b, block_k)
         ctx.save_for_backward(ra, rb)
-        ctx.block_k = block_k
         return out
 
     @staticmethod
     def backward(ctx, g):
+        if ctx.quantized:
+            if BACKWARD_MODE != "fp8":
+                raise RuntimeError("BACKWARD_MODE changed between forward and backward: this "
+                                   "graph kept FP8 residuals for the 'fp8' backward")
+            saved = list(ctx.saved_tensors)
+            res_a = (saved.pop(0), saved.pop(0)) if ctx.has_a else None
+            res_b = (saved.pop(0), saved.pop(0)) if ctx.has_b else None
+            da, db = _fp8_backward_quantized(ctx.block_k, res_a, res_b, g, ctx.a_shape,
+                                             ctx.a_dtype, ctx.b_dtype)
+            return da, db, None
         a, b = ctx.saved_tensors
         da, db = _fp8_backward(ctx.block_k, (a, b), g)
         return da, db, None
