@@ -119,6 +119,18 @@ def test_pack_bf16(dev, transpose, src, rows, cols, pad):
     assert np.all(got[:, width:] == 0)
 
 
+def test_pack_bf16_transpose_larger_than_infinity_cache(dev):
+    """The transposing tile kernel's non-temporal-store variant (output > 256 MB),
+    against torch's transpose, with row padding."""
+    rows, cols, pad = 4096, 32832 + 8, 8
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn((rows, cols), generator=g, device=dev).to(torch.bfloat16)
+    pitch = rows + pad
+    y = torch.full((cols, pitch), 7.0, dtype=torch.bfloat16, device=dev)
+    L.check(L.lib().tg_pack_bf16(L.ptr(x), L.TG_DTYPE_BF16, rows, cols, 1, L.ptr(y), pitch, L.stream_of(x)))
+    assert torch.equal(y[:, :rows], x.t()) and torch.all(y[:, rows:] == 0)
+
+
 def _bf16_bwd(a, b, g):
     old = fp8.BACKWARD_MODE
     fp8.BACKWARD_MODE = "bf16"
