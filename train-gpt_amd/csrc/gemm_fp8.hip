@@ -424,10 +424,46 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
   }
   if (kb < c.nkb) g256_compute_tail<0>(c, acc, af, kb + 1);
 
-  // Epilogue straight from registers: lane (fr, fg) holds row m = .. + fr and
-  // the four consecutive columns n = .. + 4fg .. 4fg+3 of every 16x16 tile,
-  // i.e. 8 contiguous bf16 bytes (16 f32 bytes).  Per store instruction the
-  // wave writes 16 rows x 32 (64) contiguous bytes; L2 merges the n-tiles.
+  // bf16 epilogue through LDS (the stage buffers are free after the last K
+  // block's barrier): each wave stages its 64 x 128 tile with 256-byte rows,
+  // 16-byte chunk c of row r at c ^ (r & 15) so the 16 rows one write
+  // instruction touches fall in different banks, then 16 lanes store each
+  // row's 256 bytes.  Written straight from registers, every output line was
+  // assembled from eight 32-byte pieces and the Y GEMM ran ~5% slower.
+  if (!OUT_F32 && (N % 8) == 0) {
+    __syncthreads();
+    uint8_t* wbuf = (c.wave < 2 ? g256_a0 : c.wave < 4 ? g256_b0 : c.wave < 6 ? g256_a1 : g256_b1) +
+                    (c.wave & 1) * 16384;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int r = i * 16 + fr;
+        const int chunk = (j * 2 + (fg >> 1)) ^ (r & 15);
+        const v4f v = acc[i][j];
+        *reinterpret_cast<uint2*>(wbuf + r * 256 + chunk * 16 + (fg & 1) * 8) =
+            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      }
+    // the wave reads back only what it wrote: LDS completes a wave's
+    // accesses in order, so waiting for its own writes is enough
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int k = lane & 15;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int r = q * 4 + (lane >> 4);
+      const int m = m0 + wm * 64 + r;
+      const int n = n0 + wn * 128 + k * 8;
+      const uint4 v = *reinterpret_cast<const uint4*>(wbuf + r * 256 + ((k ^ (r & 15)) * 16));
+      if (m < M && n < N)
+        *reinterpret_cast<uint4*>(reinterpret_cast<__bf16*>(C) + (int64_t)m * N + n) = v;
+    }
+    return;
+  }
+  // f32 output, or N not a multiple of 8: straight from registers.  Lane
+  // (fr, fg) holds row m = .. + fr and the four consecutive columns
+  // n = .. + 4fg .. 4fg+3 of every 16x16 tile, i.e. 8 contiguous bf16 bytes
+  // (16 f32 bytes); per store instruction the wave writes 16 rows x 32 (64)
+  // contiguous bytes.
   const bool vec_ok = (N % 4) == 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
