@@ -10,12 +10,10 @@
 // Design (gfx950, wave64):
 //   * v_mfma_f32_16x16x32_bf16, accumulating in place: no per-block scales,
 //     so the K loop is MFMA work only.
-//   * Workgroup tile 256 x 256 x 64 (128 bytes of every row per K step, the
-//     same LDS geometry as the FP8 kernel), 8 waves as 4 (M) x 2 (N), wave
-//     tile 64 x 128 = 4 x 8 MFMA tiles, 128 fp32 accumulators per lane.
-//   * Operands travel HBM -> LDS by buffer_load ... lds into two stages (one
-//     barrier per K step); every wave issues 1/8 of the next stage, one
-//     1 KiB part per compute region.
+//   * Workgroup tile 256 x 256, 8 waves as 4 (M) x 2 (N), wave tile 64 x 128
+//     = 4 x 8 MFMA tiles, 128 fp32 accumulators per lane.
+//   * Operands travel HBM -> LDS by buffer_load ... lds through a ring of four
+//     K32 stages (one barrier per stage), issued by one wave per SIMD.
 //   * dW contracts over the token axis, which is the row axis of both a and
 //     g, so the backward first packs a.T and g.T (bf16, rows padded to a
 //     multiple of 64 with zeros) and runs the same NT kernel.
@@ -32,110 +30,145 @@ __device__ __forceinline__ v4f mfma_bf16_16x16x32(const uint4& a, const uint4& b
                                                  __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
 }
 
-__shared__ __attribute__((aligned(16))) uint8_t h256_a0[256 * 128];
-__shared__ __attribute__((aligned(16))) uint8_t h256_b0[256 * 128];
-__shared__ __attribute__((aligned(16))) uint8_t h256_a1[256 * 128];
-__shared__ __attribute__((aligned(16))) uint8_t h256_b1[256 * 128];
+// ---------------------------------------------------------------------------
+// Four-stage pipeline.  A stage is one K32 slice of the workgroup tile: 256
+// rows x 64 B of A and of B, 32 KiB; four stages ring through 128 KiB of LDS,
+// so three slices (96 KiB per CU) are in flight while one is computed.  (With
+// two stages of K64, one 64 KiB step in flight, the copy stream was capped by
+// the ~1.4 us round trip to L2 / Infinity Cache at ~45 B/ns per CU; the MFMAs
+// consume a K64 step in ~0.9 us.)
+//   step s: loader waves wait for their copies of slice s (vmcnt(16): the 16
+//           DMA instructions of slices s+1 and s+2 stay outstanding); barrier
+//           (slice s complete, slice s-1 read by every wave); the loader waves
+//           issue slice s+3 into slice s-1's stage; every wave computes s.
+// Loads: waves 0-3 (one per SIMD) issue all copies, 8 per slice (rows
+// 64w .. 64w+63 of A and of B), so the other wave of each SIMD never stalls at
+// a DMA issue; loader and compute waves run separate copies of the loop.  The
+// copies are issued unconditionally: past the last slice the offset is out of
+// range and the loads read zero, which keeps the vmcnt arithmetic exact.  The
+// main loop runs whole rounds of four slices with no exit inside (with exits,
+// the compiler's wait analysis merges paths at the loop header and drains
+// every outstanding copy there).  The barrier is a bare s_barrier (a fence
+// would wait for every outstanding copy).
+// LDS rows are 64 B, 16-byte chunk c of row r at c ^ ((r >> 2) & 3): the 16
+// rows of a fragment read fall in different banks.  Tiles are computed as
+// B . A^T so that a lane holds one output row and four consecutive columns
+// (8-byte bf16 pieces for the epilogue).
+// ---------------------------------------------------------------------------
+__shared__ __attribute__((aligned(16))) uint8_t q4_a0[256 * 64];
+__shared__ __attribute__((aligned(16))) uint8_t q4_b0[256 * 64];
+__shared__ __attribute__((aligned(16))) uint8_t q4_a1[256 * 64];
+__shared__ __attribute__((aligned(16))) uint8_t q4_b1[256 * 64];
+__shared__ __attribute__((aligned(16))) uint8_t q4_a2[256 * 64];
+__shared__ __attribute__((aligned(16))) uint8_t q4_b2[256 * 64];
+__shared__ __attribute__((aligned(16))) uint8_t q4_a3[256 * 64];
+__shared__ __attribute__((aligned(16))) uint8_t q4_b3[256 * 64];
 
-template <int S> __device__ __forceinline__ uint8_t* h256_a() { return S ? h256_a1 : h256_a0; }
-template <int S> __device__ __forceinline__ uint8_t* h256_b() { return S ? h256_b1 : h256_b0; }
+template <int S> __device__ __forceinline__ uint8_t* q4_a() {
+  return S == 0 ? q4_a0 : S == 1 ? q4_a1 : S == 2 ? q4_a2 : q4_a3;
+}
+template <int S> __device__ __forceinline__ uint8_t* q4_b() {
+  return S == 0 ? q4_b0 : S == 1 ? q4_b1 : S == 2 ? q4_b2 : q4_b3;
+}
 
-struct H256Ctx {
+struct Q4Ctx {
   __amdgpu_buffer_rsrc_t ra, rb;
-  uint32_t voa[2], vob[2];    // per-lane byte offsets (k step 0) for even / odd u
-  uint32_t row8;              // 8 rows in bytes
+  uint32_t voa, vob;       // loader lane's byte offsets of slice 0, part 0
+  uint32_t row16;          // 16 rows in bytes
   int wave, nks;
-  uint32_t fa0, fa1, fb0, fb1;   // LDS byte offsets of this lane's fragment chunks
+  uint32_t fa, fb;         // LDS byte offsets of this lane's fragment chunk (tile 0)
 };
 
-// One K step is 64 parts of 1 KiB (8 rows x 128 B): wave w issues parts 0-3
-// for A rows 32w .. 32w+31 and parts 4-7 for the same B rows.
-__device__ __forceinline__ void h256_issue_part(const H256Ctx& c, uint8_t* la, uint8_t* lb, int ks,
-                                                int part) {
-  const uint32_t sofs = (uint32_t)ks * 128u + (uint32_t)(part & 3) * c.row8;
-  const int u = part & 3;
-  if (part < 4)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.ra, la + c.wave * 4096 + u * 1024, 16, c.voa[u & 1],
-                                             sofs, 0, 0);
-  else
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rb, lb + c.wave * 4096 + u * 1024, 16, c.vob[u & 1],
-                                             sofs, 0, 0);
+// slice ks into the stage at (la, lb): loader wave w fills rows 64w .. 64w+63
+// of A and of B, 16 rows per instruction
+template <bool LOADER>
+__device__ __forceinline__ void q4_issue(const Q4Ctx& c, uint8_t* la, uint8_t* lb, int ks) {
+  if (!LOADER) return;
+  const uint32_t so = ks < c.nks ? (uint32_t)ks * 64u : 0x80000000u;   // out of range: zeros
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.ra, la + c.wave * 4096 + p * 1024, 16, c.voa,
+                                             so + p * c.row16, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rb, lb + c.wave * 4096 + p * 1024, 16, c.vob,
+                                             so + p * c.row16, 0, 0);
+  }
 }
 
-template <int S>
-__device__ __forceinline__ void h256_compute(const H256Ctx& c, v4f (&acc)[4][8], int ks_next) {
-  const uint8_t* la = h256_a<S>();
-  const uint8_t* lb = h256_b<S>();
-  uint4 a0[4], a1[4];
+// s_waitcnt vmcnt(16) as the builtin (gfx9 encoding: vmcnt bits 15:14 = 1,
+// expcnt and lgkmcnt not waited), which the compiler's own wait insertion
+// takes into account; an inline-asm wait is opaque to it.
+constexpr int kWaitVm16 = (1 << 14) | (0xF << 8) | (0x7 << 4);
+
+template <int S, bool LOADER>
+__device__ __forceinline__ void q4_step(const Q4Ctx& c, int ks, v4f (&acc)[4][8]) {
+  if (LOADER) __builtin_amdgcn_s_waitcnt(kWaitVm16);
+  __builtin_amdgcn_s_barrier();
+  constexpr int kRefill = (S + 3) & 3;   // the stage slice ks - 1 occupied
+  q4_issue<LOADER>(c, q4_a<kRefill>(), q4_b<kRefill>(), ks + 3);
+  const uint8_t* la = q4_a<S>();
+  const uint8_t* lb = q4_b<S>();
+  uint4 af[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    a0[i] = *reinterpret_cast<const uint4*>(la + c.fa0 + i * 2048);
-    a1[i] = *reinterpret_cast<const uint4*>(la + c.fa1 + i * 2048);
-  }
-  uint4 b0 = *reinterpret_cast<const uint4*>(lb + c.fb0);
-  uint4 b1 = *reinterpret_cast<const uint4*>(lb + c.fb1);
-  const bool pf = ks_next < c.nks;
+  for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const uint4*>(la + c.fa + i * 1024);
+  uint4 bn = *reinterpret_cast<const uint4*>(lb + c.fb);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const uint4 cb0 = b0, cb1 = b1;
-    if (j + 1 < 8) {   // next region's B fragment one region ahead
-      b0 = *reinterpret_cast<const uint4*>(lb + c.fb0 + (j + 1) * 2048);
-      b1 = *reinterpret_cast<const uint4*>(lb + c.fb1 + (j + 1) * 2048);
-    }
-    if (pf) h256_issue_part(c, h256_a<S ^ 1>(), h256_b<S ^ 1>(), ks_next, j);
-    // lo halves of all four tiles, then hi halves: dependent MFMAs on one
-    // accumulator are four instructions apart
+    const uint4 bf = bn;
+    if (j + 1 < 8) bn = *reinterpret_cast<const uint4*>(lb + c.fb + (j + 1) * 1024);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i][j] = mfma_bf16_16x16x32(a0[i], cb0, acc[i][j]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i][j] = mfma_bf16_16x16x32(a1[i], cb1, acc[i][j]);
+    for (int i = 0; i < 4; ++i) acc[i][j] = mfma_bf16_16x16x32(bf, af[i], acc[i][j]);
   }
 }
 
-template <int S>
-__device__ __forceinline__ void h256_step(const H256Ctx& c, int ks, v4f (&acc)[4][8]) {
-  h256_compute<S>(c, acc, ks + 1);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+template <bool LOADER>
+__device__ __forceinline__ void q4_main_loop(const Q4Ctx& c, v4f (&acc)[4][8]) {
+  q4_issue<LOADER>(c, q4_a0, q4_b0, 0);
+  q4_issue<LOADER>(c, q4_a1, q4_b1, 1);
+  q4_issue<LOADER>(c, q4_a2, q4_b2, 2);
+  int ks = 0;
+  for (; ks + 4 <= c.nks; ks += 4) {
+    q4_step<0, LOADER>(c, ks, acc);
+    q4_step<1, LOADER>(c, ks + 1, acc);
+    q4_step<2, LOADER>(c, ks + 2, acc);
+    q4_step<3, LOADER>(c, ks + 3, acc);
+  }
+  if (ks < c.nks) {
+    q4_step<0, LOADER>(c, ks, acc);
+    if (ks + 1 < c.nks) {
+      q4_step<1, LOADER>(c, ks + 1, acc);
+      if (ks + 2 < c.nks) q4_step<2, LOADER>(c, ks + 2, acc);
+    }
+  }
 }
 
-// C[M, N] = bf16(A[M, K] . B[N, K]^T); K % 64 == 0, K-contiguous rows.
-__global__ __launch_bounds__(512, 1) void gemm_bf16_nt_256_kernel(const __bf16* __restrict__ A,
-                                                                  const __bf16* __restrict__ B,
-                                                                  __bf16* __restrict__ C, int M,
-                                                                  int N, int K, int tiles_m,
-                                                                  int tiles_n) {
-  H256Ctx c;
+__global__ __launch_bounds__(512, 1) void gemm_bf16_nt_q4_kernel(const __bf16* __restrict__ A,
+                                                                 const __bf16* __restrict__ B,
+                                                                 __bf16* __restrict__ C, int M, int N,
+                                                                 int K, int tiles_m, int tiles_n) {
+  Q4Ctx c;
   const int tid = threadIdx.x, lane = tid & 63;
   c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  c.nks = K >> 6;
+  c.nks = K >> 5;
   const int fr = lane & 15, fg = lane >> 4;
   const int wm = c.wave >> 1, wn = c.wave & 1;
   int tmi, tni;
   tile_of(blockIdx.x, tiles_m, tiles_n, tmi, tni);
   const int m0 = tmi * 256, n0 = tni * 256;
-  const uint32_t rowb = 2u * (uint32_t)K;   // row pitch in bytes
+  const uint32_t rowb = 2u * (uint32_t)K;
   c.ra = make_rsrc(A, (uint32_t)M * rowb);
   c.rb = make_rsrc(B, (uint32_t)N * rowb);
-  c.row8 = 8u * rowb;
-  // loader rows wave*32 + u*8 + lane/8; physical chunk lane%8 holds logical
-  // chunk (lane%8) ^ swz(row), which depends on lane/8 and the parity of u
-  const int lrow = c.wave * 32 + (lane >> 3);
-#pragma unroll
-  for (int par = 0; par < 2; ++par) {
-    const int lch = (lane & 7) ^ g256_swz(lrow + par * 8);
-    c.voa[par] = (uint32_t)(m0 + lrow) * rowb + lch * 16;
-    c.vob[par] = (uint32_t)(n0 + lrow) * rowb + lch * 16;
-  }
-  // fragments: lane (fr, fg) reads logical chunks fg and fg + 4 of row
-  // (wave tile row) + 16t + fr (k elements 8fg .. 8fg+7 and 32+8fg ..
-  // 32+8fg+7 of the step; A and B lanes agree).  Chunk pairs {2fg, 2fg + 1}
-  // make the four lane groups of a read collide in LDS (~30% slower reads).
-  const uint32_t ch0 = (uint32_t)(fg ^ g256_swz(fr)) * 16u;
-  c.fa0 = (uint32_t)(wm * 64 + fr) * 128u + ch0;
-  c.fa1 = c.fa0 ^ 64u;
-  c.fb0 = (uint32_t)(wn * 128 + fr) * 128u + ch0;
-  c.fb1 = c.fb0 ^ 64u;
+  c.row16 = 16u * rowb;
+  // DMA lane L lands at byte 16 L of its 1 KiB slot: row slot + L / 4,
+  // physical chunk L % 4, which holds logical chunk (L % 4) ^ ((L >> 4) & 3)
+  const int lrow = c.wave * 64 + (lane >> 2);   // loader waves 0-3
+  const uint32_t lch = (uint32_t)((lane & 3) ^ ((lane >> 4) & 3)) * 16u;
+  c.voa = (uint32_t)(m0 + lrow) * rowb + lch;
+  c.vob = (uint32_t)(n0 + lrow) * rowb + lch;
+  // fragment: lane (fr, fg) reads logical chunk fg (k 8fg .. 8fg+7) of row
+  // (wave tile row) + 16 t + fr, at physical chunk fg ^ ((fr >> 2) & 3)
+  const uint32_t ch = (uint32_t)(fg ^ ((fr >> 2) & 3)) * 16u;
+  c.fa = (uint32_t)(wm * 64 + fr) * 64u + ch;
+  c.fb = (uint32_t)(wn * 128 + fr) * 64u + ch;
 
   v4f acc[4][8];
 #pragma unroll
@@ -143,48 +176,44 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_nt_256_kernel(const __bf16* 
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-#pragma unroll
-  for (int p = 0; p < 8; ++p) h256_issue_part(c, h256_a0, h256_b0, 0, p);
+  if (c.wave < 4) q4_main_loop<true>(c, acc);
+  else q4_main_loop<false>(c, acc);
+
+  // epilogue: lane (fr, fg) holds row i * 16 + fr and columns j * 16 + 4 fg ..
+  // +3 of the wave tile; stage it in this wave's 16 KiB (256-byte rows,
+  // chunk c of row r at c ^ (r & 15)), then 16 lanes store each row's 256 bytes
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  int ks = 0;
-  for (; ks + 1 < c.nks; ks += 2) {
-    h256_step<0>(c, ks, acc);
-    h256_step<1>(c, ks + 1, acc);
-  }
-  if (ks < c.nks) h256_step<0>(c, ks, acc);
-
-  // bf16 epilogue through LDS: each wave stages its 64 x 128 tile as two
-  // 32-row halves of 256 B rows, then stores 16 bytes per lane.
-  uint8_t* ep = (c.wave < 4 ? h256_a0 + c.wave * 8192 : h256_b0 + (c.wave - 4) * 8192);
-  uint8_t* ep2 = (c.wave < 4 ? h256_a1 + c.wave * 8192 : h256_b1 + (c.wave - 4) * 8192);
+  uint8_t* wbuf = c.wave == 0 ? q4_a0 : c.wave == 1 ? q4_b0 : c.wave == 2 ? q4_a1 : c.wave == 3 ? q4_b1
+                : c.wave == 4 ? q4_a2 : c.wave == 5 ? q4_b2 : c.wave == 6 ? q4_a3 : q4_b3;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = i * 16 + 4 * fg + r, col = j * 16 + fr;
-        uint8_t* base = row < 32 ? ep : ep2;
-        *reinterpret_cast<__bf16*>(base + (row & 31) * 256 + col * 2) = (__bf16)acc[i][j][r];
-      }
+    for (int j = 0; j < 8; ++j) {
+      const int r = i * 16 + fr;
+      const int chunk = (j * 2 + (fg >> 1)) ^ (r & 15);
+      const v4f v = acc[i][j];
+      *reinterpret_cast<uint2*>(wbuf + r * 256 + chunk * 16 + (fg & 1) * 8) =
+          make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   const bool vec_ok = (N % 8) == 0;
+  const int k = lane & 15;
 #pragma unroll
-  for (int t = 0; t < 16; ++t) {
-    const int row = t * 4 + (lane >> 4), chunk = lane & 15;
-    const uint8_t* base = row < 32 ? ep : ep2;
-    const uint4 v = *reinterpret_cast<const uint4*>(base + (row & 31) * 256 + chunk * 16);
-    const int m = m0 + wm * 64 + row, n = n0 + wn * 128 + chunk * 8;
-    if (m < M) {
+  for (int q = 0; q < 16; ++q) {
+    const int r = q * 4 + (lane >> 4);
+    const int m = m0 + wm * 64 + r;
+    const int n = n0 + wn * 128 + k * 8;
+    const uint4 v = *reinterpret_cast<const uint4*>(wbuf + r * 256 + ((k ^ (r & 15)) * 16));
+    if (m < M && n < N) {
       __bf16* dst = C + (int64_t)m * N + n;
-      if (vec_ok && n + 8 <= N) {
+      if (vec_ok) {
         *reinterpret_cast<uint4*>(dst) = v;
       } else {
         const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-          if (n + k < N) reinterpret_cast<uint16_t*>(dst)[k] = e[k];
+        for (int t = 0; t < 8; ++t)
+          if (n + t < N) reinterpret_cast<uint16_t*>(dst)[t] = e[t];
       }
     }
   }
@@ -344,7 +373,7 @@ int launch_gemm_bf16(const __bf16* a, const __bf16* b, __bf16* c, int64_t M, int
                      hipStream_t st) {
   if (M == 0 || N == 0) return TG_OK;
   const int tiles_m = (int)((M + 255) / 256), tiles_n = (int)((N + 255) / 256);
-  hipLaunchKernelGGL(gemm_bf16_nt_256_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, st,
+  hipLaunchKernelGGL(gemm_bf16_nt_q4_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, st,
                      a, b, c, (int)M, (int)N, (int)K, tiles_m, tiles_n);
   return check_launch("gemm_bf16_nt_256");
 }
