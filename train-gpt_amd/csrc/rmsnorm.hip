@@ -331,12 +331,14 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint4* __restric
 
 // dscale[c] = bf16(sum over b of partial[b][c]) with f64 accumulation in a
 // fixed order: workgroup = 64 columns x 16 waves; wave w adds partial rows
-// w, w + 16, w + 32, ... in that order (eight loads in flight per lane), and
-// the 16 wave sums are added in wave order.
+// w, w + 16, w + 32, ... in that order, and the 16 wave sums are added in
+// wave order.  A lane keeps 32 loads in flight, all of its rows for up to 512
+// partial rows: the reduction runs on few workgroups (dim / 64), so its time
+// is the number of dependent round trips to L2.
 __global__ __launch_bounds__(1024) void rmsnorm_bwd_reduce(const float* __restrict__ partial,
                                                            int nparts, int dim,
                                                            uint16_t* __restrict__ dscale) {
-  constexpr int W = 16, U = 8;
+  constexpr int W = 16, U = 32;
   __shared__ double wsum[W][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + lane;
