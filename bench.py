@@ -255,7 +255,9 @@ def bench_norm_bwd(dev, iters):
 
 
 def bench_gemv(dev, iters):
-    """Config 5: decode GEMV on a pre-quantized W (128x128 scales), M in {1, 8, 32}."""
+    """Config 5: decode GEMV on a pre-quantized W (128x128 scales), M in {1, 8, 32};
+    M = 1 on the VALU kernel (tg_gemv_fp8_rowdot, what fp8_gemv picks), with the
+    MFMA kernel's time beside it."""
     import torch
     import _tglib as L
     lib = L.lib()
@@ -280,26 +282,31 @@ def bench_gemv(dev, iters):
         st = L.stream_of(x)
         L.check(lib.tg_quantize_rows(L.ptr(x), L.TG_DTYPE_BF16, M, C5_K, 128, L.ptr(xq), L.ptr(xs), st))
 
-        def launch(i):
-            k = i % nsets
-            L.check(lib.tg_gemv_fp8(L.ptr(xq), L.ptr(xs), L.ptr(wq[k]), L.ptr(ws[k]), 128, L.ptr(y),
-                                    M, C5_N, C5_K, 128, st))
-        us = _mean_launch_us(launch, iters)
+        def launcher(fn):
+            def launch(i):
+                k = i % nsets
+                L.check(fn(L.ptr(xq), L.ptr(xs), L.ptr(wq[k]), L.ptr(ws[k]), 128, L.ptr(y),
+                           M, C5_N, C5_K, 128, st))
+            return launch
+        # what fp8.fp8_gemv picks: the VALU kernel for 1-2 rows, the MFMA one above
+        rowdot = M <= 2
+        fn = lib.tg_gemv_fp8_rowdot if rowdot else lib.tg_gemv_fp8
+        us = _mean_launch_us(launcher(fn), iters)
+        us_mfma = _mean_launch_us(launcher(lib.tg_gemv_fp8), iters) if rowdot else us
 
         def step(i):          # x quantization + GEMV, the decode step's FP8 matmul
-            k = i % nsets
             L.check(lib.tg_quantize_rows(L.ptr(x), L.TG_DTYPE_BF16, M, C5_K, 128, L.ptr(xq), L.ptr(xs), st))
-            L.check(lib.tg_gemv_fp8(L.ptr(xq), L.ptr(xs), L.ptr(wq[k]), L.ptr(ws[k]), 128, L.ptr(y),
-                                    M, C5_N, C5_K, 128, st))
+            launcher(fn)(i)
         us_step = _mean_launch_us(step, iters)
         byts = C5_N * C5_K + ws[0].numel() * 4 + M * C5_K + M * (C5_K // 128) * 4 + 2 * M * C5_N
         gbps = byts / (us * 1e-6) / 1e9
-        out.append({"M": M, "us_per_launch": round(us, 3), "us_quant_plus_gemv": round(us_step, 3),
-                    "bytes_per_launch": byts,
+        tkey = "gemv_rowdot_m1" if rowdot else ("gemv_fp8_m16" if M <= 16 else "gemv_fp8_m32")
+        out.append({"M": M, "kernel": "gemv_rowdot_kernel" if rowdot else "gemv_fp8_kernel",
+                    "us_per_launch": round(us, 3), "us_mfma_gemv": round(us_mfma, 3),
+                    "us_quant_plus_gemv": round(us_step, 3), "bytes_per_launch": byts,
                     "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
                                  "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                                 "traffic": measured_traffic().get("gemv_fp8_m16" if M <= 16
-                                                                   else "gemv_fp8_m32")}})
+                                 "traffic": measured_traffic().get(tkey)}})
     return {"workload": "C5 decode GEMV, W e4m3 [14336, 4096] + 128x128 scales (pre-quantized), "
                         "x quantized 1x128", "by_M": out}
 

@@ -168,6 +168,15 @@ int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* w_q, const 
                 int w_scale_bn, void* out, int64_t M, int64_t N, int64_t K, int block_k,
                 void* stream);
 
+/* The same product for one or two activation rows (M <= 2, K <= 16384) on the
+ * VALU: each 128-wide block's sum is an f32 fma chain instead of the MFMA's
+ * arithmetic, so the result agrees with tg_gemv_fp8 to rounding (not bit for
+ * bit).  Faster for single-token decode: W streams through registers with no
+ * LDS staging.  Arguments as tg_gemv_fp8. */
+int tg_gemv_fp8_rowdot(const uint8_t* x_q, const float* x_s, const uint8_t* w_q, const float* w_s,
+                       int w_scale_bn, void* out, int64_t M, int64_t N, int64_t K, int block_k,
+                       void* stream);
+
 /* Quantize W.T into the pre-quantized weight format with one scale per
  * 128x128 tile (w_scale_bn == 128).  w: (K, N) bf16; w_q (N, K); w_s (ceil(N/128), K/128). */
 int tg_quantize_weight_128x128(const void* w, int64_t K, int64_t N, uint8_t* w_q, float* w_s,

@@ -38,6 +38,7 @@ SIGNATURES = {
     "tg_rms_norm_bwd_workspace": (_sz, [_i64, _i64]),
     "tg_rms_norm_bwd": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _vp, _sz, _vp]),
     "tg_gemv_fp8": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _i64, _i64, _i64, _int, _vp]),
+    "tg_gemv_fp8_rowdot": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _i64, _i64, _i64, _int, _vp]),
     "tg_quantize_weight_128x128": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "tg_gemm_bf16_nt": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "tg_pack_bf16": (_int, [_vp, _int, _i64, _i64, _int, _vp, _i64, _vp]),

@@ -742,6 +742,99 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
   }
 }
 
+// ---------------------------------------------------------------------------
+// GEMV for one or two activation rows on the VALU (no MFMA, no LDS staging of
+// W).  With M <= 2 the MFMA kernel above spends its time moving each weight
+// row through LDS so that 8 rows can feed one 16-row MFMA fragment; here each
+// wave streams whole weight rows (16 bytes per lane per 1 KiB piece, four
+// pieces in flight) and takes the dot products itself: per 16-byte piece,
+// 16 e4m3 x 16 e4m3 products (v_cvt_pk_f32_fp8, f32 fma) into one f32 block
+// partial, scaled by w_s * x_s of its 128-wide block, then a wave reduction
+// in a fixed order.  x (and its scales) sit in LDS as bytes.  Every weight
+// load is a buffer load at an offset inside the matrix.  The block
+// sums are f32 fma chains, not the MFMA's arithmetic, so outputs agree with
+// tg_gemv_fp8 / tg_gemm_fp8_nt to rounding, not bit for bit.
+// ---------------------------------------------------------------------------
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot16_e4m3(const u32x4_t& w, const uint4& x) {
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w}, xx[4] = {x.x, x.y, x.z, x.w};
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const v2f w0 = __builtin_amdgcn_cvt_pk_f32_fp8(ww[e], false);
+    const v2f w1 = __builtin_amdgcn_cvt_pk_f32_fp8(ww[e], true);
+    const v2f x0 = __builtin_amdgcn_cvt_pk_f32_fp8(xx[e], false);
+    const v2f x1 = __builtin_amdgcn_cvt_pk_f32_fp8(xx[e], true);
+    s = __builtin_fmaf(w0.x, x0.x, s);
+    s = __builtin_fmaf(w0.y, x0.y, s);
+    s = __builtin_fmaf(w1.x, x1.x, s);
+    s = __builtin_fmaf(w1.y, x1.y, s);
+  }
+  return s;
+}
+
+constexpr int kRowdotMaxK = 16384;   // x of two rows (32 KiB) + scales in LDS
+
+template <int NX, int BNS>
+__global__ __launch_bounds__(256) void gemv_rowdot_kernel(const uint8_t* __restrict__ XQ,
+                                                          const float* __restrict__ XS,
+                                                          const uint8_t* __restrict__ WQ,
+                                                          const float* __restrict__ WS,
+                                                          __bf16* __restrict__ out, int N, int K) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t rowdot_lds[];   // NX*K x bytes, NX*K/128 scales
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nkb = K >> 7;
+  float* sxs = reinterpret_cast<float*>(rowdot_lds + NX * K);
+  for (int i = tid * 16; i < NX * K; i += 256 * 16)
+    *reinterpret_cast<uint4*>(rowdot_lds + i) = *reinterpret_cast<const uint4*>(XQ + i);
+  for (int i = tid; i < NX * nkb; i += 256) sxs[i] = XS[i];
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(WQ, (uint32_t)N * (uint32_t)K);
+  const int srows = BNS == 1 ? N : (N + BNS - 1) / BNS;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(WS, (uint32_t)srows * (uint32_t)nkb * 4u);
+  const int nw = gridDim.x * 4;
+  const int npc = (K + 1023) >> 10;               // 1 KiB pieces per row
+  for (int row = blockIdx.x * 4 + wave; row < N; row += nw) {
+    float acc[NX];
+#pragma unroll
+    for (int m = 0; m < NX; ++m) acc[m] = 0.f;
+    const uint32_t rbase = (uint32_t)row * (uint32_t)K;
+    const uint32_t sbase = (uint32_t)(BNS == 1 ? row : row / BNS) * (uint32_t)nkb;
+    for (int p0 = 0; p0 < npc; p0 += 4) {
+      u32x4_t w[4];
+      float ws[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t k = (uint32_t)(p0 + q) * 1024u + lane * 16u;
+        const bool ok = k < (uint32_t)K;
+        // lanes past the row re-read its first piece (in range; not used below)
+        w[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, rbase + (ok ? k : 0u), 0, kAuxNT);
+        ws[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                              rs, (sbase + (ok ? (k >> 7) : 0u)) * 4u, 0, 0));
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t k = (uint32_t)(p0 + q) * 1024u + lane * 16u;
+        if (k < (uint32_t)K) {
+#pragma unroll
+          for (int m = 0; m < NX; ++m) {
+            const uint4 xv = *reinterpret_cast<const uint4*>(rowdot_lds + m * K + k);
+            acc[m] = __builtin_fmaf(dot16_e4m3(w[q], xv), ws[q] * sxs[m * nkb + (k >> 7)], acc[m]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < NX; ++m) {
+      float v = acc[m];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+      if (lane == 0) out[(int64_t)m * N + row] = (__bf16)v;
+    }
+  }
+}
+
 }  // namespace tg
 
 using namespace tg;
@@ -890,4 +983,37 @@ extern "C" int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* 
   TG_TRY(launch_gemv<2>(x_q, x_s, w_q, w_s, w_scale_bn, o, 32, n, k, st));
   return launch_gemv<2>(x_q + 32 * K, x_s + 32 * (K / 128), w_q, w_s, w_scale_bn, o + 32 * N, m - 32,
                         n, k, st);
+}
+
+extern "C" int tg_gemv_fp8_rowdot(const uint8_t* x_q, const float* x_s, const uint8_t* w_q,
+                                  const float* w_s, int w_scale_bn, void* out, int64_t M, int64_t N,
+                                  int64_t K, int block_k, void* stream) {
+  TG_TRY(check_gemm_args("gemv_fp8_rowdot", M, N, K, block_k, w_scale_bn));
+  if (M > 2) return einval("gemv_fp8_rowdot: M must be <= 2 (use tg_gemv_fp8)");
+  if (K > kRowdotMaxK) return einval("gemv_fp8_rowdot: K must be <= 16384");
+  if (M == 0 || N == 0) return TG_OK;
+  if (!x_q || !x_s || !w_q || !w_s || !out) return einval("gemv_fp8_rowdot: null pointer");
+  if (!aligned(x_q, 16) || !aligned(w_q, 16))
+    return einval("gemv_fp8_rowdot: operands must be 16-byte aligned");
+  if ((uint64_t)N * (uint64_t)K >= (1ull << 32) || (uint64_t)N * (uint64_t)(K / 128) * 4u >= (1ull << 32))
+    return einval("gemv_fp8_rowdot: operand too large for 32-bit buffer offsets");
+  hipStream_t st = as_stream(stream);
+  // persistent waves: up to 8 workgroups (32 waves) per CU, one wave per row at a time
+  const int64_t wgs = (N + 3) / 4, cap = 8 * (int64_t)device_cus();
+  const dim3 grid((unsigned)(wgs < cap ? wgs : cap));
+  const size_t lds = (size_t)M * (size_t)K + (size_t)M * (size_t)(K / 128) * 4;
+  auto o = reinterpret_cast<__bf16*>(out);
+  const int n = (int)N, k = (int)K;
+  if (M == 1) {
+    if (w_scale_bn == 1)
+      hipLaunchKernelGGL((gemv_rowdot_kernel<1, 1>), grid, dim3(256), lds, st, x_q, x_s, w_q, w_s, o, n, k);
+    else
+      hipLaunchKernelGGL((gemv_rowdot_kernel<1, 128>), grid, dim3(256), lds, st, x_q, x_s, w_q, w_s, o, n, k);
+  } else {
+    if (w_scale_bn == 1)
+      hipLaunchKernelGGL((gemv_rowdot_kernel<2, 1>), grid, dim3(256), lds, st, x_q, x_s, w_q, w_s, o, n, k);
+    else
+      hipLaunchKernelGGL((gemv_rowdot_kernel<2, 128>), grid, dim3(256), lds, st, x_q, x_s, w_q, w_s, o, n, k);
+  }
+  return check_launch("gemv_fp8_rowdot");
 }

@@ -140,14 +140,18 @@ class FP8Decoder:
     FP8 quantization of its output in one kernel; graph-capturable) or "sdpa"
     (torch's attention over the cached keys, the arithmetic of the prefill;
     eager only -- with it a decode step reproduces the full forward bit for bit).
+    exact_gemv: for 1-2 rows use the MFMA GEMV (the GEMM's block arithmetic)
+    rather than the faster VALU one (tg_gemv_fp8_rowdot); default: on with
+    decode_attn "sdpa" (the bit-exact mode), off with "hip".
     """
 
     def __init__(self, params, cfg: Config, layout: str = "128x128", max_batch: int = 1,
-                 decode_attn: str = "hip"):
+                 decode_attn: str = "hip", exact_gemv: bool = None):
         _check_fp8_dims(cfg)
         if decode_attn not in ("hip", "sdpa"):
             raise ValueError("decode_attn must be 'hip' or 'sdpa'")
         self.decode_attn = decode_attn
+        self.exact_gemv = decode_attn == "sdpa" if exact_gemv is None else bool(exact_gemv)
         if not 1 <= max_batch <= 64:
             raise ValueError("max_batch must be in [1, 64] (decode rows per GEMV)")
         self.cfg = cfg
@@ -182,24 +186,26 @@ class FP8Decoder:
         B, T, d = x.shape
         H, Dh = cfg.n_heads, cfg.head_dim
         h, h_q, h_s = kernels.rms_norm_fp8(x, lp["norm1"], cfg.rms_eps)
-        qkv = lp["wqkv"].matmul_prequant(h_q.reshape(B * T, d), h_s.reshape(B * T, -1))
+        qkv = lp["wqkv"].matmul_prequant(h_q.reshape(B * T, d), h_s.reshape(B * T, -1),
+                                       exact=self.exact_gemv)
         q, k, v = qkv.reshape(B, T, 3, H, Dh).permute(2, 0, 3, 1, 4).unbind(0)   # each (B, H, T, Dh)
         self.k_cache[li, :B, :, :T] = k
         self.v_cache[li, :B, :, :T] = v
         o = _attention(q, k, v, causal=True)                           # model.py:67
         o = o.transpose(1, 2).reshape(B * T, H * Dh)
-        x = x + lp["wo"].matmul(o).reshape(B, T, d)                    # model.py:68, 75
+        x = x + lp["wo"].matmul(o, exact=self.exact_gemv).reshape(B, T, d)   # model.py:68, 75
         h2, h2_q, h2_s = kernels.rms_norm_fp8(x, lp["norm2"], cfg.rms_eps)
-        u = lp["w_up"].matmul_prequant(h2_q.reshape(B * T, d), h2_s.reshape(B * T, -1))
+        u = lp["w_up"].matmul_prequant(h2_q.reshape(B * T, d), h2_s.reshape(B * T, -1),
+                                        exact=self.exact_gemv)
         u = F.relu(u).square()                                         # model.py:72 (bf16)
-        return x + lp["w_down"].matmul(u).reshape(B, T, d)             # model.py:76
+        return x + lp["w_down"].matmul(u, exact=self.exact_gemv).reshape(B, T, d)   # model.py:76
 
     def _head(self, x: torch.Tensor) -> torch.Tensor:
         """Final norm -> FP8 unembedding -> logit cap (model.py:93-97); f32 (rows, V)."""
         cfg = self.cfg
         d = x.shape[-1]
         _, xq, xs = kernels.rms_norm_fp8(x.reshape(-1, d), self.final_norm, cfg.rms_eps)
-        logits = self.unembed.matmul_prequant(xq, xs).float()
+        logits = self.unembed.matmul_prequant(xq, xs, exact=self.exact_gemv).float()
         return cfg.logit_cap * torch.tanh(logits / cfg.logit_cap)
 
     @torch.no_grad()
@@ -250,20 +256,20 @@ class FP8Decoder:
         x = self.embed[tok] + self.pos.index_select(0, t)                 # (B, d)
         _, h_q, h_s = kernels.rms_norm_fp8(x, self.layers[0]["norm1"], cfg.rms_eps)
         for li, lp in enumerate(self.layers):
-            qkv = lp["wqkv"].matmul_prequant(h_q, h_s)                      # (B, 3 H Dh)
+            qkv = lp["wqkv"].matmul_prequant(h_q, h_s, self.exact_gemv)                      # (B, 3 H Dh)
             if self.decode_attn == "hip":
                 o_q, o_s, _ = decode_attention(qkv, self.k_cache[li], self.v_cache[li], t, H)
-                a = lp["wo"].matmul_prequant(o_q, o_s)                      # model.py:68
+                a = lp["wo"].matmul_prequant(o_q, o_s, self.exact_gemv)                      # model.py:68
             else:
-                a = lp["wo"].matmul(self._sdpa_step(li, qkv, int(t.item())))
+                a = lp["wo"].matmul(self._sdpa_step(li, qkv, int(t.item())), exact=self.exact_gemv)
             # x = x + a (model.py:75) fused with norm2 -> FP8 rows
             x, h2_q, h2_s, _ = kernels.add_rms_norm_fp8(x, a, lp["norm2"], cfg.rms_eps, inplace=True)
-            u_q, u_s = fp8.quantize_relu2(lp["w_up"].matmul_prequant(h2_q, h2_s))   # model.py:72
-            m = lp["w_down"].matmul_prequant(u_q, u_s)
+            u_q, u_s = fp8.quantize_relu2(lp["w_up"].matmul_prequant(h2_q, h2_s, self.exact_gemv))   # model.py:72
+            m = lp["w_down"].matmul_prequant(u_q, u_s, self.exact_gemv)
             # x = x + m (model.py:76) fused with the next norm (norm1 or final_norm)
             nxt = self.layers[li + 1]["norm1"] if li + 1 < len(self.layers) else self.final_norm
             x, h_q, h_s, _ = kernels.add_rms_norm_fp8(x, m, nxt, cfg.rms_eps, inplace=True)
-        logits = self.unembed.matmul_prequant(h_q, h_s).float()            # model.py:96
+        logits = self.unembed.matmul_prequant(h_q, h_s, self.exact_gemv).float()            # model.py:96
         return cfg.logit_cap * torch.tanh(logits / cfg.logit_cap)           # model.py:97
 
     def _sdpa_step(self, li: int, qkv: torch.Tensor, t: int) -> torch.Tensor:

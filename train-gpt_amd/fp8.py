@@ -500,9 +500,11 @@ class QuantizedWeight:
     def to(self, device) -> "QuantizedWeight":
         return QuantizedWeight(self.q.to(device), self.scales.to(device), self.bn, self.block_k)
 
-    def matmul(self, x: torch.Tensor) -> torch.Tensor:
+    def matmul(self, x: torch.Tensor, exact: bool = False) -> torch.Tensor:
         """x (..., K) -> bf16 (..., N): fp8.py:66's quantization of x, then the
-        scaled GEMM (or, for at most 64 rows, the decode GEMV) on the kept W."""
+        scaled GEMM (or, for at most 64 rows, the decode GEMV) on the kept W.
+        exact: use the MFMA GEMV for 1-2 rows too (the GEMM's block arithmetic,
+        bit for bit) instead of the faster VALU one."""
         *lead, K = x.shape
         if K != self.shape[0]:
             raise ValueError(f"contracted-dim mismatch: a K={K}, b K={self.shape[0]}")
@@ -510,27 +512,25 @@ class QuantizedWeight:
         for d in lead:
             M *= d
         if 0 < M <= 64:
-            return fp8_gemv(x, self.q, self.scales, self.bn, self.block_k)
+            return fp8_gemv(x, self.q, self.scales, self.bn, self.block_k, exact=exact)
         a_q, a_s = quantize_fp8(x.reshape(-1, K), self.block_k)
         out = scaled_matmul(a_q.view(torch.uint8), a_s, self.q.view(torch.uint8), self.scales,
                             b_scale_bn=self.bn)
         return out.reshape(*lead, self.shape[1])
 
-    def matmul_prequant(self, x_q: torch.Tensor, x_s: torch.Tensor) -> torch.Tensor:
+    def matmul_prequant(self, x_q: torch.Tensor, x_s: torch.Tensor, exact: bool = False) -> torch.Tensor:
         """Already-quantized rows (x_q (M, K) e4m3fn, x_s (M, K/128) f32, e.g. from
         kernels.rms_norm_fp8) times the kept W -> bf16 (M, N): the decode GEMV for
-        at most 64 rows, the scaled GEMM above."""
+        at most 64 rows (exact as in matmul), the scaled GEMM above."""
         M, K = x_q.shape
         if K != self.shape[0]:
             raise ValueError(f"contracted-dim mismatch: a K={K}, b K={self.shape[0]}")
         xq = x_q.view(torch.uint8).contiguous()
         xs = x_s.contiguous().float()
         if 0 < M <= 64:
-            N = self.shape[1]
-            out = torch.empty((M, N), dtype=torch.bfloat16, device=x_q.device)
-            _L.check(_L.lib().tg_gemv_fp8(_L.ptr(xq), _L.ptr(xs), _L.ptr(self.q.view(torch.uint8)),
-                                          _L.ptr(self.scales), self.bn, _L.ptr(out), M, N, K,
-                                          self.block_k, _L.stream_of(xq)))
+            out = torch.empty((M, self.shape[1]), dtype=torch.bfloat16, device=x_q.device)
+            _gemv_prequant(xq, xs, self.q.view(torch.uint8), self.scales, self.bn, out, self.block_k,
+                           exact)
             return out
         return scaled_matmul(xq, xs, self.q.view(torch.uint8), self.scales, b_scale_bn=self.bn)
 
@@ -561,10 +561,26 @@ class QuantizedWeight:
         return w.to(device)
 
 
+ROWDOT_MAX_K = 16384
+
+
+def _gemv_prequant(xq, xs, wq, ws, bn, out, block_k, exact):
+    """out (M, N) = GEMV of quantized rows xq (M, K) u8, xs on W (wq (N, K) u8, ws).
+    1-2 rows take tg_gemv_fp8_rowdot (VALU dot products) unless exact, which
+    keeps tg_gemv_fp8 (the GEMM's MFMA block arithmetic, bit for bit)."""
+    M, K = xq.shape
+    N = wq.shape[0]
+    fn = (_L.lib().tg_gemv_fp8_rowdot if (M <= 2 and K <= ROWDOT_MAX_K and not exact)
+          else _L.lib().tg_gemv_fp8)
+    _L.check(fn(_L.ptr(xq), _L.ptr(xs), _L.ptr(wq), _L.ptr(ws), bn, _L.ptr(out), M, N, K, block_k,
+                _L.stream_of(xq)))
+
+
 def fp8_gemv(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, w_scale_bn: int = 1,
-             block_k: int = DEFAULT_BLOCK_K) -> torch.Tensor:
+             block_k: int = DEFAULT_BLOCK_K, exact: bool = False) -> torch.Tensor:
     """Decode-shape GEMM: x (..., K) bf16 (M = prod(...) <= 64 rows) times a
-    pre-quantized weight (w_q (N, K), w_s) -> (..., N) bf16."""
+    pre-quantized weight (w_q (N, K), w_s) -> (..., N) bf16.  For 1-2 rows the
+    VALU kernel is used unless exact (see _gemv_prequant)."""
     _L.require_gpu(x, w_q)
     _check_block_k(block_k)
     *lead, K = x.shape
@@ -574,8 +590,6 @@ def fp8_gemv(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, w_scale_bn: 
     x_q, x_s = quantize_fp8(x.reshape(-1, K), block_k)
     M = x_q.shape[0]
     out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
-    wq = w_q.view(torch.uint8).contiguous()
-    ws = w_s.contiguous()
-    _L.check(_L.lib().tg_gemv_fp8(_L.ptr(x_q), _L.ptr(x_s), _L.ptr(wq), _L.ptr(ws), w_scale_bn,
-                                  _L.ptr(out), M, N, K, block_k, _L.stream_of(x_q)))
+    _gemv_prequant(x_q.view(torch.uint8), x_s, w_q.view(torch.uint8).contiguous(), w_s.contiguous(),
+                   w_scale_bn, out, block_k, exact)
     return out.reshape(*lead, N)
