@@ -86,7 +86,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--norm-iters", type=int, default=200)
     p.add_argument("--only", choices=["step", "norm_quant", "norm_bwd", "gemv", "bwd_bf16",
-                                      "block_step", "xent", "decode"],
+                                      "block_step", "xent", "decode", "vendor_gemm"],
                    help="run one secondary workload alone and print its JSON object")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (calibrates the FETCH_SIZE / "
@@ -366,6 +366,60 @@ def bench_block(dev, steps=5, warm=3):
     return out
 
 
+def bench_vendor_gemm(dev, iters):
+    """Context for the GEMM roofline: this library's block-scaled FP8 GEMM and
+    bf16 GEMM beside the vendor library's (hipBLASLt through torch) plain FP8
+    GEMM (one scale per tensor, no block promotion) and bf16 GEMM at the three
+    C3 shapes, each timed alone (20 launches after 5 warm-ups)."""
+    import torch
+    import _tglib as L
+    lib = L.lib()
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    bf = torch.bfloat16
+
+    def timed(f):
+        for _ in range(5):
+            f()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(iters):
+            f()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / iters * 1e3
+
+    out = {}
+    for name, (M, N, K) in (("Y", (M3, N3, K3)), ("dX", (M3, K3, N3)), ("dW", (K3, N3, M3))):
+        a = torch.randn((M, K), generator=g, device=dev).to(bf)
+        b = torch.randn((N, K), generator=g, device=dev).to(bf)
+        st = L.stream_of(a)
+        qa = torch.empty((M, K), dtype=torch.uint8, device=dev)
+        sa = torch.empty((M, K // 128), dtype=torch.float32, device=dev)
+        qb = torch.empty((N, K), dtype=torch.uint8, device=dev)
+        sb = torch.empty((N, K // 128), dtype=torch.float32, device=dev)
+        L.check(lib.tg_quantize_rows(L.ptr(a), L.TG_DTYPE_BF16, M, K, 128, L.ptr(qa), L.ptr(sa), st))
+        L.check(lib.tg_quantize_rows(L.ptr(b), L.TG_DTYPE_BF16, N, K, 128, L.ptr(qb), L.ptr(sb), st))
+        c = torch.empty((M, N), dtype=bf, device=dev)
+        flop = 2.0 * M * N * K
+        t_ours = timed(lambda: L.check(lib.tg_gemm_fp8_nt(L.ptr(qa), L.ptr(sa), L.ptr(qb), L.ptr(sb), 1, L.ptr(c),
+                                                          L.TG_DTYPE_BF16, M, N, K, 128, st)))
+        t_ours_bf16 = timed(lambda: L.check(lib.tg_gemm_bf16_nt(L.ptr(a), L.ptr(b), L.ptr(c), M, N, K, st)))
+        a8, b8 = a.to(torch.float8_e4m3fn), b.to(torch.float8_e4m3fn)
+        one = torch.tensor(1.0, device=dev)
+        t_vendor = timed(lambda: torch._scaled_mm(a8, b8.t(), scale_a=one, scale_b=one, out_dtype=bf))
+        t_vendor_bf16 = timed(lambda: a @ b.t())
+        out[name] = {"M": M, "N": N, "K": K,
+                     "block_scaled_fp8_tflops": round(flop / t_ours / 1e6, 1),
+                     "vendor_plain_fp8_tflops": round(flop / t_vendor / 1e6, 1),
+                     "bf16_tflops": round(flop / t_ours_bf16 / 1e6, 1),
+                     "vendor_bf16_tflops": round(flop / t_vendor_bf16 / 1e6, 1)}
+    return {"workload": "C3 GEMM shapes: tg_gemm_fp8_nt (1x128 block scales) and tg_gemm_bf16_nt against "
+                        "torch._scaled_mm (per-tensor scales) and torch bf16 matmul (hipBLASLt)",
+            "by_gemm": out}
+
+
 def bench_xent(dev, iters):
     """Config 4's head: tg_logit_cap_xent_fwd / _bwd on bf16 logits [8192, 50304]
     (824 MB, larger than the Infinity Cache, so one buffer set)."""
@@ -511,7 +565,8 @@ def main():
         fn = {"norm_quant": bench_norm, "norm_bwd": bench_norm_bwd, "gemv": bench_gemv,
               "bwd_bf16": lambda d, _: bench_bwd_bf16(d, 10),
               "block_step": lambda d, _: bench_block(d), "xent": bench_xent,
-              "decode": lambda d, _: bench_decode(d)}[args.only]
+              "decode": lambda d, _: bench_decode(d),
+              "vendor_gemm": lambda d, _: bench_vendor_gemm(d, 20)}[args.only]
         print(json.dumps({args.only: fn(dev, args.norm_iters)}))
         return
     step = Step(dev)
