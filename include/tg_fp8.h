@@ -177,6 +177,27 @@ int tg_gemv_fp8_rowdot(const uint8_t* x_q, const float* x_s, const uint8_t* w_q,
                        int w_scale_bn, void* out, int64_t M, int64_t N, int64_t K, int block_k,
                        void* stream);
 
+/* Decode-step fusions of the norm / activation that feeds a GEMV (no
+ * reference counterpart: generate.py runs model.forward per token; these fuse
+ * model.py:61-62 / 71 with the projection that follows, for one or two rows):
+ *
+ * tg_rms_norm_fp8_gemv: h = the FP8 rows (bytes and 1x128 scales) that
+ * tg_rms_norm_fp8 (delta == NULL) or tg_add_rms_norm_fp8 (delta != NULL) would
+ * produce from x (M, K) bf16, gamma (K,) bf16 and eps, bit for bit; then
+ * out (M, N) = h @ W^T as tg_gemv_fp8_rowdot.  With delta, the residual sum
+ * bf16(x + delta) is also stored to xout (M, K), which must not overlap x or
+ * delta.  M <= 2, K <= 4096, K % 128 == 0; x, delta, gamma, xout 16-byte
+ * aligned.  Replaces the norm launch + the GEMV launch of a decode step.
+ *
+ * tg_relu2_fp8_gemv: h = the FP8 rows tg_quantize_rows_relu2 would produce
+ * from u (M, K) bf16 (model.py:72's relu^2), then out = h @ W^T as
+ * tg_gemv_fp8_rowdot.  M <= 2, K <= 16384. */
+int tg_rms_norm_fp8_gemv(const void* x, const void* delta, const void* gamma, float eps, void* xout,
+                         const uint8_t* w_q, const float* w_s, int w_scale_bn, void* out, int64_t M,
+                         int64_t N, int64_t K, void* stream);
+int tg_relu2_fp8_gemv(const void* u, const uint8_t* w_q, const float* w_s, int w_scale_bn, void* out,
+                      int64_t M, int64_t N, int64_t K, void* stream);
+
 /* Quantize W.T into the pre-quantized weight format with one scale per
  * 128x128 tile (w_scale_bn == 128).  w: (K, N) bf16; w_q (N, K); w_s (ceil(N/128), K/128). */
 int tg_quantize_weight_128x128(const void* w, int64_t K, int64_t N, uint8_t* w_q, float* w_s,

@@ -233,6 +233,34 @@ def test_graph_step_matches_eager(dev, B):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("B", [1, 2])
+def test_fused_step_same_bits(dev, B):
+    """A fused decode step (each norm / relu^2 quantization inside the GEMV that
+    consumes it) gives the same logits, bit for bit, as the step of separate
+    kernels on the same VALU GEMV, eager and replayed from a graph."""
+    cfg = TINY
+    params = decode.init_params(cfg, dev, seed=16)
+    fused = decode.FP8Decoder(params, cfg, max_batch=B)
+    plain = decode.FP8Decoder(params, cfg, max_batch=B, fused=False)
+    graph = decode.FP8Decoder(params, cfg, max_batch=B)
+    assert fused.fused and not plain.fused
+    graph.capture_step(B)
+    g = torch.Generator(device=dev).manual_seed(17)
+    ids = torch.randint(0, cfg.vocab_size, (B, 30), generator=g, device=dev)
+    a = [fused.prefill(ids[:, :7])]
+    b = [plain.prefill(ids[:, :7])]
+    c = [graph.prefill(ids[:, :7])]
+    for t in range(7, ids.shape[1]):
+        a.append(fused.step(ids[:, t]))
+        b.append(plain.step(ids[:, t]))
+        c.append(graph.step(ids[:, t]))
+        torch.cuda.synchronize()
+    a, b, c = torch.stack(a, 1), torch.stack(b, 1), torch.stack(c, 1)
+    assert torch.isfinite(a).all()
+    assert torch.equal(a, b) and torch.equal(a, c)
+
+
+@pytest.mark.gpu
 def test_generate_stops_on_eot(dev):
     cfg = TINY
     params = decode.init_params(cfg, dev, seed=11)

@@ -159,3 +159,102 @@ def test_gemv_rejects_large_m(dev):
     ws = torch.ones((16, 2), dtype=torch.float32, device=dev)
     with pytest.raises(ValueError, match="M must be <= 64"):
         fp8.fp8_gemv(x, wq, ws)
+
+
+# ---------------------------------------------------------------- fused prologues
+# tg_rms_norm_fp8_gemv / tg_relu2_fp8_gemv run the norm (or residual add + norm)
+# and the relu^2 quantization inside the VALU GEMV; each must give the same
+# bits as the stand-alone kernels followed by tg_gemv_fp8_rowdot, and the
+# residual sum the same bits as tg_add_rms_norm_fp8's.
+import kernels  # noqa: E402
+
+
+def _bf16_rows(rng, M, K, outliers=True):
+    x = ob.randn_bf16(rng, (M, K))
+    if outliers:   # a few large values, as in the C2 inputs
+        x = x.copy()
+        idx = rng.choice(M * K, size=max(1, M * K // 500), replace=False)
+        x.reshape(-1)[idx] = ob.randn_bf16(rng, (idx.size,), std=50.0)
+    return x
+
+
+NORM_FUSED = [(1, 1, 128), (2, 77, 640), (1, 6912, 2304), (2, 2304, 2304), (1, 3000, 4096), (2, 129, 1152),
+              (1, 50257, 2304)]
+
+
+@pytest.mark.parametrize("layout", ["128x1", "128x128"])
+@pytest.mark.parametrize("add", [False, True])
+@pytest.mark.parametrize("M,N,K", NORM_FUSED)
+def test_rms_norm_fp8_gemv_same_bits(dev, M, N, K, add, layout):
+    rng = np.random.default_rng(M * 7919 + N * 31 + K + int(add))
+    x = to_dev(_bf16_rows(rng, M, K), dev)
+    delta = to_dev(_bf16_rows(rng, M, K, outliers=False), dev)
+    gamma = to_dev(ob.randn_bf16(rng, (K,), std=0.1, mean=1.0), dev)
+    w = to_dev(ob.randn_bf16(rng, (K, N), std=0.02), dev)
+    qw = fp8.QuantizedWeight.from_weight(w, layout)
+    eps = 1e-6
+    if add:
+        xo_ref, q, s, _ = kernels.add_rms_norm_fp8(x, delta, gamma, eps)
+        xout = torch.empty_like(x)
+        got = qw.matmul_rms_norm(x, gamma, eps, delta=delta, xout=xout)
+        assert torch.equal(xout.view(torch.int16), xo_ref.view(torch.int16))
+    else:
+        _, q, s = kernels.rms_norm_fp8(x, gamma, eps)
+        got = qw.matmul_rms_norm(x, gamma, eps)
+    ref = qw.matmul_prequant(q, s)          # tg_gemv_fp8_rowdot on the stand-alone bytes
+    assert got.shape == (M, N) and got.dtype == torch.bfloat16
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+def test_rms_norm_fp8_gemv_vs_oracle(dev):
+    """One direct check of the fused path against the oracle's norm, quantizer
+    and float64 GEMV (the same-bits tests above tie it to the stand-alone
+    kernels, which are pinned there)."""
+    from oracle import norm_ref
+    rng = np.random.default_rng(12)
+    M, N, K = 2, 1000, 2304
+    x = _bf16_rows(rng, M, K)
+    g = ob.randn_bf16(rng, (K,), std=0.1)
+    w = ob.randn_bf16(rng, (K, N), std=0.02)
+    qw = fp8.QuantizedWeight.from_weight(to_dev(w, dev), "128x128")
+    got = qw.matmul_rms_norm(to_dev(x, dev), to_dev(g, dev), 1e-6)
+    _, qx, sx = norm_ref.rms_norm_fp8(x, g, 1e-6)
+    ref = fp8_ref.gemv_prequant(qx, sx, u8(qw.q), qw.scales.cpu().numpy(), qw.bn)
+    assert maxabs_rel(got, ref) <= 1e-2 and _rowdot_close(got, ref)
+
+
+RELU2_FUSED = [(1, 1, 128), (2, 129, 256), (1, 2304, 9216), (2, 2304, 9216), (1, 77, 16384), (2, 513, 16384),
+               (1, 4096, 14336)]
+
+
+@pytest.mark.parametrize("layout", ["128x1", "128x128"])
+@pytest.mark.parametrize("M,N,K", RELU2_FUSED)
+def test_relu2_fp8_gemv_same_bits(dev, M, N, K, layout):
+    rng = np.random.default_rng(M * 131 + N * 7 + K)
+    u = to_dev(_bf16_rows(rng, M, K), dev)
+    w = to_dev(ob.randn_bf16(rng, (K, N), std=0.02), dev)
+    qw = fp8.QuantizedWeight.from_weight(w, layout)
+    got = qw.matmul_relu2(u)
+    q, s = fp8.quantize_relu2(u)
+    ref = qw.matmul_prequant(q, s)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+def test_fused_gemv_errors(dev):
+    w = to_dev(ob.randn_bf16(np.random.default_rng(3), (4224, 16), std=0.02), dev)
+    qw = fp8.QuantizedWeight.from_weight(w, "128x1")
+    x = torch.zeros((1, 4224), dtype=torch.bfloat16, device=dev)
+    g = torch.ones(4224, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError, match="K must be <= 4096"):
+        qw.matmul_rms_norm(x, g, 1e-6)
+    w2 = to_dev(ob.randn_bf16(np.random.default_rng(4), (256, 16), std=0.02), dev)
+    qw2 = fp8.QuantizedWeight.from_weight(w2, "128x1")
+    x3 = torch.zeros((3, 256), dtype=torch.bfloat16, device=dev)
+    g2 = torch.ones(256, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError, match="M must be <= 2"):
+        qw2.matmul_rms_norm(x3, g2, 1e-6)
+    with pytest.raises(ValueError, match="M must be <= 2"):
+        qw2.matmul_relu2(x3)
+    x1 = torch.zeros((1, 256), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError, match="must not overlap"):
+        qw2.matmul_rms_norm(x1, g2, 1e-6, delta=torch.zeros_like(x1), xout=x1)

@@ -20,6 +20,7 @@
 //     range tiles are walked in groups of 8 tile-rows for L2 reuse of B.
 #include <type_traits>
 
+#include "row_ops.h"
 #include "tg_device.h"
 #include "tg_host.h"
 #include "gemm_tile.h"
@@ -746,14 +747,29 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
 // GEMV for one or two activation rows on the VALU (no MFMA, no LDS staging of
 // W).  With M <= 2 the MFMA kernel above spends its time moving each weight
 // row through LDS so that 8 rows can feed one 16-row MFMA fragment; here each
-// wave streams whole weight rows (16 bytes per lane per 1 KiB piece, four
-// pieces in flight) and takes the dot products itself: per 16-byte piece,
-// 16 e4m3 x 16 e4m3 products (v_cvt_pk_f32_fp8, f32 fma) into one f32 block
-// partial, scaled by w_s * x_s of its 128-wide block, then a wave reduction
-// in a fixed order.  x (and its scales) sit in LDS as bytes.  Every weight
-// load is a buffer load at an offset inside the matrix.  The block
-// sums are f32 fma chains, not the MFMA's arithmetic, so outputs agree with
-// tg_gemv_fp8 / tg_gemm_fp8_nt to rounding, not bit for bit.
+// wave streams whole weight rows and takes the dot products itself.
+//   * A unit is 4 KiB of one weight row: four 1 KiB loads (16 bytes per lane)
+//     and the four W scales of those lanes.  A wave owns rows gw, gw + nw, ...
+//     (nw = waves in the grid), walked unit by unit with two units in flight.
+//   * Per 16-byte piece: 16 e4m3 x 16 e4m3 products (v_cvt_pk_f32_fp8, f32
+//     fma chain) into the block partial, scaled by w_s * x_s of its 128-wide
+//     block; at a row's end a 64-lane butterfly, and the row's sum is parked
+//     in lane (row index & 63) until 64 rows (or the wave's last row) are
+//     stored together.
+//   * x bytes and scales sit in LDS.  The prologue that fills them is one of:
+//       PRO_X      copy of already-quantized x_q / x_s
+//       PRO_NORM   rmsnorm of x (optionally after the residual add x + delta,
+//                  which workgroup 0 also stores) -> FP8 rows, by the same
+//                  row routine as the norm kernel (same bits)
+//       PRO_RELU2  bf16(relu(u)^2) -> FP8 rows, as quant_rows_kernel<RELU2>
+//     Its loads are issued first, then the first unit's weight loads, so the
+//     prologue's arithmetic overlaps the first HBM round trip.
+//   * Every load is a buffer load at an offset inside its matrix (lanes past
+//     a row re-read the row's first piece and are masked out of the sum); the
+//     loop runs whole pairs of units with no exit inside it, so the compiler's
+//     wait counts stay exact.
+// The block sums are f32 fma chains, not the MFMA's arithmetic, so outputs
+// agree with tg_gemv_fp8 / tg_gemm_fp8_nt to rounding, not bit for bit.
 // ---------------------------------------------------------------------------
 typedef float v2f __attribute__((ext_vector_type(2)));
 
@@ -775,63 +791,227 @@ __device__ __forceinline__ float dot16_e4m3(const u32x4_t& w, const uint4& x) {
 }
 
 constexpr int kRowdotMaxK = 16384;   // x of two rows (32 KiB) + scales in LDS
+constexpr int kRowdotNormMaxK = 4096;
+enum { PRO_X = 0, PRO_NORM = 1, PRO_NORM_ADD = 2, PRO_RELU2 = 3 };
 
-template <int NX, int BNS>
-__global__ __launch_bounds__(256) void gemv_rowdot_kernel(const uint8_t* __restrict__ XQ,
-                                                          const float* __restrict__ XS,
-                                                          const uint8_t* __restrict__ WQ,
-                                                          const float* __restrict__ WS,
-                                                          __bf16* __restrict__ out, int N, int K) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t rowdot_lds[];   // NX*K x bytes, NX*K/128 scales
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nkb = K >> 7;
-  float* sxs = reinterpret_cast<float*>(rowdot_lds + NX * K);
-  for (int i = tid * 16; i < NX * K; i += 256 * 16)
-    *reinterpret_cast<uint4*>(rowdot_lds + i) = *reinterpret_cast<const uint4*>(XQ + i);
-  for (int i = tid; i < NX * nkb; i += 256) sxs[i] = XS[i];
-  __syncthreads();
+struct RowdotIn {
+  const uint8_t* xq;      // PRO_X: (M, K) e4m3 bytes
+  const float* xs;        // PRO_X: (M, K/128) scales
+  const uint4* x;         // PRO_NORM*: (M, K) bf16 rows; PRO_RELU2: u (M, K) bf16
+  const uint4* delta;     // PRO_NORM_ADD: (M, K) bf16
+  const uint4* gamma;     // PRO_NORM*: (K,) bf16
+  uint4* xout;            // PRO_NORM_ADD: (M, K) bf16 residual sum (workgroup 0 stores it)
+  float eps;
+};
+
+struct RowdotUnit {
+  u32x4_t w[4];
+  float s[4];
+};
+
+// unit (row, g): 1 KiB pieces 4g .. 4g+3 of weight row `row`
+__device__ __forceinline__ void rowdot_load(RowdotUnit& U, const __amdgpu_buffer_rsrc_t& rw,
+                                            const __amdgpu_buffer_rsrc_t& rs, int row, int g, int K,
+                                            int nkb, int bns, int lane) {
+  const uint32_t rbase = (uint32_t)row * (uint32_t)K;
+  const uint32_t sbase = (uint32_t)(bns == 1 ? row : row >> 7) * (uint32_t)nkb;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t k = (uint32_t)(g * 4 + q) * 1024u + lane * 16u;
+    const bool ok = k < (uint32_t)K;
+    U.w[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, rbase + (ok ? k : 0u), 0, kAuxNT);
+    U.s[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                           rs, (sbase + (ok ? (k >> 7) : 0u)) * 4u, 0, 0));
+  }
+}
+
+template <int NX>
+__device__ __forceinline__ void rowdot_compute(const RowdotUnit& U, const uint8_t* xl, const float* sxs,
+                                               int g, int K, int nkb, int lane, float (&acc)[NX]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t k = (uint32_t)(g * 4 + q) * 1024u + lane * 16u;
+    const bool ok = k < (uint32_t)K;
+    const uint32_t kk = ok ? k : 0u;
+#pragma unroll
+    for (int m = 0; m < NX; ++m) {
+      const uint4 xv = *reinterpret_cast<const uint4*>(xl + m * K + kk);
+      const float t = __builtin_fmaf(dot16_e4m3(U.w[q], xv), U.s[q] * sxs[m * nkb + (kk >> 7)], acc[m]);
+      acc[m] = ok ? t : acc[m];
+    }
+  }
+}
+
+// XL: 4 KiB pieces of x staged by PRO_X (NX * K <= 4096 * XL), or 16-byte
+// chunks of u per thread for PRO_RELU2 (NX * K <= 2048 * XL); J: chunks per
+// lane of the norm row (K <= 512 * J).
+template <int NX, int PRO, int XL, int J>
+__global__ __launch_bounds__(256) void gemv_rowdot_kernel(RowdotIn in, const uint8_t* __restrict__ WQ,
+                                                          const float* __restrict__ WS, int bns,
+                                                          __bf16* __restrict__ out, int N, int K,
+                                                          int sx_off) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t rowdot_lds[];   // x bytes, then x scales
+  uint8_t* xl = rowdot_lds;
+  float* sxs = reinterpret_cast<float*>(rowdot_lds + sx_off);
+  // the wave index through readfirstlane: the row loop is uniform control flow to the compiler
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nkb = K >> 7, nch = K >> 3;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(WQ, (uint32_t)N * (uint32_t)K);
-  const int srows = BNS == 1 ? N : (N + BNS - 1) / BNS;
+  const int srows = bns == 1 ? N : (N + 127) >> 7;
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(WS, (uint32_t)srows * (uint32_t)nkb * 4u);
-  const int nw = gridDim.x * 4;
-  const int npc = (K + 1023) >> 10;               // 1 KiB pieces per row
-  for (int row = blockIdx.x * 4 + wave; row < N; row += nw) {
-    float acc[NX];
+  const int nw = gridDim.x * 4, gw = blockIdx.x * 4 + wave;
+  const int G = (K + 4095) >> 12;                      // units per row
+  const int nrows = gw < N ? (N - 1 - gw) / nw + 1 : 0;
+  const int nu = nrows * G;
+
+  // ---- prologue loads ----
+  u32x4_t xr[PRO == PRO_X ? XL : 1];
+  float xsr = 0.f;
+  uint4 nx[J], nd[J], ng[J];
+  uint4 rv[PRO == PRO_RELU2 ? XL : 1];
+  if (PRO == PRO_X) {
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(in.xq, (uint32_t)(NX * K));
+    const __amdgpu_buffer_rsrc_t rxs = make_rsrc(in.xs, (uint32_t)(NX * nkb) * 4u);
 #pragma unroll
-    for (int m = 0; m < NX; ++m) acc[m] = 0.f;
-    const uint32_t rbase = (uint32_t)row * (uint32_t)K;
-    const uint32_t sbase = (uint32_t)(BNS == 1 ? row : row / BNS) * (uint32_t)nkb;
-    for (int p0 = 0; p0 < npc; p0 += 4) {
-      u32x4_t w[4];
-      float ws[4];
+    for (int j = 0; j < XL; ++j)   // past NX * K: out of range, reads zero
+      xr[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(j * 4096 + tid * 16), 0, 0);
+    xsr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxs, (uint32_t)tid * 4u, 0, 0));
+  } else if (PRO == PRO_NORM || PRO == PRO_NORM_ADD) {
+    // unconditional buffer loads: chunks past the row and the rows of waves
+    // >= NX fall outside the buffers and read zero
+    const uint32_t rbytes = (uint32_t)(NX * K) * 2u;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(in.x, rbytes);
+    const __amdgpu_buffer_rsrc_t rd = make_rsrc(PRO == PRO_NORM_ADD ? (const void*)in.delta : (const void*)in.x, rbytes);
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(in.gamma, (uint32_t)K * 2u);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t k = (uint32_t)(p0 + q) * 1024u + lane * 16u;
-        const bool ok = k < (uint32_t)K;
-        // lanes past the row re-read its first piece (in range; not used below)
-        w[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, rbase + (ok ? k : 0u), 0, kAuxNT);
-        ws[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                              rs, (sbase + (ok ? (k >> 7) : 0u)) * 4u, 0, 0));
+    for (int j = 0; j < J; ++j) {
+      const int c = lane + 64 * j;
+      const uint32_t xo = c < nch ? (uint32_t)(wave * nch + c) * 16u : rbytes;
+      const u32x4_t vx = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+      nx[j] = make_uint4(vx.x, vx.y, vx.z, vx.w);
+      if (PRO == PRO_NORM_ADD) {
+        const u32x4_t vd = __builtin_amdgcn_raw_buffer_load_b128(rd, xo, 0, 0);
+        nd[j] = make_uint4(vd.x, vd.y, vd.z, vd.w);
+      } else {
+        nd[j] = make_uint4(0, 0, 0, 0);
       }
+      const u32x4_t vg = __builtin_amdgcn_raw_buffer_load_b128(rg, c < nch ? (uint32_t)c * 16u : (uint32_t)K * 2u, 0, 0);
+      ng[j] = make_uint4(vg.x, vg.y, vg.z, vg.w);
+    }
+  } else {
+    const __amdgpu_buffer_rsrc_t ru = make_rsrc(in.x, (uint32_t)(NX * K) * 2u);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t k = (uint32_t)(p0 + q) * 1024u + lane * 16u;
-        if (k < (uint32_t)K) {
+    for (int r = 0; r < XL; ++r) {   // past NX * K: out of range, reads zero
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(ru, (uint32_t)(tid + 256 * r) * 16u, 0, 0);
+      rv[r] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+  }
+
+  // ---- first unit's weight loads, after the prologue's (loads complete in
+  // order, so the prologue's arithmetic can start before these arrive) ----
+  __builtin_amdgcn_sched_barrier(0);
+  RowdotUnit A, B;
+  rowdot_load(A, rw, rs, gw < N ? gw : N - 1, 0, K, nkb, bns, lane);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- prologue arithmetic -> LDS ----
+  if (PRO == PRO_X) {
+    // unconditional writes: a skipped write would leave its load outstanding
+    // to the compiler, which then waits for every load at the loop header
 #pragma unroll
-          for (int m = 0; m < NX; ++m) {
-            const uint4 xv = *reinterpret_cast<const uint4*>(rowdot_lds + m * K + k);
-            acc[m] = __builtin_fmaf(dot16_e4m3(w[q], xv), ws[q] * sxs[m * nkb + (k >> 7)], acc[m]);
-          }
+    for (int j = 0; j < XL; ++j) *reinterpret_cast<u32x4_t*>(xl + j * 4096 + tid * 16) = xr[j];
+    sxs[tid] = xsr;
+  } else if (PRO == PRO_NORM || PRO == PRO_NORM_ADD) {
+    if (wave < NX) {
+      float gm[J][8];
+#pragma unroll
+      for (int j = 0; j < J; ++j) unpack8(ng[j], gm[j]);
+      uint4 yo[J];
+      uint2 qo[J];
+      float so[J];
+      norm_row<J, true, false, PRO == PRO_NORM_ADD>(nx, nd, gm, lane, nch, (float)K, in.eps, yo, qo, so);
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nch) {
+          *reinterpret_cast<uint2*>(xl + wave * K + c * 8) = qo[j];
+          if ((lane & 15) == 0) sxs[wave * nkb + (c >> 4)] = so[j];
+          if (PRO == PRO_NORM_ADD && blockIdx.x == 0) in.xout[wave * nch + c] = nx[j];
         }
       }
     }
+  } else {
+#pragma unroll
+    for (int r = 0; r < XL; ++r) {
+      const int c = tid + 256 * r;   // chunk of the flattened (NX, K) rows; 16 chunks = one block
+      float v[8];
+      unpack8(rv[r], v);
+      relu2_bf16(v);
+      const float sc = block_scale_bf16(row16_max_u32(absmax8(v)));   // uniform: DPP
+      if (c < NX * nch) {
+        *reinterpret_cast<uint2*>(xl + c * 8) = quant8<true>(v, sc);
+        if ((lane & 15) == 0) sxs[c >> 4] = sc;
+      }
+    }
+  }
+  __syncthreads();
+  if (nu == 0) return;
+
+  float acc[NX], res[NX];
+#pragma unroll
+  for (int m = 0; m < NX; ++m) acc[m] = res[m] = 0.f;
+  auto finish = [&](int jr) {            // row jr of this wave is complete
 #pragma unroll
     for (int m = 0; m < NX; ++m) {
       float v = acc[m];
 #pragma unroll
       for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-      if (lane == 0) out[(int64_t)m * N + row] = (__bf16)v;
+      res[m] = lane == (jr & 63) ? v : res[m];
+      acc[m] = 0.f;
     }
+    if ((jr & 63) == 63 || jr == nrows - 1) {   // store rows (jr & ~63) .. jr
+      const int r = gw + ((jr & ~63) + lane) * nw;
+      if (lane <= (jr & 63)) {
+#pragma unroll
+        for (int m = 0; m < NX; ++m) out[(int64_t)m * N + r] = (__bf16)res[m];
+      }
+    }
+  };
+  auto next = [&](int& r, int& g, int& j) {
+    if (++g == G) {
+      g = 0;
+      r += nw;
+      ++j;
+    }
+  };
+  int row = gw, g = 0, j = 0;   // unit = (row j of this wave, 4 KiB group g)
+  const int pairs = (nu - 1) >> 1;
+  for (int it = 0; it < pairs; ++it) {
+    int row1 = row, g1 = g, j1 = j;
+    next(row1, g1, j1);
+    rowdot_load(B, rw, rs, row1, g1, K, nkb, bns, lane);
+    rowdot_compute<NX>(A, xl, sxs, g, K, nkb, lane, acc);
+    if (g == G - 1) finish(j);
+    int row2 = row1, g2 = g1, j2 = j1;
+    next(row2, g2, j2);
+    rowdot_load(A, rw, rs, row2, g2, K, nkb, bns, lane);
+    rowdot_compute<NX>(B, xl, sxs, g1, K, nkb, lane, acc);
+    if (g1 == G - 1) finish(j1);
+    row = row2;
+    g = g2;
+    j = j2;
+  }
+  if ((nu & 1) == 0) {
+    int row1 = row, g1 = g, j1 = j;
+    next(row1, g1, j1);
+    rowdot_load(B, rw, rs, row1, g1, K, nkb, bns, lane);
+    rowdot_compute<NX>(A, xl, sxs, g, K, nkb, lane, acc);
+    if (g == G - 1) finish(j);
+    rowdot_compute<NX>(B, xl, sxs, g1, K, nkb, lane, acc);
+    finish(j1);
+  } else {
+    rowdot_compute<NX>(A, xl, sxs, g, K, nkb, lane, acc);
+    finish(j);
   }
 }
 
@@ -985,35 +1165,145 @@ extern "C" int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* 
                         n, k, st);
 }
 
+template <int NX, int PRO, int XL, int J>
+static void launch_rowdot_k(const RowdotIn& in, const uint8_t* w_q, const float* w_s, int bns, __bf16* o,
+                            int n, int k, int sx_off, size_t lds, hipStream_t st) {
+  // persistent waves, one wave per weight row at a time: as many workgroups
+  // as fit on the CUs at once (registers: once per instantiation; LDS: 160 KiB
+  // per CU), at most 8 per CU, so that no workgroup waits for a free slot
+  static int occ_regs = 0;
+  if (occ_regs <= 0) {
+    int v = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_rowdot_kernel<NX, PRO, XL, J>, 256, 0) !=
+            hipSuccess || v <= 0)
+      v = 4;
+    occ_regs = v;
+  }
+  int per_cu = occ_regs < 8 ? occ_regs : 8;
+  const int by_lds = (int)((160 * 1024) / (lds > 0 ? lds : 1));
+  if (by_lds < per_cu) per_cu = by_lds < 1 ? 1 : by_lds;
+  const int64_t wgs = ((int64_t)n + 3) / 4, cap = (int64_t)per_cu * device_cus();
+  hipLaunchKernelGGL((gemv_rowdot_kernel<NX, PRO, XL, J>), dim3((unsigned)(wgs < cap ? wgs : cap)), dim3(256),
+                     lds, st, in, w_q, w_s, bns, o, n, k, sx_off);
+}
+
+// PRO_X: XL 4 KiB pieces of x; PRO_RELU2: XL 16-byte chunks of u per thread;
+// PRO_NORM*: J chunks of the norm row per lane.
+template <int NX, int PRO>
+static int launch_rowdot(const RowdotIn& in, const uint8_t* w_q, const float* w_s, int bns, __bf16* o,
+                         int n, int k, hipStream_t st) {
+  if constexpr (PRO == PRO_X) {
+    const int need = (NX * k + 4095) / 4096;
+    const int sx_off = (need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8) * 4096;
+    const size_t lds = (size_t)sx_off + 1024;
+    if (need <= 1) launch_rowdot_k<NX, PRO, 1, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+    else if (need <= 2) launch_rowdot_k<NX, PRO, 2, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+    else if (need <= 4) launch_rowdot_k<NX, PRO, 4, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+    else launch_rowdot_k<NX, PRO, 8, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+  } else {
+    const int sx_off = NX * k;   // a multiple of 128
+    const size_t lds = (size_t)sx_off + (size_t)NX * (k / 128) * 4;
+    if constexpr (PRO == PRO_RELU2) {
+      const int need = (NX * k + 2047) / 2048;
+      if (need <= 1) launch_rowdot_k<NX, PRO, 1, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (need <= 2) launch_rowdot_k<NX, PRO, 2, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (need <= 4) launch_rowdot_k<NX, PRO, 4, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (need <= 8) launch_rowdot_k<NX, PRO, 8, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else launch_rowdot_k<NX, PRO, 16, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+    } else {
+      const int jneed = (k / 8 + 63) / 64;
+      if (jneed <= 1) launch_rowdot_k<NX, PRO, 1, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (jneed <= 2) launch_rowdot_k<NX, PRO, 1, 2>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (jneed <= 4) launch_rowdot_k<NX, PRO, 1, 4>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (jneed <= 5) launch_rowdot_k<NX, PRO, 1, 5>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else launch_rowdot_k<NX, PRO, 1, 8>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+    }
+  }
+  return TG_OK;
+}
+
+static int rowdot_common_checks(const char* who, int64_t M, int64_t N, int64_t K, int w_scale_bn,
+                                const uint8_t* w_q, const float* w_s, const void* out, int64_t kmax) {
+  TG_TRY(check_gemm_args(who, M, N, K, 128, w_scale_bn));
+  char msg[160];
+  const char* what = nullptr;
+  if (M > 2) what = "M must be <= 2 (use tg_gemv_fp8)";
+  else if (K > kmax) what = kmax == kRowdotMaxK ? "K must be <= 16384" : "K must be <= 4096";
+  else if (M == 0 || N == 0) return TG_OK;
+  else if (!w_q || !w_s || !out) what = "null pointer";
+  else if (!aligned(w_q, 16)) what = "operands must be 16-byte aligned";
+  else if ((uint64_t)N * (uint64_t)K >= (1ull << 32) || (uint64_t)N * (uint64_t)(K / 128) * 4u >= (1ull << 32))
+    what = "operand too large for 32-bit buffer offsets";
+  if (!what) return TG_OK;
+  snprintf(msg, sizeof(msg), "%s: %s", who, what);
+  return einval(msg);
+}
+
+static bool ranges_overlap(const void* a, const void* b, size_t bytes) {
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return x < y + bytes && y < x + bytes;
+}
+
 extern "C" int tg_gemv_fp8_rowdot(const uint8_t* x_q, const float* x_s, const uint8_t* w_q,
                                   const float* w_s, int w_scale_bn, void* out, int64_t M, int64_t N,
                                   int64_t K, int block_k, void* stream) {
-  TG_TRY(check_gemm_args("gemv_fp8_rowdot", M, N, K, block_k, w_scale_bn));
-  if (M > 2) return einval("gemv_fp8_rowdot: M must be <= 2 (use tg_gemv_fp8)");
-  if (K > kRowdotMaxK) return einval("gemv_fp8_rowdot: K must be <= 16384");
+  if (block_k != 128) return einval("block_k must be 128");
+  TG_TRY(rowdot_common_checks("gemv_fp8_rowdot", M, N, K, w_scale_bn, w_q, w_s, out, kRowdotMaxK));
   if (M == 0 || N == 0) return TG_OK;
-  if (!x_q || !x_s || !w_q || !w_s || !out) return einval("gemv_fp8_rowdot: null pointer");
-  if (!aligned(x_q, 16) || !aligned(w_q, 16))
-    return einval("gemv_fp8_rowdot: operands must be 16-byte aligned");
-  if ((uint64_t)N * (uint64_t)K >= (1ull << 32) || (uint64_t)N * (uint64_t)(K / 128) * 4u >= (1ull << 32))
-    return einval("gemv_fp8_rowdot: operand too large for 32-bit buffer offsets");
-  hipStream_t st = as_stream(stream);
-  // persistent waves: up to 8 workgroups (32 waves) per CU, one wave per row at a time
-  const int64_t wgs = (N + 3) / 4, cap = 8 * (int64_t)device_cus();
-  const dim3 grid((unsigned)(wgs < cap ? wgs : cap));
-  const size_t lds = (size_t)M * (size_t)K + (size_t)M * (size_t)(K / 128) * 4;
+  if (!x_q || !x_s) return einval("gemv_fp8_rowdot: null pointer");
+  if (!aligned(x_q, 16)) return einval("gemv_fp8_rowdot: operands must be 16-byte aligned");
+  RowdotIn in{};
+  in.xq = x_q;
+  in.xs = x_s;
   auto o = reinterpret_cast<__bf16*>(out);
-  const int n = (int)N, k = (int)K;
-  if (M == 1) {
-    if (w_scale_bn == 1)
-      hipLaunchKernelGGL((gemv_rowdot_kernel<1, 1>), grid, dim3(256), lds, st, x_q, x_s, w_q, w_s, o, n, k);
-    else
-      hipLaunchKernelGGL((gemv_rowdot_kernel<1, 128>), grid, dim3(256), lds, st, x_q, x_s, w_q, w_s, o, n, k);
-  } else {
-    if (w_scale_bn == 1)
-      hipLaunchKernelGGL((gemv_rowdot_kernel<2, 1>), grid, dim3(256), lds, st, x_q, x_s, w_q, w_s, o, n, k);
-    else
-      hipLaunchKernelGGL((gemv_rowdot_kernel<2, 128>), grid, dim3(256), lds, st, x_q, x_s, w_q, w_s, o, n, k);
-  }
+  hipStream_t st = as_stream(stream);
+  if (M == 1) TG_TRY((launch_rowdot<1, PRO_X>(in, w_q, w_s, w_scale_bn, o, (int)N, (int)K, st)));
+  else TG_TRY((launch_rowdot<2, PRO_X>(in, w_q, w_s, w_scale_bn, o, (int)N, (int)K, st)));
   return check_launch("gemv_fp8_rowdot");
+}
+
+extern "C" int tg_rms_norm_fp8_gemv(const void* x, const void* delta, const void* gamma, float eps,
+                                    void* xout, const uint8_t* w_q, const float* w_s, int w_scale_bn,
+                                    void* out, int64_t M, int64_t N, int64_t K, void* stream) {
+  TG_TRY(rowdot_common_checks("rms_norm_fp8_gemv", M, N, K, w_scale_bn, w_q, w_s, out, kRowdotNormMaxK));
+  if (M == 0 || N == 0) return TG_OK;
+  if (!x || !gamma || (delta && !xout)) return einval("rms_norm_fp8_gemv: null pointer");
+  if (!aligned(x, 16) || !aligned(gamma, 16) || (delta && (!aligned(delta, 16) || !aligned(xout, 16))))
+    return einval("rms_norm_fp8_gemv: x, delta, gamma and xout must be 16-byte aligned");
+  const size_t rb = (size_t)M * (size_t)K * 2;
+  if (delta && (ranges_overlap(xout, x, rb) || ranges_overlap(xout, delta, rb)))
+    return einval("rms_norm_fp8_gemv: xout must not overlap x or delta (other workgroups read them "
+                  "while workgroup 0 stores xout)");
+  RowdotIn in{};
+  in.x = reinterpret_cast<const uint4*>(x);
+  in.delta = reinterpret_cast<const uint4*>(delta);
+  in.gamma = reinterpret_cast<const uint4*>(gamma);
+  in.xout = reinterpret_cast<uint4*>(xout);
+  in.eps = eps;
+  auto o = reinterpret_cast<__bf16*>(out);
+  hipStream_t st = as_stream(stream);
+  const int n = (int)N, k = (int)K;
+  if (delta) {
+    if (M == 1) TG_TRY((launch_rowdot<1, PRO_NORM_ADD>(in, w_q, w_s, w_scale_bn, o, n, k, st)));
+    else TG_TRY((launch_rowdot<2, PRO_NORM_ADD>(in, w_q, w_s, w_scale_bn, o, n, k, st)));
+  } else {
+    if (M == 1) TG_TRY((launch_rowdot<1, PRO_NORM>(in, w_q, w_s, w_scale_bn, o, n, k, st)));
+    else TG_TRY((launch_rowdot<2, PRO_NORM>(in, w_q, w_s, w_scale_bn, o, n, k, st)));
+  }
+  return check_launch("rms_norm_fp8_gemv");
+}
+
+extern "C" int tg_relu2_fp8_gemv(const void* u, const uint8_t* w_q, const float* w_s, int w_scale_bn,
+                                 void* out, int64_t M, int64_t N, int64_t K, void* stream) {
+  TG_TRY(rowdot_common_checks("relu2_fp8_gemv", M, N, K, w_scale_bn, w_q, w_s, out, kRowdotMaxK));
+  if (M == 0 || N == 0) return TG_OK;
+  if (!u) return einval("relu2_fp8_gemv: null pointer");
+  if (!aligned(u, 16)) return einval("relu2_fp8_gemv: u must be 16-byte aligned");
+  RowdotIn in{};
+  in.x = reinterpret_cast<const uint4*>(u);
+  auto o = reinterpret_cast<__bf16*>(out);
+  hipStream_t st = as_stream(stream);
+  if (M == 1) TG_TRY((launch_rowdot<1, PRO_RELU2>(in, w_q, w_s, w_scale_bn, o, (int)N, (int)K, st)));
+  else TG_TRY((launch_rowdot<2, PRO_RELU2>(in, w_q, w_s, w_scale_bn, o, (int)N, (int)K, st)));
+  return check_launch("relu2_fp8_gemv");
 }

@@ -12,6 +12,7 @@
 #include <stdarg.h>
 #include <string.h>
 
+#include "row_ops.h"
 #include "tg_device.h"
 #include "tg_host.h"
 
@@ -50,35 +51,6 @@ __device__ __forceinline__ void load_chunk(const void* __restrict__ x, int64_t c
   }
 }
 
-// Quantize 8 values of one block with scale sc; bf16-valued inputs use the
-// exact reciprocal-refinement divide, f32 inputs the IEEE divide.
-template <bool BF16_VALUES>
-__device__ __forceinline__ uint2 quant8(const float (&v)[8], float sc) {
-  Divider d(sc);
-  uint2 out;
-  if (d.fast) {
-    float t[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) t[i] = BF16_VALUES ? d.div(v[i]) : v[i] / sc;
-    out.x = e4m3x4(t[0], t[1], t[2], t[3]);
-    out.y = e4m3x4(t[4], t[5], t[6], t[7]);
-  } else {
-    uint32_t b[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) b[i] = e4m3_nonfinite_scale(v[i], sc);
-    out.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-    out.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
-  }
-  return out;
-}
-
-__device__ __forceinline__ uint32_t absmax8(const float (&v)[8]) {
-  uint32_t m = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) m = max(m, __float_as_uint(v[i]) & 0x7FFFFFFFu);
-  return m;
-}
-
 // RELU2: the values quantized are bf16(relu(x)^2) (model.py:72's activation
 // as bf16 tensor ops: relu exact, the square rounded once), for bf16 x.
 template <bool F32_IN, int UNROLL, bool RELU2 = false>
@@ -92,17 +64,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const void* __restrict_
   for (int u = 0; u < UNROLL; ++u) {
     int64_t c = base + u * 256;
     load_chunk<F32_IN>(x, c, c < nchunks, v[u]);
-    if (RELU2) {
-#pragma unroll
-      for (int i = 0; i < 8; i += 2) {
-        // IEEE maximum keeps NaN (jnp.maximum / torch relu propagate it)
-        const float a = __builtin_elementwise_maximum(v[u][i], 0.0f);
-        const float b = __builtin_elementwise_maximum(v[u][i + 1], 0.0f);
-        const uint32_t w = pack_bf16x2(a * a, b * b);
-        v[u][i] = bf16lo(w);
-        v[u][i + 1] = bf16hi(w);
-      }
-    }
+    if (RELU2) relu2_bf16(v[u]);
   }
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {

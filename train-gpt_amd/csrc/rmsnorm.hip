@@ -14,16 +14,11 @@
 // 128-element scale block is one 16-lane DPP row.  gamma stays in registers
 // while the wave walks rows with a grid stride.  x is read once; y, q and the
 // scales are written once.
+#include "row_ops.h"
 #include "tg_device.h"
 #include "tg_host.h"
 
 namespace tg {
-
-// max(|a|, |b|, |c|) with NaN propagation (IEEE maximum: v_maximum3_f32)
-__device__ __forceinline__ float amax3(float a, float b, float c) {
-  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(__builtin_fabsf(a), __builtin_fabsf(b)),
-                                       __builtin_fabsf(c));
-}
 
 // FULL: every lane owns exactly J chunks of every row (dim == 512 * J), so
 // no per-chunk guards are emitted.  Each wave walks rows with a stride of the
@@ -69,81 +64,29 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint4* __restrict__ 
     if (ADD) load_row(delta, wave0, nd);
   }
   for (int64_t row = wave0; row < rows; row += wstride) {
-    float xf[J][8];
+    uint4 cur[J], cd[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      xf[j][0] = bf16lo(nxt[j].x); xf[j][1] = bf16hi(nxt[j].x);
-      xf[j][2] = bf16lo(nxt[j].y); xf[j][3] = bf16hi(nxt[j].y);
-      xf[j][4] = bf16lo(nxt[j].z); xf[j][5] = bf16hi(nxt[j].z);
-      xf[j][6] = bf16lo(nxt[j].w); xf[j][7] = bf16hi(nxt[j].w);
-    }
-    if (ADD) {
-      // residual sum in bf16: each sum rounded once (RNE), stored, then normed
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const uint32_t dw[4] = {nd[j].x, nd[j].y, nd[j].z, nd[j].w};
-        uint32_t sw[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          sw[e] = pack_bf16x2(xf[j][2 * e] + bf16lo(dw[e]), xf[j][2 * e + 1] + bf16hi(dw[e]));
-          xf[j][2 * e] = bf16lo(sw[e]);
-          xf[j][2 * e + 1] = bf16hi(sw[e]);
-        }
-        const int c = lane + 64 * j;
-        if (FULL || c < nch) xout[row * nch + c] = make_uint4(sw[0], sw[1], sw[2], sw[3]);
-      }
+      cur[j] = nxt[j];
+      cd[j] = ADD ? nd[j] : make_uint4(0, 0, 0, 0);
     }
     if (row + wstride < rows) {                                // prefetch the next row
       load_row(x, row + wstride, nxt);
       if (ADD) load_row(delta, row + wstride, nd);
     }
-
-    double acc = 0.0;
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc += (double)(xf[j][e] * xf[j][e]);
-    acc = wave_sum_f64(acc);
-    const float var = (float)acc / dimf;
-    const float ve = var + eps;
-    const float rb = round_bf16((float)(1.0 / __builtin_sqrt((double)ve)));
-
+    uint4 yo[J];
+    uint2 qo[J];
+    float so[J];
+    norm_row<J, QUANT, FULL, ADD>(cur, cd, g, lane, nch, dimf, eps, yo, qo, so);
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const int c = lane + 64 * j;
-      float yv[8];
-      uint4 o;
-      uint32_t* ow = reinterpret_cast<uint32_t*>(&o);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t tp = pack_bf16x2(xf[j][2 * e] * rb, xf[j][2 * e + 1] * rb);
-        const uint32_t yp = pack_bf16x2(bf16lo(tp) * g[j][2 * e], bf16hi(tp) * g[j][2 * e + 1]);
-        ow[e] = yp;
-        yv[2 * e] = bf16lo(yp);
-        yv[2 * e + 1] = bf16hi(yp);
-      }
-      if ((FULL || c < nch) && y) stg_stream(&y[row * nch + c], o);
-      if (QUANT) {
-        const float m = amax3(amax3(yv[0], yv[1], yv[2]), amax3(yv[3], yv[4], yv[5]),
-                              __builtin_elementwise_maximum(__builtin_fabsf(yv[6]), __builtin_fabsf(yv[7])));
-        // wave-uniform: all lanes take part in the DPP reduction
-        const uint32_t mb = row16_max_u32(__float_as_uint(m));
-        const float sc = block_scale_bf16(mb);
-        if (FULL || c < nch) {
-          Divider d(sc);
-          uint2 qo;
-          if (d.fast) {
-            qo.x = e4m3x4(d.div(yv[0]), d.div(yv[1]), d.div(yv[2]), d.div(yv[3]));
-            qo.y = e4m3x4(d.div(yv[4]), d.div(yv[5]), d.div(yv[6]), d.div(yv[7]));
-          } else {
-            uint32_t b[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) b[e] = e4m3_nonfinite_scale(yv[e], sc);
-            qo.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-            qo.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
-          }
-          stg_stream(&q[row * nch + c], qo);
-          if ((lane & 15) == 0) s[row * (nch >> 4) + (c >> 4)] = sc;
+      if (FULL || c < nch) {
+        if (ADD) xout[row * nch + c] = cur[j];   // residual sum in bf16
+        if (y) stg_stream(&y[row * nch + c], yo[j]);
+        if (QUANT) {
+          stg_stream(&q[row * nch + c], qo[j]);
+          if ((lane & 15) == 0) s[row * (nch >> 4) + (c >> 4)] = so[j];
         }
       }
     }

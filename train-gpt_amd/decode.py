@@ -143,15 +143,23 @@ class FP8Decoder:
     exact_gemv: for 1-2 rows use the MFMA GEMV (the GEMM's block arithmetic)
     rather than the faster VALU one (tg_gemv_fp8_rowdot); default: on with
     decode_attn "sdpa" (the bit-exact mode), off with "hip".
+    fused: with the VALU GEMV and at most 2 rows, a decode step runs each norm
+    (or residual add + norm) and the relu^2 quantization inside the GEMV that
+    consumes them (tg_rms_norm_fp8_gemv, tg_relu2_fp8_gemv): 5 kernels per
+    layer instead of 8, the same bits.  Default: on where it applies.
     """
 
     def __init__(self, params, cfg: Config, layout: str = "128x128", max_batch: int = 1,
-                 decode_attn: str = "hip", exact_gemv: bool = None):
+                 decode_attn: str = "hip", exact_gemv: bool = None, fused: bool = None):
         _check_fp8_dims(cfg)
         if decode_attn not in ("hip", "sdpa"):
             raise ValueError("decode_attn must be 'hip' or 'sdpa'")
         self.decode_attn = decode_attn
         self.exact_gemv = decode_attn == "sdpa" if exact_gemv is None else bool(exact_gemv)
+        can_fuse = not self.exact_gemv and max_batch <= 2 and cfg.d_model <= 4096
+        if fused and not can_fuse:
+            raise ValueError("fused decode steps need exact_gemv=False, max_batch <= 2 and d_model <= 4096")
+        self.fused = can_fuse if fused is None else bool(fused)
         if not 1 <= max_batch <= 64:
             raise ValueError("max_batch must be in [1, 64] (decode rows per GEMV)")
         self.cfg = cfg
@@ -251,6 +259,8 @@ class FP8Decoder:
 
     # -- graph-capturable decode step: the position lives in device memory --
     def _step_dev(self, tok: torch.Tensor, t: torch.Tensor, B: int) -> torch.Tensor:
+        if self.fused:
+            return self._step_dev_fused(tok, t, B)
         cfg = self.cfg
         H = cfg.n_heads
         x = self.embed[tok] + self.pos.index_select(0, t)                 # (B, d)
@@ -270,6 +280,33 @@ class FP8Decoder:
             nxt = self.layers[li + 1]["norm1"] if li + 1 < len(self.layers) else self.final_norm
             x, h_q, h_s, _ = kernels.add_rms_norm_fp8(x, m, nxt, cfg.rms_eps, inplace=True)
         logits = self.unembed.matmul_prequant(h_q, h_s, self.exact_gemv).float()            # model.py:96
+        return cfg.logit_cap * torch.tanh(logits / cfg.logit_cap)           # model.py:97
+
+    def _step_dev_fused(self, tok: torch.Tensor, t: torch.Tensor, B: int) -> torch.Tensor:
+        """_step_dev with each norm / relu^2 quantization inside the GEMV that
+        consumes it.  The residual stream alternates between two buffers
+        (a fused kernel reads one while its workgroup 0 writes the other)."""
+        cfg = self.cfg
+        H, eps = cfg.n_heads, cfg.rms_eps
+        xa = self.embed[tok] + self.pos.index_select(0, t)                # (B, d)
+        xb = torch.empty_like(xa)
+        qkv = self.layers[0]["wqkv"].matmul_rms_norm(xa, self.layers[0]["norm1"], eps)   # model.py:61-64
+        for li, lp in enumerate(self.layers):
+            if self.decode_attn == "hip":
+                o_q, o_s, _ = decode_attention(qkv, self.k_cache[li], self.v_cache[li], t, H)
+                a = lp["wo"].matmul_prequant(o_q, o_s)                     # model.py:68
+            else:
+                a = lp["wo"].matmul(self._sdpa_step(li, qkv, int(t.item())))
+            # x = x + a (model.py:75), norm2, w_up (model.py:71-72)
+            u = lp["w_up"].matmul_rms_norm(xa, lp["norm2"], eps, delta=a, xout=xb)
+            m = lp["w_down"].matmul_relu2(u)                                # model.py:72-73
+            # x = x + m (model.py:76), then the next layer's norm1 and q|k|v, or
+            # the final norm and the unembedding (model.py:93-96)
+            last = li + 1 == len(self.layers)
+            nxt = self.final_norm if last else self.layers[li + 1]["norm1"]
+            w = self.unembed if last else self.layers[li + 1]["wqkv"]
+            qkv = w.matmul_rms_norm(xb, nxt, eps, delta=m, xout=xa)
+        logits = qkv.float()
         return cfg.logit_cap * torch.tanh(logits / cfg.logit_cap)           # model.py:97
 
     def _sdpa_step(self, li: int, qkv: torch.Tensor, t: int) -> torch.Tensor:

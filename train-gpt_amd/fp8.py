@@ -534,6 +534,48 @@ class QuantizedWeight:
             return out
         return scaled_matmul(xq, xs, self.q.view(torch.uint8), self.scales, b_scale_bn=self.bn)
 
+    def matmul_rms_norm(self, x: torch.Tensor, gamma: torch.Tensor, eps: float,
+                        delta: torch.Tensor = None, xout: torch.Tensor = None) -> torch.Tensor:
+        """The norm that feeds this weight, fused with the GEMV, for 1-2 rows
+        (tg_rms_norm_fp8_gemv): out (M, N) bf16 = the FP8 rows of
+        rms_norm(x [+ delta]) (kernels.py:30-33, fp8.py:39-47) times the kept W.
+        With delta, xout (M, K) receives the residual sum bf16(x + delta); it
+        must not overlap x or delta.  Same bits as kernels.rms_norm_fp8 /
+        add_rms_norm_fp8 followed by matmul_prequant (the VALU GEMV)."""
+        K, N = self.shape
+        if x.dim() != 2 or x.shape[1] != K or x.dtype != torch.bfloat16:
+            raise ValueError(f"matmul_rms_norm: x must be bf16 (M, {K})")
+        if gamma.shape != (K,) or gamma.dtype != torch.bfloat16:
+            raise ValueError(f"matmul_rms_norm: gamma must be bf16 ({K},)")
+        if delta is not None:
+            if delta.shape != x.shape or delta.dtype != torch.bfloat16:
+                raise ValueError("matmul_rms_norm: delta must be bf16 with x's shape")
+            if xout is None or xout.shape != x.shape or xout.dtype != torch.bfloat16 or not xout.is_contiguous():
+                raise ValueError("matmul_rms_norm: with delta, xout must be a contiguous bf16 tensor of x's shape")
+        _L.require_gpu(x, self.q)
+        x = x.contiguous()
+        d = delta.contiguous() if delta is not None else None
+        out = torch.empty((x.shape[0], N), dtype=torch.bfloat16, device=x.device)
+        _L.check(_L.lib().tg_rms_norm_fp8_gemv(
+            _L.ptr(x), _L.ptr(d) if d is not None else None, _L.ptr(gamma.contiguous()), float(eps),
+            _L.ptr(xout) if d is not None else None, _L.ptr(self.q.view(torch.uint8)), _L.ptr(self.scales),
+            self.bn, _L.ptr(out), x.shape[0], N, K, _L.stream_of(x)))
+        return out
+
+    def matmul_relu2(self, u: torch.Tensor) -> torch.Tensor:
+        """FP8 rows of bf16(relu(u)^2) (model.py:72) times the kept W, fused, for
+        1-2 rows (tg_relu2_fp8_gemv); the same bits as quantize_relu2 followed by
+        matmul_prequant (the VALU GEMV)."""
+        K, N = self.shape
+        if u.dim() != 2 or u.shape[1] != K or u.dtype != torch.bfloat16:
+            raise ValueError(f"matmul_relu2: u must be bf16 (M, {K})")
+        _L.require_gpu(u, self.q)
+        u = u.contiguous()
+        out = torch.empty((u.shape[0], N), dtype=torch.bfloat16, device=u.device)
+        _L.check(_L.lib().tg_relu2_fp8_gemv(_L.ptr(u), _L.ptr(self.q.view(torch.uint8)), _L.ptr(self.scales),
+                                            self.bn, _L.ptr(out), u.shape[0], N, K, _L.stream_of(u)))
+        return out
+
     def state_dict(self):
         return {"q": self.q, "scales": self.scales}
 
