@@ -81,8 +81,10 @@ def measured_traffic():
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    # the GPU clock ramps for ~30 ms after idle (the first ~40 C3 steps run
+    # 5-25% slower than the steady state), so the default warm-up covers it
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=60)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--norm-iters", type=int, default=200)
     p.add_argument("--only", choices=["step", "norm_quant", "norm_bwd", "gemv", "bwd_bf16",
