@@ -867,7 +867,9 @@ __global__ __launch_bounds__(256) void gemv_rowdot_kernel(RowdotIn in, const uin
   // ---- prologue loads ----
   u32x4_t xr[PRO == PRO_X ? XL : 1];
   float xsr = 0.f;
-  uint4 nx[J], nd[J], ng[J];
+  uint4 nx[J], nd[J];
+  constexpr int CI = PRO == PRO_NORM || PRO == PRO_NORM_ADD ? (NX * J * 64 + 255) / 256 : 1;   // chunks per thread
+  uint4 ng[CI];
   uint4 rv[PRO == PRO_RELU2 ? XL : 1];
   if (PRO == PRO_X) {
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(in.xq, (uint32_t)(NX * K));
@@ -895,8 +897,15 @@ __global__ __launch_bounds__(256) void gemv_rowdot_kernel(RowdotIn in, const uin
       } else {
         nd[j] = make_uint4(0, 0, 0, 0);
       }
-      const u32x4_t vg = __builtin_amdgcn_raw_buffer_load_b128(rg, c < nch ? (uint32_t)c * 16u : (uint32_t)K * 2u, 0, 0);
-      ng[j] = make_uint4(vg.x, vg.y, vg.z, vg.w);
+    }
+    // gamma for this thread's chunks of the second phase (chunk c of the
+    // flattened (NX, K) rows uses gamma chunk c mod nch)
+#pragma unroll
+    for (int i = 0; i < CI; ++i) {
+      const int c = tid + 256 * i;
+      const uint32_t go = c < NX * nch ? (uint32_t)(c % nch) * 16u : (uint32_t)K * 2u;
+      const u32x4_t vg = __builtin_amdgcn_raw_buffer_load_b128(rg, go, 0, 0);
+      ng[i] = make_uint4(vg.x, vg.y, vg.z, vg.w);
     }
   } else {
     const __amdgpu_buffer_rsrc_t ru = make_rsrc(in.x, (uint32_t)(NX * K) * 2u);
@@ -922,22 +931,40 @@ __global__ __launch_bounds__(256) void gemv_rowdot_kernel(RowdotIn in, const uin
     for (int j = 0; j < XL; ++j) *reinterpret_cast<u32x4_t*>(xl + j * 4096 + tid * 16) = xr[j];
     sxs[tid] = xsr;
   } else if (PRO == PRO_NORM || PRO == PRO_NORM_ADD) {
+    // phase 1: wave m < NX takes row m's statistics (the norm kernel's own
+    // routine and lane layout, so the same f64 sum) and parks the residual
+    // sums (bf16) and r in LDS; phase 2: the 256 threads norm and quantize
+    // 8-element chunks, 16 consecutive chunks (one scale block) per DPP row
+    uint4* sums = reinterpret_cast<uint4*>(rowdot_lds + ((sx_off + NX * nkb * 4 + 15) & ~15));
+    float* rbs = reinterpret_cast<float*>(sums + NX * nch);
     if (wave < NX) {
-      float gm[J][8];
-#pragma unroll
-      for (int j = 0; j < J; ++j) unpack8(ng[j], gm[j]);
-      uint4 yo[J];
-      uint2 qo[J];
-      float so[J];
-      norm_row<J, true, false, PRO == PRO_NORM_ADD>(nx, nd, gm, lane, nch, (float)K, in.eps, yo, qo, so);
+      const float rb = norm_row_rb<J, PRO == PRO_NORM_ADD>(nx, nd, (float)K, in.eps);
 #pragma unroll
       for (int j = 0; j < J; ++j) {
         const int c = lane + 64 * j;
         if (c < nch) {
-          *reinterpret_cast<uint2*>(xl + wave * K + c * 8) = qo[j];
-          if ((lane & 15) == 0) sxs[wave * nkb + (c >> 4)] = so[j];
+          sums[wave * nch + c] = nx[j];
           if (PRO == PRO_NORM_ADD && blockIdx.x == 0) in.xout[wave * nch + c] = nx[j];
         }
+      }
+      if (lane == 0) rbs[wave] = rb;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < CI; ++i) {
+      const int c = tid + 256 * i;
+      const bool valid = c < NX * nch;
+      const int m = valid ? c / nch : 0;
+      const uint4 xc = valid ? sums[c] : make_uint4(0, 0, 0, 0);
+      float g[8];
+      unpack8(ng[i], g);
+      uint4 y;
+      uint2 q;
+      float sc;
+      norm_chunk<true>(xc, g, rbs[m], valid, y, q, sc);
+      if (valid) {
+        *reinterpret_cast<uint2*>(xl + c * 8) = q;
+        if ((lane & 15) == 0) sxs[c >> 4] = sc;
       }
     }
   } else {
@@ -1202,7 +1229,11 @@ static int launch_rowdot(const RowdotIn& in, const uint8_t* w_q, const float* w_
     else launch_rowdot_k<NX, PRO, 8, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
   } else {
     const int sx_off = NX * k;   // a multiple of 128
-    const size_t lds = (size_t)sx_off + (size_t)NX * (k / 128) * 4;
+    // x bytes, x scales; for the norm prologues also the bf16 residual sums and r
+    const size_t lds = PRO == PRO_RELU2
+                           ? (size_t)sx_off + (size_t)NX * (k / 128) * 4
+                           : (((size_t)sx_off + (size_t)NX * (k / 128) * 4 + 15) & ~(size_t)15) +
+                                 (size_t)NX * k * 2 + 16;
     if constexpr (PRO == PRO_RELU2) {
       const int need = (NX * k + 2047) / 2048;
       if (need <= 1) launch_rowdot_k<NX, PRO, 1, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);

@@ -3,7 +3,8 @@
 // ones:
 //   norm_row   rmsnorm of one row by one wave (/root/reference/kernels.py:30-33),
 //              optionally after the bf16 residual add, and its FP8 rows
-//              (/root/reference/fp8.py:39-47)
+//              (/root/reference/fp8.py:39-47); norm_row_rb + norm_chunk are its
+//              two halves (row statistics by one wave, then any 8-element chunk)
 //   quant8     8 values of one 128-element block -> e4m3fn bytes
 //   relu2_bf16 bf16(relu(x)^2) (/root/reference/model.py:72 on bf16 tensors)
 #pragma once
@@ -65,21 +66,15 @@ __device__ __forceinline__ void relu2_bf16(float (&v)[8]) {
   }
 }
 
-// One row of _rms_norm_pure by one wave64; lane l holds the 16-byte chunks
-// l + 64j (j < J) of the row, nch chunks in all (FULL: nch == 64 J, no guards).
+// The statistics of one row of _rms_norm_pure, by one wave64; lane l holds
+// the 16-byte chunks l + 64j (j < J) of the row (chunks past the row are zero).
 //   var = mean(f32(x)^2)   f32 squares summed in f64, rounded to f32, / D in f32
 //   r   = bf16(rsqrt(var + eps))   (f64 1/sqrt, correctly rounded)
-//   y   = bf16(bf16(x * r) * g)
 // ADD: x is first replaced by the bf16 residual sum x + delta (each sum
-// rounded once), returned in xv for the caller to store.  QUANT: qo gets the
-// chunk's e4m3fn bytes and so its block scale (a 128-element block is one
-// 16-lane DPP row, so all 16 lanes of a block hold the same so).  Chunks past
-// nch read as zero and produce values the caller does not store.  Every lane
-// of the wave must call this (cross-lane sums and DPP maxima).
-template <int J, bool QUANT, bool FULL, bool ADD>
-__device__ __forceinline__ void norm_row(uint4 (&xv)[J], const uint4 (&dv)[J], const float (&g)[J][8],
-                                         int lane, int nch, float dimf, float eps, uint4 (&yo)[J],
-                                         uint2 (&qo)[J], float (&so)[J]) {
+// rounded once), returned in xv.  Returns r (the same in every lane).  Every
+// lane of the wave must call this (cross-lane sum).
+template <int J, bool ADD>
+__device__ __forceinline__ float norm_row_rb(uint4 (&xv)[J], const uint4 (&dv)[J], float dimf, float eps) {
   float xf[J][8];
 #pragma unroll
   for (int j = 0; j < J; ++j) unpack8(xv[j], xf[j]);
@@ -105,45 +100,61 @@ __device__ __forceinline__ void norm_row(uint4 (&xv)[J], const uint4 (&dv)[J], c
   acc = wave_sum_f64(acc);
   const float var = (float)acc / dimf;
   const float ve = var + eps;
-  const float rb = round_bf16((float)(1.0 / __builtin_sqrt((double)ve)));
+  return round_bf16((float)(1.0 / __builtin_sqrt((double)ve)));
+}
 
+// y = bf16(bf16(x * r) * g) of one 8-element chunk and, with QUANT, its
+// e4m3fn bytes q and block scale s (fp8.py:39-47 on the bf16 y).  The 16
+// lanes of a DPP row must hold the 16 chunks of one 128-element block, and
+// every lane must call this (DPP maximum); `valid` only gates the divide.
+template <bool QUANT>
+__device__ __forceinline__ void norm_chunk(const uint4& xc, const float (&g)[8], float rb, bool valid,
+                                           uint4& y, uint2& q, float& s) {
+  float xf[8], yv[8];
+  unpack8(xc, xf);
+  uint32_t ow[4];
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int c = lane + 64 * j;
-    float yv[8];
-    uint32_t ow[4];
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t tp = pack_bf16x2(xf[2 * e] * rb, xf[2 * e + 1] * rb);
+    const uint32_t yp = pack_bf16x2(bf16lo(tp) * g[2 * e], bf16hi(tp) * g[2 * e + 1]);
+    ow[e] = yp;
+    yv[2 * e] = bf16lo(yp);
+    yv[2 * e + 1] = bf16hi(yp);
+  }
+  y = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+  if (QUANT) {
+    const float m = amax3(amax3(yv[0], yv[1], yv[2]), amax3(yv[3], yv[4], yv[5]),
+                          __builtin_elementwise_maximum(__builtin_fabsf(yv[6]), __builtin_fabsf(yv[7])));
+    const uint32_t mb = row16_max_u32(__float_as_uint(m));   // all lanes take part
+    const float sc = block_scale_bf16(mb);
+    s = sc;
+    q = make_uint2(0, 0);
+    if (valid) {
+      Divider d(sc);
+      if (d.fast) {
+        q.x = e4m3x4(d.div(yv[0]), d.div(yv[1]), d.div(yv[2]), d.div(yv[3]));
+        q.y = e4m3x4(d.div(yv[4]), d.div(yv[5]), d.div(yv[6]), d.div(yv[7]));
+      } else {
+        uint32_t b[8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t tp = pack_bf16x2(xf[j][2 * e] * rb, xf[j][2 * e + 1] * rb);
-      const uint32_t yp = pack_bf16x2(bf16lo(tp) * g[j][2 * e], bf16hi(tp) * g[j][2 * e + 1]);
-      ow[e] = yp;
-      yv[2 * e] = bf16lo(yp);
-      yv[2 * e + 1] = bf16hi(yp);
-    }
-    yo[j] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
-    if (QUANT) {
-      const float m = amax3(amax3(yv[0], yv[1], yv[2]), amax3(yv[3], yv[4], yv[5]),
-                            __builtin_elementwise_maximum(__builtin_fabsf(yv[6]), __builtin_fabsf(yv[7])));
-      // wave-uniform: all lanes take part in the DPP reduction
-      const uint32_t mb = row16_max_u32(__float_as_uint(m));
-      const float sc = block_scale_bf16(mb);
-      so[j] = sc;
-      qo[j] = make_uint2(0, 0);
-      if (FULL || c < nch) {
-        Divider d(sc);
-        if (d.fast) {
-          qo[j].x = e4m3x4(d.div(yv[0]), d.div(yv[1]), d.div(yv[2]), d.div(yv[3]));
-          qo[j].y = e4m3x4(d.div(yv[4]), d.div(yv[5]), d.div(yv[6]), d.div(yv[7]));
-        } else {
-          uint32_t b[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) b[e] = e4m3_nonfinite_scale(yv[e], sc);
-          qo[j].x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-          qo[j].y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
-        }
+        for (int e = 0; e < 8; ++e) b[e] = e4m3_nonfinite_scale(yv[e], sc);
+        q.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+        q.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
       }
     }
   }
+}
+
+// One row of _rms_norm_pure by one wave64 (norm_row_rb, then norm_chunk for
+// each of the lane's chunks); outputs per chunk: yo (bf16 y), qo (e4m3 bytes),
+// so (block scale).  FULL: nch == 64 J (no guards).
+template <int J, bool QUANT, bool FULL, bool ADD>
+__device__ __forceinline__ void norm_row(uint4 (&xv)[J], const uint4 (&dv)[J], const float (&g)[J][8],
+                                         int lane, int nch, float dimf, float eps, uint4 (&yo)[J],
+                                         uint2 (&qo)[J], float (&so)[J]) {
+  const float rb = norm_row_rb<J, ADD>(xv, dv, dimf, eps);
+#pragma unroll
+  for (int j = 0; j < J; ++j) norm_chunk<QUANT>(xv[j], g[j], rb, FULL || lane + 64 * j < nch, yo[j], qo[j], so[j]);
 }
 
 }  // namespace tg
