@@ -19,6 +19,7 @@
 // not read back from the cache.
 #include "tg_device.h"
 #include "tg_host.h"
+#include "gemm_tile.h"
 
 namespace tg {
 
@@ -34,22 +35,83 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// One group of kAttnUnroll key slices per lane: keys (i0 + u) * 16 + 4 wave + kr.
+// Rows at or past S fall outside the buffer and read zero (they are never used).
+struct KvGroup {
+  uint4 k[kAttnUnroll], v[kAttnUnroll];
+};
+
+__device__ __forceinline__ void kv_load(KvGroup& G, const __amdgpu_buffer_rsrc_t& rk,
+                                        const __amdgpu_buffer_rsrc_t& rv, int64_t i0, int wave, int kr,
+                                        int dl) {
+#pragma unroll
+  for (int u = 0; u < kAttnUnroll; ++u) {
+    const int64_t j = (i0 + u) * (4 * kAttnWaves) + 4 * wave + kr;
+    const uint32_t off = (uint32_t)((j * kAttnDh + dl * 8) * 2);   // S <= 2^23 keeps this below 2^32
+    const u32x4_t a = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
+    const u32x4_t b = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+    G.k[u] = make_uint4(a.x, a.y, a.z, a.w);
+    G.v[u] = make_uint4(b.x, b.y, b.z, b.w);
+  }
+}
+
+// online-softmax update of a lane row with the keys of group G; keys past t
+// are skipped, key t is the new (k, v) from the projection output
+__device__ __forceinline__ void kv_step(const KvGroup& G, int64_t i0, int64_t t, int wave, int kr,
+                                        const float (&qf)[8], const uint4& knew, const uint4& vnew, float scale,
+                                        float& m, float& l, float (&acc)[8]) {
+#pragma unroll
+  for (int u = 0; u < kAttnUnroll; ++u) {
+    const int64_t j = (i0 + u) * (4 * kAttnWaves) + 4 * wave + kr;
+    const uint4 k = j < t ? G.k[u] : knew, v = j < t ? G.v[u] : vnew;
+    float d = qf[0] * bf16lo(k.x);
+    d = __builtin_fmaf(qf[1], bf16hi(k.x), d);
+    d = __builtin_fmaf(qf[2], bf16lo(k.y), d);
+    d = __builtin_fmaf(qf[3], bf16hi(k.y), d);
+    d = __builtin_fmaf(qf[4], bf16lo(k.z), d);
+    d = __builtin_fmaf(qf[5], bf16hi(k.z), d);
+    d = __builtin_fmaf(qf[6], bf16lo(k.w), d);
+    d = __builtin_fmaf(qf[7], bf16hi(k.w), d);
+    const float sc = row16_sum(d) * scale;
+    if (j <= t) {                                        // uniform over the 16-lane row
+      const float mn = sc > m ? sc : m;
+      const float corr = __expf(m - mn), p = __expf(sc - mn);
+      l = l * corr + p;
+      acc[0] = __builtin_fmaf(p, bf16lo(v.x), acc[0] * corr);
+      acc[1] = __builtin_fmaf(p, bf16hi(v.x), acc[1] * corr);
+      acc[2] = __builtin_fmaf(p, bf16lo(v.y), acc[2] * corr);
+      acc[3] = __builtin_fmaf(p, bf16hi(v.y), acc[3] * corr);
+      acc[4] = __builtin_fmaf(p, bf16lo(v.z), acc[4] * corr);
+      acc[5] = __builtin_fmaf(p, bf16hi(v.z), acc[5] * corr);
+      acc[6] = __builtin_fmaf(p, bf16lo(v.w), acc[6] * corr);
+      acc[7] = __builtin_fmaf(p, bf16hi(v.w), acc[7] * corr);
+      m = mn;
+    }
+  }
+}
+
 __global__ __launch_bounds__(kAttnWaves * 64) void decode_attention_kernel(
     const uint16_t* __restrict__ qkv, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
     const int64_t* __restrict__ tpos, uint8_t* __restrict__ oq, float* __restrict__ os,
     uint16_t* __restrict__ ob, int H, int S, float scale) {
   const int bh = blockIdx.x;
   const int b = bh / H, h = bh - b * H;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int dl = lane & 15, kr = lane >> 4;            // dims 8 dl .. +7 of key row kr
-  const int64_t t = *tpos;
   const int hd = H * kAttnDh;
+  const uint16_t* row = qkv + (int64_t)b * 3 * hd;
+  const int64_t cbase = ((int64_t)b * H + h) * S * kAttnDh;   // (b, h, 0, 0) of the caches
+  // the first key group's loads do not wait for t: rows past t are read and
+  // not used, rows past S read zero (the buffers span this head's S rows)
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc + cbase, (uint32_t)S * kAttnDh * 2u);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + cbase, (uint32_t)S * kAttnDh * 2u);
+  KvGroup A, B;
+  kv_load(A, rk, rv, 0, wave, kr, dl);
+  const int64_t t = *tpos;
   if (t < 0 || t >= S) {                   // position outside the cache: touch nothing
     if (threadIdx.x == 0) os[(int64_t)b * H + h] = __builtin_nanf("");
     return;
   }
-  const uint16_t* row = qkv + (int64_t)b * 3 * hd;
-  const int64_t cbase = ((int64_t)b * H + h) * S * kAttnDh;   // (b, h, 0, 0) of the caches
 
   float qf[8];
   {
@@ -64,55 +126,24 @@ __global__ __launch_bounds__(kAttnWaves * 64) void decode_attention_kernel(
     *reinterpret_cast<uint4*>(vc + cbase + t * kAttnDh + dl * 8) = vnew;
   }
 
-  // online softmax over keys j = 16 i + 4 wave + kr (i = 0, 1, ...), j <= t
+  // online softmax over keys j = 16 i + 4 wave + kr (i = 0, 1, ...), j <= t;
+  // two key groups in flight: the next group's loads go out before the
+  // current group's arithmetic (whole pairs in the loop, no exit inside it)
   float m = -__builtin_inff(), l = 0.0f, acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
   const int64_t nk = t + 1;
   const int64_t ngroups = (nk + 4 * kAttnWaves - 1) / (4 * kAttnWaves);
-  for (int64_t i0 = 0; i0 < ngroups; i0 += kAttnUnroll) {
-    uint4 kv[kAttnUnroll], vv[kAttnUnroll];
-    int64_t js[kAttnUnroll];
-#pragma unroll
-    for (int u = 0; u < kAttnUnroll; ++u) {
-      const int64_t j = (i0 + u) * (4 * kAttnWaves) + 4 * wave + kr;
-      js[u] = j;
-      if (j < t) {
-        kv[u] = *reinterpret_cast<const uint4*>(kc + cbase + j * kAttnDh + dl * 8);
-        vv[u] = *reinterpret_cast<const uint4*>(vc + cbase + j * kAttnDh + dl * 8);
-      } else {
-        kv[u] = knew;
-        vv[u] = vnew;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kAttnUnroll; ++u) {
-      const uint4 k = kv[u], v = vv[u];
-      float d = qf[0] * bf16lo(k.x);
-      d = __builtin_fmaf(qf[1], bf16hi(k.x), d);
-      d = __builtin_fmaf(qf[2], bf16lo(k.y), d);
-      d = __builtin_fmaf(qf[3], bf16hi(k.y), d);
-      d = __builtin_fmaf(qf[4], bf16lo(k.z), d);
-      d = __builtin_fmaf(qf[5], bf16hi(k.z), d);
-      d = __builtin_fmaf(qf[6], bf16lo(k.w), d);
-      d = __builtin_fmaf(qf[7], bf16hi(k.w), d);
-      const float s = row16_sum(d) * scale;
-      if (js[u] <= t) {                                  // uniform over the 16-lane row
-        const float mn = s > m ? s : m;
-        const float corr = __expf(m - mn), p = __expf(s - mn);
-        l = l * corr + p;
-        acc[0] = __builtin_fmaf(p, bf16lo(v.x), acc[0] * corr);
-        acc[1] = __builtin_fmaf(p, bf16hi(v.x), acc[1] * corr);
-        acc[2] = __builtin_fmaf(p, bf16lo(v.y), acc[2] * corr);
-        acc[3] = __builtin_fmaf(p, bf16hi(v.y), acc[3] * corr);
-        acc[4] = __builtin_fmaf(p, bf16lo(v.z), acc[4] * corr);
-        acc[5] = __builtin_fmaf(p, bf16hi(v.z), acc[5] * corr);
-        acc[6] = __builtin_fmaf(p, bf16lo(v.w), acc[6] * corr);
-        acc[7] = __builtin_fmaf(p, bf16hi(v.w), acc[7] * corr);
-        m = mn;
-      }
-    }
+  const int64_t nit = (ngroups + kAttnUnroll - 1) / kAttnUnroll;   // >= 1
+  int64_t i0 = 0;
+  for (int64_t p = 0; p + 1 < nit; p += 2) {
+    kv_load(B, rk, rv, i0 + kAttnUnroll, wave, kr, dl);
+    kv_step(A, i0, t, wave, kr, qf, knew, vnew, scale, m, l, acc);
+    kv_load(A, rk, rv, i0 + 2 * kAttnUnroll, wave, kr, dl);
+    kv_step(B, i0 + kAttnUnroll, t, wave, kr, qf, knew, vnew, scale, m, l, acc);
+    i0 += 2 * kAttnUnroll;
   }
+  if (nit & 1) kv_step(A, i0, t, wave, kr, qf, knew, vnew, scale, m, l, acc);
 
   // merge the 16 partial states (4 key rows x 4 waves) in a fixed order
   __shared__ float sm[16], sl[16];
@@ -177,7 +208,7 @@ extern "C" int tg_decode_attention(const void* qkv, void* k_cache, void* v_cache
   if (head_dim != kAttnDh) return einval("decode_attention: head_dim must be 128 (one scale block)");
   if (B < 0 || H <= 0 || S <= 0) return einval("decode_attention: bad shape");
   if (B == 0) return TG_OK;
-  if (B * H > 0x7FFFFFFF || S > 0x7FFFFFFF) return einval("decode_attention: shape too large");
+  if (B * H > 0x7FFFFFFF || S > (1 << 23)) return einval("decode_attention: shape too large (S <= 2^23)");
   if (!qkv || !k_cache || !v_cache || !t || !o_q || !o_s) return einval("decode_attention: null pointer");
   if (!aligned(qkv, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(o_q, 8) ||
       (o && !aligned(o, 16)))
