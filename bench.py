@@ -88,7 +88,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--norm-iters", type=int, default=200)
     p.add_argument("--only", choices=["step", "norm_quant", "norm_bwd", "gemv", "bwd_bf16",
-                                      "block_step", "xent", "decode", "vendor_gemm"],
+                                      "block_step", "xent", "decode", "vendor_gemm", "c1"],
                    help="run one secondary workload alone and print its JSON object")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (calibrates the FETCH_SIZE / "
@@ -422,6 +422,84 @@ def bench_vendor_gemm(dev, iters):
             "by_gemm": out}
 
 
+def _dequant(q, s):
+    """e4m3 bytes (R, C) uint8 and 1x128 scales (R, C/128) f32 -> f32 (R, C)."""
+    import torch
+    return q.view(torch.float8_e4m3fn).float() * s.repeat_interleave(128, dim=1)
+
+
+def _maxrel(a, b):
+    d = (a.float() - b.float()).abs().max()
+    return round(float(d / b.float().abs().max().clamp_min(1e-30)), 6)
+
+
+def step_accuracy(step, rows=256):
+    """Error of the step's three FP8 GEMM outputs on their first `rows` rows,
+    max-abs-normalised, against the f32 product of the same dequantized bytes
+    (the parity bar) and against a bf16 matmul of the unquantized operands
+    (f32 accumulation: the error FP8 adds), both computed by torch on the GPU
+    outside the timed region."""
+    import torch
+    r = rows
+    xf, wf, dyf = step.x.float(), step.w.float(), step.dy.float()
+    out = {"rows_checked": r}
+    ref = _dequant(step.qx[:r], step.sx[:r]) @ _dequant(step.qwt, step.swt).t()
+    out["y_vs_dequant_f32"] = _maxrel(step.y[:r], ref)
+    out["y_vs_bf16_matmul"] = _maxrel(step.y[:r], xf[:r] @ wf)
+    ref = _dequant(step.qdy[:r], step.sdy[:r]) @ _dequant(step.qw, step.sw).t()
+    out["dx_vs_dequant_f32"] = _maxrel(step.dx[:r], ref)
+    out["dx_vs_bf16_matmul"] = _maxrel(step.dx[:r], dyf[:r] @ wf.t())
+    ref = _dequant(step.qxt[:r], step.sxt[:r]) @ _dequant(step.qdyt, step.sdyt).t()
+    out["dw_vs_dequant_f32"] = _maxrel(step.dw[:r], ref)
+    out["dw_vs_bf16_matmul"] = _maxrel(step.dw[:r], xf.t()[:r] @ dyf)
+    del xf, wf, dyf, ref
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_c1(dev, iters):
+    """Config 1: the forward block_scaled_matmul at x[2048,768] . W[768,3072]
+    (tg_block_scaled_matmul: both quantizations + the GEMM), and the GEMM alone
+    on the quantized operands; launch-bound at this size (1.9 us at peak)."""
+    import torch
+    import _tglib as L
+    lib = L.lib()
+    M, K, N = 2048, 768, 3072
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    x = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn((K, N), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    st = L.stream_of(x)
+    ws_bytes = lib.tg_block_scaled_matmul_workspace(M, N, K, 128)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+
+    def fwd(i):
+        L.check(lib.tg_block_scaled_matmul(L.ptr(x), L.ptr(w), L.ptr(y), M, N, K, 128, L.ptr(ws),
+                                           ws_bytes, st))
+    us = _mean_launch_us(fwd, iters)
+    qx = torch.empty((M, K), dtype=torch.uint8, device=dev)
+    sx = torch.empty((M, K // 128), dtype=torch.float32, device=dev)
+    qwt = torch.empty((N, K), dtype=torch.uint8, device=dev)
+    swt = torch.empty((N, K // 128), dtype=torch.float32, device=dev)
+    L.check(lib.tg_quantize_rows(L.ptr(x), L.TG_DTYPE_BF16, M, K, 128, L.ptr(qx), L.ptr(sx), st))
+    L.check(lib.tg_quantize_cols(L.ptr(w), L.TG_DTYPE_BF16, K, N, 128, L.ptr(qwt), L.ptr(swt), st))
+    y2 = torch.empty_like(y)
+
+    def gemm(i):
+        L.check(lib.tg_gemm_fp8_nt(L.ptr(qx), L.ptr(sx), L.ptr(qwt), L.ptr(swt), 1, L.ptr(y2),
+                                   L.TG_DTYPE_BF16, M, N, K, 128, st))
+    us_gemm = _mean_launch_us(gemm, iters)
+    flop = 2.0 * M * N * K
+    ref = _dequant(qx, sx) @ _dequant(qwt, swt).t()
+    return {"workload": "C1 block_scaled_matmul forward, x[2048,768] bf16, W[768,3072] bf16, 1x128 scales",
+            "us_per_call": round(us, 3), "tflops_with_quantization": round(flop / us / 1e6, 1),
+            "us_gemm": round(us_gemm, 3), "tflops_gemm": round(flop / us_gemm / 1e6, 1),
+            "y_vs_dequant_f32": _maxrel(y, ref),
+            "y_vs_bf16_matmul": _maxrel(y, x.float() @ w.float()),
+            "same_bits_composite_vs_gemm": bool(torch.equal(y.view(torch.int16), y2.view(torch.int16)))}
+
+
 def bench_xent(dev, iters):
     """Config 4's head: tg_logit_cap_xent_fwd / _bwd on bf16 logits [8192, 50304]
     (824 MB, larger than the Infinity Cache, so one buffer set)."""
@@ -568,7 +646,8 @@ def main():
               "bwd_bf16": lambda d, _: bench_bwd_bf16(d, 10),
               "block_step": lambda d, _: bench_block(d), "xent": bench_xent,
               "decode": lambda d, _: bench_decode(d),
-              "vendor_gemm": lambda d, _: bench_vendor_gemm(d, 20)}[args.only]
+              "vendor_gemm": lambda d, _: bench_vendor_gemm(d, 20),
+              "c1": bench_c1}[args.only]
         print(json.dumps({args.only: fn(dev, args.norm_iters)}))
         return
     step = Step(dev)
@@ -590,9 +669,11 @@ def main():
     gemm_ms = sum(s.elapsed_time(e) for s, e in ev) / len(ev)
     gemm_tflops = GEMM_FLOP / (gemm_ms * 1e-3) / 1e12
     value = STEP_FLOP / (ms_step * 1e-3) / 1e12
+    accuracy = step_accuracy(step)
     if args.only == "step":
-        norm = norm_bwd = gemv = bwd_bf16 = block_step = xent = dec = None
+        norm = norm_bwd = gemv = bwd_bf16 = block_step = xent = dec = c1 = None
     else:
+        c1 = bench_c1(dev, args.norm_iters)
         norm = bench_norm(dev, args.norm_iters)
         norm_bwd = bench_norm_bwd(dev, args.norm_iters)
         gemv = bench_gemv(dev, args.norm_iters)
@@ -613,6 +694,8 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": FP8_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic().get("gemm_fp8_nt_256")},
+        "accuracy": accuracy,
+        "c1": c1,
         "norm_quant": norm,
         "norm_bwd": norm_bwd,
         "gemv": gemv,
@@ -623,7 +706,7 @@ def main():
     }
     if args.only == "step":                      # the headline step alone (no secondary workloads)
         out = {k: out[k] for k in ("metric", "value", "unit", "ms_per_step", "gemm_us_per_launch",
-                                   "roofline")}
+                                   "roofline", "accuracy")}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))
