@@ -151,10 +151,9 @@ class Step:
         L, lib, st, p = self.L, self.lib, self.stream, self.L.ptr
         # forward (fp8.py:66,68,70-78); x.T along M and W along N are the
         # backward's operands, kept from the same reads
-        L.check(lib.tg_quantize_dual(p(self.x), M3, K3, 128, p(self.qx), p(self.sx), p(self.qxt),
-                                     p(self.sxt), st))
-        L.check(lib.tg_quantize_dual(p(self.w), K3, N3, 128, p(self.qw), p(self.sw), p(self.qwt),
-                                     p(self.swt), st))
+        L.check(lib.tg_quantize_dual_pair(p(self.x), M3, K3, p(self.qx), p(self.sx), p(self.qxt),
+                                          p(self.sxt), p(self.w), K3, N3, p(self.qw), p(self.sw),
+                                          p(self.qwt), p(self.swt), 128, st))
         self._gemm(self.qx, self.sx, self.qwt, self.swt, self.y, M3, N3, K3, ev)
         # dY along N (for dX) and dY.T along M (for dW) from one read of dY
         L.check(lib.tg_quantize_dual(p(self.dy), M3, N3, 128, p(self.qdy), p(self.sdy), p(self.qdyt),

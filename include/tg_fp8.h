@@ -61,6 +61,17 @@ int tg_quantize_cols(const void* x, int x_dtype, int64_t rows, int64_t cols, int
 int tg_quantize_dual(const void* x, int64_t rows, int64_t cols, int block_k, uint8_t* q,
                      float* scales, uint8_t* q_t, float* scales_t, void* stream);
 
+/* tg_quantize_dual of two tensors in one launch: the forward of fp8.py:50-78
+ * quantizes both operands (fp8.py:66 a along K, fp8.py:68 b.T along K); with
+ * the backward's forms kept from the same reads this is x along K + x.T along
+ * M and W along N + W.T along K.  Each tensor's outputs are bit-identical to
+ * tg_quantize_dual on it alone; a tensor with rows or cols 0 is skipped (its
+ * pointers may then be null).  The two tensors' outputs must not overlap. */
+int tg_quantize_dual_pair(const void* x0, int64_t rows0, int64_t cols0, uint8_t* q0, float* scales0,
+                          uint8_t* q_t0, float* scales_t0, const void* x1, int64_t rows1,
+                          int64_t cols1, uint8_t* q1, float* scales1, uint8_t* q_t1,
+                          float* scales_t1, int block_k, void* stream);
+
 /* jax.nn.scaled_matmul + bf16 cast as called at fp8.py:70-78 ("NT" layout):
  * c[m, n] = sum_kb a_s[m, kb] * b_s[n / b_scale_bn, kb] * sum_{k in kb} a_q[m, k] * b_q[n, k]
  * a_q: (M, K) e4m3fn, a_s: (M, K/128) f32; b_q: (N, K) e4m3fn;

@@ -119,6 +119,50 @@ def test_quantize_dual_equals_separate(dev, shape):
     assert np.array_equal(f32_bits(s), f32_bits(s1)) and np.array_equal(f32_bits(st), f32_bits(s2))
 
 
+@pytest.mark.parametrize("shapes", [((8192, 2048), (2048, 8192)),     # C3's x and W
+                                    ((384, 256), (8192, 8192)),      # job 1 at slot 6: identity order
+                                    ((1024, 1024), (8192, 8192)),    # job 1 at slot 64: XCD-blocked
+                                    ((128, 128), (256, 640))])
+def test_quantize_dual_pair_equals_dual(dev, shapes):
+    """tg_quantize_dual_pair = tg_quantize_dual on each tensor, bit for bit, with
+    the special-value rows of the oracle test planted in both tensors."""
+    rng = np.random.default_rng(sum(map(sum, shapes)))
+    xs = []
+    for shape in shapes:
+        x = ob.randn_bf16(rng, shape, std=0.02)
+        k = min(256, shape[1])
+        x[:10, :k] = _special_rows(rng, k)
+        xs.append(to_dev(x, dev))
+    pair = fp8.quantize_fp8_dual_pair(xs[0], xs[1])
+    for x, got in zip(xs, pair):
+        want = fp8.quantize_fp8_dual(x)
+        for g, w in zip(got, want):
+            if g.dtype == torch.float32:
+                assert np.array_equal(f32_bits(g), f32_bits(w))
+            else:
+                assert torch.equal(g.view(torch.uint8), w.view(torch.uint8))
+
+
+def test_quantize_dual_pair_skips_empty(dev):
+    """A tensor with no rows is skipped (null pointers allowed); the other is quantized."""
+    import _tglib as L
+    rng = np.random.default_rng(12)
+    x = to_dev(ob.randn_bf16(rng, (256, 384)), dev)
+    q = torch.empty((256, 384), dtype=torch.uint8, device=dev)
+    s = torch.empty((256, 3), dtype=torch.float32, device=dev)
+    qt = torch.empty((384, 256), dtype=torch.uint8, device=dev)
+    st = torch.empty((384, 2), dtype=torch.float32, device=dev)
+    P = L.ptr
+    L.check(L.lib().tg_quantize_dual_pair(None, 0, 384, None, None, None, None, P(x), 256, 384, P(q),
+                                          P(s), P(qt), P(st), 128, L.stream_of(x)))
+    want = fp8.quantize_fp8_dual(x)
+    assert torch.equal(q, want[0].view(torch.uint8)) and torch.equal(qt, want[2].view(torch.uint8))
+    assert np.array_equal(f32_bits(s), f32_bits(want[1])) and np.array_equal(f32_bits(st), f32_bits(want[3]))
+    with pytest.raises(ValueError, match="multiples of 128"):
+        L.check(L.lib().tg_quantize_dual_pair(P(x), 256, 384, P(q), P(s), P(qt), P(st), P(x), 200, 384,
+                                              P(q), P(s), P(qt), P(st), 128, L.stream_of(x)))
+
+
 def test_quantize_dual_special_values(dev):
     """Edge-case blocks in both directions against the oracle."""
     rng = np.random.default_rng(6)

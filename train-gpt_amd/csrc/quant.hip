@@ -10,6 +10,7 @@
 // load per lane), i.e. exactly one DPP row, so the block amax is four DPP
 // max steps with no LDS traffic.
 #include <stdarg.h>
+#include <stdio.h>
 #include <string.h>
 
 #include "row_ops.h"
@@ -207,25 +208,51 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(const uint16_t* __restr
 // blocks), which keeps a row-scale line on one XCD and a column-scale line on
 // two.  The host sets it when gridDim.x % 32 == 0, gridDim.y % 16 == 0 and
 // each XCD's share is a multiple of 512 tiles.
+//
+// One launch may carry two tensors (DualJobs): slots [0, nblk0) take the tiles
+// of job 0 and the rest those of job 1, each in its own row-major tile order
+// (gx tiles along x).  Two 1024-tile tensors (C3's x and W) then fill the
+// machine twice over and the second tensor's loads overlap the first one's
+// stores, where two launches each run one wave of workgroups.
+struct DualJob {
+  const uint4* x;
+  int64_t rows, cols;
+  uint2* q;
+  float* s;
+  uint8_t* qt;
+  float* st;
+  int gx, gy, xcd_blocks;
+};
+struct DualJobs {
+  DualJob job[2];
+  int nblk0;   // tiles of job 0; gridDim.x - nblk0 are job 1's
+};
+
 template <bool ROWS, bool GUARD>
-__global__ __launch_bounds__(256) void quant_dual_kernel(const uint4* __restrict__ x, int64_t rows,
-                                                         int64_t cols, uint2* __restrict__ q,
-                                                         float* __restrict__ s,
-                                                         uint8_t* __restrict__ qt,
-                                                         float* __restrict__ st, int xcd_blocks) {
+__global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
   // the raw tile (row pitch 272 B); once every column is in registers the
   // same memory stages the transposed bytes (column pitch 144 B)
   __shared__ uint32_t tile[128 * 68];
   uint32_t* tq = tile;
   const int tid = threadIdx.x;
-  int tx = blockIdx.x, ty = blockIdx.y;
-  if (xcd_blocks) {
-    const int slot = blockIdx.x + gridDim.x * blockIdx.y;
-    const int per_xcd = gridDim.x * gridDim.y / 8;
+  const bool second = (int)blockIdx.x >= jobs.nblk0;
+  const DualJob& J = second ? jobs.job[1] : jobs.job[0];
+  const uint4* __restrict__ x = J.x;
+  const int64_t rows = J.rows, cols = J.cols;
+  uint2* __restrict__ q = J.q;
+  float* __restrict__ s = J.s;
+  uint8_t* __restrict__ qt = J.qt;
+  float* __restrict__ st = J.st;
+  const int slot = (int)blockIdx.x - (second ? jobs.nblk0 : 0);
+  int tx = slot % J.gx, ty = slot / J.gx;
+  if (J.xcd_blocks) {
+    // slot % 8 is the XCD: the host sets xcd_blocks only on a job that
+    // starts at a multiple of 8
+    const int per_xcd = J.gx * J.gy / 8;
     const int t = (slot & 7) * per_xcd + (slot >> 3);     // position in XCD-contiguous order
     const int blk = t >> 9, w = t & 511;
-    tx = (blk % (gridDim.x / 32)) * 32 + (w & 31);
-    ty = (blk / (gridDim.x / 32)) * 16 + (w >> 5);
+    tx = (blk % (J.gx / 32)) * 32 + (w & 31);
+    ty = (blk / (J.gx / 32)) * 16 + (w >> 5);
   }
   const int64_t c0 = (int64_t)tx * 128, r0 = (int64_t)ty * 128;
   const int ch = tid & 15, rr = tid >> 4;
@@ -301,20 +328,47 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(const uint4* __restrict
   }
 }
 
+// One DualJob over x (rows, cols) in 128 x 128 tiles (a narrower last tile
+// along cols).  xcd_ok: the job's first slot is a multiple of 8, so the
+// XCD-blocked order may be used (when the tile grid has its shape).
+constexpr int64_t kDualMaxTiles = int64_t(1) << 23;   // slots fit one 1-D grid of 256-thread groups
+
+static int dual_job(DualJob& j, const char* who, const void* x, int64_t rows, int64_t cols, uint8_t* q,
+                    float* s, uint8_t* q_t, float* s_t, bool xcd_ok) {
+  const int64_t gx = (cols + 127) / 128, gy = rows / 128;
+  if (gx * gy > kDualMaxTiles) {
+    char msg[160];
+    snprintf(msg, sizeof msg, "%s: (rows / 128) x (cols / 128) must be <= %lld tiles", who,
+             (long long)kDualMaxTiles);
+    return einval(msg);
+  }
+  j.x = reinterpret_cast<const uint4*>(x);
+  j.rows = rows;
+  j.cols = cols;
+  j.q = reinterpret_cast<uint2*>(q);
+  j.s = s;
+  j.qt = q_t;
+  j.st = s_t;
+  j.gx = (int)gx;
+  j.gy = (int)gy;
+  j.xcd_blocks = xcd_ok && gx % 32 == 0 && gy % 16 == 0 && (gx * gy / 8) % 512 == 0;
+  return TG_OK;
+}
+
 int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, float* s_t,
                       hipStream_t st) {
   if (rows == 0 || cols == 0) return TG_OK;
   if (rows / 128 > 65535) return einval("quantize_cols: rows / 128 must be <= 65535");
   if (cols % 8 == 0 && aligned(x, 16)) {
     // 128 x 128 tiles: column pairs per LDS read, 64-byte contiguous stores
-    const dim3 g128((unsigned)((cols + 127) / 128), (unsigned)(rows / 128));
-    auto X = reinterpret_cast<const uint4*>(x);
+    DualJobs jobs{};
+    TG_TRY(dual_job(jobs.job[0], "quantize_cols", x, rows, cols, nullptr, nullptr, q_t, s_t, false));
+    jobs.nblk0 = jobs.job[0].gx * jobs.job[0].gy;
+    const dim3 grid((unsigned)jobs.nblk0);
     if (cols % 128 == 0)
-      hipLaunchKernelGGL((quant_dual_kernel<false, false>), g128, dim3(256), 0, st, X, rows, cols,
-                         nullptr, nullptr, q_t, s_t, 0);
+      hipLaunchKernelGGL((quant_dual_kernel<false, false>), grid, dim3(256), 0, st, jobs);
     else
-      hipLaunchKernelGGL((quant_dual_kernel<false, true>), g128, dim3(256), 0, st, X, rows, cols,
-                         nullptr, nullptr, q_t, s_t, 0);
+      hipLaunchKernelGGL((quant_dual_kernel<false, true>), grid, dim3(256), 0, st, jobs);
     return check_launch("quant_cols");
   }
   // rows not 16-byte aligned: the element-load kernel
@@ -328,14 +382,32 @@ int launch_quant_dual(const void* x, int64_t rows, int64_t cols, uint8_t* q, flo
                       float* s_t, hipStream_t st) {
   if (rows == 0 || cols == 0) return TG_OK;
   if (rows % 128 || cols % 128) return einval("quantize_dual: rows and cols must be multiples of 128");
-  if (rows / 128 > 65535) return einval("quantize_dual: rows / 128 must be <= 65535");
-  const int64_t gx = cols / 128, gy = rows / 128;
-  const int xcd_blocks =
-      gx % 32 == 0 && gy % 16 == 0 && (gx * gy / 8) % 512 == 0 && gx * gy < (int64_t(1) << 31);
-  hipLaunchKernelGGL((quant_dual_kernel<true, false>), dim3((unsigned)gx, (unsigned)gy), dim3(256), 0,
-                     st, reinterpret_cast<const uint4*>(x), rows, cols, reinterpret_cast<uint2*>(q), s,
-                     q_t, s_t, xcd_blocks);
+  DualJobs jobs{};
+  TG_TRY(dual_job(jobs.job[0], "quantize_dual", x, rows, cols, q, s, q_t, s_t, true));
+  jobs.nblk0 = jobs.job[0].gx * jobs.job[0].gy;
+  hipLaunchKernelGGL((quant_dual_kernel<true, false>), dim3((unsigned)jobs.nblk0), dim3(256), 0, st,
+                     jobs);
   return check_launch("quant_dual");
+}
+
+int launch_quant_dual_pair(const void* x0, int64_t rows0, int64_t cols0, uint8_t* q0, float* s0,
+                           uint8_t* qt0, float* st0, const void* x1, int64_t rows1, int64_t cols1,
+                           uint8_t* q1, float* s1, uint8_t* qt1, float* st1, hipStream_t st) {
+  const bool e0 = rows0 == 0 || cols0 == 0, e1 = rows1 == 0 || cols1 == 0;
+  if (e0 && e1) return TG_OK;
+  if (e0) return launch_quant_dual(x1, rows1, cols1, q1, s1, qt1, st1, st);
+  if (e1) return launch_quant_dual(x0, rows0, cols0, q0, s0, qt0, st0, st);
+  if (rows0 % 128 || cols0 % 128 || rows1 % 128 || cols1 % 128)
+    return einval("quantize_dual_pair: rows and cols must be multiples of 128");
+  DualJobs jobs{};
+  TG_TRY(dual_job(jobs.job[0], "quantize_dual_pair", x0, rows0, cols0, q0, s0, qt0, st0, true));
+  jobs.nblk0 = jobs.job[0].gx * jobs.job[0].gy;
+  TG_TRY(dual_job(jobs.job[1], "quantize_dual_pair", x1, rows1, cols1, q1, s1, qt1, st1,
+                  jobs.nblk0 % 8 == 0));
+  const int64_t total = (int64_t)jobs.nblk0 + (int64_t)jobs.job[1].gx * jobs.job[1].gy;
+  if (total > kDualMaxTiles) return einval("quantize_dual_pair: too many 128 x 128 tiles");
+  hipLaunchKernelGGL((quant_dual_kernel<true, false>), dim3((unsigned)total), dim3(256), 0, st, jobs);
+  return check_launch("quant_dual_pair");
 }
 
 // ---------------------------------------------------------------------------
@@ -543,4 +615,20 @@ extern "C" int tg_quantize_dual(const void* x, int64_t rows, int64_t cols, int b
   if (!aligned(x, 16) || !aligned(q, 8) || !aligned(q_t, 16))
     return einval("quantize_dual: x and q_t must be 16-byte, q 8-byte aligned");
   return launch_quant_dual(x, rows, cols, q, s, q_t, s_t, as_stream(stream));
+}
+
+extern "C" int tg_quantize_dual_pair(const void* x0, int64_t rows0, int64_t cols0, uint8_t* q0,
+                                     float* s0, uint8_t* q_t0, float* s_t0, const void* x1,
+                                     int64_t rows1, int64_t cols1, uint8_t* q1, float* s1,
+                                     uint8_t* q_t1, float* s_t1, int block_k, void* stream) {
+  if (block_k != 128) return einval("quantize_dual_pair: block_k must be 128");
+  if (rows0 < 0 || cols0 < 0 || rows1 < 0 || cols1 < 0) return einval("quantize_dual_pair: bad shape");
+  const bool u0 = rows0 > 0 && cols0 > 0, u1 = rows1 > 0 && cols1 > 0;
+  if ((u0 && (!x0 || !q0 || !s0 || !q_t0 || !s_t0)) || (u1 && (!x1 || !q1 || !s1 || !q_t1 || !s_t1)))
+    return einval("quantize_dual_pair: null pointer");
+  if ((u0 && (!aligned(x0, 16) || !aligned(q0, 8) || !aligned(q_t0, 16))) ||
+      (u1 && (!aligned(x1, 16) || !aligned(q1, 8) || !aligned(q_t1, 16))))
+    return einval("quantize_dual_pair: x and q_t must be 16-byte, q 8-byte aligned");
+  return launch_quant_dual_pair(x0, rows0, cols0, q0, s0, q_t0, s_t0, x1, rows1, cols1, q1, s1, q_t1,
+                                s_t1, as_stream(stream));
 }

@@ -150,6 +150,33 @@ def quantize_fp8_dual(x: torch.Tensor, block_k: int = DEFAULT_BLOCK_K):
     return q.view(e4), s, qt.view(e4), st
 
 
+def quantize_fp8_dual_pair(x0: torch.Tensor, x1: torch.Tensor, block_k: int = DEFAULT_BLOCK_K):
+    """quantize_fp8_dual of two tensors in one launch (the forward's a and b,
+    fp8.py:66,68, with the backward's forms from the same reads): returns the
+    two 4-tuples, bit for bit those of quantize_fp8_dual on each tensor."""
+    _L.require_gpu(x0, x1)
+    _check_block_k(block_k)
+    xs, outs, args = [], [], []
+    for x in (x0, x1):
+        if x.dim() != 2 or x.dtype != torch.bfloat16:
+            raise ValueError("quantize_fp8_dual_pair needs 2-D bfloat16 tensors")
+        R, C = x.shape
+        if R % block_k or C % block_k:
+            raise ValueError(f"K={R if R % block_k else C} not divisible by block_k={block_k}")
+        x = x.contiguous()
+        u8, f32 = torch.uint8, torch.float32
+        o = (torch.empty((R, C), dtype=u8, device=x.device),
+             torch.empty((R, C // block_k), dtype=f32, device=x.device),
+             torch.empty((C, R), dtype=u8, device=x.device),
+             torch.empty((C, R // block_k), dtype=f32, device=x.device))
+        xs.append(x)
+        outs.append(o)
+        args += [_L.ptr(x), R, C] + [_L.ptr(t) for t in o]
+    _L.check(_L.lib().tg_quantize_dual_pair(*args, block_k, _L.stream_of(xs[0])))
+    e4 = torch.float8_e4m3fn
+    return tuple((q.view(e4), s, qt.view(e4), st) for q, s, qt, st in outs)
+
+
 def scaled_matmul(a_q, a_s, b_q, b_s, b_scale_bn: int = 1, out_dtype=torch.bfloat16):
     """The scaled GEMM of fp8.py:70-76 on already-quantized operands ("NT"):
     a_q (M, K), b_q (N, K) e4m3fn; a_s (M, K/128), b_s (N or ceil(N/128), K/128) f32.
@@ -278,6 +305,12 @@ def _fp8_forward_quantized_residuals(a, b, block_k, need_da, need_db):
     """
     leading, K, N = _validate(a, b, block_k)
     a_2d = a.reshape(-1, K)
+    if need_db and need_da:
+        # a along K + a.T along M, and b along N + b.T along K: one launch
+        (qa, sa, qat, sat), (qb, sb, qbt, sbt) = quantize_fp8_dual_pair(a_2d, b, block_k)
+        u8 = torch.uint8
+        out = scaled_matmul(qa.view(u8), sa, qbt.view(u8), sbt)     # fp8.py:70-78
+        return out.reshape(*leading, N), (qat, sat), (qb, sb)
     if need_db:
         qa, sa, qat, sat = quantize_fp8_dual(a_2d, block_k)    # a along K, a.T along M
         res_a = (qat, sat)
