@@ -49,7 +49,11 @@ def test_layout_known_answer(dev):
                                    (300, 136, 1024), (2048, 3072, 768),
                                    # >= 128 tiles of 256 x 256: the large-tile kernel, with ragged
                                    # M / N edges and odd / even numbers of K blocks
-                                   (2100, 4000, 384), (4096, 4096, 256), (3000, 2900, 640)])
+                                   (2100, 4000, 384), (4096, 4096, 256), (3000, 2900, 640),
+                                   # more tiles than CUs: workgroups loop over 1-2 tiles, the next
+                                   # tile's first K block loaded during the current one's last;
+                                   # one K block per tile, and an odd count with N % 8 != 0
+                                   (5000, 5000, 128), (4300, 4404, 384)])
 def test_scaled_gemm_random(dev, M, N, K):
     rng = np.random.default_rng(M * 7 + N)
     a = ob.bf16_to_f32(ob.randn_bf16(rng, (M, K)))
@@ -66,9 +70,9 @@ def test_scaled_gemm_random(dev, M, N, K):
     np.testing.assert_array_equal(c16, ob.f32_to_bf16(c32))
 
 
-def test_scaled_gemm_weight_tiles_128x128(dev):
-    rng = np.random.default_rng(21)
-    M, N, K = 96, 300, 512
+@pytest.mark.parametrize("M,N,K", [(96, 300, 512), (4300, 4400, 384)])
+def test_scaled_gemm_weight_tiles_128x128(dev, M, N, K):
+    rng = np.random.default_rng(21 + M)
     a = ob.bf16_to_f32(ob.randn_bf16(rng, (M, K)))
     w_t = ob.bf16_to_f32(ob.randn_bf16(rng, (N, K), std=0.02))
     qa, sa = fp8_ref.quantize_fp8(a)

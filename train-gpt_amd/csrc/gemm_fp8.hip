@@ -191,6 +191,8 @@ __global__ __launch_bounds__(256, 2) void gemm_fp8_nt_kernel(
 // does not alias the fragment reads from the other and puts no wait
 // between them.
 // ---------------------------------------------------------------------------
+template <int V> using IntC = std::integral_constant<int, V>;
+
 __shared__ __attribute__((aligned(16))) uint8_t g256_a0[256 * 128];
 __shared__ __attribute__((aligned(16))) uint8_t g256_b0[256 * 128];
 __shared__ __attribute__((aligned(16))) float g256_s0[512];
@@ -255,7 +257,9 @@ __device__ __forceinline__ void promote4(v4f& acc, const v4f& p, float sa, const
   acc[3] = __builtin_fmaf(p[3], sa * sb.w, acc[3]);
 }
 
-// One K block kb from stage S.  MFMAs of n-tile j are issued while the 16x16
+// One K block from stage S; the copies issued here are those of the next K
+// block (kb_next of the tile the loader offsets in c point at; none if !more).
+// MFMAs of n-tile j are issued while the 16x16
 // results of n-tile j-1 are promoted (8 VALU per MFMA), so at most two tiles
 // of partial results are live and the VALU work runs in the MFMA shadow; the
 // B fragment and column scale of n-tile j+1 are read from LDS one region
@@ -267,7 +271,7 @@ __device__ __forceinline__ void promote4(v4f& acc, const v4f& p, float sa, const
 // LDS of stage S, so after the barrier stage S is free for block kb+2.
 template <int S>
 __device__ __forceinline__ void g256_compute_tail(const G256Ctx& c, v4f (&acc)[4][8], v8i (&af)[4],
-                                                  int kb_next) {
+                                                  int kb_next, bool more) {
   const uint8_t* lb = g256_b<S>();
   const float* ls = g256_s<S>();
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
@@ -283,8 +287,7 @@ __device__ __forceinline__ void g256_compute_tail(const G256Ctx& c, v4f (&acc)[4
   float4 sbn = read_sb(1);
   v4f pc[4];
   float4 sbc = read_sb(0);
-  const bool more = kb_next < c.nkb;                 // wave-uniform
-  const bool pf = more && c.wave < 4;                // loader waves
+  const bool pf = more && c.wave < 4;                // loader waves (more: wave-uniform)
   if (pf) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, p);
@@ -355,108 +358,51 @@ __device__ __forceinline__ void g256_compute_tail(const G256Ctx& c, v4f (&acc)[4
   for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][7]));
 }
 
-template <int BNS, bool OUT_F32>
-__global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
-    const uint8_t* __restrict__ A, const float* __restrict__ SA, const uint8_t* __restrict__ B,
-    const float* __restrict__ SB, void* __restrict__ C, int M, int N, int K, int tiles_m,
-    int tiles_n) {
-  G256Ctx c;
-  const int tid = threadIdx.x, lane = tid & 63;
-  c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: keeps descriptors in SGPRs
-  c.nkb = K >> 7;
+// The 64 x 128 result tile of one wave (output rows m0w.., columns n0w..).
+// bf16 with N % 8 == 0: through LDS stage S, which no wave reads once the
+// tile's last K block has passed its barrier: 8 KiB per wave, two halves of
+// 32 rows, each staged with 256-byte rows (16-byte chunk c of row r at
+// c ^ (r & 15), so the 16 rows one write instruction touches fall in
+// different banks) and then stored by 16 lanes per row (256 bytes).  A wave
+// reads back only what it wrote, and LDS completes a wave's accesses in
+// order, so waiting for its own writes is enough and the second half's writes
+// cannot overtake the first half's reads.  Written straight from registers,
+// every output line was assembled from eight 32-byte pieces and the Y GEMM
+// ran ~5% slower.
+template <int S, bool OUT_F32>
+__device__ __forceinline__ void g256_store_tile(const v4f (&acc)[4][8], void* __restrict__ C, int M,
+                                                int N, int m0w, int n0w, int wave, int lane_in) {
+  // an opaque copy of the lane index: the store addresses derive from it, so
+  // the compiler cannot hoist them out of the tile loop (where ~20 of them
+  // would stay live across the K loop and spill)
+  int lane = lane_in;
+  asm volatile("" : "+v"(lane));
   const int fr = lane & 15, fg = lane >> 4;
-  const int wm = c.wave >> 1, wn = c.wave & 1;
-  int tmi, tni;
-  tile_of(blockIdx.x, tiles_m, tiles_n, tmi, tni);
-  const int m0 = tmi * 256, n0 = tni * 256;
-
-  const int nsb = BNS == 1 ? N : (N + 127) / 128;
-  c.ra = make_rsrc(A, (uint32_t)M * (uint32_t)K);
-  c.rb = make_rsrc(B, (uint32_t)N * (uint32_t)K);
-  c.row8 = 8u * (uint32_t)K;
-  // loader slot: LDS row wave*32 + u*8 + lane/8, physical chunk lane%8 holds
-  // logical chunk (lane%8) ^ swz(row); swz(row) only depends on lane/8 and
-  // on the parity of u (wave*32 + u*8 with u even / odd).
-  const int lrow = c.wave * 32 + (lane >> 3);
-#pragma unroll
-  for (int par = 0; par < 2; ++par) {
-    const int lch = (lane & 7) ^ g256_swz(lrow + par * 8);
-    c.voa[par] = (uint32_t)(m0 + lrow) * (uint32_t)K + lch * 16;
-    c.vob[par] = (uint32_t)(n0 + lrow) * (uint32_t)K + lch * 16;
-  }
-  const int sidx = (c.wave & 3) * 64 + lane;
-  c.rsa = make_rsrc(SA, (uint32_t)M * c.nkb * 4u);
-  c.vosa = (uint32_t)(m0 + sidx) * c.nkb * 4u;
-  c.rsb = make_rsrc(SB, (uint32_t)nsb * c.nkb * 4u);
-  c.vosb = (uint32_t)((n0 + sidx) / BNS) * c.nkb * 4u;
-  // fragment chunks: lane (fr, fg) feeds the MFMA logical chunks fg and
-  // fg + 4 of row r = (wave tile row) + 16 * t + fr (A and B lanes agree, so
-  // the K order inside the block is free); they sit at physical positions
-  // fg ^ swz(r) and (fg + 4) ^ swz(r), and swz(r) == swz(fr) because the
-  // other terms are multiples of 16.  With chunk pairs {2fg, 2fg + 1}
-  // instead, the four lane groups of a read collide in LDS and reads run
-  // about 30% slower.
-  const uint32_t ch0 = (uint32_t)(fg ^ g256_swz(fr)) * 16u;
-  c.fa0 = (uint32_t)(wm * 64 + fr) * 128u + ch0;
-  c.fa1 = c.fa0 ^ 64u;
-  c.fb0 = (uint32_t)(wn * 128 + fr) * 128u + ch0;
-  c.fb1 = c.fb0 ^ 64u;
-  c.fsa = wm * 64 + fr;                 // A-row scale of output row fr
-  c.fsb = 256 + wn * 128 + 4 * fg;      // B-column scales of columns 4fg .. 4fg+3
-
-  v4f acc[4][8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  g256_issue<0>(c, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  int kb = 0;
-  v8i af[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    af[i] = as_v8i(*reinterpret_cast<const uint4*>(g256_a0 + c.fa0 + i * 2048),
-                   *reinterpret_cast<const uint4*>(g256_a0 + c.fa1 + i * 2048));
-  for (; kb + 1 < c.nkb; kb += 2) {
-    g256_compute_tail<0>(c, acc, af, kb + 1);
-    g256_compute_tail<1>(c, acc, af, kb + 2);
-  }
-  if (kb < c.nkb) g256_compute_tail<0>(c, acc, af, kb + 1);
-
-  // bf16 epilogue through LDS (the stage buffers are free after the last K
-  // block's barrier): each wave stages its 64 x 128 tile with 256-byte rows,
-  // 16-byte chunk c of row r at c ^ (r & 15) so the 16 rows one write
-  // instruction touches fall in different banks, then 16 lanes store each
-  // row's 256 bytes.  Written straight from registers, every output line was
-  // assembled from eight 32-byte pieces and the Y GEMM ran ~5% slower.
   if (!OUT_F32 && (N % 8) == 0) {
-    __syncthreads();
-    uint8_t* wbuf = (c.wave < 2 ? g256_a0 : c.wave < 4 ? g256_b0 : c.wave < 6 ? g256_a1 : g256_b1) +
-                    (c.wave & 1) * 16384;
+    uint8_t* wbuf = (wave < 4 ? g256_a<S>() : g256_b<S>()) + (wave & 3) * 8192;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int r = i * 16 + fr;
-        const int chunk = (j * 2 + (fg >> 1)) ^ (r & 15);
-        const v4f v = acc[i][j];
-        *reinterpret_cast<uint2*>(wbuf + r * 256 + chunk * 16 + (fg & 1) * 8) =
-            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int r = ii * 16 + fr;
+          const int chunk = (j * 2 + (fg >> 1)) ^ (r & 15);
+          const v4f v = acc[2 * h + ii][j];
+          *reinterpret_cast<uint2*>(wbuf + r * 256 + chunk * 16 + (fg & 1) * 8) =
+              make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const int k = lane & 15;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int r = q * 4 + (lane >> 4);
+        const int m = m0w + h * 32 + r;
+        const int n = n0w + k * 8;
+        const uint4 v = *reinterpret_cast<const uint4*>(wbuf + r * 256 + ((k ^ (r & 15)) * 16));
+        if (m < M && n < N)
+          *reinterpret_cast<uint4*>(reinterpret_cast<__bf16*>(C) + (int64_t)m * N + n) = v;
       }
-    // the wave reads back only what it wrote: LDS completes a wave's
-    // accesses in order, so waiting for its own writes is enough
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    const int k = lane & 15;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int r = q * 4 + (lane >> 4);
-      const int m = m0 + wm * 64 + r;
-      const int n = n0 + wn * 128 + k * 8;
-      const uint4 v = *reinterpret_cast<const uint4*>(wbuf + r * 256 + ((k ^ (r & 15)) * 16));
-      if (m < M && n < N)
-        *reinterpret_cast<uint4*>(reinterpret_cast<__bf16*>(C) + (int64_t)m * N + n) = v;
     }
     return;
   }
@@ -468,11 +414,11 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
   const bool vec_ok = (N % 4) == 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int m = m0 + wm * 64 + i * 16 + fr;
+    const int m = m0w + i * 16 + fr;
     if (m >= M) continue;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int n = n0 + wn * 128 + j * 16 + 4 * fg;
+      const int n = n0w + j * 16 + 4 * fg;
       const v4f v = acc[i][j];
       if (OUT_F32) {
         float* dst = reinterpret_cast<float*>(C) + (int64_t)m * N + n;
@@ -497,12 +443,166 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
   }
 }
 
+// Persistent over tiles: workgroup b takes launch slots b, b + G, b + 2G, ...
+// (G = gridDim.x, a multiple of 8, so every slot of a workgroup belongs to its
+// XCD and tile_of's XCD-aware order holds).  The K blocks of all its tiles
+// form one stream: during a tile's last K block the copies of the next tile's
+// block 0 go into the other stage, so the next tile's first load overlaps this
+// tile's last block and its epilogue (which stages through the stage the last
+// block used) instead of starting cold in a new workgroup.
+template <int BNS, bool OUT_F32>
+__global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ SA, const uint8_t* __restrict__ B,
+    const float* __restrict__ SB, void* __restrict__ C, int M, int N, int K, int tiles_m,
+    int tiles_n) {
+  G256Ctx c;
+  const int tid = threadIdx.x, lane = tid & 63;
+  c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: keeps descriptors in SGPRs
+  c.nkb = K >> 7;
+  const int fr = lane & 15, fg = lane >> 4;
+  const int wm = c.wave >> 1, wn = c.wave & 1;
+  const int ntiles = tiles_m * tiles_n;
+
+  const int nsb = BNS == 1 ? N : (N + 127) / 128;
+  c.ra = make_rsrc(A, (uint32_t)M * (uint32_t)K);
+  c.rb = make_rsrc(B, (uint32_t)N * (uint32_t)K);
+  c.row8 = 8u * (uint32_t)K;
+  // loader slot: LDS row wave*32 + u*8 + lane/8, physical chunk lane%8 holds
+  // logical chunk (lane%8) ^ swz(row); swz(row) only depends on lane/8 and
+  // on the parity of u (wave*32 + u*8 with u even / odd).
+  const int lrow = c.wave * 32 + (lane >> 3);
+  int slot = blockIdx.x;
+  int tm_cur, tn_cur;
+  tile_of(slot, tiles_m, tiles_n, tm_cur, tn_cur);
+  uint32_t lm0 = (uint32_t)tm_cur * 256u, ln0 = (uint32_t)tn_cur * 256u;   // the loader's tile
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int lch = (lane & 7) ^ g256_swz(lrow + par * 8);
+    c.voa[par] = (lm0 + lrow) * (uint32_t)K + lch * 16;
+    c.vob[par] = (ln0 + lrow) * (uint32_t)K + lch * 16;
+  }
+  const int sidx = (c.wave & 3) * 64 + lane;
+  c.rsa = make_rsrc(SA, (uint32_t)M * c.nkb * 4u);
+  c.vosa = (lm0 + sidx) * c.nkb * 4u;
+  c.rsb = make_rsrc(SB, (uint32_t)nsb * c.nkb * 4u);
+  c.vosb = ((ln0 + sidx) / BNS) * c.nkb * 4u;
+  // move the loader to the tile of launch slot `s`: every per-lane offset is
+  // (tile origin + lane part) * stride, so the move adds a workgroup-uniform
+  // difference (mod 2^32) and no lane part stays live.  Rows past M / N keep
+  // landing past the buffer's end in the per-lane offset and read as zero.
+  // With BNS = 128, (n0 + sidx) / 128 = n0 / 128 + sidx / 128 (n0 % 256 == 0),
+  // so the scale offset moves by n0 / 128 - ln0 / 128 rows.
+  auto point_loader = [&](int s) {
+    int tm, tn;
+    tile_of(s, tiles_m, tiles_n, tm, tn);
+    const uint32_t m0 = (uint32_t)tm * 256u, n0 = (uint32_t)tn * 256u;
+    const uint32_t da = (m0 - lm0) * (uint32_t)K, db = (n0 - ln0) * (uint32_t)K;
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      c.voa[par] += da;
+      c.vob[par] += db;
+    }
+    c.vosa += (m0 - lm0) * c.nkb * 4u;
+    c.vosb += (n0 / BNS - ln0 / BNS) * c.nkb * 4u;   // divide first: n0 - ln0 may wrap
+    lm0 = m0;
+    ln0 = n0;
+  };
+  // fragment chunks: lane (fr, fg) feeds the MFMA logical chunks fg and
+  // fg + 4 of row r = (wave tile row) + 16 * t + fr (A and B lanes agree, so
+  // the K order inside the block is free); they sit at physical positions
+  // fg ^ swz(r) and (fg + 4) ^ swz(r), and swz(r) == swz(fr) because the
+  // other terms are multiples of 16.  With chunk pairs {2fg, 2fg + 1}
+  // instead, the four lane groups of a read collide in LDS and reads run
+  // about 30% slower.
+  const uint32_t ch0 = (uint32_t)(fg ^ g256_swz(fr)) * 16u;
+  c.fa0 = (uint32_t)(wm * 64 + fr) * 128u + ch0;
+  c.fa1 = c.fa0 ^ 64u;
+  c.fb0 = (uint32_t)(wn * 128 + fr) * 128u + ch0;
+  c.fb1 = c.fb0 ^ 64u;
+  c.fsa = wm * 64 + fr;                 // A-row scale of output row fr
+  c.fsb = 256 + wn * 128 + 4 * fg;      // B-column scales of columns 4fg .. 4fg+3
+
+  v4f acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // this workgroup's tiles, and the K blocks of all of them as one stream
+  const int my_tiles = (ntiles - slot + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int nsteps = my_tiles * c.nkb;
+
+  g256_issue<0>(c, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  v8i af[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    af[i] = as_v8i(*reinterpret_cast<const uint4*>(g256_a0 + c.fa0 + i * 2048),
+                   *reinterpret_cast<const uint4*>(g256_a0 + c.fa1 + i * 2048));
+
+  // One step of the stream from stage S: K block kb of the current tile.  At
+  // a tile's last block the loader moves on to the next slot first, and after
+  // it the tile's results leave through stage S (free: no wave reads it after
+  // the block's barrier) before the accumulators restart from zero.
+  int kb = 0, step = 0;
+  auto one_step = [&](auto stage) {
+    constexpr int S = decltype(stage)::value;
+    const bool last = kb + 1 == c.nkb;
+    const bool more = step + 1 < nsteps;
+    if (last && more) point_loader(slot + (int)gridDim.x);
+    g256_compute_tail<S>(c, acc, af, last ? 0 : kb + 1, more);
+    ++step;
+    if (!last) {
+      ++kb;
+      return;
+    }
+    g256_store_tile<S, OUT_F32>(acc, C, M, N, tm_cur * 256 + wm * 64, tn_cur * 256 + wn * 128, c.wave,
+                                lane);
+    if (more) {
+      // every wave is done reading stage S before the next block's copies land there
+      __syncthreads();
+      slot += gridDim.x;
+      tile_of(slot, tiles_m, tiles_n, tm_cur, tn_cur);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+    kb = 0;
+  };
+  while (step + 1 < nsteps) {
+    one_step(IntC<0>{});
+    one_step(IntC<1>{});
+  }
+  if (step < nsteps) one_step(IntC<0>{});
+}
+
+// Compute units of the current device (cached per device id).
+static int device_cus() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] <= 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cached[dev] = v;
+  }
+  return cached[dev];
+}
+
 template <int BNS, bool OUT_F32>
 static int launch_gemm_256(const uint8_t* a_q, const float* a_s, const uint8_t* b_q,
                            const float* b_s, void* c, int M, int N, int K, hipStream_t st) {
   const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
-  hipLaunchKernelGGL((gemm_fp8_nt_256_kernel<BNS, OUT_F32>), dim3((unsigned)(tiles_m * tiles_n)),
-                     dim3(512), 0, st, a_q, a_s, b_q, b_s, c, M, N, K, tiles_m, tiles_n);
+  // one workgroup per CU (135 KiB of LDS each), looping over its tiles; the
+  // grid stays a multiple of 8 so that a workgroup's slots share its XCD
+  const int ntiles = tiles_m * tiles_n;
+  const int slots = device_cus() & ~7;
+  const int grid = ntiles <= slots || slots == 0 ? ntiles : slots;
+  hipLaunchKernelGGL((gemm_fp8_nt_256_kernel<BNS, OUT_F32>), dim3((unsigned)grid), dim3(512), 0, st,
+                     a_q, a_s, b_q, b_s, c, M, N, K, tiles_m, tiles_n);
   return check_launch("gemm_fp8_nt_256");
 }
 
@@ -576,7 +676,6 @@ template <int S> __device__ __forceinline__ uint8_t* gemv_stage() {
   return S == 0 ? gemv_lds0 : S == 1 ? gemv_lds1 : gemv_lds2;
 }
 
-template <int V> using IntC = std::integral_constant<int, V>;
 
 template <int MT, int BNS>
 __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict__ XQ,
@@ -1138,19 +1237,6 @@ extern "C" int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, cons
   return launch_gemm_fp8(qat, sat, qgt, sgt, 1, db, TG_DTYPE_BF16, K, N, M, st);  // dW = a.T . g
 }
 
-// Compute units of the current device (cached per device id).
-static int device_cus() {
-  static int cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cached[dev] <= 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
-      v = 256;
-    cached[dev] = v;
-  }
-  return cached[dev];
-}
 
 // Rows per workgroup: equal rows per CU, a multiple of 8, at most 64.
 template <int MT>
