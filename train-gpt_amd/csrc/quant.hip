@@ -318,13 +318,17 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
   col_words(f1, sc1, 2 * cp + 1);
   __syncthreads();
   // eight lanes per column, lane k writing bytes 16k .. 16k + 15: each store
-  // instruction writes eight whole 128-byte columns (full lines)
+  // instruction writes eight whole 128-byte columns (full lines).  Ordinary
+  // (not non-temporal) stores: the transposed operands are read by the next
+  // GEMMs (W.T by the forward's, x.T and dY.T by dW), and written around the
+  // Infinity Cache they came back from HBM with each dY.T panel read by one
+  // XCD only, which left dW ~15% slower than dX inside the C3 step.
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
     const int n = (tid >> 3) + 32 * p, k = tid & 7;
     if (GUARD && c0 + n >= cols) continue;
     const uint4 val = *reinterpret_cast<const uint4*>(&tq[n * 36 + 4 * k]);
-    stg_stream(reinterpret_cast<uint4*>(qt + (c0 + n) * rows + r0) + k, val);
+    *(reinterpret_cast<uint4*>(qt + (c0 + n) * rows + r0) + k) = val;
   }
 }
 
