@@ -3,7 +3,17 @@
 Bar (north star): bit-exact quantized operands; GEMM outputs within 1e-2
 max-abs-normalised error of the oracle (float64 dequant GEMM of the same
 quantized operands, fp8_ref.dequant_gemm_nt); the bf16 output is the RNE of
-the f32 accumulator.  The error against a plain bf16 matmul is printed.
+the f32 accumulator.  The f32 output is held much tighter, to F32_TOL.
+Measured on gfx950 (C3-like data, K = 256 .. 2048, both tile paths): the f32
+output is 1.5e-5 .. 1.9e-5 of max|ref| away from the float64 oracle, while a
+CPU emulation of the same promotion with exactly rounded block sums stays at
+7e-8 .. 1.8e-7, so the error is the FP8 MFMA's own block summation (it does
+not round the exact 128-product sum once).  F32_TOL = 5e-5 sits above that
+with margin and far below what a scale applied to the wrong row, column or
+K block produces (one block of 16 off by 1% already moves the output by
+~1e-3 of max|ref|).  Structured operands with power-of-two scales give exact
+known answers on the persistent 256 x 256 tile path.  The error against a
+plain bf16 matmul is printed.
 """
 import numpy as np
 import pytest
@@ -17,6 +27,7 @@ from oracle import fp8_ref
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-2
+F32_TOL = 5e-5
 
 
 def _gemm(qa, sa, qb, sb, dev, bn=1, out=torch.bfloat16):
@@ -61,10 +72,9 @@ def test_scaled_gemm_random(dev, M, N, K):
     qa, sa = fp8_ref.quantize_fp8(a)
     qb, sb = fp8_ref.quantize_fp8(b)
     ref = fp8_ref.dequant_gemm_nt(qa, sa, qb, sb)
-    for out in (torch.bfloat16, torch.float32):
-        c = _gemm(qa, sa, qb, sb, dev, out=out)
-        assert maxabs_rel(c, ref) <= TOL
+    assert maxabs_rel(_gemm(qa, sa, qb, sb, dev), ref) <= TOL
     c32 = _gemm(qa, sa, qb, sb, dev, out=torch.float32).cpu().numpy()
+    assert maxabs_rel(c32, ref) <= F32_TOL
     # the bf16 output is the RNE of the f32 accumulator (fp8.py:78)
     c16 = _gemm(qa, sa, qb, sb, dev).view(torch.int16).cpu().numpy().view(np.uint16)
     np.testing.assert_array_equal(c16, ob.f32_to_bf16(c32))
@@ -78,7 +88,43 @@ def test_scaled_gemm_weight_tiles_128x128(dev, M, N, K):
     qa, sa = fp8_ref.quantize_fp8(a)
     qw, sw = fp8_ref.quantize_weight_128x128(w_t)
     c = _gemm(qa, sa, qw, sw, dev, bn=128, out=torch.float32)
-    assert maxabs_rel(c, fp8_ref.gemv_prequant(qa, sa, qw, sw, bn=128)) <= TOL
+    assert maxabs_rel(c, fp8_ref.gemv_prequant(qa, sa, qw, sw, bn=128)) <= F32_TOL
+
+
+def _structured_operands(M, N, K, bn):
+    """Exact known answer with row-, column- and K-block-dependent scales.
+
+    Bytes: qa[m, k] = 1.0 for even k, 2.0 for odd k; qb[n, k] = 1.0 or 2.0 by
+    (k // 2) % 2, so every 128-wide block sums to 32 * (1 + 2 + 2 + 4) = 288
+    only if A and B fragments pair the same K positions.  Scales are powers
+    of two that differ per row, column (or 128-column group) and K block:
+    every product and partial sum is exact in f32, so the f32 output equals
+    288 * (sa @ sb.T) exactly.
+    """
+    k = np.arange(K)
+    qa = np.broadcast_to(np.where(k % 2 == 0, 0x38, 0x40).astype(np.uint8), (M, K)).copy()
+    qb = np.broadcast_to(np.where((k // 2) % 2 == 0, 0x38, 0x40).astype(np.uint8), (N, K)).copy()
+    nkb = K // 128
+    kb = np.arange(nkb)
+    sa = np.exp2(((np.arange(M)[:, None] * 7 + kb[None, :] * 3) % 5) - 2).astype(np.float32)
+    rows_b = N if bn == 1 else (N + 127) // 128
+    sb = np.exp2(((np.arange(rows_b)[:, None] * 5 + kb[None, :] * 11) % 7) - 3).astype(np.float32)
+    sb_full = sb if bn == 1 else np.repeat(sb, 128, axis=0)[:N]
+    want = 288.0 * (sa.astype(np.float64) @ sb_full.astype(np.float64).T)
+    return qa, sa, qb, sb, want
+
+
+@pytest.mark.parametrize("bn", [1, 128])
+@pytest.mark.parametrize("M,N,K", [(5000, 5000, 384), (4300, 4404, 384), (8192, 8192, 2048)])
+def test_layout_known_answer_persistent_tiles(dev, M, N, K, bn):
+    """>= 128 tiles of 256 x 256 (the kernel bench.py times), with workgroups
+    walking several tiles, ragged edges and both weight-scale layouts; the C3
+    shape included.  Exact equality in f32, RNE of it in bf16."""
+    qa, sa, qb, sb, want = _structured_operands(M, N, K, bn)
+    c32 = _gemm(qa, sa, qb, sb, dev, bn=bn, out=torch.float32).cpu().numpy()
+    np.testing.assert_array_equal(c32, want.astype(np.float32))
+    c16 = _gemm(qa, sa, qb, sb, dev, bn=bn).view(torch.int16).cpu().numpy().view(np.uint16)
+    np.testing.assert_array_equal(c16, ob.f32_to_bf16(want.astype(np.float32)))
 
 
 def test_block_scaled_matmul_c1(dev):
@@ -163,8 +209,8 @@ def test_gemm_c3_full_size_sampled(dev):
     y = fp8.block_scaled_matmul(a, b)
     y.backward(to_dev(g_u, dev))
     torch.cuda.synchronize()
-    rows = np.sort(rng.choice(M, 48, replace=False))
-    cols = np.sort(rng.choice(N, 48, replace=False))
+    rows = np.sort(rng.choice(M, 256, replace=False))
+    cols = np.sort(rng.choice(N, 256, replace=False))
     a32, b32, g32 = (ob.bf16_to_f32(v) for v in (a_u, b_u, g_u))
     qa, sa = fp8_ref.quantize_fp8(a32[rows])
     qbt, sbt = fp8_ref.quantize_fp8(np.ascontiguousarray(b32.T))

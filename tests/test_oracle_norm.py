@@ -2,6 +2,10 @@
 
 * the bf16 ops after the variance are checked against torch's own bf16
   arithmetic on the oracle's r (x * r and * scale are single roundings);
+* both post-variance paths (the pure path's three bf16 roundings and the
+  Pallas kernel's two f32 roundings + one bf16 rounding, kernels.py:49-53)
+  against exact rational arithmetic, element by element, on rows where the
+  two paths differ;
 * the variance against an exact (fractions) mean of squares;
 * the rsqrt against correctly rounded 1/sqrt (fractions, squared bracket);
 * constant rows and scale invariance as closed forms;
@@ -65,6 +69,79 @@ def test_constant_rows_and_scale_invariance():
     x, g = _inputs(rng, (16, 1024))
     x2 = ob.f32_to_bf16(ob.bf16_to_f32(x) * 4)      # exact scaling by a power of two
     np.testing.assert_array_equal(norm_ref.rms_norm_pure(x, g, 0.0), norm_ref.rms_norm_pure(x2, g, 0.0))
+
+
+def _round_sig(v: Fraction, bits: int) -> Fraction:
+    """v rounded to `bits` significant bits, ties to even (normal range; exact)."""
+    if v == 0:
+        return v
+    a = abs(v)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    ulp = Fraction(2) ** (e - bits + 1)
+    q = a / ulp
+    n = q.numerator // q.denominator
+    rem = q - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return (n * ulp) if v > 0 else -(n * ulp)
+
+
+def _f32(v):
+    return _round_sig(v, 24)
+
+
+def _bf16(v):
+    return _round_sig(v, 8)
+
+
+def test_single_and_double_rounding_exact_rational():
+    """kernels.py:49-53 (y = bf16(f32(f32(x * rnorm) * scale)), rnorm unrounded
+    f32) and kernels.py:30-33 (r = bf16(rnorm), t = bf16(x * r), y = bf16(t *
+    scale)), element by element in exact rationals from the oracle's rnorm
+    (itself pinned by test_variance_and_rsqrt_exact).  The rows are chosen so
+    the two paths differ in a large share of elements: an oracle that fell
+    back to the pure path, or rounded rnorm to bf16 first, fails here."""
+    rng = np.random.default_rng(5)
+    x, g = _inputs(rng, (3, 1024))
+    _, r = norm_ref.row_inv_rms(x, 1e-6)
+    single = ob.bf16_to_f32(norm_ref.rms_norm_single_rounding(x, g, 1e-6))
+    pure = ob.bf16_to_f32(norm_ref.rms_norm_pure(x, g, 1e-6))
+    xf, gf = ob.bf16_to_f32(x), ob.bf16_to_f32(g)
+    gq = [Fraction(float(v)) for v in gf]
+    differ = 0
+    for i in range(x.shape[0]):
+        rn = Fraction(float(r[i]))
+        rb = _bf16(rn)
+        for j in range(x.shape[1]):
+            xv = Fraction(float(xf[i, j]))
+            want_single = _bf16(_f32(_f32(xv * rn) * gq[j]))
+            want_pure = _bf16(_bf16(xv * rb) * gq[j])
+            assert Fraction(float(single[i, j])) == want_single, (i, j)
+            assert Fraction(float(pure[i, j])) == want_pure, (i, j)
+            differ += want_single != want_pure
+    assert differ > 0.2 * x.size
+
+
+def test_single_rounding_matches_torch_f32_and_differs_from_pure_at_c2():
+    """The same single-rounding arithmetic by torch's f32 multiply and RNE bf16
+    cast (independent of the oracle's own rounding), on C2-distributed rows
+    (seed 1, 0.1% outliers x50, gamma = 1 + N(0, 0.1^2)); there the two
+    reference variants differ in roughly a third of the elements."""
+    rng = np.random.default_rng(1)
+    x, g = _inputs(rng, (256, 2048))
+    _, r = norm_ref.row_inv_rms(x, 1e-6)
+    tx = torch.from_numpy(ob.bf16_to_f32(x))
+    tr = torch.from_numpy(r)[:, None]
+    tg = torch.from_numpy(ob.bf16_to_f32(g))
+    want = ((tx * tr) * tg).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    single = norm_ref.rms_norm_single_rounding(x, g, 1e-6)
+    np.testing.assert_array_equal(single, want)
+    rate = float(np.mean(single != norm_ref.rms_norm_pure(x, g, 1e-6)))
+    assert 0.25 < rate < 0.5, rate
 
 
 def test_fused_is_quantize_of_norm_and_c_agrees():

@@ -10,9 +10,7 @@ import os
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-# TG_LIB_PATH selects another build of the same library (for A/B timing of
-# kernel variants); by default the in-tree build is loaded.
-LIB_PATH = os.environ.get("TG_LIB_PATH") or os.path.join(_HERE, "libtg_fp8.so")
+LIB_PATH = os.path.join(_HERE, "libtg_fp8.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "tg_fp8.h")
 
 TG_OK, TG_EINVAL, TG_EHIP = 0, 1, 2

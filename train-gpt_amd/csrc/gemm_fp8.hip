@@ -4,7 +4,11 @@
 //   c[m, n] = bf16( sum_kb sa[m, kb] * sb[n, kb] * sum_{k in kb} qa[m, k] * qb[n, k] )
 // with e4m3fn operands and one fp32 scale per 128-wide K block.
 //
-// Design (gfx950, wave64):
+// Two kernels: gemm_fp8_nt_256_kernel (256 x 256 tiles on 32 x 32 x 64
+// MFMAs, persistent; used once a launch has >= 128 tiles, see its own
+// comment) and gemm_fp8_nt_kernel below (128 x 128 tiles) for smaller shapes.
+//
+// Design of the 128 x 128 kernel (gfx950, wave64):
 //   * v_mfma_f32_16x16x128_f8f6f4: one MFMA consumes exactly one 128-wide
 //     scale block, so its 16x16 fp32 result P is promoted immediately:
 //     acc = fma(P, sa[m] * sb[n], acc).  The promotion is VALU work that
@@ -18,6 +22,7 @@
 //   * Tile order: consecutive workgroup ids go to different XCDs, so ids are
 //     remapped to give each XCD a contiguous range of tiles, and within that
 //     range tiles are walked in groups of 8 tile-rows for L2 reuse of B.
+#include <mutex>
 #include <type_traits>
 
 #include "row_ops.h"
@@ -179,50 +184,160 @@ __global__ __launch_bounds__(256, 2) void gemm_fp8_nt_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Large-tile variant: workgroup tile 256 x 256 x 128, 8 waves (4 along M x 2
-// along N), wave tile 64 x 128 (4 x 8 MFMA tiles).  Operands travel HBM -> LDS
-// with buffer_load_dwordx4 ... lds (no VGPR staging): each lane's 16-byte
-// chunk lands at LDS offset lane * 16 of its wave's 1 KiB slot, so the XOR
-// swizzle is applied to the global offset a lane fetches.  Rows past M / N
-// fall outside the buffer's range and read as zero.  Per-lane state is one
-// 32-bit offset per operand; the row step and the K-block step ride in SGPR
-// offsets.  The two stages are distinct __shared__ objects and the K loop is
-// unrolled by two, so the compiler sees that the prefetch into one stage
-// does not alias the fragment reads from the other and puts no wait
+// Large-tile kernel: workgroup tile 256 x 256 x 128, 8 waves (4 along M x 2
+// along N), wave tile 64 x 128.  Operands travel HBM -> LDS with
+// buffer_load_dwordx4 ... lds (no VGPR staging): each lane's 16-byte chunk
+// lands at LDS offset lane * 16 of its wave's 1 KiB slot, so the XOR swizzle
+// is applied to the global offset a lane fetches.  Rows past M / N fall
+// outside the buffer's range and read as zero.  Per-lane state is one 32-bit
+// offset per operand; the row step and the K-block step ride in SGPR offsets.
+// The two stages are distinct __shared__ objects and the K loop is unrolled
+// by two, so the compiler's per-object alias scopes tell the prefetch into
+// one stage from the fragment reads of the other and it puts no wait
 // between them.
 // ---------------------------------------------------------------------------
 template <int V> using IntC = std::integral_constant<int, V>;
 
-__shared__ __attribute__((aligned(16))) uint8_t g256_a0[256 * 128];
+// The compiler lays out LDS objects by size, then by name.  A DS read's
+// immediate offset is 16 bits, so reads of an object past 64 KiB cost an
+// address add each; the B stages, read twice as often as the A stages, sort
+// first (the A stages' names start with z so that they sort last).
 __shared__ __attribute__((aligned(16))) uint8_t g256_b0[256 * 128];
-__shared__ __attribute__((aligned(16))) float g256_s0[512];
-__shared__ __attribute__((aligned(16))) uint8_t g256_a1[256 * 128];
 __shared__ __attribute__((aligned(16))) uint8_t g256_b1[256 * 128];
+__shared__ __attribute__((aligned(16))) uint8_t g256_za0[256 * 128];
+__shared__ __attribute__((aligned(16))) uint8_t g256_za1[256 * 128];
+__shared__ __attribute__((aligned(16))) float g256_s0[512];
 __shared__ __attribute__((aligned(16))) float g256_s1[512];
 
-template <int S> __device__ __forceinline__ uint8_t* g256_a() { return S ? g256_a1 : g256_a0; }
+template <int S> __device__ __forceinline__ uint8_t* g256_a() { return S ? g256_za1 : g256_za0; }
 template <int S> __device__ __forceinline__ uint8_t* g256_b() { return S ? g256_b1 : g256_b0; }
 template <int S> __device__ __forceinline__ float* g256_s() { return S ? g256_s1 : g256_s0; }
 
-struct G256Ctx {
+// ---------------------------------------------------------------------------
+// 256 x 256 x 128 workgroup tile on v_mfma_f32_32x32x64_f8f6f4.
+//
+// The block-scale promotion costs two VALU per output and K block (the scale
+// product and the fma), which is as many VALU cycles as the matrix pipe
+// needs for the block's MFMAs.  A 32 x 32 x 64 MFMA pair covers a 32 x 32
+// tile's 128-wide block with half as many MFMA issues as four 16 x 16 x 128
+// MFMAs, and measured on gfx950 the MFMA + promotion mix runs ~20% faster on
+// it (two waves per SIMD, each overlapping its own MFMAs with the promotion
+// of its previous tile).
+//
+// Layout (8 waves, two per SIMD): wave w owns rows wm * 64 .. +63 (wm = w/2)
+// and columns wn * 128 .. +127 (wn = w%2) of the tile: 2 x 4 tiles of
+// 32 x 32.  Each tile is computed as B.A^T (B fragment in the MFMA's A slot),
+// so lane (c = lane % 32, g = lane / 32) holds output row m = c and the 16
+// columns n = 8q + 4g + t (register 4q + t) of the tile: one A-row scale per
+// tile and 16 B-column scales.  The column scales are spread over the lane's
+// quad: quad lane k keeps the four values n = 8q + 4g + k (q = 0..3) and the
+// promotion's multiply reads lane t's value through a quad_perm DPP source,
+// so 4 registers per tile hold what 16 would.  The LDS copy of the B scales
+// is permuted (within each group of 32 rows, float (4g + k) * 4 + q holds row
+// 8q + 4g + k) so that those four values are one 16-byte read.
+//
+// Steps: tile t = (i, j) = (t % 2, t / 2) for t = 0..7 per K block.  Step t
+// issues the MFMA pair of tile t and, between and after the two MFMAs, the
+// promotion of the previous tile (the previous K block's tile 7 in step 0),
+// so the promotion always runs in the shadow of the wave's own MFMAs.  The
+// fragment chunks a lane feeds (16-byte logical chunks 4h + 2g and
+// 4h + 2g + 1 of its row for K half h) pair the same K positions in A and B.
+// ---------------------------------------------------------------------------
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16f mfma_f8_32x32x64(const v8i& a, const v8i& b, const v16f& c) {
+  // format codes 0/0 = FP8 E4M3 for A and B; zero scale operands select the
+  // unscaled v_mfma_f32_32x32x64_f8f6f4
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// v broadcast from quad lane T to the four lanes of each quad (folded into
+// the consuming VALU op as a DPP source).
+template <int T>
+__device__ __forceinline__ float quad_bcast(float v) {
+  constexpr int ctrl = T | (T << 2) | (T << 4) | (T << 6);
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, true));
+}
+
+// acc[4q + t] += p[4q + t] * (sa * sb[n = 8q + 4g + t]) for q = 2h, 2h + 1;
+// sbl[q] holds the column scale of n = 8q + 4g + (lane % 4).
+__device__ __forceinline__ void w32_promote_half(v16f& acc, const v16f& p, float sa, const float4& sbl,
+                                                 int h) {
+  const float s0 = h == 0 ? sbl.x : sbl.z, s1 = h == 0 ? sbl.y : sbl.w;
+  float t[8] = {quad_bcast<0>(s0) * sa, quad_bcast<1>(s0) * sa, quad_bcast<2>(s0) * sa,
+                quad_bcast<3>(s0) * sa, quad_bcast<0>(s1) * sa, quad_bcast<1>(s1) * sa,
+                quad_bcast<2>(s1) * sa, quad_bcast<3>(s1) * sa};
+  // all eight products first, then the eight fmas: a DPP multiply's result
+  // read by the next instruction, or its destination (the value disabled
+  // lanes keep) written by the previous one, costs a wait state
+  asm volatile("" : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]));
+  asm volatile("" : "+v"(t[4]), "+v"(t[5]), "+v"(t[6]), "+v"(t[7]));
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc[8 * h + k] = __builtin_fmaf(p[8 * h + k], t[k], acc[8 * h + k]);
+}
+
+struct W32Ctx {
   __amdgpu_buffer_rsrc_t ra, rb, rsa, rsb;
   uint32_t voa[2], vob[2];    // per-lane byte offsets (kb = 0) for even / odd u
   uint32_t vosa, vosb;
   uint32_t row8;              // 8 rows of A / B in bytes (8 * K)
   int wave, nkb;
-  uint32_t fa0, fa1, fb0, fb1;   // LDS byte offsets of this lane's fragment chunks
-  uint32_t fsa, fsb;             // LDS float offsets of this lane's scales
+  // LDS byte addresses of this lane's fragment chunks [K half][chunk] and
+  // scales in stage 0 (lds_addr of the stage-0 object included)
+  uint32_t fa[2][2], fb[2][2];
+  uint32_t fsa;                  // A-row scale of m-tile 0
+  uint32_t fsb;                  // B-column scales (this lane's quad share) of n-tile 0
 };
 
-// Loads of one K block into a stage, in 16 parts issued by the four loader
-// waves (waves 0-3; each covers its own LDS slot w and slot w + 4):
-// parts 0-7 are A rows (slot w, then w + 4; four 1 KiB row groups each),
-// parts 8-15 B rows; part 0 also loads this wave's 64 A-row scales and 64
-// B-row scales.  A DMA instruction stalls its wave for a while at issue, so
-// the loads ride on half of the waves and two parts per compute region: on
-// every SIMD one wave keeps issuing MFMAs while the other feeds LDS.
-__device__ __forceinline__ void g256_issue_part(const G256Ctx& c, uint8_t* la, uint8_t* lb,
-                                                float* ls, int kb, int part) {
+// The carried promotion state: the MFMA result of the previous tile and the
+// scales it is promoted with.
+struct W32Prev {
+  v16f p;
+  float sa;
+  float4 sb;
+};
+
+typedef __attribute__((address_space(3))) const uint8_t lds_cu8;
+
+// 32-bit LDS address of a __shared__ object (a link-time constant).
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(const T* p) {
+  return (uint32_t)(size_t)(lds_cu8*)p;   // C-style cast: generic -> LDS address space
+}
+// The stage-S copy of stage-0 LDS address a0 inside object objS: the pointer
+// derives from objS itself, so the compiler's per-object alias scopes still
+// tell these reads apart from the copies landing in the other stage (a read
+// based on the stage-0 object would wait for every copy in flight), while
+// the address stays one register plus an immediate offset.
+template <typename T>
+__device__ __forceinline__ lds_cu8* w32_at(const T* obj0, const T* objS, uint32_t a0) {
+  return (lds_cu8*)objS + (a0 - lds_addr(obj0));
+}
+__device__ __forceinline__ u32x4_t lds_ld16(lds_cu8* p) {
+  return *(const __attribute__((address_space(3))) u32x4_t*)p;
+}
+template <int S>
+__device__ __forceinline__ v8i w32_frag_a(const W32Ctx& c, int i, int h) {
+  return as_v8i(lds_ld16(w32_at(g256_za0, g256_a<S>(), c.fa[h][0]) + i * 4096),
+                lds_ld16(w32_at(g256_za0, g256_a<S>(), c.fa[h][1]) + i * 4096));
+}
+template <int S>
+__device__ __forceinline__ v8i w32_frag_b(const W32Ctx& c, int j, int h) {
+  return as_v8i(lds_ld16(w32_at(g256_b0, g256_b<S>(), c.fb[h][0]) + j * 4096),
+                lds_ld16(w32_at(g256_b0, g256_b<S>(), c.fb[h][1]) + j * 4096));
+}
+template <int S>
+__device__ __forceinline__ float4 w32_sb(const W32Ctx& c, int j) {
+  const u32x4_t v = lds_ld16(w32_at(g256_s0, g256_s<S>(), c.fsb) + j * 128);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+template <int S>
+__device__ __forceinline__ float w32_sa(const W32Ctx& c, int i) {
+  return __uint_as_float(*(const __attribute__((address_space(3))) uint32_t*)(w32_at(g256_s0, g256_s<S>(), c.fsa) + i * 128));
+}
+
+__device__ __forceinline__ void w32_issue_part(const W32Ctx& c, uint8_t* la, uint8_t* lb, float* ls,
+                                               int kb, int part) {
   const uint32_t kofs = (uint32_t)kb * 128u;
   const int slot = c.wave + ((part >> 2) & 1) * 4;
   const int u = part & 3;
@@ -239,227 +354,207 @@ __device__ __forceinline__ void g256_issue_part(const G256Ctx& c, uint8_t* la, u
   }
 }
 
-template <int S>
-__device__ __forceinline__ void g256_issue(const G256Ctx& c, int kb) {
-  if (c.wave < 4) {
-#pragma unroll
-    for (int p = 0; p < 16; ++p) g256_issue_part(c, g256_a<S>(), g256_b<S>(), g256_s<S>(), kb, p);
+// The fragment and scale registers of one K block.  bf holds the current
+// n-tile's two K halves; each half is replaced by the next n-tile's as soon
+// as the last MFMA that reads it has issued, so one MFMA pair plus one
+// promotion covers every LDS read's latency with 16 registers in use.
+struct W32Regs {
+  v8i af[2][2];     // A fragments [m-tile][K half]
+  v8i bf[2];        // B fragment of the current n-tile [K half]
+  float4 sb;        // column scales of the current n-tile (this lane's quad share)
+  float sa[2];      // A-row scales [m-tile]
+};
+
+// Step T of a K block from stage S: the MFMA pair of tile (i, j) = (T % 2,
+// T / 2) and the promotion of prev (the previous tile) into acc_prev.  On
+// odd steps the B registers move on to n-tile j + 1 (step 7: to the next K
+// block's n-tile 0 and A fragments of m-tile 1, from stage S ^ 1).
+template <int S, int T, typename F>
+__device__ __forceinline__ void w32_step(const W32Ctx& c, v16f& acc_prev, W32Prev& prev, W32Regs& r,
+                                         bool more, F&& copies) {
+  constexpr int i = T & 1, j = T >> 1;
+  constexpr bool next_n = i == 1 && j < 3;           // B registers move to n-tile j + 1
+  constexpr bool next_blk = T == 7;                  // ... to the next block's n-tile 0
+  const v16f zero = {};
+  // register fence: the promotion of the previous tile stays in this step
+  asm volatile("" : "+v"(acc_prev));
+  v16f t = mfma_f8_32x32x64(r.bf[0], r.af[i][0], zero);
+  // the loader waves' copies go out behind the first MFMA, whose 64 cycles
+  // hide the issue stall of the DMA instructions
+  copies();
+  if (next_n) r.bf[0] = w32_frag_b<S>(c, j + 1, 0);
+  if (next_blk && more) r.bf[0] = w32_frag_b<S ^ 1>(c, 0, 0);
+  w32_promote_half(acc_prev, prev.p, prev.sa, prev.sb, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);     // MFMA K half 0
+  if (next_n || next_blk) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // its B half's successor
+  __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);    // promotion, first half
+  const v16f pn = mfma_f8_32x32x64(r.bf[1], r.af[i][1], t);
+  const float sa_cur = r.sa[i];
+  const float4 sb_cur = r.sb;
+  if (next_n) {
+    r.bf[1] = w32_frag_b<S>(c, j + 1, 1);
+    r.sb = w32_sb<S>(c, j + 1);
   }
+  if (next_blk && more) {
+    r.bf[1] = w32_frag_b<S ^ 1>(c, 0, 1);
+    r.sb = w32_sb<S ^ 1>(c, 0);
+    r.af[1][0] = w32_frag_a<S ^ 1>(c, 1, 0);
+    r.af[1][1] = w32_frag_a<S ^ 1>(c, 1, 1);
+    r.sa[0] = w32_sa<S ^ 1>(c, 0);
+    r.sa[1] = w32_sa<S ^ 1>(c, 1);
+  }
+  w32_promote_half(acc_prev, prev.p, prev.sa, prev.sb, 1);
+  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);     // MFMA K half 1
+  if (next_n) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+  if (next_blk) __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+  __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);    // promotion, second half
+  asm volatile("" : "+v"(acc_prev) : "v"(pn));
+  prev.p = pn;
+  prev.sa = sa_cur;
+  prev.sb = sb_cur;
 }
 
-// The 256 kernel computes each 16x16 tile as B.A^T (B fragment in the MFMA's
-// A slot), so lane (fr, fg) holds output row m = fr and the four consecutive
-// columns n = 4fg .. 4fg+3: one A-row scale and four B-column scales.
-__device__ __forceinline__ void promote4(v4f& acc, const v4f& p, float sa, const float4& sb) {
-  acc[0] = __builtin_fmaf(p[0], sa * sb.x, acc[0]);
-  acc[1] = __builtin_fmaf(p[1], sa * sb.y, acc[1]);
-  acc[2] = __builtin_fmaf(p[2], sa * sb.z, acc[2]);
-  acc[3] = __builtin_fmaf(p[3], sa * sb.w, acc[3]);
-}
-
-// One K block from stage S; the copies issued here are those of the next K
-// block (kb_next of the tile the loader offsets in c point at; none if !more).
-// MFMAs of n-tile j are issued while the 16x16
-// results of n-tile j-1 are promoted (8 VALU per MFMA), so at most two tiles
-// of partial results are live and the VALU work runs in the MFMA shadow; the
-// B fragment and column scale of n-tile j+1 are read from LDS one region
-// ahead.  The A fragments of block kb arrive in af (read during the previous
-// block's last region).  All copies of block kb+1 into the other stage are
-// issued by region 6; the wave then waits for its copies and meets the others
-// at the barrier, and region 7 (MFMAs of n-tile 7, promotions of tiles 6 and
-// 7) overlaps the LDS reads of block kb+1's A fragments.  Region 7 reads no
-// LDS of stage S, so after the barrier stage S is free for block kb+2.
+// One K block from stage S.  r holds this block's A fragments, n-tile 0's B
+// fragment and column scales and the A-row scales (read by the previous
+// block); on return the next block's (when `more`).  The loader waves (0-3)
+// issue the copies of K block kb_next of the tile the loader offsets point at
+// into stage S ^ 1 during steps 0-6; the barrier before step 7 is where every
+// copy has landed and every wave is done reading stage S ^ 1's previous
+// block.  m-tile 0's A fragments are dead after step 6's MFMAs and take the
+// next block's right after the barrier.
 template <int S>
-__device__ __forceinline__ void g256_compute_tail(const G256Ctx& c, v4f (&acc)[4][8], v8i (&af)[4],
-                                                  int kb_next, bool more) {
-  const uint8_t* lb = g256_b<S>();
-  const float* ls = g256_s<S>();
-  const v4f zero = {0.f, 0.f, 0.f, 0.f};
-  auto read_b = [&](int j) {
-    return as_v8i(*reinterpret_cast<const uint4*>(lb + c.fb0 + j * 2048),
-                  *reinterpret_cast<const uint4*>(lb + c.fb1 + j * 2048));
-  };
-  float sav[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) sav[i] = ls[c.fsa + i * 16];
-  auto read_sb = [&](int j) { return *reinterpret_cast<const float4*>(ls + c.fsb + j * 16); };
-  v8i bn = read_b(1);
-  float4 sbn = read_sb(1);
-  v4f pc[4];
-  float4 sbc = read_sb(0);
+__device__ __forceinline__ void w32_block(const W32Ctx& c, v16f (&acc)[2][4], W32Prev& prev, W32Regs& r,
+                                          int kb_next, bool more) {
   const bool pf = more && c.wave < 4;                // loader waves (more: wave-uniform)
-  if (pf) {
+  auto issue = [&](int p) {
+    w32_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, p);
+  };
+  auto dma = [&](int t) {
+    if (pf) {
+      if (t == 0) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, p);
+        for (int p = 0; p < 4; ++p) issue(p);
+      } else {
+        issue(2 * t + 2);
+        issue(2 * t + 3);
+      }
+    }
+  };
+  w32_step<S, 0>(c, acc[1][3], prev, r, more, [&] { dma(0); });
+  w32_step<S, 1>(c, acc[0][0], prev, r, more, [&] { dma(1); });
+  w32_step<S, 2>(c, acc[1][0], prev, r, more, [&] { dma(2); });
+  w32_step<S, 3>(c, acc[0][1], prev, r, more, [&] { dma(3); });
+  w32_step<S, 4>(c, acc[1][1], prev, r, more, [&] { dma(4); });
+  w32_step<S, 5>(c, acc[0][2], prev, r, more, [&] { dma(5); });
+  w32_step<S, 6>(c, acc[1][2], prev, r, more, [&] { dma(6); });
+  // every copy of block kb+1 was issued by step 6: wait for this wave's, then
+  // for everybody's (and for every wave to be done with stage S ^ 1)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (more) {
+    r.af[0][0] = w32_frag_a<S ^ 1>(c, 0, 0);
+    r.af[0][1] = w32_frag_a<S ^ 1>(c, 0, 1);
   }
-  {
-    const v8i bf = read_b(0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pc[i] = mfma_f8_16x16x128(bf, af[i], zero);
-  }
-#pragma unroll
-  for (int j = 1; j < 8; ++j) {
-    v8i bf = bn;
-    const float4 sbj = sbn;
-    if (j + 1 < 8) {
-      bn = read_b(j + 1);
-      sbn = read_sb(j + 1);
-    }
-    if (j == 7) {
-      // every copy of block kb+1 was issued by region 6: wait for this
-      // wave's, then for everybody's (and for every wave to be done with the
-      // LDS reads of stage S)
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-    }
-    // register fences: the MFMAs of tile j and the promotions of tile j-1 may
-    // not rise above this point and must be done at the fence below.  Left
-    // free, the compiler either batches all MFMAs of the K block (32 partial
-    // tiles alive: spills) or places each promotion right behind its own
-    // MFMA (MFMA and VALU serialize).
-    asm volatile("" : "+v"(bf));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][j - 1]));
-    if (pf && j < 7) {
-      g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, 2 * j + 2);
-      g256_issue_part(c, g256_a<S ^ 1>(), g256_b<S ^ 1>(), g256_s<S ^ 1>(), kb_next, 2 * j + 3);
-    }
-    v4f pn[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pn[i] = mfma_f8_16x16x128(bf, af[i], zero);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) promote4(acc[i][j - 1], pc[i], sav[i], sbc);
-    // issue order MFMA / 8 VALU x 4: the promotion of tile j-1 co-executes
-    // with the MFMAs of tile j
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);   // 8 VALU
-    }
-    // the fence also takes tile j's MFMA results as inputs: without it the
-    // compiler sinks each MFMA down to the promotion that reads it and the
-    // MFMA / VALU pairs serialize
-#pragma unroll
-    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][j - 1]) : "v"(pn[i]));
-    if (j == 7 && more) {
-      const uint8_t* la = g256_a<S ^ 1>();
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = as_v8i(*reinterpret_cast<const uint4*>(la + c.fa0 + i * 2048),
-                       *reinterpret_cast<const uint4*>(la + c.fa1 + i * 2048));
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pc[i] = pn[i];
-    sbc = sbj;
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) promote4(acc[i][7], pc[i], sav[i], sbc);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i][7]));
+  w32_step<S, 7>(c, acc[0][3], prev, r, more, [] {});
 }
 
-// The 64 x 128 result tile of one wave (output rows m0w.., columns n0w..).
-// bf16 with N % 8 == 0: through LDS stage S, which no wave reads once the
-// tile's last K block has passed its barrier: 8 KiB per wave, two halves of
-// 32 rows, each staged with 256-byte rows (16-byte chunk c of row r at
-// c ^ (r & 15), so the 16 rows one write instruction touches fall in
-// different banks) and then stored by 16 lanes per row (256 bytes).  A wave
-// reads back only what it wrote, and LDS completes a wave's accesses in
-// order, so waiting for its own writes is enough and the second half's writes
-// cannot overtake the first half's reads.  Written straight from registers,
-// every output line was assembled from eight 32-byte pieces and the Y GEMM
-// ran ~5% slower.
+// The 64 x 128 result tile of one wave (rows m0w.., columns n0w..).  bf16
+// with N % 8 == 0: through LDS stage S (free once the tile's last K block has
+// passed its barrier), 8 KiB per wave, one 32-row m-tile at a time: lane
+// (c, g) writes the 8-byte pieces p = 8j + 2q + g of row c at slot p ^ c
+// (distinct banks for the 32 rows one write instruction touches), then 16
+// lanes per row read the row's 256 bytes back (pieces 2k, 2k + 1 sit in one
+// 16-byte slot, swapped when the row is odd) and store them whole.  A wave
+// reads back only what it wrote and LDS completes a wave's accesses in
+// order, so waiting for its own writes is enough.
 template <int S, bool OUT_F32>
-__device__ __forceinline__ void g256_store_tile(const v4f (&acc)[4][8], void* __restrict__ C, int M,
-                                                int N, int m0w, int n0w, int wave, int lane_in) {
+__device__ __forceinline__ void w32_store_tile(const v16f (&acc)[2][4], void* __restrict__ C, int M, int N,
+                                               int m0w, int n0w, int wave, int lane_in) {
   // an opaque copy of the lane index: the store addresses derive from it, so
-  // the compiler cannot hoist them out of the tile loop (where ~20 of them
-  // would stay live across the K loop and spill)
+  // the compiler cannot hoist them out of the tile loop (where they would
+  // stay live across the K loop)
   int lane = lane_in;
   asm volatile("" : "+v"(lane));
-  const int fr = lane & 15, fg = lane >> 4;
+  const int cl = lane & 31, g = lane >> 5;
   if (!OUT_F32 && (N % 8) == 0) {
     uint8_t* wbuf = (wave < 4 ? g256_a<S>() : g256_b<S>()) + (wave & 3) * 8192;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int i = 0; i < 2; ++i) {
 #pragma unroll
-      for (int ii = 0; ii < 2; ++ii)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int r = ii * 16 + fr;
-          const int chunk = (j * 2 + (fg >> 1)) ^ (r & 15);
-          const v4f v = acc[2 * h + ii][j];
-          *reinterpret_cast<uint2*>(wbuf + r * 256 + chunk * 16 + (fg & 1) * 8) =
-              make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        for (int q = 0; q < 4; ++q) {
+          const int p = 8 * j + 2 * q + g;
+          const v16f& v = acc[i][j];
+          *reinterpret_cast<uint2*>(wbuf + cl * 256 + (p ^ cl) * 8) =
+              make_uint2(pack_bf16x2(v[4 * q], v[4 * q + 1]), pack_bf16x2(v[4 * q + 2], v[4 * q + 3]));
         }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       const int k = lane & 15;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int r = q * 4 + (lane >> 4);
-        const int m = m0w + h * 32 + r;
+      for (int qq = 0; qq < 8; ++qq) {
+        const int r = qq * 4 + (lane >> 4);
+        uint4 v = *reinterpret_cast<const uint4*>(wbuf + r * 256 + ((2 * k) ^ (r & 30)) * 8);
+        if (r & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+        const int m = m0w + 32 * i + r;
         const int n = n0w + k * 8;
-        const uint4 v = *reinterpret_cast<const uint4*>(wbuf + r * 256 + ((k ^ (r & 15)) * 16));
         if (m < M && n < N)
           *reinterpret_cast<uint4*>(reinterpret_cast<__bf16*>(C) + (int64_t)m * N + n) = v;
       }
     }
     return;
   }
-  // f32 output, or N not a multiple of 8: straight from registers.  Lane
-  // (fr, fg) holds row m = .. + fr and the four consecutive columns
-  // n = .. + 4fg .. 4fg+3 of every 16x16 tile, i.e. 8 contiguous bf16 bytes
-  // (16 f32 bytes); per store instruction the wave writes 16 rows x 32 (64)
-  // contiguous bytes.
+  // f32 output, or N not a multiple of 8: straight from registers; lane
+  // (c, g) holds row c and the four consecutive columns 8q + 4g .. +3 of
+  // every n-tile
   const bool vec_ok = (N % 4) == 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = m0w + i * 16 + fr;
+  for (int i = 0; i < 2; ++i) {
+    const int m = m0w + 32 * i + cl;
     if (m >= M) continue;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int n = n0w + j * 16 + 4 * fg;
-      const v4f v = acc[i][j];
-      if (OUT_F32) {
-        float* dst = reinterpret_cast<float*>(C) + (int64_t)m * N + n;
-        if (vec_ok && n + 4 <= N) {
-          *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-        } else {
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (n + r < N) dst[r] = v[r];
-        }
-      } else {
-        __bf16* dst = reinterpret_cast<__bf16*>(C) + (int64_t)m * N + n;
-        if (vec_ok && n + 4 <= N) {
-          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-        } else {
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0w + 32 * j + 8 * q + 4 * g;
+        const v16f& v = acc[i][j];
+        if (OUT_F32) {
+          float* dst = reinterpret_cast<float*>(C) + (int64_t)m * N + n;
+          if (vec_ok && n + 4 <= N) {
+            *reinterpret_cast<float4*>(dst) = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+          } else {
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (n + r < N) dst[r] = (__bf16)v[r];
+            for (int t = 0; t < 4; ++t)
+              if (n + t < N) dst[t] = v[4 * q + t];
+          }
+        } else {
+          __bf16* dst = reinterpret_cast<__bf16*>(C) + (int64_t)m * N + n;
+          if (vec_ok && n + 4 <= N) {
+            *reinterpret_cast<uint2*>(dst) =
+                make_uint2(pack_bf16x2(v[4 * q], v[4 * q + 1]), pack_bf16x2(v[4 * q + 2], v[4 * q + 3]));
+          } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              if (n + t < N) dst[t] = (__bf16)v[4 * q + t];
+          }
         }
       }
-    }
   }
 }
 
-// Persistent over tiles: workgroup b takes launch slots b, b + G, b + 2G, ...
-// (G = gridDim.x, a multiple of 8, so every slot of a workgroup belongs to its
-// XCD and tile_of's XCD-aware order holds).  The K blocks of all its tiles
-// form one stream: during a tile's last K block the copies of the next tile's
-// block 0 go into the other stage, so the next tile's first load overlaps this
-// tile's last block and its epilogue (which stages through the stage the last
-// block used) instead of starting cold in a new workgroup.
+// Persistent over tiles: workgroup b takes launch
+// slots b, b + G, ... (G a multiple of 8, so its slots stay on its XCD) and
+// walks the K blocks of all its tiles as one stream; a tile's last K block
+// copies the next tile's block 0 into the other stage.
 template <int BNS, bool OUT_F32>
 __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ SA, const uint8_t* __restrict__ B,
     const float* __restrict__ SB, void* __restrict__ C, int M, int N, int K, int tiles_m,
     int tiles_n) {
-  G256Ctx c;
+  W32Ctx c;
   const int tid = threadIdx.x, lane = tid & 63;
   c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: keeps descriptors in SGPRs
   c.nkb = K >> 7;
-  const int fr = lane & 15, fg = lane >> 4;
   const int wm = c.wave >> 1, wn = c.wave & 1;
   const int ntiles = tiles_m * tiles_n;
 
@@ -469,7 +564,7 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
   c.row8 = 8u * (uint32_t)K;
   // loader slot: LDS row wave*32 + u*8 + lane/8, physical chunk lane%8 holds
   // logical chunk (lane%8) ^ swz(row); swz(row) only depends on lane/8 and
-  // on the parity of u (wave*32 + u*8 with u even / odd).
+  // on the parity of u (wave*32 + u*8 with u even / odd)
   const int lrow = c.wave * 32 + (lane >> 3);
   int slot = blockIdx.x;
   int tm_cur, tn_cur;
@@ -481,17 +576,20 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
     c.voa[par] = (lm0 + lrow) * (uint32_t)K + lch * 16;
     c.vob[par] = (ln0 + lrow) * (uint32_t)K + lch * 16;
   }
-  const int sidx = (c.wave & 3) * 64 + lane;
+  // scales: LDS float (wave & 3) * 64 + lane of each scale region; the A rows
+  // in order, the B rows permuted within groups of 32 (see the layout note)
+  const int mu = lane & 31;
+  const int sidx_a = (c.wave & 3) * 64 + lane;
+  const int sidx_b = (c.wave & 3) * 64 + (lane & 32) + 8 * (mu & 3) + 4 * (mu >> 4) + ((mu >> 2) & 3);
   c.rsa = make_rsrc(SA, (uint32_t)M * c.nkb * 4u);
-  c.vosa = (lm0 + sidx) * c.nkb * 4u;
+  c.vosa = (lm0 + sidx_a) * c.nkb * 4u;
   c.rsb = make_rsrc(SB, (uint32_t)nsb * c.nkb * 4u);
-  c.vosb = ((ln0 + sidx) / BNS) * c.nkb * 4u;
+  c.vosb = ((ln0 + sidx_b) / BNS) * c.nkb * 4u;
   // move the loader to the tile of launch slot `s`: every per-lane offset is
   // (tile origin + lane part) * stride, so the move adds a workgroup-uniform
-  // difference (mod 2^32) and no lane part stays live.  Rows past M / N keep
-  // landing past the buffer's end in the per-lane offset and read as zero.
-  // With BNS = 128, (n0 + sidx) / 128 = n0 / 128 + sidx / 128 (n0 % 256 == 0),
-  // so the scale offset moves by n0 / 128 - ln0 / 128 rows.
+  // difference (mod 2^32).  Rows past M / N keep landing past the buffer's
+  // end and read as zero.  With BNS = 128, (n0 + sidx_b) / 128 = n0 / 128 +
+  // sidx_b / 128 (n0 % 256 == 0, sidx_b < 256).
   auto point_loader = [&](int s) {
     int tm, tn;
     tile_of(s, tiles_m, tiles_n, tm, tn);
@@ -507,67 +605,89 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
     lm0 = m0;
     ln0 = n0;
   };
-  // fragment chunks: lane (fr, fg) feeds the MFMA logical chunks fg and
-  // fg + 4 of row r = (wave tile row) + 16 * t + fr (A and B lanes agree, so
-  // the K order inside the block is free); they sit at physical positions
-  // fg ^ swz(r) and (fg + 4) ^ swz(r), and swz(r) == swz(fr) because the
-  // other terms are multiples of 16.  With chunk pairs {2fg, 2fg + 1}
-  // instead, the four lane groups of a read collide in LDS and reads run
-  // about 30% slower.
-  const uint32_t ch0 = (uint32_t)(fg ^ g256_swz(fr)) * 16u;
-  c.fa0 = (uint32_t)(wm * 64 + fr) * 128u + ch0;
-  c.fa1 = c.fa0 ^ 64u;
-  c.fb0 = (uint32_t)(wn * 128 + fr) * 128u + ch0;
-  c.fb1 = c.fb0 ^ 64u;
-  c.fsa = wm * 64 + fr;                 // A-row scale of output row fr
-  c.fsb = 256 + wn * 128 + 4 * fg;      // B-column scales of columns 4fg .. 4fg+3
+  // fragment chunks: lane (cl, g) feeds logical chunks 4h + 2g and 4h + 2g + 1
+  // of row (tile row) + cl for K half h, at physical chunk (logical) ^ swz(row)
+  // with swz(row) == swz(cl) (the tile rows are multiples of 32)
+  const int cl = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t pat = (uint32_t)cl * 128u + (uint32_t)(((4 * h + 2 * g + e) ^ g256_swz(cl)) * 16);
+      c.fa[h][e] = lds_addr(g256_za0) + (uint32_t)(wm * 64) * 128u + pat;
+      c.fb[h][e] = lds_addr(g256_b0) + (uint32_t)(wn * 128) * 128u + pat;
+    }
+  c.fsa = lds_addr(g256_s0) + (uint32_t)(wm * 64 + cl) * 4u;                             // A-row scale of row cl
+  c.fsb = lds_addr(g256_s0) + (uint32_t)(256 + wn * 128 + (g * 4 + (lane & 3)) * 4) * 4u;   // B-column scales
+  // opaque from here on: the compiler would otherwise cancel the stage-0 base
+  // against w32_at's subtraction and re-add the (large) object address per read
+  asm volatile("" : "+v"(c.fa[0][0]), "+v"(c.fa[0][1]), "+v"(c.fa[1][0]), "+v"(c.fa[1][1]));
+  asm volatile("" : "+v"(c.fb[0][0]), "+v"(c.fb[0][1]), "+v"(c.fb[1][0]), "+v"(c.fb[1][1]));
+  asm volatile("" : "+v"(c.fsa), "+v"(c.fsb));
 
-  v4f acc[4][8];
+  v16f acc[2][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j) acc[i][j] = v16f{};
 
   // this workgroup's tiles, and the K blocks of all of them as one stream
   const int my_tiles = (ntiles - slot + (int)gridDim.x - 1) / (int)gridDim.x;
   const int nsteps = my_tiles * c.nkb;
 
-  g256_issue<0>(c, 0);
+  if (c.wave < 4) {
+#pragma unroll
+    for (int p = 0; p < 16; ++p) w32_issue_part(c, g256_za0, g256_b0, g256_s0, 0, p);
+  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  v8i af[4];
+  W32Regs r;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    af[i] = as_v8i(*reinterpret_cast<const uint4*>(g256_a0 + c.fa0 + i * 2048),
-                   *reinterpret_cast<const uint4*>(g256_a0 + c.fa1 + i * 2048));
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) r.af[i][h] = w32_frag_a<0>(c, i, h);
+  r.bf[0] = w32_frag_b<0>(c, 0, 0);
+  r.bf[1] = w32_frag_b<0>(c, 0, 1);
+  r.sb = w32_sb<0>(c, 0);
+  r.sa[0] = w32_sa<0>(c, 0);
+  r.sa[1] = w32_sa<0>(c, 1);
+  // nothing to promote before the first tile: a zero product with zero
+  // scales into acc[1][3], which stays zero
+  W32Prev prev;
+  prev.p = v16f{};
+  prev.sa = 0.0f;
+  prev.sb = make_float4(0.f, 0.f, 0.f, 0.f);
 
-  // One step of the stream from stage S: K block kb of the current tile.  At
-  // a tile's last block the loader moves on to the next slot first, and after
-  // it the tile's results leave through stage S (free: no wave reads it after
-  // the block's barrier) before the accumulators restart from zero.
   int kb = 0, step = 0;
   auto one_step = [&](auto stage) {
     constexpr int S = decltype(stage)::value;
     const bool last = kb + 1 == c.nkb;
     const bool more = step + 1 < nsteps;
     if (last && more) point_loader(slot + (int)gridDim.x);
-    g256_compute_tail<S>(c, acc, af, last ? 0 : kb + 1, more);
+    w32_block<S>(c, acc, prev, r, last ? 0 : kb + 1, more);
     ++step;
     if (!last) {
       ++kb;
       return;
     }
-    g256_store_tile<S, OUT_F32>(acc, C, M, N, tm_cur * 256 + wm * 64, tn_cur * 256 + wn * 128, c.wave,
-                                lane);
+    // the tile's last step promoted tile 6; tile 7's promotion has no MFMA of
+    // this tile left to hide behind
+    w32_promote_half(acc[1][3], prev.p, prev.sa, prev.sb, 0);
+    w32_promote_half(acc[1][3], prev.p, prev.sa, prev.sb, 1);
+    prev.p = v16f{};
+    prev.sa = 0.0f;
+    prev.sb = make_float4(0.f, 0.f, 0.f, 0.f);
+    w32_store_tile<S, OUT_F32>(acc, C, M, N, tm_cur * 256 + wm * 64, tn_cur * 256 + wn * 128, c.wave,
+                               lane);
     if (more) {
-      // every wave is done reading stage S before the next block's copies land there
+      // every wave is done with stage S before the next block's copies land there
       __syncthreads();
       slot += gridDim.x;
       tile_of(slot, tiles_m, tiles_n, tm_cur, tn_cur);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 4; ++j) acc[i][j] = v16f{};
     }
     kb = 0;
   };
@@ -578,17 +698,22 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
   if (step < nsteps) one_step(IntC<0>{});
 }
 
-// Compute units of the current device (cached per device id).
+// Compute units of the current device, queried once per device id.  Entry
+// points may be called concurrently from several host threads (an XLA FFI
+// handler runs on XLA's thread pool), so the one-time query is guarded by a
+// per-device std::call_once.
 static int device_cus() {
-  static int cached[64];
+  constexpr int kMaxDev = 64;
+  static std::once_flag once[kMaxDev];
+  static int cached[kMaxDev];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cached[dev] <= 0) {
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) dev = 0;
+  std::call_once(once[dev], [dev] {
     int v = 0;
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
       v = 256;
     cached[dev] = v;
-  }
+  });
   return cached[dev];
 }
 
@@ -613,12 +738,20 @@ static int launch_gemm_cfg(const uint8_t* a_q, const float* a_s, const uint8_t* 
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   const size_t lds = (size_t)2 * (BM + BN) * 128 + (size_t)2 * (BM + BN) * 4;
   auto kern = gemm_fp8_nt_kernel<TM, TN, BNS, OUT_F32>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-      return check_launch("gemm_fp8 (set LDS size)");
-    attr_set = true;
+  // the dynamic-LDS limit is a per-device function attribute: set once per
+  // device (thread-safe, see device_cus)
+  constexpr int kMaxDev = 64;
+  static std::once_flag once[kMaxDev];
+  static hipError_t attr_rc[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) dev = 0;
+  std::call_once(once[dev], [&] {
+    attr_rc[dev] = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  });
+  if (attr_rc[dev] != hipSuccess) {
+    set_error("gemm_fp8 (set LDS size): %s", hipGetErrorString(attr_rc[dev]));
+    return TG_EHIP;
   }
   hipLaunchKernelGGL(kern, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), lds, st, a_q, a_s, b_q,
                      b_s, c, M, N, K, tiles_m, tiles_n);
@@ -1284,14 +1417,14 @@ static void launch_rowdot_k(const RowdotIn& in, const uint8_t* w_q, const float*
   // persistent waves, one wave per weight row at a time: as many workgroups
   // as fit on the CUs at once (registers: once per instantiation; LDS: 160 KiB
   // per CU), at most 8 per CU, so that no workgroup waits for a free slot
-  static int occ_regs = 0;
-  if (occ_regs <= 0) {
+  // (a function-local static: its initializer runs once, thread-safely)
+  static const int occ_regs = [] {
     int v = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_rowdot_kernel<NX, PRO, XL, J>, 256, 0) !=
             hipSuccess || v <= 0)
       v = 4;
-    occ_regs = v;
-  }
+    return v;
+  }();
   int per_cu = occ_regs < 8 ? occ_regs : 8;
   const int by_lds = (int)((160 * 1024) / (lds > 0 ? lds : 1));
   if (by_lds < per_cu) per_cu = by_lds < 1 ? 1 : by_lds;
