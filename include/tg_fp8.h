@@ -92,6 +92,21 @@ int tg_block_scaled_matmul(const void* a, const void* b, void* out, int64_t M, i
                            int64_t K, int block_k, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* tg_block_scaled_matmul without a caller workspace, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  The quantized
+ * operands live in a static device array of TG_NOALLOC_SCRATCH_BYTES (each
+ * device the library runs on holds it until the process ends), whose address
+ * is resolved once per device; the call allocates nothing.  Shapes whose
+ * workspace (tg_block_scaled_matmul_workspace) exceeds it return TG_EINVAL;
+ * C3's forward (8192 x 2048 x 8192) needs 34.6 MB.  Output bits equal
+ * tg_block_scaled_matmul's.  All calls on one device share the array: calls
+ * that overlap on one device (different streams, or host threads) race;
+ * serialize them.  a, b 16-byte aligned. */
+#define TG_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int tg_block_scaled_matmul_noalloc(const void* a, const void* b, void* out, int64_t M, int64_t N,
+                                   int64_t K, int block_k, void* stream);
+
 /* Device workspace (bytes) of tg_block_scaled_matmul_bwd_fp8. */
 size_t tg_block_scaled_matmul_bwd_workspace(int64_t M, int64_t N, int64_t K, int block_k);
 

@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(_HERE, "libtg_fp8.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "tg_fp8.h")
 
 TG_OK, TG_EINVAL, TG_EHIP = 0, 1, 2
+TG_NOALLOC_SCRATCH_BYTES = 64 << 20     # include/tg_fp8.h
 TG_DTYPE_BF16, TG_DTYPE_F32 = 0, 1
 
 _vp, _i64, _int, _f32, _sz = (ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
@@ -30,6 +31,7 @@ SIGNATURES = {
     "tg_gemm_fp8_nt": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _int, _vp]),
     "tg_block_scaled_matmul_workspace": (_sz, [_i64, _i64, _i64, _int]),
     "tg_block_scaled_matmul": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp, _sz, _vp]),
+    "tg_block_scaled_matmul_noalloc": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
     "tg_block_scaled_matmul_bwd_workspace": (_sz, [_i64, _i64, _i64, _int]),
     "tg_block_scaled_matmul_bwd_fp8": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int,
                                               _vp, _sz, _vp]),
