@@ -1,0 +1,60 @@
+"""The XLA FFI handlers (train-gpt_amd/csrc/ffi/tg_xla_ffi.cc) against the C ABI
+and the registration table, checked on the CPU: jaxlib is not installed here,
+so the handlers are not compiled (the build step says so and skips)."""
+import os
+import re
+
+import _tglib as L
+import build
+import xla_ffi
+
+SRC = build.FFI_SRC
+
+
+def _code(path):
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.sub(r"//[^\n]*", "", text)
+
+
+def _declared():
+    return set(re.findall(r"\b(tg_[a-z0-9_]+)\s*\(", _code(L.HEADER_PATH)))
+
+
+def test_handlers_call_only_declared_entry_points():
+    called = set(re.findall(r"\b(tg_[a-z0-9_]+)\s*\(", _code(SRC))) - {"tg_last_error"}
+    abi_calls = {n for n in called if not n.startswith("tg_ffi_")}
+    assert abi_calls, "no C-ABI calls found"
+    assert abi_calls <= _declared(), sorted(abi_calls - _declared())
+
+
+def test_handler_symbols_match_the_registration_table():
+    defined = re.findall(r"XLA_FFI_DEFINE_HANDLER_SYMBOL\(\s*(tg_ffi_[a-z0-9_]+)\s*,", _code(SRC))
+    assert len(defined) == len(set(defined))
+    assert sorted(defined) == sorted(sym for sym, _ in xla_ffi.HANDLERS.values())
+    # every entry point a handler is listed as wrapping is declared and called
+    code = _code(SRC)
+    for target, (sym, abi) in xla_ffi.HANDLERS.items():
+        for name in abi:
+            assert name in _declared(), (target, name)
+            assert re.search(rf"\b{name}\s*\(", code), (target, name)
+
+
+def test_every_compute_path_of_the_reference_has_a_handler():
+    # fp8.py:39-47, 50-78 (+ the kept-weight GEMM), 85-98 (both rules);
+    # kernels.py:30-33, fused norm -> quant, 104-118
+    wrapped = {n for _, abi in xla_ffi.HANDLERS.values() for n in abi}
+    for name in ("tg_quantize_rows", "tg_block_scaled_matmul", "tg_block_scaled_matmul_bwd_fp8",
+                 "tg_block_scaled_matmul_bwd_bf16", "tg_rms_norm", "tg_rms_norm_fp8",
+                 "tg_rms_norm_bwd", "tg_gemm_fp8_nt"):
+        assert name in wrapped, name
+
+
+def test_build_step_skips_without_jax(capsys):
+    try:
+        import jax  # noqa: F401
+    except ImportError:
+        assert build.build_xla_ffi() is None
+        assert "skipping the XLA FFI handlers" in capsys.readouterr().out
+    else:  # jaxlib present: the handlers must build
+        assert os.path.exists(build.build_xla_ffi())

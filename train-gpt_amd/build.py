@@ -54,6 +54,36 @@ def build_library(verbose: bool = False) -> str:
     return LIB
 
 
+FFI_SRC = os.path.join(CSRC, "ffi", "tg_xla_ffi.cc")
+FFI_LIB = os.path.join(HERE, "libtg_xla_ffi.so")
+
+
+def build_xla_ffi(verbose: bool = False):
+    """Compile the XLA FFI handlers (csrc/ffi/tg_xla_ffi.cc) into libtg_xla_ffi.so.
+
+    They need xla/ffi/api/ffi.h, which jaxlib ships (jax.ffi.include_dir()).
+    Where jax is not importable the step is skipped with a message and None is
+    returned; the C ABI (libtg_fp8.so) does not depend on it.
+    """
+    try:
+        import jax
+        inc = jax.ffi.include_dir()
+    except Exception as e:  # jax / jaxlib absent, or too old for jax.ffi
+        print(f"skipping the XLA FFI handlers: jax.ffi.include_dir() is unavailable "
+              f"({e.__class__.__name__}: {e})")
+        return None
+    root = os.path.dirname(HERE)
+    cmd = [HIPCC, "-std=c++17", "-O2", "-fPIC", "-shared", "-I", inc, "-I", os.path.join(root, "include"),
+           FFI_SRC, "-L", HERE, "-ltg_fp8", "-Wl,-rpath,$ORIGIN", "-o", FFI_LIB]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"XLA FFI handlers failed to build:\n{r.stdout}\n{r.stderr}")
+    if verbose:
+        print(f"built {FFI_LIB}")
+    return FFI_LIB
+
+
 if __name__ == "__main__":
     build_library(verbose=True)
+    build_xla_ffi(verbose=True)
     sys.exit(0)
