@@ -156,6 +156,14 @@ int tg_block_scaled_matmul_bwd_bf16(const void* a, int a_dtype, const void* b, i
 int tg_rms_norm(const void* x, const void* scale, void* y, int64_t rows, int64_t dim, float eps,
                 void* stream);
 
+/* _rms_norm_pure (kernels.py:30-33) for any float dtypes: x (rows, dim) and
+ * scale (dim,) each bf16 or f32 (x_dtype / scale_dtype); y (rows, dim) is f32
+ * when either is f32, else bf16 (jnp's promotion of x_n * scale).
+ * r = rsqrt(mean(x^2) + eps) rounded to x's dtype, x_n = x * r rounded to
+ * x's dtype, y = x_n * scale.  Any dim; bf16/bf16 takes tg_rms_norm's kernel. */
+int tg_rms_norm_ex(const void* x, int x_dtype, const void* scale, int scale_dtype, void* y,
+                   int64_t rows, int64_t dim, float eps, void* stream);
+
 /* Fused RMSNorm -> FP8 quantize (the composition of kernels.py:30-33 and
  * fp8.py:39-47 on the bf16 norm output, from one read of x):
  * y (rows, dim) bf16, q (rows, dim) e4m3fn, s (rows, dim/block_k) f32. */
@@ -178,12 +186,20 @@ size_t tg_rms_norm_bwd_workspace(int64_t rows, int64_t dim);
  *   rnorm = rsqrt(mean(x^2) + eps), normed = x * rnorm, gs = dy * scale
  *   dx = bf16(rnorm * (gs - normed * mean(gs * normed)))   (rows, dim)
  *   dscale = bf16(sum over rows of dy * normed)            (dim,)
- * x, dy, dx bf16 (rows, dim); scale, dscale bf16 (dim,); dim % 8 == 0 and
- * dim <= 4096.  dscale is summed in a fixed order (identical on every call);
- * rows == 0 gives dscale = 0. */
+ * x, dy, dx bf16 (rows, dim); scale, dscale bf16 (dim,); dim % 8 == 0 (widths
+ * above 4096 take tg_rms_norm_bwd_ex's general kernels).  dscale is summed in
+ * a fixed order (identical on every call); rows == 0 gives dscale = 0. */
 int tg_rms_norm_bwd(const void* x, const void* scale, const void* dy, void* dx, void* dscale,
                     int64_t rows, int64_t dim, float eps, void* workspace, size_t workspace_bytes,
                     void* stream);
+
+/* The same backward for any float dtypes: x, scale, dy each bf16 or f32 (their
+ * *_dtype codes); dx is written in x's dtype, dscale in scale's (the
+ * .astype(x.dtype) / .astype(scale.dtype) of kernels.py:115-117); any dim.
+ * Workspace as tg_rms_norm_bwd_workspace. */
+int tg_rms_norm_bwd_ex(const void* x, int x_dtype, const void* scale, int scale_dtype, const void* dy,
+                       int dy_dtype, void* dx, void* dscale, int64_t rows, int64_t dim, float eps,
+                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* Decode-shape GEMM with a pre-quantized weight (no reference function; the
  * reference re-quantizes W every call at fp8.py:68):

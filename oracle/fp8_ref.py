@@ -147,6 +147,25 @@ def fp8_backward_bf16(a_bf16, b_bf16, g_bf16):
     return g2 @ b.T, a2.T @ g2
 
 
+def quantize_fp8_partial(x_f32: np.ndarray, block_k: int = DEFAULT_BLOCK_K):
+    """quantize_fp8 along the last axis with a trailing partial block.
+
+    fp8.py:39-47 defines whole blocks only.  A trailing block of K % block_k
+    elements is quantized over its valid elements, i.e. as a zero-padded whole
+    block (zeros raise no amax and add nothing to a dot product).  Returns
+    (q (..., K) uint8, scales (..., ceil(K / block_k)) f32).
+    """
+    x = np.asarray(x_f32, dtype=np.float32)
+    *lead, K = x.shape
+    Kp = -(-K // block_k) * block_k
+    if Kp == K:
+        return quantize_fp8(x, block_k)
+    xp = np.zeros((*lead, Kp), dtype=np.float32)
+    xp[..., :K] = x
+    q, s = quantize_fp8(xp, block_k)
+    return q[..., :K], s
+
+
 def fp8_backward_fp8(a_bf16, b_bf16, g_bf16, block_k: int = DEFAULT_BLOCK_K):
     """FP8 backward: the forward composition reused for both gradients.
 
@@ -155,7 +174,10 @@ def fp8_backward_fp8(a_bf16, b_bf16, g_bf16, block_k: int = DEFAULT_BLOCK_K):
       dX = fwd(g, b.T)   -> A = g row-quantized along N, B = b row-quantized along N
       dW = fwd(a.T, g)   -> A = a.T quantized along M, B = g.T quantized along M
     Returns (dx_f64 (M,K), dw_f64 (K,N), operands) where operands holds the
-    four quantized (bytes, scales) pairs for bit-exact checks.
+    four quantized (bytes, scales) pairs for bit-exact checks.  When N (dX's
+    contraction) or M (dW's) is not a multiple of block_k, the operands are
+    zero-padded along it (quantize_fp8_partial's trailing block); the
+    operands returned are then those of the padded problem.
     """
     a = bf16_to_f32(a_bf16)
     b = bf16_to_f32(b_bf16)
@@ -164,12 +186,18 @@ def fp8_backward_fp8(a_bf16, b_bf16, g_bf16, block_k: int = DEFAULT_BLOCK_K):
     N = b.shape[1]
     a2 = a.reshape(-1, K)
     g2 = g.reshape(-1, N)
+    M = a2.shape[0]
+    Mp, Np = -(-M // block_k) * block_k, -(-N // block_k) * block_k
+    if (Mp, Np) != (M, N):
+        a2 = np.pad(a2, ((0, Mp - M), (0, 0)))
+        b = np.pad(b, ((0, 0), (0, Np - N)))
+        g2 = np.pad(g2, ((0, Mp - M), (0, Np - N)))
     qg, sg = quantize_fp8(g2, block_k)                          # (M, N) along N
     qb, sb = quantize_fp8(b, block_k)                           # (K, N) along N
     qat, sat = quantize_fp8(np.ascontiguousarray(a2.T), block_k)   # (K, M) along M
     qgt, sgt = quantize_fp8(np.ascontiguousarray(g2.T), block_k)   # (N, M) along M
-    dx = dequant_gemm_nt(qg, sg, qb, sb, block_k)
-    dw = dequant_gemm_nt(qat, sat, qgt, sgt, block_k)
+    dx = dequant_gemm_nt(qg, sg, qb, sb, block_k)[:M]
+    dw = dequant_gemm_nt(qat, sat, qgt, sgt, block_k)[:, :N]
     ops = {"g_rows": (qg, sg), "b_rows": (qb, sb), "a_cols": (qat, sat), "g_cols": (qgt, sgt)}
     return dx, dw, ops
 

@@ -50,6 +50,31 @@ def rms_norm_pure(x_bf16: np.ndarray, g_bf16: np.ndarray, eps: float) -> np.ndar
     return y
 
 
+def rms_norm_pure_any(x_f32, x_is_bf16: bool, g_f32, eps):
+    """``_rms_norm_pure`` (kernels.py:30-33) for any float dtypes, on values.
+
+    x_f32 holds x's values (bf16-representable when x_is_bf16), g_f32 the
+    scale's.  r = rsqrt(var + eps) and x_n = x * r are rounded to x's dtype;
+    y = x_n * scale in f32 (the caller rounds to bf16 when both are bf16).
+    Returns y as f32 values.
+    """
+    x = np.asarray(x_f32, dtype=np.float32)
+    g = np.asarray(g_f32, dtype=np.float32)
+    D = x.shape[-1]
+    with np.errstate(over="ignore", invalid="ignore", under="ignore"):
+        sq = (x * x).astype(np.float32)
+        ssum = np.sum(sq.astype(np.float64), axis=-1).astype(np.float32)
+        var = (ssum / np.float32(D)).astype(np.float32)
+        v = (var + np.float32(eps)).astype(np.float32)
+        r = (1.0 / np.sqrt(v.astype(np.float64))).astype(np.float32)[..., None]
+        if x_is_bf16:
+            r = bf16_to_f32(f32_to_bf16(r))
+        t = (x * r).astype(np.float32)
+        if x_is_bf16:
+            t = bf16_to_f32(f32_to_bf16(t))
+        return (t * g).astype(np.float32)
+
+
 def rms_norm_single_rounding(x_bf16, g_bf16, eps):
     """The Pallas kernel's arithmetic (kernels.py:49-53): f32 x * rnorm * scale, one bf16 rounding."""
     x = bf16_to_f32(x_bf16)
@@ -72,15 +97,20 @@ def rms_norm_fp8(x_bf16, g_bf16, eps, block_k: int = 128):
 
 
 def rms_norm_vjp(x_bf16, g_bf16, eps, dy_bf16):
-    """``_bwd`` (kernels.py:104-118) in float64.
+    """``_bwd`` (kernels.py:104-118) in float64 on bf16 bit patterns (see rms_norm_vjp_vals)."""
+    return rms_norm_vjp_vals(bf16_to_f32(x_bf16), bf16_to_f32(g_bf16), eps, bf16_to_f32(dy_bf16))
+
+
+def rms_norm_vjp_vals(x_f32, g_f32, eps, dy_f32):
+    """``_bwd`` (kernels.py:104-118) in float64 on the operands' values (any dtype).
 
     normed = x * rsqrt(mean(x^2) + eps); gs = dy * scale;
     grad_x = rnorm * (gs - normed * mean(gs * normed)); grad_scale = sum(dy * normed).
     Returns (grad_x f64, grad_scale f64).
     """
-    x = bf16_to_f32(x_bf16).astype(np.float64)
-    g = bf16_to_f32(g_bf16).astype(np.float64)
-    dy = bf16_to_f32(dy_bf16).astype(np.float64)
+    x = np.asarray(x_f32, dtype=np.float64)
+    g = np.asarray(g_f32, dtype=np.float64)
+    dy = np.asarray(dy_f32, dtype=np.float64)
     var = np.mean(x * x, axis=-1, keepdims=True)
     rn = 1.0 / np.sqrt(var + eps)
     normed = x * rn

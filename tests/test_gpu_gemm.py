@@ -197,6 +197,29 @@ def test_fp8_backward(dev, M, N, K):
     assert same_scales(sat.cpu().numpy(), ops["a_cols"][1])
 
 
+@pytest.mark.parametrize("lead,K,N", [((200,), 256, 200), ((256,), 384, 200), ((200,), 128, 384),
+                                      ((3,), 128, 8), ((2, 100), 256, 128)])
+def test_fp8_backward_ragged(dev, lead, K, N):
+    """M or N not a multiple of 128 (fp8.py:85-98 accepts any shape): the FP8
+    rule on zero-padded operands, i.e. the trailing partial block quantized
+    over its valid elements (oracle: fp8_ref.fp8_backward_fp8)."""
+    rng = np.random.default_rng(sum(lead) + 3 * N + K)
+    a_u = ob.randn_bf16(rng, (*lead, K))
+    b_u = ob.randn_bf16(rng, (K, N), std=0.02)
+    g_u = ob.randn_bf16(rng, (*lead, N), std=1e-3)
+    a = to_dev(a_u, dev).requires_grad_(True)
+    b = to_dev(b_u, dev).requires_grad_(True)
+    y = fp8.block_scaled_matmul(a, b)
+    y.backward(to_dev(g_u, dev))
+    dx_ref, dw_ref, _ = fp8_ref.fp8_backward_fp8(a_u, b_u, g_u)
+    assert a.grad.shape == a.shape and b.grad.shape == b.shape
+    assert maxabs_rel(a.grad.reshape(-1, K), dx_ref) <= TOL
+    assert maxabs_rel(b.grad, dw_ref) <= TOL
+    dx_bf, dw_bf = fp8_ref.fp8_backward_bf16(a_u, b_u, g_u)
+    print(f"ragged bwd {tuple(a.shape)}x{tuple(b.shape)}: dX err vs bf16 rule "
+          f"{maxabs_rel(a.grad.reshape(-1, K), dx_bf):.3e}, dW {maxabs_rel(b.grad, dw_bf):.3e}")
+
+
 def test_gemm_c3_full_size_sampled(dev):
     """Config 3 forward+backward at full size; rows/columns sampled against the oracle."""
     rng = np.random.default_rng(2)

@@ -87,13 +87,15 @@ def test_rms_norm_special_rows(dev):
 def test_rms_norm_errors(dev):
     x = torch.zeros((2, 100), dtype=torch.bfloat16, device=dev)
     g = torch.ones(100, dtype=torch.bfloat16, device=dev)
-    with pytest.raises(ValueError, match="multiple of 8"):
-        kernels.rms_norm(x, g, 1e-6)
     with pytest.raises(ValueError, match="not divisible by block_k"):
         kernels.rms_norm_fp8(torch.zeros((2, 200), dtype=torch.bfloat16, device=dev),
                              torch.ones(200, dtype=torch.bfloat16, device=dev), 1e-6)
     with pytest.raises(TypeError):
-        kernels.rms_norm(x.float(), g, 1e-6)
+        kernels.rms_norm(x.half(), g, 1e-6)
+    with pytest.raises(TypeError):
+        kernels.rms_norm_fp8(x.float(), g, 1e-6)
+    with pytest.raises(ValueError, match="scale must have shape"):
+        kernels.rms_norm(x, g[:50], 1e-6)
 
 
 @pytest.mark.parametrize("shape", [(1, 2304), (8, 2048), (5, 768), (3, 16384)])
@@ -128,3 +130,29 @@ def test_add_rms_norm_fp8_without_y(dev):
     _, q_o, s_o = norm_ref.rms_norm_fp8(xs, g, 1e-5)
     np.testing.assert_array_equal(u8(q), q_o)
     assert same_scales(s.cpu().numpy(), s_o)
+
+
+@pytest.mark.parametrize("x_dt,g_dt,D", [(torch.float32, torch.float32, 2048), (torch.float32, torch.bfloat16, 1000),
+                                        (torch.bfloat16, torch.float32, 2304), (torch.bfloat16, torch.bfloat16, 20000),
+                                        (torch.bfloat16, torch.bfloat16, 100)])
+def test_rms_norm_any_dtype_and_width(dev, x_dt, g_dt, D):
+    """_rms_norm_pure (kernels.py:30-33) keeps x's dtype for r and x * r and returns
+    the promoted dtype (f32 when either operand is f32); bit-exact against
+    norm_ref.rms_norm_pure_any, including a width the bf16 kernel does not take."""
+    rng = np.random.default_rng(D)
+    x = (rng.standard_normal((37, D)) * np.where(rng.random((37, D)) < 1e-3, 50, 1)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    if x_dt == torch.bfloat16:
+        x = ob.bf16_to_f32(ob.f32_to_bf16(x))
+    if g_dt == torch.bfloat16:
+        g = ob.bf16_to_f32(ob.f32_to_bf16(g))
+    xt = torch.from_numpy(x).to(dev).to(x_dt)
+    gt = torch.from_numpy(g).to(dev).to(g_dt)
+    y = kernels._rms_norm_pure(xt, gt, 1e-6)
+    want = norm_ref.rms_norm_pure_any(x, x_dt == torch.bfloat16, g, 1e-6)
+    out_dt = torch.float32 if torch.float32 in (x_dt, g_dt) else torch.bfloat16
+    assert y.dtype == out_dt and y.shape == xt.shape
+    if out_dt == torch.bfloat16:
+        np.testing.assert_array_equal(bf16_bits(y), ob.f32_to_bf16(want))
+    else:
+        np.testing.assert_array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))

@@ -84,9 +84,34 @@ def test_rms_norm_bwd_constant_rows(dev):
     assert float(dg.float().abs().max()) < 1e-3
 
 
-def test_rms_norm_bwd_rejects_large_dim(dev):
-    x = torch.zeros((2, 8192), dtype=torch.bfloat16, device=dev, requires_grad=True)
-    g = torch.ones((8192,), dtype=torch.bfloat16, device=dev, requires_grad=True)
-    y = kernels.rms_norm(x, g, 1e-6)
-    with pytest.raises(ValueError, match="4096"):
-        y.backward(torch.ones_like(y))
+@pytest.mark.parametrize("x_dt,g_dt,D", [(torch.float32, torch.float32, 2048), (torch.float32, torch.bfloat16, 1000),
+                                        (torch.bfloat16, torch.float32, 512), (torch.bfloat16, torch.bfloat16, 8192),
+                                        (torch.bfloat16, torch.bfloat16, 100)])
+def test_rms_norm_bwd_any_dtype_and_width(dev, x_dt, g_dt, D):
+    """kernels.py:104-118 for f32 / mixed operands and a width above the bf16
+    kernel's 4096: dx in x's dtype, dscale in scale's, against the float64 VJP;
+    dscale identical on a second call (fixed summation order)."""
+    rng = np.random.default_rng(D + 1)
+    x = rng.standard_normal((300, D)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    if x_dt == torch.bfloat16:
+        x = ob.bf16_to_f32(ob.f32_to_bf16(x))
+    if g_dt == torch.bfloat16:
+        g = ob.bf16_to_f32(ob.f32_to_bf16(g))
+    out_dt = torch.float32 if torch.float32 in (x_dt, g_dt) else torch.bfloat16
+    dy = (rng.standard_normal((300, D)) * 1e-2).astype(np.float32)
+    if out_dt == torch.bfloat16:
+        dy = ob.bf16_to_f32(ob.f32_to_bf16(dy))
+    xt = torch.from_numpy(x).to(dev).to(x_dt).requires_grad_(True)
+    gt = torch.from_numpy(g).to(dev).to(g_dt).requires_grad_(True)
+    y = kernels.rms_norm(xt, gt, 1e-6)
+    y.backward(torch.from_numpy(dy).to(dev).to(out_dt))
+    gx, gg = norm_ref.rms_norm_vjp_vals(x, g, 1e-6, dy)
+    assert xt.grad.dtype == x_dt and gt.grad.dtype == g_dt
+    tol = TOL if torch.bfloat16 in (x_dt, g_dt) else 1e-5
+    assert maxabs_rel(xt.grad, gx) <= (TOL if x_dt == torch.bfloat16 else tol)
+    assert maxabs_rel(gt.grad, gg) <= (TOL if g_dt == torch.bfloat16 else 1e-4)
+    first = gt.grad.clone()
+    gt.grad = None
+    kernels.rms_norm(xt, gt, 1e-6).backward(torch.from_numpy(dy).to(dev).to(out_dt))
+    assert torch.equal(gt.grad, first)

@@ -41,6 +41,29 @@ def test_bf16_ops_match_torch():
     np.testing.assert_array_equal(y, norm_ref.rms_norm_pure(x, g, 1e-6))
 
 
+def test_any_dtype_path_matches_torch_and_the_bf16_path():
+    """rms_norm_pure_any: f32 x (r and x * r unrounded f32) and bf16 x with an f32
+    scale, against torch's f32 / bf16 CPU arithmetic on the oracle's rsqrt; with
+    both bf16 its bf16 rounding equals rms_norm_pure."""
+    rng = np.random.default_rng(6)
+    xb, gb = _inputs(rng, (32, 1024))
+    x32 = (rng.standard_normal((32, 1024)) * 2).astype(np.float32)
+    g32 = (1 + 0.1 * rng.standard_normal(1024)).astype(np.float32)
+    # f32 x, f32 scale
+    var = (np.sum((x32 * x32).astype(np.float64), axis=-1).astype(np.float32) / np.float32(1024)).astype(np.float32)
+    r = (1.0 / np.sqrt((var + np.float32(1e-6)).astype(np.float64))).astype(np.float32)
+    want = ((torch.from_numpy(x32) * torch.from_numpy(r)[:, None]) * torch.from_numpy(g32)).numpy()
+    np.testing.assert_array_equal(norm_ref.rms_norm_pure_any(x32, False, g32, 1e-6), want)
+    # bf16 x, f32 scale: x_n in bf16, then an f32 product
+    _, rb = norm_ref.row_inv_rms(xb, 1e-6)
+    xn = _t(xb) * _t(ob.f32_to_bf16(rb))[:, None]                    # bf16 x bf16 -> bf16
+    want = (xn.float() * torch.from_numpy(g32)).numpy()
+    np.testing.assert_array_equal(norm_ref.rms_norm_pure_any(ob.bf16_to_f32(xb), True, g32, 1e-6), want)
+    # both bf16
+    y = norm_ref.rms_norm_pure_any(ob.bf16_to_f32(xb), True, ob.bf16_to_f32(gb), 1e-6)
+    np.testing.assert_array_equal(ob.f32_to_bf16(y), norm_ref.rms_norm_pure(xb, gb, 1e-6))
+
+
 def test_variance_and_rsqrt_exact():
     rng = np.random.default_rng(1)
     x, _ = _inputs(rng, (6, 2304))

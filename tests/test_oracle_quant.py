@@ -107,3 +107,24 @@ def test_weight_128x128_tiles():
     assert s[1, 1] == np.float32(np.max(np.abs(w_t[128:, 128:]))) / np.float32(448)
     deq = fp8_ref.e4m3fn_decode(q) * np.repeat(np.repeat(s, 128, 0)[:200], 128, 1)
     assert np.max(np.abs(deq - w_t)) <= np.max(np.abs(w_t)) * 2.0 ** -4
+
+
+def test_partial_trailing_block_is_its_valid_elements():
+    """quantize_fp8_partial: the trailing block's scale is max(amax of its
+    valid elements / 448, 1e-30) and its bytes e4m3(x / s), computed here
+    directly (no padding), including an all-zero trailing block."""
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((5, 200)) * np.array([1, 3, 0.01, 100, 1])[:, None]).astype(np.float32)
+    x[4, 128:] = 0.0
+    q, s = fp8_ref.quantize_fp8_partial(x)
+    assert q.shape == (5, 200) and s.shape == (5, 2)
+    q_whole, s_whole = fp8_ref.quantize_fp8(x[:, :128])
+    np.testing.assert_array_equal(q[:, :128], q_whole)
+    np.testing.assert_array_equal(s[:, :1], s_whole)
+    tail = x[:, 128:]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        s_tail = np.maximum(np.max(np.abs(tail), axis=1) / np.float32(448.0), np.float32(1e-30)).astype(np.float32)
+        q_tail = fp8_ref.e4m3fn_encode((tail / s_tail[:, None]).astype(np.float32))
+    np.testing.assert_array_equal(s[:, 1], s_tail)
+    np.testing.assert_array_equal(q[:, 128:], q_tail)
+    assert s[4, 1] == np.float32(1e-30) and np.all(q[4, 128:] == 0)

@@ -45,8 +45,8 @@ def test_every_compute_path_of_the_reference_has_a_handler():
     # kernels.py:30-33, fused norm -> quant, 104-118
     wrapped = {n for _, abi in xla_ffi.HANDLERS.values() for n in abi}
     for name in ("tg_quantize_rows", "tg_block_scaled_matmul", "tg_block_scaled_matmul_bwd_fp8",
-                 "tg_block_scaled_matmul_bwd_bf16", "tg_rms_norm", "tg_rms_norm_fp8",
-                 "tg_rms_norm_bwd", "tg_gemm_fp8_nt"):
+                 "tg_block_scaled_matmul_bwd_bf16", "tg_rms_norm_ex", "tg_rms_norm_fp8",
+                 "tg_rms_norm_bwd_ex", "tg_gemm_fp8_nt"):
         assert name in wrapped, name
 
 

@@ -36,9 +36,12 @@ SIGNATURES = {
     "tg_block_scaled_matmul_bwd_fp8": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int,
                                               _vp, _sz, _vp]),
     "tg_rms_norm": (_int, [_vp, _vp, _vp, _i64, _i64, _f32, _vp]),
+    "tg_rms_norm_ex": (_int, [_vp, _int, _vp, _int, _vp, _i64, _i64, _f32, _vp]),
     "tg_rms_norm_fp8": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _int, _vp]),
     "tg_rms_norm_bwd_workspace": (_sz, [_i64, _i64]),
     "tg_rms_norm_bwd": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _vp, _sz, _vp]),
+    "tg_rms_norm_bwd_ex": (_int, [_vp, _int, _vp, _int, _vp, _int, _vp, _vp, _i64, _i64, _f32, _vp,
+                                  _sz, _vp]),
     "tg_gemv_fp8": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _i64, _i64, _i64, _int, _vp]),
     "tg_gemv_fp8_rowdot": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _i64, _i64, _i64, _int, _vp]),
     "tg_rms_norm_fp8_gemv": (_int, [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _vp, _i64, _i64, _i64, _vp]),

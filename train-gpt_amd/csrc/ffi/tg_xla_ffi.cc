@@ -150,12 +150,19 @@ ffi::Error BlockScaledMatmulBwdBf16(hipStream_t stream, ffi::ScratchAllocator sc
                                                 db->untyped_data(), M, N, K, ws, ws_bytes, stream));
 }
 
-// _rms_norm_pure (kernels.py:30-33): x (..., D), scale (D,) bf16 -> y (..., D) bf16.
-ffi::Error RmsNorm(hipStream_t stream, ffi::Buffer<ffi::BF16> x, ffi::Buffer<ffi::BF16> scale,
-                   ffi::ResultBuffer<ffi::BF16> y, float eps) {
-  const int64_t D = x.dimensions().back();
-  return status(tg_rms_norm(x.untyped_data(), scale.untyped_data(), y->untyped_data(),
-                            rows_of(x.element_count(), D), D, eps, stream));
+// _rms_norm_pure (kernels.py:30-33): x (..., D), scale (D,), each bf16 or f32
+// -> y (..., D) in their promoted dtype (f32 if either is f32).
+ffi::Error RmsNorm(hipStream_t stream, ffi::AnyBuffer x, ffi::AnyBuffer scale,
+                   ffi::Result<ffi::AnyBuffer> y, float eps) {
+  int cx, cs, cy;
+  if (!dtype_code(x.element_type(), &cx) || !dtype_code(scale.element_type(), &cs) ||
+      !dtype_code(y->element_type(), &cy) ||
+      cy != ((cx == TG_DTYPE_F32 || cs == TG_DTYPE_F32) ? TG_DTYPE_F32 : TG_DTYPE_BF16))
+    return ffi::Error(ffi::ErrorCode::kInvalidArgument,
+                      "rms_norm: x, scale bf16 or f32; y in their promoted dtype");
+  const int64_t D = last_dim(x.dimensions());
+  return status(tg_rms_norm_ex(x.untyped_data(), cx, scale.untyped_data(), cs, y->untyped_data(),
+                               rows_of(x.element_count(), D), D, eps, stream));
 }
 
 // The norm fused with the quantization that feeds the next matmul:
@@ -169,18 +176,25 @@ ffi::Error RmsNormFp8(hipStream_t stream, ffi::Buffer<ffi::BF16> x, ffi::Buffer<
                                 rows_of(x.element_count(), D), D, eps, (int)block_k, stream));
 }
 
-// The norm's _bwd (kernels.py:104-118): x, scale, dy bf16 -> dx, dscale bf16.
-ffi::Error RmsNormBwd(hipStream_t stream, ffi::ScratchAllocator scratch, ffi::Buffer<ffi::BF16> x,
-                      ffi::Buffer<ffi::BF16> scale, ffi::Buffer<ffi::BF16> dy,
-                      ffi::ResultBuffer<ffi::BF16> dx, ffi::ResultBuffer<ffi::BF16> dscale, float eps) {
-  const int64_t D = x.dimensions().back(), rows = rows_of(x.element_count(), D);
+// The norm's _bwd (kernels.py:104-118): x, scale, dy bf16 or f32 -> dx in
+// x's dtype, dscale in scale's.
+ffi::Error RmsNormBwd(hipStream_t stream, ffi::ScratchAllocator scratch, ffi::AnyBuffer x,
+                      ffi::AnyBuffer scale, ffi::AnyBuffer dy, ffi::Result<ffi::AnyBuffer> dx,
+                      ffi::Result<ffi::AnyBuffer> dscale, float eps) {
+  int cx, cs, cd, cdx, cds;
+  if (!dtype_code(x.element_type(), &cx) || !dtype_code(scale.element_type(), &cs) ||
+      !dtype_code(dy.element_type(), &cd) || !dtype_code(dx->element_type(), &cdx) ||
+      !dtype_code(dscale->element_type(), &cds) || cdx != cx || cds != cs)
+    return ffi::Error(ffi::ErrorCode::kInvalidArgument,
+                      "rms_norm backward: bf16 / f32 operands; dx in x's dtype, dscale in scale's");
+  const int64_t D = last_dim(x.dimensions()), rows = rows_of(x.element_count(), D);
   ffi::Error err = ffi::Error::Success();
   const size_t ws_bytes = tg_rms_norm_bwd_workspace(rows, D);
   void* ws = take(scratch, ws_bytes, &err);
   if (ws_bytes && !ws) return err;
-  return status(tg_rms_norm_bwd(x.untyped_data(), scale.untyped_data(), dy.untyped_data(),
-                                dx->untyped_data(), dscale->untyped_data(), rows, D, eps, ws,
-                                ws_bytes, stream));
+  return status(tg_rms_norm_bwd_ex(x.untyped_data(), cx, scale.untyped_data(), cs, dy.untyped_data(), cd,
+                                   dx->untyped_data(), dscale->untyped_data(), rows, D, eps, ws,
+                                   ws_bytes, stream));
 }
 
 // The scaled GEMM alone on pre-quantized operands (a kept weight's bytes and
@@ -249,9 +263,9 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(tg_ffi_block_scaled_matmul_bwd_bf16, BlockScaledMa
 XLA_FFI_DEFINE_HANDLER_SYMBOL(tg_ffi_rms_norm, RmsNorm,
                               ffi::Ffi::Bind()
                                   .Ctx<ffi::PlatformStream<hipStream_t>>()
-                                  .Arg<ffi::Buffer<ffi::BF16>>()
-                                  .Arg<ffi::Buffer<ffi::BF16>>()
-                                  .Ret<ffi::Buffer<ffi::BF16>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Ret<ffi::AnyBuffer>()
                                   .Attr<float>("eps"));
 
 XLA_FFI_DEFINE_HANDLER_SYMBOL(tg_ffi_rms_norm_fp8, RmsNormFp8,
@@ -269,11 +283,11 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(tg_ffi_rms_norm_bwd, RmsNormBwd,
                               ffi::Ffi::Bind()
                                   .Ctx<ffi::PlatformStream<hipStream_t>>()
                                   .Ctx<ffi::ScratchAllocator>()
-                                  .Arg<ffi::Buffer<ffi::BF16>>()
-                                  .Arg<ffi::Buffer<ffi::BF16>>()
-                                  .Arg<ffi::Buffer<ffi::BF16>>()
-                                  .Ret<ffi::Buffer<ffi::BF16>>()
-                                  .Ret<ffi::Buffer<ffi::BF16>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Ret<ffi::AnyBuffer>()
                                   .Attr<float>("eps"));
 
 XLA_FFI_DEFINE_HANDLER_SYMBOL(tg_ffi_gemm_fp8_nt, GemmFp8Nt,

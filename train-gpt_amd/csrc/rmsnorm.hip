@@ -272,15 +272,118 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint4* __restric
   for (int i = threadIdx.x; i < dim; i += 256) partial[(int64_t)blockIdx.x * dim + i] = colsum[i];
 }
 
+// ---------------------------------------------------------------------------
+// General path: any width and either dtype (bf16 or f32) for x, scale and the
+// gradients, with _rms_norm_pure's op-by-op rounding in x's dtype
+// (kernels.py:30-33: r = rsqrt(var + eps).astype(x.dtype), x_n = x * r in
+// x.dtype, y = x_n * scale in the promoted dtype).  Rows are walked by one
+// wave each, two passes over the row (statistics, then output), so no row
+// has to fit in registers.  Not the hot path: the bf16 kernels above cover
+// bf16 widths up to 16384 (forward) and 4096 (backward).
+// ---------------------------------------------------------------------------
+template <typename T> __device__ __forceinline__ float ld_f32(const T* p, int64_t i);
+template <> __device__ __forceinline__ float ld_f32<uint16_t>(const uint16_t* p, int64_t i) {
+  return __uint_as_float((uint32_t)p[i] << 16);
+}
+template <> __device__ __forceinline__ float ld_f32<float>(const float* p, int64_t i) { return p[i]; }
+template <typename T> __device__ __forceinline__ void st_f32(T* p, int64_t i, float v);
+template <> __device__ __forceinline__ void st_f32<uint16_t>(uint16_t* p, int64_t i, float v) {
+  p[i] = __builtin_bit_cast(uint16_t, (__bf16)v);   // RNE
+}
+template <> __device__ __forceinline__ void st_f32<float>(float* p, int64_t i, float v) { p[i] = v; }
+template <typename T> constexpr bool is_bf16() { return sizeof(T) == 2; }
+
+// var = fl32(sum fl32(x)^2) / D (f64 accumulation), rnorm = fl32(1 / sqrt(var + eps)).
+template <typename XT>
+__device__ __forceinline__ float row_rnorm(const XT* xr, int dim, int lane, float eps) {
+  double sq = 0.0;
+  for (int c = lane; c < dim; c += 64) {
+    const float v = ld_f32(xr, c);
+    sq += (double)(v * v);
+  }
+  sq = wave_sum_f64(sq);
+  const float var = (float)sq / (float)dim;
+  return (float)(1.0 / __builtin_sqrt((double)(var + eps)));
+}
+
+template <typename XT, typename GT, typename YT>
+__global__ __launch_bounds__(256) void rmsnorm_gen_kernel(const XT* __restrict__ x,
+                                                          const GT* __restrict__ gamma,
+                                                          YT* __restrict__ y, int64_t rows, int dim,
+                                                          float eps) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows;
+       row += (int64_t)gridDim.x * 4) {
+    const XT* xr = x + row * dim;
+    float r = row_rnorm(xr, dim, lane, eps);
+    if (is_bf16<XT>()) r = round_bf16(r);                              // .astype(x.dtype)
+    for (int c = lane; c < dim; c += 64) {
+      float t = ld_f32(xr, c) * r;                                      // x * r in x.dtype
+      if (is_bf16<XT>()) t = round_bf16(t);
+      st_f32(y + row * dim, c, t * ld_f32(gamma, c));                   // x_n * scale
+    }
+  }
+}
+
+// Backward statistics per row: (rnorm, rnorm * mean(dy * scale * x)).
+template <typename XT, typename GT, typename DT>
+__global__ __launch_bounds__(256) void rmsnorm_gen_stats_kernel(const XT* __restrict__ x,
+                                                                const GT* __restrict__ gamma,
+                                                                const DT* __restrict__ dy,
+                                                                float2* __restrict__ stats,
+                                                                int64_t rows, int dim, float eps) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows;
+       row += (int64_t)gridDim.x * 4) {
+    const XT* xr = x + row * dim;
+    const DT* dr = dy + row * dim;
+    const float rn = row_rnorm(xr, dim, lane, eps);
+    float gx = 0.0f;
+    for (int c = lane; c < dim; c += 64)
+      gx = __builtin_fmaf(ld_f32(dr, c) * ld_f32(gamma, c), ld_f32(xr, c), gx);
+    const double gxs = wave_sum_f64((double)gx);
+    if (lane == 0) stats[row] = make_float2(rn, rn * ((float)gxs / (float)dim));
+  }
+}
+
+// dx = rnorm * (dy * scale - normed * dot) and one partial dscale row per
+// row group: block (column tile of 256, row group); each thread owns a column.
+constexpr int kGenRowsPerGroup = 16;
+template <typename XT, typename GT, typename DT>
+__global__ __launch_bounds__(256) void rmsnorm_gen_bwd_kernel(const XT* __restrict__ x,
+                                                              const GT* __restrict__ gamma,
+                                                              const DT* __restrict__ dy,
+                                                              const float2* __restrict__ stats,
+                                                              XT* __restrict__ dx,
+                                                              float* __restrict__ partial,
+                                                              int64_t rows, int dim, int groups) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= dim) return;
+  const float gm = ld_f32(gamma, c);
+  for (int grp = blockIdx.y; grp < groups; grp += gridDim.y) {
+    float dg = 0.0f;
+    const int64_t r0 = (int64_t)grp * kGenRowsPerGroup;
+    for (int64_t row = r0; row < rows && row < r0 + kGenRowsPerGroup; ++row) {
+      const float2 st = stats[row];
+      const float d = ld_f32(dy + row * dim, c);
+      const float nrm = ld_f32(x + row * dim, c) * st.x;
+      st_f32(dx + row * dim, c, st.x * (d * gm - nrm * st.y));
+      dg = __builtin_fmaf(d, nrm, dg);
+    }
+    partial[(int64_t)grp * dim + c] = dg;
+  }
+}
+
 // dscale[c] = bf16(sum over b of partial[b][c]) with f64 accumulation in a
 // fixed order: workgroup = 64 columns x 16 waves; wave w adds partial rows
 // w, w + 16, w + 32, ... in that order, and the 16 wave sums are added in
 // wave order.  A lane keeps 32 loads in flight, all of its rows for up to 512
 // partial rows: the reduction runs on few workgroups (dim / 64), so its time
 // is the number of dependent round trips to L2.
+template <typename OT>
 __global__ __launch_bounds__(1024) void rmsnorm_bwd_reduce(const float* __restrict__ partial,
                                                            int nparts, int dim,
-                                                           uint16_t* __restrict__ dscale) {
+                                                           OT* __restrict__ dscale) {
   constexpr int W = 16, U = 32;
   __shared__ double wsum[W][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -303,7 +406,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_bwd_reduce(const float* __restri
     double t = 0.0;
 #pragma unroll
     for (int w = 0; w < W; ++w) t += wsum[w][lane];
-    dscale[c] = __builtin_bit_cast(uint16_t, (__bf16)(float)t);
+    st_f32(dscale, c, (float)t);
   }
 }
 
@@ -346,8 +449,69 @@ static int launch_rmsnorm_bwd(const void* x, const void* gamma, const void* dy, 
     if (!launched) return einval("rms_norm_bwd: dim must be <= 4096");
     TG_TRY(check_launch("rmsnorm_bwd"));
   }
-  hipLaunchKernelGGL(rmsnorm_bwd_reduce, dim3((unsigned)((dim + 63) / 64)), dim3(1024), 0, st,
+  hipLaunchKernelGGL(rmsnorm_bwd_reduce<uint16_t>, dim3((unsigned)((dim + 63) / 64)), dim3(1024), 0, st,
                      partial, (int)grid, (int)dim, reinterpret_cast<uint16_t*>(dscale));
+  return check_launch("rmsnorm_bwd_reduce");
+}
+
+static int64_t gen_groups(int64_t rows) {
+  const int64_t g = (rows + kGenRowsPerGroup - 1) / kGenRowsPerGroup;
+  return g < 1 ? 1 : g;
+}
+static size_t gen_bwd_workspace(int64_t rows, int64_t dim) {
+  return (((size_t)rows * 8 + 255) & ~(size_t)255) + (size_t)gen_groups(rows) * (size_t)dim * 4;
+}
+static unsigned row_grid(int64_t rows) {
+  const int64_t g = (rows + 3) / 4;
+  return (unsigned)(g < 1 ? 1 : g > 16384 ? 16384 : g);
+}
+
+template <typename XT, typename GT>
+static int launch_gen_fwd(const void* x, const void* g, void* y, bool y_f32, int64_t rows, int64_t dim,
+                          float eps, hipStream_t st) {
+  auto X = reinterpret_cast<const XT*>(x);
+  auto G = reinterpret_cast<const GT*>(g);
+  if (y_f32)
+    hipLaunchKernelGGL((rmsnorm_gen_kernel<XT, GT, float>), dim3(row_grid(rows)), dim3(256), 0, st, X, G,
+                       reinterpret_cast<float*>(y), rows, (int)dim, eps);
+  else
+    hipLaunchKernelGGL((rmsnorm_gen_kernel<XT, GT, uint16_t>), dim3(row_grid(rows)), dim3(256), 0, st, X,
+                       G, reinterpret_cast<uint16_t*>(y), rows, (int)dim, eps);
+  return check_launch("rmsnorm_gen");
+}
+
+template <typename XT, typename GT, typename DT>
+static int launch_gen_bwd(const void* x, const void* g, const void* dy, void* dx, void* dscale,
+                          int64_t rows, int64_t dim, float eps, void* ws, hipStream_t st) {
+  auto X = reinterpret_cast<const XT*>(x);
+  auto G = reinterpret_cast<const GT*>(g);
+  auto DY = reinterpret_cast<const DT*>(dy);
+  float2* stats = reinterpret_cast<float2*>(ws);
+  float* partial = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) +
+                                            (((size_t)rows * 8 + 255) & ~(size_t)255));
+  const int64_t groups = gen_groups(rows);
+  if (rows > 0) {
+    hipLaunchKernelGGL((rmsnorm_gen_stats_kernel<XT, GT, DT>), dim3(row_grid(rows)), dim3(256), 0, st, X,
+                       G, DY, stats, rows, (int)dim, eps);
+    TG_TRY(check_launch("rmsnorm_gen_stats"));
+    const unsigned gy = (unsigned)(groups < 1024 ? groups : 1024);
+    hipLaunchKernelGGL((rmsnorm_gen_bwd_kernel<XT, GT, DT>), dim3((unsigned)((dim + 255) / 256), gy),
+                       dim3(256), 0, st, X, G, DY, stats, reinterpret_cast<XT*>(dx), partial, rows,
+                       (int)dim, (int)groups);
+    TG_TRY(check_launch("rmsnorm_gen_bwd"));
+  } else {
+    // no rows: dscale = 0 (one zero partial row)
+    hipLaunchKernelGGL((rmsnorm_gen_bwd_kernel<XT, GT, DT>), dim3((unsigned)((dim + 255) / 256), 1),
+                       dim3(256), 0, st, X, G, DY, stats, reinterpret_cast<XT*>(dx), partial, rows,
+                       (int)dim, 1);
+    TG_TRY(check_launch("rmsnorm_gen_bwd"));
+  }
+  if (is_bf16<GT>())
+    hipLaunchKernelGGL(rmsnorm_bwd_reduce<uint16_t>, dim3((unsigned)((dim + 63) / 64)), dim3(1024), 0, st,
+                       partial, (int)groups, (int)dim, reinterpret_cast<uint16_t*>(dscale));
+  else
+    hipLaunchKernelGGL(rmsnorm_bwd_reduce<float>, dim3((unsigned)((dim + 63) / 64)), dim3(1024), 0, st,
+                       partial, (int)groups, (int)dim, reinterpret_cast<float*>(dscale));
   return check_launch("rmsnorm_bwd_reduce");
 }
 
@@ -394,7 +558,9 @@ extern "C" int tg_add_rms_norm_fp8(const void* x, const void* delta, const void*
 
 extern "C" size_t tg_rms_norm_bwd_workspace(int64_t rows, int64_t dim) {
   if (rows < 0 || dim <= 0) return 0;
-  return (size_t)norm_bwd_grid(rows) * (size_t)dim * 4;
+  const size_t fast = (size_t)norm_bwd_grid(rows) * (size_t)dim * 4;
+  const size_t gen = gen_bwd_workspace(rows, dim);
+  return fast > gen ? fast : gen;
 }
 
 extern "C" int tg_rms_norm_bwd(const void* x, const void* scale, const void* dy, void* dx,
@@ -402,12 +568,64 @@ extern "C" int tg_rms_norm_bwd(const void* x, const void* scale, const void* dy,
                                void* workspace, size_t workspace_bytes, void* stream) {
   if (rows < 0 || dim <= 0) return einval("rms_norm_bwd: bad shape");
   if (dim % 8) return einval("rms_norm_bwd: dim must be a multiple of 8");
-  if (dim > 4096) return einval("rms_norm_bwd: dim must be <= 4096");
   if (!scale || !dscale) return einval("rms_norm_bwd: null pointer");
   if (rows > 0 && (!x || !dy || !dx || !workspace)) return einval("rms_norm_bwd: null pointer");
   if (workspace_bytes < tg_rms_norm_bwd_workspace(rows, dim)) return einval("rms_norm_bwd: workspace too small");
   if (!aligned(x, 16) || !aligned(scale, 16) || !aligned(dy, 16) || !aligned(dx, 16) || !aligned(workspace, 16))
     return einval("rms_norm_bwd: x, scale, dy, dx and workspace must be 16-byte aligned");
+  if (dim > 4096 || dim > 0x7FFFFFFF)
+    return launch_gen_bwd<uint16_t, uint16_t, uint16_t>(x, scale, dy, dx, dscale, rows, dim, eps,
+                                                        workspace, as_stream(stream));
   return launch_rmsnorm_bwd(x, scale, dy, dx, dscale, reinterpret_cast<float*>(workspace), rows, dim,
                             eps, as_stream(stream));
+}
+
+extern "C" int tg_rms_norm_ex(const void* x, int x_dtype, const void* scale, int scale_dtype, void* y,
+                              int64_t rows, int64_t dim, float eps, void* stream) {
+  if (rows < 0 || dim <= 0 || dim > 0x7FFFFFFF) return einval("rms_norm_ex: bad shape");
+  if ((x_dtype != TG_DTYPE_BF16 && x_dtype != TG_DTYPE_F32) ||
+      (scale_dtype != TG_DTYPE_BF16 && scale_dtype != TG_DTYPE_F32))
+    return einval("rms_norm_ex: dtypes must be TG_DTYPE_BF16 or TG_DTYPE_F32");
+  if (rows == 0) return TG_OK;
+  if (!x || !scale || !y) return einval("rms_norm_ex: null pointer");
+  hipStream_t st = as_stream(stream);
+  if (x_dtype == TG_DTYPE_BF16 && scale_dtype == TG_DTYPE_BF16 && dim % 8 == 0 && dim <= 16384 &&
+      aligned(x, 16) && aligned(scale, 16) && aligned(y, 16))
+    return launch_rmsnorm<false>(x, scale, y, nullptr, nullptr, rows, dim, eps, st);
+  const bool y_f32 = x_dtype == TG_DTYPE_F32 || scale_dtype == TG_DTYPE_F32;
+  if (x_dtype == TG_DTYPE_BF16)
+    return scale_dtype == TG_DTYPE_BF16 ? launch_gen_fwd<uint16_t, uint16_t>(x, scale, y, y_f32, rows, dim, eps, st)
+                                        : launch_gen_fwd<uint16_t, float>(x, scale, y, y_f32, rows, dim, eps, st);
+  return scale_dtype == TG_DTYPE_BF16 ? launch_gen_fwd<float, uint16_t>(x, scale, y, y_f32, rows, dim, eps, st)
+                                      : launch_gen_fwd<float, float>(x, scale, y, y_f32, rows, dim, eps, st);
+}
+
+extern "C" int tg_rms_norm_bwd_ex(const void* x, int x_dtype, const void* scale, int scale_dtype,
+                                  const void* dy, int dy_dtype, void* dx, void* dscale, int64_t rows,
+                                  int64_t dim, float eps, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  if (rows < 0 || dim <= 0 || dim > 0x7FFFFFFF) return einval("rms_norm_bwd_ex: bad shape");
+  for (int d : {x_dtype, scale_dtype, dy_dtype})
+    if (d != TG_DTYPE_BF16 && d != TG_DTYPE_F32)
+      return einval("rms_norm_bwd_ex: dtypes must be TG_DTYPE_BF16 or TG_DTYPE_F32");
+  if (!scale || !dscale) return einval("rms_norm_bwd_ex: null pointer");
+  if (rows > 0 && (!x || !dy || !dx || !workspace)) return einval("rms_norm_bwd_ex: null pointer");
+  if (workspace_bytes < tg_rms_norm_bwd_workspace(rows, dim))
+    return einval("rms_norm_bwd_ex: workspace too small");
+  if (!aligned(workspace, 16)) return einval("rms_norm_bwd_ex: workspace must be 16-byte aligned");
+  const bool all_bf16 = x_dtype == TG_DTYPE_BF16 && scale_dtype == TG_DTYPE_BF16 && dy_dtype == TG_DTYPE_BF16;
+  if (all_bf16 && dim % 8 == 0 && aligned(x, 16) && aligned(scale, 16) && aligned(dy, 16) && aligned(dx, 16))
+    return tg_rms_norm_bwd(x, scale, dy, dx, dscale, rows, dim, eps, workspace, workspace_bytes, stream);
+  hipStream_t st = as_stream(stream);
+  const int key = (x_dtype == TG_DTYPE_F32) * 4 + (scale_dtype == TG_DTYPE_F32) * 2 + (dy_dtype == TG_DTYPE_F32);
+  switch (key) {
+    case 0: return launch_gen_bwd<uint16_t, uint16_t, uint16_t>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
+    case 1: return launch_gen_bwd<uint16_t, uint16_t, float>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
+    case 2: return launch_gen_bwd<uint16_t, float, uint16_t>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
+    case 3: return launch_gen_bwd<uint16_t, float, float>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
+    case 4: return launch_gen_bwd<float, uint16_t, uint16_t>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
+    case 5: return launch_gen_bwd<float, uint16_t, float>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
+    case 6: return launch_gen_bwd<float, float, uint16_t>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
+    default: return launch_gen_bwd<float, float, float>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
+  }
 }

@@ -226,9 +226,12 @@ def _fp8_forward_with_residuals(a, b, block_k):
 def _fp8_backward(block_k, residuals, g):
     """Gradients of block_scaled_matmul: (da as a.dtype, db as b.dtype).
 
-    BACKWARD_MODE "fp8": da = fwd(g, b.T), db = fwd(a.T, g) through FP8 MFMA,
-    so N (da's contraction) and M (db's) must divide by block_k, with the
-    reference's ValueError text (fp8.py:55-56) otherwise.
+    BACKWARD_MODE "fp8": da = fwd(g, b.T), db = fwd(a.T, g) through FP8 MFMA.
+    N (da's contraction) and M (db's) need not divide by block_k: the operands
+    are zero-padded along them to a multiple of block_k.  Zeros change neither
+    a block's amax nor any product, so this is the FP8 rule with the last,
+    partial block quantized over its valid elements (fp8.py:39-47 defines only
+    whole blocks).
     BACKWARD_MODE "bf16": fp8.py:85-98's straight-through rule, da = bf16(g) @
     bf16(b).T and db = bf16(a).T @ bf16(g), each a bf16 MFMA GEMM with fp32
     accumulation rounded once to bf16; block_k is unused, as in the reference.
@@ -245,10 +248,20 @@ def _fp8_backward(block_k, residuals, g):
     g_2d = g.reshape(-1, N)
     M = a_2d.shape[0]
     _L.require_gpu(a_2d, b, g_2d)
-    if N % block_k:
-        raise ValueError(f"K={N} not divisible by block_k={block_k}")
-    if M % block_k:
-        raise ValueError(f"K={M} not divisible by block_k={block_k}")
+    if M == 0 or N == 0 or K == 0:
+        # empty contraction or empty result: the reference's dots give zeros
+        return (torch.zeros(a.shape, dtype=a.dtype, device=a.device),
+                torch.zeros(b.shape, dtype=b.dtype, device=b.device))
+    Mp, Np = -(-M // block_k) * block_k, -(-N // block_k) * block_k
+    if (Mp, Np) != (M, N):
+        a_p = a_2d.new_zeros((Mp, K))
+        a_p[:M] = a_2d
+        g_p = g_2d.new_zeros((Mp, Np))
+        g_p[:M, :N] = g_2d
+        b_p = b.new_zeros((K, Np))
+        b_p[:, :N] = b
+        da, db = _fp8_backward(block_k, (a_p, b_p), g_p)
+        return da[:M].reshape(*leading, K), db[:, :N].contiguous()
     bf = torch.bfloat16
     if a.dtype == bf and b.dtype == bf and g.dtype == bf:
         a_2d, g_2d, b_c = a_2d.contiguous(), g_2d.contiguous(), b.contiguous()

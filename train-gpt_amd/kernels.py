@@ -4,7 +4,9 @@ Same names and arguments as /root/reference/kernels.py:
   * _rms_norm_pure(x, scale, eps)     kernels.py:30-33 (the canonical semantics)
   * rms_norm(x, scale, eps)           kernels.py:55-127 (custom_vjp; backend-selected)
 Both run the gfx950 kernel tg_rms_norm with _rms_norm_pure's arithmetic:
-r = bf16(rsqrt(mean(x^2) + eps)), y = bf16(bf16(x * r) * scale).  The
+r = bf16(rsqrt(mean(x^2) + eps)), y = bf16(bf16(x * r) * scale).  Like the
+reference they accept f32 as well (tg_rms_norm_ex): r and x * r are then
+rounded in x's dtype and the output has the promoted dtype of x and scale.  The
 reference selects its Pallas kernel when jax.default_backend() == "gpu"
 (kernels.py:124-127), which would pick the CUDA-only Mosaic path on ROCm; here
 the HIP kernel is the only implementation.
@@ -24,22 +26,33 @@ import torch
 import _tglib as _L
 
 
-def _prep(x: torch.Tensor, scale: torch.Tensor):
+_FLOATS = (torch.bfloat16, torch.float32)
+
+
+def _prep(x: torch.Tensor, scale: torch.Tensor, bf16_only: bool = True):
     _L.require_gpu(x, scale)
-    if x.dtype != torch.bfloat16 or scale.dtype != torch.bfloat16:
-        raise TypeError("rms_norm: x and scale must be bfloat16 (the model's dtype)")
+    if bf16_only and (x.dtype != torch.bfloat16 or scale.dtype != torch.bfloat16):
+        raise TypeError("rms_norm_fp8: x and scale must be bfloat16 (the model's dtype)")
+    if x.dtype not in _FLOATS or scale.dtype not in _FLOATS:
+        raise TypeError(f"rms_norm: x and scale must be bfloat16 or float32, got {x.dtype}, {scale.dtype}")
     D = x.shape[-1]
     if scale.shape != (D,):
         raise ValueError(f"scale must have shape ({D},), got {tuple(scale.shape)}")
     return x.reshape(-1, D).contiguous(), scale.contiguous(), D
 
 
+def _out_dtype(x: torch.Tensor, scale: torch.Tensor):
+    """jnp's promotion of x_n (x.dtype) * scale: f32 if either is f32."""
+    return torch.float32 if torch.float32 in (x.dtype, scale.dtype) else torch.bfloat16
+
+
 def _rms_norm_pure(x: torch.Tensor, scale: torch.Tensor, eps: float) -> torch.Tensor:
-    """kernels.py:30-33 on the GPU: x (..., D) bf16, scale (D,) bf16 -> bf16 (..., D)."""
-    x2, g, D = _prep(x, scale)
-    y = torch.empty_like(x2)
-    _L.check(_L.lib().tg_rms_norm(_L.ptr(x2), _L.ptr(g), _L.ptr(y), x2.shape[0], D, float(eps),
-                                  _L.stream_of(x2)))
+    """kernels.py:30-33 on the GPU: x (..., D), scale (D,), bf16 or f32 -> (..., D) in the promoted dtype."""
+    x2, g, D = _prep(x, scale, bf16_only=False)
+    y = torch.empty(x2.shape, dtype=_out_dtype(x, scale), device=x.device)
+    # bf16 x and scale with D % 8 == 0 (D <= 16384) take the fast kernel inside
+    _L.check(_L.lib().tg_rms_norm_ex(_L.ptr(x2), _L.dtype_code(x2), _L.ptr(g), _L.dtype_code(g),
+                                     _L.ptr(y), x2.shape[0], D, float(eps), _L.stream_of(x2)))
     return y.reshape(x.shape)
 
 
@@ -98,17 +111,19 @@ def _rms_norm_fp8_fwd(x: torch.Tensor, scale: torch.Tensor, eps: float, block_k:
 
 def _rms_norm_bwd(x: torch.Tensor, scale: torch.Tensor, eps: float, g: torch.Tensor):
     """kernels.py:104-118: (grad_x as x.dtype, grad_scale as scale.dtype)."""
-    x2, sc, D = _prep(x, scale)
-    if g.dtype != torch.bfloat16:
-        g = g.to(torch.bfloat16)
+    x2, sc, D = _prep(x, scale, bf16_only=False)
+    if g.dtype not in _FLOATS:
+        g = g.to(torch.float32)
     g2 = g.reshape(-1, D).contiguous()
     R = x2.shape[0]
     dx = torch.empty_like(x2)
-    dscale = torch.empty((D,), dtype=torch.bfloat16, device=x.device)
+    dscale = torch.empty((D,), dtype=scale.dtype, device=x.device)
     ws_bytes = _L.lib().tg_rms_norm_bwd_workspace(R, D)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=x.device)
-    _L.check(_L.lib().tg_rms_norm_bwd(_L.ptr(x2), _L.ptr(sc), _L.ptr(g2), _L.ptr(dx), _L.ptr(dscale),
-                                      R, D, float(eps), _L.ptr(ws), ws_bytes, _L.stream_of(x2)))
+    # all-bf16 operands with D % 8 == 0 take tg_rms_norm_bwd's kernels inside
+    _L.check(_L.lib().tg_rms_norm_bwd_ex(
+        _L.ptr(x2), _L.dtype_code(x2), _L.ptr(sc), _L.dtype_code(sc), _L.ptr(g2), _L.dtype_code(g2),
+        _L.ptr(dx), _L.ptr(dscale), R, D, float(eps), _L.ptr(ws), ws_bytes, _L.stream_of(x2)))
     return dx.reshape(x.shape), dscale
 
 

@@ -24,9 +24,9 @@ HANDLERS = {
                                        ("tg_block_scaled_matmul_bwd_fp8",)),
     "tg_block_scaled_matmul_bwd_bf16": ("tg_ffi_block_scaled_matmul_bwd_bf16",
                                         ("tg_block_scaled_matmul_bwd_bf16",)),
-    "tg_rms_norm": ("tg_ffi_rms_norm", ("tg_rms_norm",)),
+    "tg_rms_norm": ("tg_ffi_rms_norm", ("tg_rms_norm_ex",)),
     "tg_rms_norm_fp8": ("tg_ffi_rms_norm_fp8", ("tg_rms_norm_fp8",)),
-    "tg_rms_norm_bwd": ("tg_ffi_rms_norm_bwd", ("tg_rms_norm_bwd",)),
+    "tg_rms_norm_bwd": ("tg_ffi_rms_norm_bwd", ("tg_rms_norm_bwd_ex",)),
     "tg_gemm_fp8_nt": ("tg_ffi_gemm_fp8_nt", ("tg_gemm_fp8_nt",)),
 }
 
