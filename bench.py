@@ -111,6 +111,33 @@ def copy_probe(mib: int) -> None:
     print(json.dumps({"copy_probe_bytes": mib * (1 << 20)}))
 
 
+def c3_inputs():
+    """Config 3's bf16 inputs (seed 2): x [8192, 2048] ~N(0,1), W [2048, 8192]
+    ~N(0, 0.02^2), dY [8192, 8192] ~N(0, 1e-3^2), as bf16 bit patterns from
+    numpy's default_rng (RNE from f32)."""
+    import numpy as np
+    from oracle import bf16 as ob
+    rng = np.random.default_rng(2)
+    return (ob.randn_bf16(rng, (M3, K3)), ob.randn_bf16(rng, (K3, N3), std=0.02),
+            ob.randn_bf16(rng, (M3, N3), std=1e-3))
+
+
+def host_cpu():
+    """(usable host cores, CPU model name)."""
+    import os
+    cores = len(os.sched_getaffinity(0))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return cores, model
+
+
 class Step:
     """Config-3 forward + FP8 backward through the C ABI with preallocated buffers."""
 
@@ -118,12 +145,12 @@ class Step:
         import torch
         import _tglib as L
         self.L, self.lib, self.torch = L, L.lib(), torch
-        g = torch.Generator(device=dev)
-        g.manual_seed(2)
         bf = torch.bfloat16
-        self.x = torch.randn((M3, K3), generator=g, device=dev).to(bf)
-        self.w = (torch.randn((K3, N3), generator=g, device=dev) * 0.02).to(bf)
-        self.dy = (torch.randn((M3, N3), generator=g, device=dev) * 1e-3).to(bf)
+        # config 3's inputs (seed 2), drawn once on the host; the CPU baseline
+        # runs on these same arrays
+        self.host = c3_inputs()
+        to_dev = lambda u16: torch.from_numpy(u16.view("int16")).view(bf).to(dev)
+        self.x, self.w, self.dy = (to_dev(a) for a in self.host)
         u8, f32 = torch.uint8, torch.float32
         e = lambda *s: torch.empty(s, dtype=u8, device=dev)
         f = lambda *s: torch.empty(s, dtype=f32, device=dev)
@@ -430,6 +457,14 @@ def _dequant(q, s):
     return q.view(torch.float8_e4m3fn).float() * s.repeat_interleave(128, dim=1)
 
 
+def _dequant_tiles(q, s, n):
+    """f32 values of a weight quantized with one scale per 128x128 tile:
+    q (N, K) e4m3 bytes, s (ceil(N/128), K/128)."""
+    import torch
+    full = s.repeat_interleave(128, dim=0)[:n].repeat_interleave(128, dim=1)
+    return q.view(torch.float8_e4m3fn).float() * full
+
+
 def _maxrel(a, b):
     d = (a.float() - b.float()).abs().max()
     return round(float(d / b.float().abs().max().clamp_min(1e-30)), 6)
@@ -494,12 +529,34 @@ def bench_c1(dev, iters):
     us_gemm = _mean_launch_us(gemm, iters)
     flop = 2.0 * M * N * K
     ref = _dequant(qx, sx) @ _dequant(qwt, swt).t()
+    # the config's literal wording: one scale per 128x128 tile of W
+    qw8 = torch.empty((N, K), dtype=torch.uint8, device=dev)
+    sw8 = torch.empty(((N + 127) // 128, K // 128), dtype=torch.float32, device=dev)
+    y8 = torch.empty_like(y)
+
+    def fwd_128x128(i):
+        L.check(lib.tg_quantize_rows(L.ptr(x), L.TG_DTYPE_BF16, M, K, 128, L.ptr(qx), L.ptr(sx), st))
+        L.check(lib.tg_quantize_weight_128x128(L.ptr(w), K, N, L.ptr(qw8), L.ptr(sw8), st))
+        L.check(lib.tg_gemm_fp8_nt(L.ptr(qx), L.ptr(sx), L.ptr(qw8), L.ptr(sw8), 128, L.ptr(y8),
+                                   L.TG_DTYPE_BF16, M, N, K, 128, st))
+
+    def gemm_128x128(i):
+        L.check(lib.tg_gemm_fp8_nt(L.ptr(qx), L.ptr(sx), L.ptr(qw8), L.ptr(sw8), 128, L.ptr(y8),
+                                   L.TG_DTYPE_BF16, M, N, K, 128, st))
+    us8 = _mean_launch_us(fwd_128x128, iters)
+    us8_gemm = _mean_launch_us(gemm_128x128, iters)
+    ref8 = _dequant(qx, sx) @ (_dequant_tiles(qw8, sw8, N)).t()
     return {"workload": "C1 block_scaled_matmul forward, x[2048,768] bf16, W[768,3072] bf16, 1x128 scales",
             "us_per_call": round(us, 3), "tflops_with_quantization": round(flop / us / 1e6, 1),
             "us_gemm": round(us_gemm, 3), "tflops_gemm": round(flop / us_gemm / 1e6, 1),
             "y_vs_dequant_f32": _maxrel(y, ref),
             "y_vs_bf16_matmul": _maxrel(y, x.float() @ w.float()),
-            "same_bits_composite_vs_gemm": bool(torch.equal(y.view(torch.int16), y2.view(torch.int16)))}
+            "same_bits_composite_vs_gemm": bool(torch.equal(y.view(torch.int16), y2.view(torch.int16))),
+            "w_scales_128x128": {
+                "us_per_call": round(us8, 3), "tflops_with_quantization": round(flop / us8 / 1e6, 1),
+                "us_gemm": round(us8_gemm, 3), "tflops_gemm": round(flop / us8_gemm / 1e6, 1),
+                "y_vs_dequant_f32": _maxrel(y8, ref8),
+                "y_vs_bf16_matmul": _maxrel(y8, x.float() @ w.float())}}
 
 
 def bench_xent(dev, iters):
@@ -588,19 +645,16 @@ def bench_decode(dev, steps=32, prompt=128):
     return out
 
 
-def cpu_baseline(rows=8192, repeats=5):
+def cpu_baseline(inputs, repeats=5):
     """The CPU oracle on the step: quantize (C oracle) and the dequantized f32
-    GEMMs (numpy/BLAS) of fwd + FP8 bwd over `rows` of the 8192 token rows,
+    GEMMs (numpy/BLAS) of fwd + FP8 bwd on the GPU step's own input arrays,
     best of `repeats` after one warm-up (the reference's own timing method,
-    bench.py:118-135).  FLOP counted = 3 * 2 * rows * 2048 * 8192."""
+    bench.py:118-135).  FLOP counted = 3 * 2 * 8192 * 2048 * 8192."""
     import numpy as np
     from threadpoolctl import threadpool_info
-    from oracle import bf16 as ob
     from oracle import cbind, fp8_ref
-    rng = np.random.default_rng(2)
-    x = ob.randn_bf16(rng, (rows, K3))
-    w = ob.randn_bf16(rng, (K3, N3), std=0.02)
-    dy = ob.randn_bf16(rng, (rows, N3), std=1e-3)
+    x, w, dy = inputs
+    rows = x.shape[0]
     dec = lambda q, s: (fp8_ref.E4M3FN_VALUES[q].reshape(q.shape[0], -1, 128)
                         * s[:, :, None]).reshape(q.shape[0], -1)
     def one_step():
@@ -626,10 +680,13 @@ def cpu_baseline(rows=8192, repeats=5):
     dt = min(times)
     flop = 3 * 2.0 * rows * K3 * N3
     threads = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    host_cores, model = host_cpu()
     return {"value": round(flop / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"C3 fwd+FP8 bwd on {rows} of 8192 token rows, best of {repeats} "
-                      f"({total:.1f} s of CPU time): C oracle quantizers single-thread, numpy "
-                      f"f32 dequant GEMMs on {threads} BLAS threads"}
+            "host_cores": host_cores, "cpu_model": model,
+            "threads": {"quantizers": 1, "blas_gemm": threads},
+            "sample": f"C3 fwd+FP8 bwd on all {rows} token rows of the GPU step's own input arrays "
+                      f"(numpy default_rng(2)), best of {repeats} ({total:.1f} s of CPU time): C oracle "
+                      f"quantizers single-thread, numpy f32 dequant GEMMs on {threads} BLAS threads"}
 
 
 def main():
@@ -694,7 +751,7 @@ def main():
         "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp8e4m3 (f32 accumulate, bf16 io)",
-        "data": "synthetic (torch GPU RNG, seeded)",
+        "data": "synthetic (numpy default_rng(2), the same arrays as cpu_baseline)",
         "config": {"workload": "C3 block_scaled_matmul fwd + FP8 bwd, x[8192,2048] W[2048,8192] "
                                "dY[8192,8192] bf16, 1x128 scales (quantization included)",
                    "M": M3, "K": K3, "N": N3, "block_k": 128},
@@ -716,7 +773,7 @@ def main():
         out = {k: out[k] for k in ("metric", "value", "unit", "ms_per_step", "gemm_us_per_launch",
                                    "roofline", "accuracy")}
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline()
+        out["cpu_baseline"] = cpu_baseline(step.host)
     print(json.dumps(out))
 
 

@@ -148,6 +148,30 @@ def test_block_scaled_matmul_c1(dev):
     print(f"C1 rel err vs oracle {err:.3e}, vs bf16 matmul {maxabs_rel(y, bf):.3e}")
 
 
+def test_c1_weight_tiles_128x128(dev):
+    """Config 1 with its literal weight scales, one per 128x128 tile of W:
+    x [2048, 768] ~N(0,1), W [768, 3072] ~N(0, 0.02^2), seed 0.  W's bytes and
+    scales bit-exact against the oracle, the f32 GEMM output within F32_TOL of
+    the float64 dequant product, the bf16 output its RNE."""
+    rng = np.random.default_rng(0)
+    x = ob.randn_bf16(rng, (2048, 768))
+    w = ob.randn_bf16(rng, (768, 3072), std=0.02)
+    qw, sw, bn = fp8.quantize_weight(to_dev(w, dev), "128x128")
+    assert bn == 128 and sw.shape == (24, 6)
+    qw_o, sw_o = fp8_ref.quantize_weight_128x128(np.ascontiguousarray(ob.bf16_to_f32(w).T))
+    np.testing.assert_array_equal(u8(qw), qw_o)
+    assert same_scales(sw.cpu().numpy(), sw_o)
+    qx, sx = fp8_ref.quantize_fp8(ob.bf16_to_f32(x))
+    ref = fp8_ref.gemv_prequant(qx, sx, qw_o, sw_o, bn=128)
+    c32 = _gemm(qx, sx, qw_o, sw_o, dev, bn=128, out=torch.float32).cpu().numpy()
+    assert maxabs_rel(c32, ref) <= F32_TOL
+    c16 = _gemm(qx, sx, qw_o, sw_o, dev, bn=128).view(torch.int16).cpu().numpy().view(np.uint16)
+    np.testing.assert_array_equal(c16, ob.f32_to_bf16(c32))
+    bf = ob.bf16_to_f32(x).astype(np.float64) @ ob.bf16_to_f32(w).astype(np.float64)
+    print(f"C1 128x128 W scales: f32 err vs oracle {maxabs_rel(c32, ref):.3e}, "
+          f"vs bf16 matmul {maxabs_rel(c32, bf):.3e}")
+
+
 def test_block_scaled_matmul_leading_dims_and_errors(dev):
     rng = np.random.default_rng(1)
     x = ob.randn_bf16(rng, (2, 3, 256))
