@@ -9,7 +9,9 @@ quantize x along K and x.T along M (one read of x), W.T along K and W along N
 dY) -> GEMM dX, GEMM dW.  Every kernel is a C-ABI call into libtg_fp8.so on
 torch's current stream; the step allocates nothing.
 
-value        = 3 * 2*8192*2048*8192 FLOP / step time (TFLOP/s, quantization included)
+value        = 3 * 2*8192*2048*8192 FLOP / step time (TFLOP/s, quantization included),
+               timed over exactly --steps steps after an untimed 150 ms clock-settle
+               phase of the same step (reported as clock_settle) and --warmup steps
 roofline     = the GEMM kernel: 2*M*N*K FLOP per launch / its mean launch time
                (HIP events around each GEMM launch, in a second pass of the
                same steps right after the timed region: an event record on
@@ -39,10 +41,14 @@ xent         = config 4's head: fused logit cap + cross entropy (losses.py) on
 decode       = KV-cached decode (decode.py) of the reference model config:
                ms per decode step at batch 1 and 8, and the kept FP8 weights +
                KV cache read per step against 8 TB/s
+io_floor     = (--only) config 2's bytes moved by csrc/probe/io_floor.hip with
+               the fused norm kernel's access pattern and no arithmetic: the
+               attainable rate of that read / write mix, beside the real kernel
 cpu_baseline = the CPU oracle (numpy + C) on a row sample of the same step
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                      [--only step|norm_quant|norm_bwd|gemv|bwd_bf16|block_step|xent|decode]
+                      [--only step|norm_quant|norm_bwd|gemv|bwd_bf16|block_step|xent|decode|
+                              vendor_gemm|c1|io_floor]
 """
 import argparse
 import json
@@ -64,9 +70,19 @@ C2_ROWS, C2_D = 8 * 1024, 2048
 C2_BYTES = C2_ROWS * C2_D * (2 + 2 + 1) + C2_ROWS * (C2_D // 128) * 4 + C2_D * 2
 C2_BWD_BYTES = C2_ROWS * C2_D * (2 + 2 + 2) + 2 * C2_D * 2
 C5_K, C5_N = 4096, 14336
+CLOCK_SETTLE_MS = 150.0        # untimed steps before the warm-up (the clock ramps ~30 ms after idle)
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "bench_hbm_traffic_counters.md")
+
+
+def under_counter_collection() -> bool:
+    """True inside `rocprofv3 --pmc` (its launcher exports ROCPROF_COUNTER_COLLECTION=1).
+    A full bench run under counter collection once died with SIGSEGV in a
+    profiler host thread; the only part of that run no single-workload counter
+    pass had covered besides the C4 block step was the decode workload's
+    captured-graph replay, so the decode workload is left out in that mode."""
+    return os.environ.get("ROCPROF_COUNTER_COLLECTION", "") == "1"
 
 
 def measured_traffic():
@@ -84,14 +100,14 @@ def measured_traffic():
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    # the GPU clock ramps for ~30 ms after idle (the first ~40 C3 steps run
-    # 5-25% slower than the steady state), so the default warm-up covers it
+    # the clock ramp after idle is covered by the CLOCK_SETTLE_MS phase in
+    # main(), ahead of these warm-up steps
     p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=60)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--norm-iters", type=int, default=200)
     p.add_argument("--only", choices=["step", "norm_quant", "norm_bwd", "gemv", "bwd_bf16",
-                                      "block_step", "xent", "decode", "vendor_gemm", "c1"],
+                                      "block_step", "xent", "decode", "vendor_gemm", "c1", "io_floor"],
                    help="run one secondary workload alone and print its JSON object")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (calibrates the FETCH_SIZE / "
@@ -236,6 +252,81 @@ def bench_norm(dev, iters):
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
                          "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
                          "traffic": measured_traffic().get("rmsnorm_fp8")}}
+
+
+def bench_io_floor(dev, iters):
+    """The I/O floor of config 2's fused norm -> FP8 kernel: libtg_probe.so's
+    io_floor_kernel moves the same bytes on the same launch shape with no
+    arithmetic (read-only, bf16 copy, config 2's read / write mix, writes only),
+    for 1, 2, 4 and 8 rows per wave, timed like `norm_quant` beside the real
+    kernel over the same rotating buffer sets."""
+    import ctypes
+    import torch
+    import _tglib as L
+    import build as tg_build
+    lib = L.lib()
+    if not os.path.exists(tg_build.PROBE_LIB):
+        raise RuntimeError(f"{tg_build.PROBE_LIB} is missing: run python train-gpt_amd/build.py")
+    probe = ctypes.CDLL(tg_build.PROBE_LIB)
+    probe.tg_probe_io_floor.restype = ctypes.c_int
+    probe.tg_probe_io_floor.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    nsets = 5
+    xs = [torch.randn((C2_ROWS, C2_D), generator=g, device=dev).to(torch.bfloat16) for _ in range(nsets)]
+    ys = [torch.empty((C2_ROWS, C2_D), dtype=torch.bfloat16, device=dev) for _ in range(nsets)]
+    qs = [torch.empty((C2_ROWS, C2_D), dtype=torch.uint8, device=dev) for _ in range(nsets)]
+    ss = [torch.empty((C2_ROWS, C2_D // 128), dtype=torch.float32, device=dev) for _ in range(nsets)]
+    gamma = torch.ones((C2_D,), dtype=torch.bfloat16, device=dev)
+    st = L.stream_of(gamma)
+    xb, qb, sb = C2_ROWS * C2_D * 2, C2_ROWS * C2_D, C2_ROWS * (C2_D // 128) * 4
+    modes = {0: ("read x", xb), 1: ("read x, write y (bf16 copy)", 2 * xb),
+             2: ("read x, write y, q, scales (config 2's mix)", 2 * xb + qb + sb),
+             3: ("write y, q, scales", xb + qb + sb)}
+
+    def rate(us, byts):
+        gbps = byts / (us * 1e-6) / 1e9
+        return {"us_per_launch": round(us, 3), "bytes_per_launch": byts, "GB/s": round(gbps, 1),
+                "frac_of_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4)}
+
+    out = {"workload": "I/O floor of C2: rows 8192 x 2048 bf16, the fused norm kernel's access pattern "
+                       "without arithmetic (csrc/probe/io_floor.hip)", "modes": []}
+    for mode, (what, byts) in modes.items():
+        row = {"mode": mode, "traffic": what}
+        for rpw in (1, 2, 4, 8):
+            def launch(i, mode=mode, rpw=rpw):
+                k = i % nsets
+                L.check(probe.tg_probe_io_floor(mode, L.ptr(xs[k]), L.ptr(ys[k]), L.ptr(qs[k]), L.ptr(ss[k]),
+                                                C2_ROWS, rpw, st))
+            row[f"rows_per_wave_{rpw}"] = rate(_mean_launch_us(launch, iters), byts)
+        out["modes"].append(row)
+
+    def norm(i):
+        k = i % nsets
+        L.check(lib.tg_rms_norm_fp8(L.ptr(xs[k]), L.ptr(gamma), L.ptr(ys[k]), L.ptr(qs[k]), L.ptr(ss[k]),
+                                    C2_ROWS, C2_D, 1e-6, 128, st))
+    out["rms_norm_fp8_same_run"] = rate(_mean_launch_us(norm, iters), C2_BYTES)
+    # the same bf16 copy by torch's own copy kernel, and the mix at 4x the rows
+    # (a longer transfer: the launch's fixed ramp-up and drain weigh less)
+    out["torch_copy_same_bytes"] = rate(_mean_launch_us(lambda i: ys[i % nsets].copy_(xs[i % nsets]), iters),
+                                        2 * xb)
+    big = [torch.empty((4 * C2_ROWS, C2_D), dtype=torch.bfloat16, device=dev) for _ in range(2)]
+    bigy = [torch.empty_like(b) for b in big]
+    bigq = [torch.empty((4 * C2_ROWS, C2_D), dtype=torch.uint8, device=dev) for _ in range(2)]
+    bigs = [torch.empty((4 * C2_ROWS, C2_D // 128), dtype=torch.float32, device=dev) for _ in range(2)]
+    for b in big:
+        b.normal_()
+
+    def mix4(i):
+        k = i % 2
+        L.check(probe.tg_probe_io_floor(2, L.ptr(big[k]), L.ptr(bigy[k]), L.ptr(bigq[k]), L.ptr(bigs[k]),
+                                        4 * C2_ROWS, 2, st))
+    out["mix_at_4x_rows"] = rate(_mean_launch_us(mix4, max(iters // 4, 10)), 4 * (2 * xb + qb + sb))
+    mix = [r for r in out["modes"] if r["mode"] == 2][0]
+    best = max(mix[k]["GB/s"] for k in mix if k.startswith("rows_per_wave"))
+    out["norm_vs_best_mix_floor"] = round(out["rms_norm_fp8_same_run"]["GB/s"] / best, 4)
+    return out
 
 
 def _mean_launch_us(launch, iters, warm=5):
@@ -700,16 +791,32 @@ def main():
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
+    if args.only == "decode" and under_counter_collection():
+        print(json.dumps({"error": "the decode workload replays a captured HIP graph and is not run "
+                                   "under rocprofv3 counter collection"}))
+        sys.exit(2)
     if args.only and args.only != "step":
         fn = {"norm_quant": bench_norm, "norm_bwd": bench_norm_bwd, "gemv": bench_gemv,
               "bwd_bf16": lambda d, _: bench_bwd_bf16(d, 10),
               "block_step": lambda d, _: bench_block(d), "xent": bench_xent,
               "decode": lambda d, _: bench_decode(d),
               "vendor_gemm": lambda d, _: bench_vendor_gemm(d, 20),
-              "c1": bench_c1}[args.only]
+              "c1": bench_c1, "io_floor": bench_io_floor}[args.only]
         print(json.dumps({args.only: fn(dev, args.norm_iters)}))
         return
     step = Step(dev)
+    # Clock settle: after idle the GPU clock ramps for ~30 ms (the first ~40
+    # C3 steps run 5-25% slower than the steady state a training loop runs
+    # at), so untimed steps run for CLOCK_SETTLE_MS of wall time before the
+    # requested warm-up steps; both are reported, and the timed region below
+    # is exactly --steps full steps.
+    settle_steps, t_settle = 0, time.perf_counter()
+    while (time.perf_counter() - t_settle) * 1e3 < CLOCK_SETTLE_MS:
+        for _ in range(10):
+            step.run()
+        torch.cuda.synchronize()
+        settle_steps += 10
+    settle_ms = (time.perf_counter() - t_settle) * 1e3
     for _ in range(args.warmup):
         step.run()
     torch.cuda.synchronize()
@@ -745,11 +852,13 @@ def main():
         bwd_bf16 = bench_bwd_bf16(dev, 10)
         block_step = bench_block(dev)
         xent = bench_xent(dev, args.norm_iters)
-        dec = bench_decode(dev)
+        dec = (bench_decode(dev) if not under_counter_collection() else
+               {"skipped": "captured-graph replay is not run under rocprofv3 counter collection"})
     out = {
         "metric": "FP8 block-scaled GEMM TFLOP/s (% fp8 MFMA peak); RMSNorm+quant HBM GB/s",
         "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
+        "warmup": args.warmup, "clock_settle": {"steps": settle_steps, "ms": round(settle_ms, 1)},
+        "ms_per_step": round(ms_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp8e4m3 (f32 accumulate, bf16 io)",
         "data": "synthetic (numpy default_rng(2), the same arrays as cpu_baseline)",
         "config": {"workload": "C3 block_scaled_matmul fwd + FP8 bwd, x[8192,2048] W[2048,8192] "

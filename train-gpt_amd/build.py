@@ -54,6 +54,25 @@ def build_library(verbose: bool = False) -> str:
     return LIB
 
 
+PROBE_SRC = os.path.join(CSRC, "probe", "io_floor.hip")
+PROBE_LIB = os.path.join(HERE, "libtg_probe.so")
+
+
+def build_probe(verbose: bool = False) -> str:
+    """Compile bench.py's I/O-floor probe (csrc/probe/io_floor.hip) into
+    libtg_probe.so, linked against libtg_fp8.so for its error reporting.  It is
+    measurement tooling: nothing in the package loads it."""
+    tmp = PROBE_LIB + ".tmp"
+    cmd = [HIPCC, *FLAGS, "-shared", PROBE_SRC, "-L", HERE, "-ltg_fp8", "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"probe build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, PROBE_LIB)
+    if verbose:
+        print(f"built {PROBE_LIB}")
+    return PROBE_LIB
+
+
 FFI_SRC = os.path.join(CSRC, "ffi", "tg_xla_ffi.cc")
 FFI_LIB = os.path.join(HERE, "libtg_xla_ffi.so")
 
@@ -85,5 +104,6 @@ def build_xla_ffi(verbose: bool = False):
 
 if __name__ == "__main__":
     build_library(verbose=True)
+    build_probe(verbose=True)
     build_xla_ffi(verbose=True)
     sys.exit(0)

@@ -698,25 +698,6 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
   if (step < nsteps) one_step(IntC<0>{});
 }
 
-// Compute units of the current device, queried once per device id.  Entry
-// points may be called concurrently from several host threads (an XLA FFI
-// handler runs on XLA's thread pool), so the one-time query is guarded by a
-// per-device std::call_once.
-static int device_cus() {
-  constexpr int kMaxDev = 64;
-  static std::once_flag once[kMaxDev];
-  static int cached[kMaxDev];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) dev = 0;
-  std::call_once(once[dev], [dev] {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
-      v = 256;
-    cached[dev] = v;
-  });
-  return cached[dev];
-}
-
 template <int BNS, bool OUT_F32>
 static int launch_gemm_256(const uint8_t* a_q, const float* a_s, const uint8_t* b_q,
                            const float* b_s, void* c, int M, int N, int K, hipStream_t st) {

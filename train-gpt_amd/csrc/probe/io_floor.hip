@@ -1,0 +1,87 @@
+// Measurement probe (not part of the product library): the HBM traffic of the
+// fused RMSNorm -> FP8 kernel (rmsnorm_kernel<4, true, true> in rmsnorm.hip)
+// with its arithmetic taken out, so that bench.py can time the I/O floor of
+// config 2's exact read / write mix on the same launch shape.
+//
+// Access pattern, as in the norm kernel at dim 2048: one wave64 per row, lane
+// l owns the 16-byte chunks l + 64 j (j < 4) of its row, rows walked with a
+// grid stride, the next row's x loaded (non-temporal) before the current one
+// is stored; y as 16-byte and q as 8-byte non-temporal stores per chunk, one
+// f32 scale per 128-element block from the first lane of each 16-lane group.
+//
+// mode 0: read x only (one f32 per row is written so the loads stay live)
+// mode 1: read x, write y                      (a bf16 copy)
+// mode 2: read x, write y, q and the scales    (config 2's mix)
+// mode 3: write y, q and the scales, read nothing
+#include "../tg_device.h"
+#include "../tg_host.h"
+
+namespace tg {
+
+template <int MODE>
+__global__ __launch_bounds__(256) void io_floor_kernel(const uint4* __restrict__ x, uint4* __restrict__ y,
+                                                       uint2* __restrict__ q, float* __restrict__ s,
+                                                       int64_t rows) {
+  constexpr int J = 4, NCH = 256;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave0 = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t wstride = (int64_t)gridDim.x * 4;
+  auto load_row = [&](int64_t row, uint4 (&v)[J]) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      if (MODE == 3) v[j] = make_uint4((uint32_t)row, (uint32_t)lane, (uint32_t)j, 0u);
+      else v[j] = ldg_stream(x + row * NCH + lane + 64 * j);
+    }
+  };
+  uint4 nxt[J];
+  if (wave0 < rows) load_row(wave0, nxt);
+  for (int64_t row = wave0; row < rows; row += wstride) {
+    uint4 cur[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) cur[j] = nxt[j];
+    if (row + wstride < rows) load_row(row + wstride, nxt);
+    if (MODE == 0) {
+      uint32_t acc = 0;
+#pragma unroll
+      for (int j = 0; j < J; ++j) acc ^= cur[j].x ^ cur[j].y ^ cur[j].z ^ cur[j].w;
+      if (lane == 0) s[row] = __uint_as_float(acc);
+      continue;
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int c = lane + 64 * j;
+      stg_stream(&y[row * NCH + c], cur[j]);
+      if (MODE >= 2) {
+        stg_stream(&q[row * NCH + c], make_uint2(cur[j].x ^ cur[j].z, cur[j].y ^ cur[j].w));
+        if ((lane & 15) == 0) s[row * (NCH >> 4) + (c >> 4)] = __uint_as_float(cur[j].x);
+      }
+    }
+  }
+}
+
+}  // namespace tg
+
+// rows x 2048 bf16 input; the grid is sized like the norm kernel's for the
+// given rows per wave (at least 512 workgroups, at most 16384).
+extern "C" int tg_probe_io_floor(int mode, const void* x, void* y, void* q, float* s, int64_t rows,
+                                 int rows_per_wave, void* stream) {
+  using namespace tg;
+  if (mode < 0 || mode > 3 || rows <= 0 || rows_per_wave <= 0) return einval("tg_probe_io_floor: bad arguments");
+  if ((mode != 3 && !x) || (mode != 0 && !y) || (mode >= 2 && !q) || !s)
+    return einval("tg_probe_io_floor: null pointer");
+  int64_t grid = (rows + 4 * rows_per_wave - 1) / (4 * rows_per_wave);
+  if (grid < 512) grid = (rows + 3) / 4 < 512 ? (rows + 3) / 4 : 512;
+  if (grid > 16384) grid = 16384;
+  auto st = static_cast<hipStream_t>(stream);
+  auto X = reinterpret_cast<const uint4*>(x);
+  auto Y = reinterpret_cast<uint4*>(y);
+  auto Q = reinterpret_cast<uint2*>(q);
+  const dim3 g((unsigned)grid), b(256);
+  switch (mode) {
+    case 0: hipLaunchKernelGGL(io_floor_kernel<0>, g, b, 0, st, X, Y, Q, s, rows); break;
+    case 1: hipLaunchKernelGGL(io_floor_kernel<1>, g, b, 0, st, X, Y, Q, s, rows); break;
+    case 2: hipLaunchKernelGGL(io_floor_kernel<2>, g, b, 0, st, X, Y, Q, s, rows); break;
+    default: hipLaunchKernelGGL(io_floor_kernel<3>, g, b, 0, st, X, Y, Q, s, rows); break;
+  }
+  return check_launch("io_floor");
+}

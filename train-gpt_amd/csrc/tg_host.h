@@ -5,6 +5,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "../../include/tg_fp8.h"
 
 namespace tg {
@@ -26,6 +28,26 @@ inline int check_launch(const char* kernel) {
 }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Compute units of the current device, queried once per device id.  Entry
+// points may be called concurrently from several host threads (an XLA FFI
+// handler runs on XLA's thread pool), so the one-time query is guarded by a
+// per-device std::call_once (one instance program-wide: an inline function's
+// statics are shared by every translation unit).
+inline int device_cus() {
+  constexpr int kMaxDev = 64;
+  static std::once_flag once[kMaxDev];
+  static int cached[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) dev = 0;
+  std::call_once(once[dev], [dev] {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cached[dev] = v;
+  });
+  return cached[dev];
+}
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
