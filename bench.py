@@ -879,8 +879,8 @@ def main():
         "decode": dec,
     }
     if args.only == "step":                      # the headline step alone (no secondary workloads)
-        out = {k: out[k] for k in ("metric", "value", "unit", "ms_per_step", "gemm_us_per_launch",
-                                   "roofline", "accuracy")}
+        out = {k: out[k] for k in ("metric", "value", "unit", "steps", "warmup", "clock_settle", "ms_per_step",
+                                   "gemm_us_per_launch", "roofline", "accuracy")}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(step.host)
     print(json.dumps(out))
