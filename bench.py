@@ -7,7 +7,8 @@ seeded), the kernel sequence of fp8.block_scaled_matmul's autograd path:
 quantize x along K and x.T along M (one read of x), W.T along K and W along N
 (one read of W) -> GEMM Y; quantize dY along N and dY.T along M (one read of
 dY) -> GEMM dX, GEMM dW.  Every kernel is a C-ABI call into libtg_fp8.so on
-torch's current stream; the step allocates nothing.
+torch's current stream (the *_km entry points: scales kept K-block-major, as
+the autograd path keeps them); the step allocates nothing.
 
 value        = 3 * 2*8192*2048*8192 FLOP / step time (TFLOP/s, quantization included),
                timed over exactly --steps steps after an untimed 150 ms clock-settle
@@ -170,12 +171,14 @@ class Step:
         u8, f32 = torch.uint8, torch.float32
         e = lambda *s: torch.empty(s, dtype=u8, device=dev)
         f = lambda *s: torch.empty(s, dtype=f32, device=dev)
-        self.qx, self.sx = e(M3, K3), f(M3, K3 // 128)          # x along K
-        self.qwt, self.swt = e(N3, K3), f(N3, K3 // 128)        # W.T along K
-        self.qdy, self.sdy = e(M3, N3), f(M3, N3 // 128)        # dY along N
-        self.qw, self.sw = e(K3, N3), f(K3, N3 // 128)          # W along N
-        self.qxt, self.sxt = e(K3, M3), f(K3, M3 // 128)        # X.T along M
-        self.qdyt, self.sdyt = e(N3, M3), f(N3, M3 // 128)      # dY.T along M
+        # scales K-block-major, (K/128, rows): the layout fp8.block_scaled_matmul's
+        # autograd path and the composites keep (tg_quantize_dual*_km, tg_gemm_fp8_nt_km)
+        self.qx, self.sx = e(M3, K3), f(K3 // 128, M3)          # x along K
+        self.qwt, self.swt = e(N3, K3), f(K3 // 128, N3)        # W.T along K
+        self.qdy, self.sdy = e(M3, N3), f(N3 // 128, M3)        # dY along N
+        self.qw, self.sw = e(K3, N3), f(N3 // 128, K3)          # W along N
+        self.qxt, self.sxt = e(K3, M3), f(M3 // 128, K3)        # X.T along M
+        self.qdyt, self.sdyt = e(N3, M3), f(M3 // 128, N3)      # dY.T along M
         self.y = torch.empty((M3, N3), dtype=bf, device=dev)
         self.dx = torch.empty((M3, K3), dtype=bf, device=dev)
         self.dw = torch.empty((K3, N3), dtype=bf, device=dev)
@@ -187,8 +190,8 @@ class Step:
         if ev is not None:
             s, e = self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True)
             s.record()
-        L.check(self.lib.tg_gemm_fp8_nt(L.ptr(qa), L.ptr(sa), L.ptr(qb), L.ptr(sb), 1, L.ptr(c),
-                                        L.TG_DTYPE_BF16, M, N, K, 128, self.stream))
+        L.check(self.lib.tg_gemm_fp8_nt_km(L.ptr(qa), L.ptr(sa), L.ptr(qb), L.ptr(sb), 1, L.ptr(c),
+                                           L.TG_DTYPE_BF16, M, N, K, 128, self.stream))
         if ev is not None:
             e.record()
             ev.append((s, e))
@@ -197,13 +200,13 @@ class Step:
         L, lib, st, p = self.L, self.lib, self.stream, self.L.ptr
         # forward (fp8.py:66,68,70-78); x.T along M and W along N are the
         # backward's operands, kept from the same reads
-        L.check(lib.tg_quantize_dual_pair(p(self.x), M3, K3, p(self.qx), p(self.sx), p(self.qxt),
-                                          p(self.sxt), p(self.w), K3, N3, p(self.qw), p(self.sw),
-                                          p(self.qwt), p(self.swt), 128, st))
+        L.check(lib.tg_quantize_dual_pair_km(p(self.x), M3, K3, p(self.qx), p(self.sx), p(self.qxt),
+                                             p(self.sxt), p(self.w), K3, N3, p(self.qw), p(self.sw),
+                                             p(self.qwt), p(self.swt), 128, st))
         self._gemm(self.qx, self.sx, self.qwt, self.swt, self.y, M3, N3, K3, ev)
         # dY along N (for dX) and dY.T along M (for dW) from one read of dY
-        L.check(lib.tg_quantize_dual(p(self.dy), M3, N3, 128, p(self.qdy), p(self.sdy), p(self.qdyt),
-                                     p(self.sdyt), st))
+        L.check(lib.tg_quantize_dual_km(p(self.dy), M3, N3, 128, p(self.qdy), p(self.sdy), p(self.qdyt),
+                                        p(self.sdyt), st))
         # dX = dY . W.T
         self._gemm(self.qdy, self.sdy, self.qw, self.sw, self.dx, M3, K3, N3, ev)
         # dW = X.T . dY
@@ -571,13 +574,13 @@ def step_accuracy(step, rows=256):
     r = rows
     xf, wf, dyf = step.x.float(), step.w.float(), step.dy.float()
     out = {"rows_checked": r}
-    ref = _dequant(step.qx[:r], step.sx[:r]) @ _dequant(step.qwt, step.swt).t()
+    ref = _dequant(step.qx[:r], step.sx.t()[:r]) @ _dequant(step.qwt, step.swt.t()).t()
     out["y_vs_dequant_f32"] = _maxrel(step.y[:r], ref)
     out["y_vs_bf16_matmul"] = _maxrel(step.y[:r], xf[:r] @ wf)
-    ref = _dequant(step.qdy[:r], step.sdy[:r]) @ _dequant(step.qw, step.sw).t()
+    ref = _dequant(step.qdy[:r], step.sdy.t()[:r]) @ _dequant(step.qw, step.sw.t()).t()
     out["dx_vs_dequant_f32"] = _maxrel(step.dx[:r], ref)
     out["dx_vs_bf16_matmul"] = _maxrel(step.dx[:r], dyf[:r] @ wf.t())
-    ref = _dequant(step.qxt[:r], step.sxt[:r]) @ _dequant(step.qdyt, step.sdyt).t()
+    ref = _dequant(step.qxt[:r], step.sxt.t()[:r]) @ _dequant(step.qdyt, step.sdyt.t()).t()
     out["dw_vs_dequant_f32"] = _maxrel(step.dw[:r], ref)
     out["dw_vs_bf16_matmul"] = _maxrel(step.dw[:r], xf.t()[:r] @ dyf)
     del xf, wf, dyf, ref

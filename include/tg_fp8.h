@@ -72,6 +72,20 @@ int tg_quantize_dual_pair(const void* x0, int64_t rows0, int64_t cols0, uint8_t*
                           int64_t cols1, uint8_t* q1, float* scales1, uint8_t* q_t1,
                           float* scales_t1, int block_k, void* stream);
 
+/* K-block-major scales.  The same quantizations (fp8.py:39-47, the bytes
+ * bit-identical) with every scale array stored transposed: scales of x along
+ * its rows as (cols/block_k, rows), scales of x.T as (rows/block_k, cols), i.e.
+ * scales_km[kb * rows + r] == scales[r * (cols/block_k) + kb].  This is the
+ * layout tg_gemm_fp8_nt_km reads (a K block's row scales contiguous), which the
+ * composites below use internally; the reference's own layout is the one
+ * above. */
+int tg_quantize_dual_km(const void* x, int64_t rows, int64_t cols, int block_k, uint8_t* q,
+                        float* scales_km, uint8_t* q_t, float* scales_t_km, void* stream);
+int tg_quantize_dual_pair_km(const void* x0, int64_t rows0, int64_t cols0, uint8_t* q0,
+                             float* scales0_km, uint8_t* q_t0, float* scales_t0_km, const void* x1,
+                             int64_t rows1, int64_t cols1, uint8_t* q1, float* scales1_km,
+                             uint8_t* q_t1, float* scales_t1_km, int block_k, void* stream);
+
 /* jax.nn.scaled_matmul + bf16 cast as called at fp8.py:70-78 ("NT" layout):
  * c[m, n] = sum_kb a_s[m, kb] * b_s[n / b_scale_bn, kb] * sum_{k in kb} a_q[m, k] * b_q[n, k]
  * a_q: (M, K) e4m3fn, a_s: (M, K/128) f32; b_q: (N, K) e4m3fn;
@@ -81,6 +95,14 @@ int tg_quantize_dual_pair(const void* x0, int64_t rows0, int64_t cols0, uint8_t*
 int tg_gemm_fp8_nt(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s,
                    int b_scale_bn, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
                    int block_k, void* stream);
+
+/* tg_gemm_fp8_nt (jax.nn.scaled_matmul, fp8.py:70-76) on K-block-major scales:
+ * a_s_km (K/128, M) and b_s_km (K/128, N) (or (K/128, ceil(N/128)) when
+ * b_scale_bn == 128), the transposes of tg_gemm_fp8_nt's a_s and b_s.  Same
+ * kernels, same output bits; a K block's scales are read as contiguous runs. */
+int tg_gemm_fp8_nt_km(const uint8_t* a_q, const float* a_s_km, const uint8_t* b_q,
+                      const float* b_s_km, int b_scale_bn, void* c, int c_dtype, int64_t M, int64_t N,
+                      int64_t K, int block_k, void* stream);
 
 /* Device workspace (bytes) tg_block_scaled_matmul needs for its quantized operands. */
 size_t tg_block_scaled_matmul_workspace(int64_t M, int64_t N, int64_t K, int block_k);

@@ -127,6 +127,33 @@ def test_layout_known_answer_persistent_tiles(dev, M, N, K, bn):
     np.testing.assert_array_equal(c16, ob.f32_to_bf16(want.astype(np.float32)))
 
 
+@pytest.mark.parametrize("M,N,K,bn", [(5000, 5000, 384, 1), (4300, 4404, 384, 128), (8192, 2048, 8192, 1),
+                                      (200, 136, 384, 1), (96, 4404, 256, 128), (2048, 3072, 768, 1)])
+def test_gemm_km_same_bits(dev, M, N, K, bn):
+    """tg_gemm_fp8_nt_km (scales K-block-major) = tg_gemm_fp8_nt on the
+    transposed scales, bit for bit, in bf16 and f32, on the persistent 256-tile
+    path (>= 128 tiles, ragged edges, both weight-scale layouts) and the
+    128-tile path.  (The composites use this path internally; their parity
+    tests cover it end to end.)"""
+    import _tglib as L
+    rng = np.random.default_rng(M + N + K + bn)
+    qa, sa = fp8_ref.quantize_fp8(ob.bf16_to_f32(ob.randn_bf16(rng, (M, K))))
+    if bn == 1:
+        qb, sb = fp8_ref.quantize_fp8(ob.bf16_to_f32(ob.randn_bf16(rng, (N, K), std=0.02)))
+    else:
+        qb, sb = fp8_ref.quantize_weight_128x128(ob.bf16_to_f32(ob.randn_bf16(rng, (N, K), std=0.02)))
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    for out in (torch.bfloat16, torch.float32):
+        want = _gemm(qa, sa, qb, sb, dev, bn=bn, out=out)
+        got = torch.empty_like(want)
+        code = L.TG_DTYPE_F32 if out == torch.float32 else L.TG_DTYPE_BF16
+        A, SA, B, SB = t(qa), t(sa.T), t(qb), t(sb.T)
+        L.check(L.lib().tg_gemm_fp8_nt_km(L.ptr(A), L.ptr(SA), L.ptr(B), L.ptr(SB), bn, L.ptr(got), code,
+                                          M, N, K, 128, L.stream_of(A)))
+        assert torch.equal(got.view(torch.int32 if out == torch.float32 else torch.int16),
+                           want.view(torch.int32 if out == torch.float32 else torch.int16))
+
+
 def test_block_scaled_matmul_c1(dev):
     """Config 1: x [2048, 768] ~N(0,1), W [768, 3072] ~N(0, 0.02^2), seed 0."""
     rng = np.random.default_rng(0)

@@ -143,6 +143,34 @@ def test_quantize_dual_pair_equals_dual(dev, shapes):
                 assert torch.equal(g.view(torch.uint8), w.view(torch.uint8))
 
 
+@pytest.mark.parametrize("shape", [(128, 128), (256, 384), (1024, 640), (8192, 8192), (16384, 4096)])
+def test_quantize_dual_km_is_the_transposed_scale_layout(dev, shape):
+    """tg_quantize_dual_km: the bytes of tg_quantize_dual, every scale array
+    stored K-block-major (scales_km[kb, r] == scales[r, kb]), bit for bit, with
+    special-value rows planted (NaN / inf scales land in the right slot)."""
+    rng = np.random.default_rng(sum(shape) + 21)
+    x = ob.randn_bf16(rng, shape, std=0.02)
+    x[:10, :128] = _special_rows(rng, 128)
+    xd = to_dev(x, dev)
+    q, s, qt, st = fp8.quantize_fp8_dual(xd)
+    kq, ks, kqt, kst = fp8._quantize_dual_km(xd, 128)
+    assert ks.shape == (shape[1] // 128, shape[0]) and kst.shape == (shape[0] // 128, shape[1])
+    assert torch.equal(kq, q.view(torch.uint8)) and torch.equal(kqt, qt.view(torch.uint8))
+    assert np.array_equal(f32_bits(ks), f32_bits(s).T) and np.array_equal(f32_bits(kst), f32_bits(st).T)
+
+
+@pytest.mark.parametrize("shapes", [((8192, 2048), (2048, 8192)), ((384, 256), (1024, 640))])
+def test_quantize_dual_pair_km(dev, shapes):
+    """tg_quantize_dual_pair_km = tg_quantize_dual_km on each tensor, bit for bit."""
+    rng = np.random.default_rng(sum(map(sum, shapes)) + 5)
+    xs = [to_dev(ob.randn_bf16(rng, s, std=0.02), dev) for s in shapes]
+    pair = fp8._quantize_dual_pair_km(xs[0], xs[1], 128)
+    for x, got in zip(xs, pair):
+        want = fp8._quantize_dual_km(x, 128)
+        for g, w in zip(got, want):
+            assert np.array_equal(f32_bits(g), f32_bits(w)) if g.dtype == torch.float32 else torch.equal(g, w)
+
+
 def test_quantize_dual_pair_skips_empty(dev):
     """A tensor with no rows is skipped (null pointers allowed); the other is quantized."""
     import _tglib as L

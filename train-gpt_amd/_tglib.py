@@ -28,7 +28,11 @@ SIGNATURES = {
     "tg_quantize_dual": (_int, [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp]),
     "tg_quantize_dual_pair": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp,
                                      _vp, _vp, _int, _vp]),
+    "tg_quantize_dual_km": (_int, [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp]),
+    "tg_quantize_dual_pair_km": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp,
+                                        _vp, _vp, _int, _vp]),
     "tg_gemm_fp8_nt": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _int, _vp]),
+    "tg_gemm_fp8_nt_km": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _int, _vp]),
     "tg_block_scaled_matmul_workspace": (_sz, [_i64, _i64, _i64, _int]),
     "tg_block_scaled_matmul": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp, _sz, _vp]),
     "tg_block_scaled_matmul_noalloc": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),

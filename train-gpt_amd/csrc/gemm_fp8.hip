@@ -56,7 +56,8 @@ __device__ __forceinline__ v8i as_v8i(const u32x4_t& lo, const u32x4_t& hi) {
 // Cache-policy operand of the raw buffer loads: nt (streaming, read once).
 constexpr int kAuxNT = 2;
 
-template <int TM, int TN, int BNS, bool OUT_F32>
+// SKM: scales K-block-major (see gemm_fp8_nt_256_kernel).
+template <int TM, int TN, int BNS, bool OUT_F32, bool SKM>
 __global__ __launch_bounds__(256, 2) void gemm_fp8_nt_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ SA, const uint8_t* __restrict__ B,
     const float* __restrict__ SB, void* __restrict__ C, int M, int N, int K, int tiles_m,
@@ -95,10 +96,11 @@ __global__ __launch_bounds__(256, 2) void gemm_fp8_nt_kernel(
     }
     if (tid < BM) {
       const int m = m0 + tid;
-      rs = m < M ? SA[(int64_t)m * nkb + kb] : 0.0f;
+      rs = m < M ? SA[SKM ? (int64_t)kb * M + m : (int64_t)m * nkb + kb] : 0.0f;
     } else if (tid < BM + BN) {
       const int n = n0 + tid - BM;
-      rs = n < N ? SB[(int64_t)(n / BNS) * nkb + kb] : 0.0f;
+      const int64_t nsb = BNS == 1 ? N : (N + BNS - 1) / BNS;
+      rs = n < N ? SB[SKM ? (int64_t)kb * nsb + n / BNS : (int64_t)(n / BNS) * nkb + kb] : 0.0f;
     }
   };
   auto lstore = [&](int stage) {
@@ -280,6 +282,7 @@ struct W32Ctx {
   __amdgpu_buffer_rsrc_t ra, rb, rsa, rsb;
   uint32_t voa[2], vob[2];    // per-lane byte offsets (kb = 0) for even / odd u
   uint32_t vosa, vosb;
+  uint32_t skb_a, skb_b;      // bytes from one K block's scales to the next (4, or rows x 4 K-block-major)
   uint32_t row8;              // 8 rows of A / B in bytes (8 * K)
   int wave, nkb;
   // LDS byte addresses of this lane's fragment chunks [K half][chunk] and
@@ -349,8 +352,8 @@ __device__ __forceinline__ void w32_issue_part(const W32Ctx& c, uint8_t* la, uin
     __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rb, lb + slot * 4096 + u * 1024, 16, c.vob[u & 1],
                                              sofs, 0, 0);
   if (part == 0) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rsa, ls + c.wave * 64, 4, c.vosa, (uint32_t)kb * 4u, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rsb, ls + 256 + c.wave * 64, 4, c.vosb, (uint32_t)kb * 4u, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rsa, ls + c.wave * 64, 4, c.vosa, (uint32_t)kb * c.skb_a, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rsb, ls + 256 + c.wave * 64, 4, c.vosb, (uint32_t)kb * c.skb_b, 0, 0);
   }
 }
 
@@ -546,7 +549,13 @@ __device__ __forceinline__ void w32_store_tile(const v16f (&acc)[2][4], void* __
 // slots b, b + G, ... (G a multiple of 8, so its slots stay on its XCD) and
 // walks the K blocks of all its tiles as one stream; a tile's last K block
 // copies the next tile's block 0 into the other stage.
-template <int BNS, bool OUT_F32>
+//
+// SKM: scales stored K-block-major, SA[kb * M + m] and SB[kb * nsb + n / BNS]
+// (the transpose of the reference's (rows, K/128) layout).  A K block's 64
+// row scales per loader lane group are then 256 contiguous bytes instead of
+// 64 rows K/32 bytes apart, which takes the scale copies from 64 cache lines
+// per instruction to two.
+template <int BNS, bool OUT_F32, bool SKM>
 __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ SA, const uint8_t* __restrict__ B,
     const float* __restrict__ SB, void* __restrict__ C, int M, int N, int K, int tiles_m,
@@ -581,10 +590,13 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
   const int mu = lane & 31;
   const int sidx_a = (c.wave & 3) * 64 + lane;
   const int sidx_b = (c.wave & 3) * 64 + (lane & 32) + 8 * (mu & 3) + 4 * (mu >> 4) + ((mu >> 2) & 3);
+  const uint32_t srow_a = SKM ? 4u : c.nkb * 4u, srow_b = SKM ? 4u : c.nkb * 4u;   // bytes per scale row
+  c.skb_a = SKM ? (uint32_t)M * 4u : 4u;
+  c.skb_b = SKM ? (uint32_t)nsb * 4u : 4u;
   c.rsa = make_rsrc(SA, (uint32_t)M * c.nkb * 4u);
-  c.vosa = (lm0 + sidx_a) * c.nkb * 4u;
+  c.vosa = (lm0 + sidx_a) * srow_a;
   c.rsb = make_rsrc(SB, (uint32_t)nsb * c.nkb * 4u);
-  c.vosb = ((ln0 + sidx_b) / BNS) * c.nkb * 4u;
+  c.vosb = ((ln0 + sidx_b) / BNS) * srow_b;
   // move the loader to the tile of launch slot `s`: every per-lane offset is
   // (tile origin + lane part) * stride, so the move adds a workgroup-uniform
   // difference (mod 2^32).  Rows past M / N keep landing past the buffer's
@@ -600,8 +612,8 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
       c.voa[par] += da;
       c.vob[par] += db;
     }
-    c.vosa += (m0 - lm0) * c.nkb * 4u;
-    c.vosb += (n0 / BNS - ln0 / BNS) * c.nkb * 4u;   // divide first: n0 - ln0 may wrap
+    c.vosa += (m0 - lm0) * srow_a;
+    c.vosb += (n0 / BNS - ln0 / BNS) * srow_b;   // divide first: n0 - ln0 may wrap
     lm0 = m0;
     ln0 = n0;
   };
@@ -698,7 +710,7 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
   if (step < nsteps) one_step(IntC<0>{});
 }
 
-template <int BNS, bool OUT_F32>
+template <int BNS, bool OUT_F32, bool SKM>
 static int launch_gemm_256(const uint8_t* a_q, const float* a_s, const uint8_t* b_q,
                            const float* b_s, void* c, int M, int N, int K, hipStream_t st) {
   const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
@@ -707,18 +719,18 @@ static int launch_gemm_256(const uint8_t* a_q, const float* a_s, const uint8_t* 
   const int ntiles = tiles_m * tiles_n;
   const int slots = device_cus() & ~7;
   const int grid = ntiles <= slots || slots == 0 ? ntiles : slots;
-  hipLaunchKernelGGL((gemm_fp8_nt_256_kernel<BNS, OUT_F32>), dim3((unsigned)grid), dim3(512), 0, st,
+  hipLaunchKernelGGL((gemm_fp8_nt_256_kernel<BNS, OUT_F32, SKM>), dim3((unsigned)grid), dim3(512), 0, st,
                      a_q, a_s, b_q, b_s, c, M, N, K, tiles_m, tiles_n);
   return check_launch("gemm_fp8_nt_256");
 }
 
-template <int TM, int TN, int BNS, bool OUT_F32>
+template <int TM, int TN, int BNS, bool OUT_F32, bool SKM>
 static int launch_gemm_cfg(const uint8_t* a_q, const float* a_s, const uint8_t* b_q,
                            const float* b_s, void* c, int M, int N, int K, hipStream_t st) {
   constexpr int BM = 2 * TM * 16, BN = 2 * TN * 16;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   const size_t lds = (size_t)2 * (BM + BN) * 128 + (size_t)2 * (BM + BN) * 4;
-  auto kern = gemm_fp8_nt_kernel<TM, TN, BNS, OUT_F32>;
+  auto kern = gemm_fp8_nt_kernel<TM, TN, BNS, OUT_F32, SKM>;
   // the dynamic-LDS limit is a per-device function attribute: set once per
   // device (thread-safe, see device_cus)
   constexpr int kMaxDev = 64;
@@ -739,26 +751,35 @@ static int launch_gemm_cfg(const uint8_t* a_q, const float* a_s, const uint8_t* 
   return check_launch("gemm_fp8_nt");
 }
 
+template <bool SKM>
+static int launch_gemm_fp8_layout(const uint8_t* a_q, const float* a_s, const uint8_t* b_q,
+                                  const float* b_s, int b_scale_bn, void* c, bool f32, int m, int n,
+                                  int k, bool big, hipStream_t st) {
+  if (big) {
+    if (b_scale_bn == 1)
+      return f32 ? launch_gemm_256<1, true, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st)
+                 : launch_gemm_256<1, false, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st);
+    return f32 ? launch_gemm_256<128, true, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st)
+               : launch_gemm_256<128, false, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st);
+  }
+  if (b_scale_bn == 1)
+    return f32 ? launch_gemm_cfg<4, 4, 1, true, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st)
+               : launch_gemm_cfg<4, 4, 1, false, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st);
+  return f32 ? launch_gemm_cfg<4, 4, 128, true, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st)
+             : launch_gemm_cfg<4, 4, 128, false, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st);
+}
+
 int launch_gemm_fp8(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s,
                     int b_scale_bn, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
-                    hipStream_t st) {
+                    hipStream_t st, bool skm) {
   if (M == 0 || N == 0) return TG_OK;
   const int m = (int)M, n = (int)N, k = (int)K;
   const bool f32 = c_dtype == TG_DTYPE_F32;
   // 256 x 256 tiles once they fill the chip (>= 128 workgroups), else 128 x 128
   const bool fits32 = (uint64_t)M * (uint64_t)K < (1ull << 31) && (uint64_t)N * (uint64_t)K < (1ull << 31);
-  if (fits32 && ((M + 255) / 256) * ((N + 255) / 256) >= 128) {
-    if (b_scale_bn == 1)
-      return f32 ? launch_gemm_256<1, true>(a_q, a_s, b_q, b_s, c, m, n, k, st)
-                 : launch_gemm_256<1, false>(a_q, a_s, b_q, b_s, c, m, n, k, st);
-    return f32 ? launch_gemm_256<128, true>(a_q, a_s, b_q, b_s, c, m, n, k, st)
-               : launch_gemm_256<128, false>(a_q, a_s, b_q, b_s, c, m, n, k, st);
-  }
-  if (b_scale_bn == 1)
-    return f32 ? launch_gemm_cfg<4, 4, 1, true>(a_q, a_s, b_q, b_s, c, m, n, k, st)
-               : launch_gemm_cfg<4, 4, 1, false>(a_q, a_s, b_q, b_s, c, m, n, k, st);
-  return f32 ? launch_gemm_cfg<4, 4, 128, true>(a_q, a_s, b_q, b_s, c, m, n, k, st)
-             : launch_gemm_cfg<4, 4, 128, false>(a_q, a_s, b_q, b_s, c, m, n, k, st);
+  const bool big = fits32 && ((M + 255) / 256) * ((N + 255) / 256) >= 128;
+  return skm ? launch_gemm_fp8_layout<true>(a_q, a_s, b_q, b_s, b_scale_bn, c, f32, m, n, k, big, st)
+             : launch_gemm_fp8_layout<false>(a_q, a_s, b_q, b_s, b_scale_bn, c, f32, m, n, k, big, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -1269,15 +1290,29 @@ static int check_gemm_args(const char* who, int64_t M, int64_t N, int64_t K, int
   return TG_OK;
 }
 
-extern "C" int tg_gemm_fp8_nt(const uint8_t* a_q, const float* a_s, const uint8_t* b_q,
-                              const float* b_s, int b_scale_bn, void* c, int c_dtype, int64_t M,
-                              int64_t N, int64_t K, int block_k, void* stream) {
-  TG_TRY(check_gemm_args("gemm_fp8_nt", M, N, K, block_k, b_scale_bn));
+static int gemm_fp8_nt_entry(const char* who, const uint8_t* a_q, const float* a_s, const uint8_t* b_q,
+                             const float* b_s, int b_scale_bn, void* c, int c_dtype, int64_t M,
+                             int64_t N, int64_t K, int block_k, void* stream, bool skm) {
+  TG_TRY(check_gemm_args(who, M, N, K, block_k, b_scale_bn));
   if (c_dtype != TG_DTYPE_BF16 && c_dtype != TG_DTYPE_F32) return einval("gemm_fp8_nt: bad c_dtype");
   if (M == 0 || N == 0) return TG_OK;
   if (!a_q || !a_s || !b_q || !b_s || !c) return einval("gemm_fp8_nt: null pointer");
   if (!aligned(a_q, 16) || !aligned(b_q, 16)) return einval("gemm_fp8_nt: operands must be 16-byte aligned");
-  return launch_gemm_fp8(a_q, a_s, b_q, b_s, b_scale_bn, c, c_dtype, M, N, K, as_stream(stream));
+  return launch_gemm_fp8(a_q, a_s, b_q, b_s, b_scale_bn, c, c_dtype, M, N, K, as_stream(stream), skm);
+}
+
+extern "C" int tg_gemm_fp8_nt(const uint8_t* a_q, const float* a_s, const uint8_t* b_q,
+                              const float* b_s, int b_scale_bn, void* c, int c_dtype, int64_t M,
+                              int64_t N, int64_t K, int block_k, void* stream) {
+  return gemm_fp8_nt_entry("gemm_fp8_nt", a_q, a_s, b_q, b_s, b_scale_bn, c, c_dtype, M, N, K, block_k,
+                           stream, false);
+}
+
+extern "C" int tg_gemm_fp8_nt_km(const uint8_t* a_q, const float* a_s_km, const uint8_t* b_q,
+                                 const float* b_s_km, int b_scale_bn, void* c, int c_dtype, int64_t M,
+                                 int64_t N, int64_t K, int block_k, void* stream) {
+  return gemm_fp8_nt_entry("gemm_fp8_nt_km", a_q, a_s_km, b_q, b_s_km, b_scale_bn, c, c_dtype, M, N, K,
+                           block_k, stream, true);
 }
 
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1298,9 +1333,10 @@ static int block_scaled_matmul_on(const void* a, const void* b, void* out, int64
   float* sa = reinterpret_cast<float*>(p);   p += align256((size_t)M * nkb * 4);
   uint8_t* qb = p;                 p += align256((size_t)N * K);
   float* sb = reinterpret_cast<float*>(p);
-  TG_TRY(launch_quant_rows(a, TG_DTYPE_BF16, M, K, qa, sa, st));     // fp8.py:66
-  TG_TRY(launch_quant_cols(b, K, N, qb, sb, st));                     // fp8.py:68
-  return launch_gemm_fp8(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, K, st);   // fp8.py:70-78
+  // the composite's own workspace: scales K-block-major (the GEMM's cheaper scale reads)
+  TG_TRY(launch_quant_rows(a, TG_DTYPE_BF16, M, K, qa, sa, st, true));     // fp8.py:66
+  TG_TRY(launch_quant_cols(b, K, N, qb, sb, st, true));                     // fp8.py:68
+  return launch_gemm_fp8(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, K, st, true);   // fp8.py:70-78
 }
 
 extern "C" int tg_block_scaled_matmul(const void* a, const void* b, void* out, int64_t M,
@@ -1402,12 +1438,13 @@ extern "C" int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, cons
   float* sat = reinterpret_cast<float*>(p);   p += align256((size_t)K * mkb * 4);
   uint8_t* qgt = p;   p += align256((size_t)N * M);
   float* sgt = reinterpret_cast<float*>(p);
-  // g along N and g.T along M from one read of g
-  TG_TRY(launch_quant_dual(g, M, N, qg, sg, qgt, sgt, st));
-  TG_TRY(launch_quant_rows(b, TG_DTYPE_BF16, K, N, qb, sb, st));
-  TG_TRY(launch_gemm_fp8(qg, sg, qb, sb, 1, da, TG_DTYPE_BF16, M, K, N, st));    // dX = g . b.T
-  TG_TRY(launch_quant_cols(a, M, K, qat, sat, st));
-  return launch_gemm_fp8(qat, sat, qgt, sgt, 1, db, TG_DTYPE_BF16, K, N, M, st);  // dW = a.T . g
+  // g along N and g.T along M from one read of g; every scale array of the
+  // workspace K-block-major
+  TG_TRY(launch_quant_dual(g, M, N, qg, sg, qgt, sgt, st, true));
+  TG_TRY(launch_quant_rows(b, TG_DTYPE_BF16, K, N, qb, sb, st, true));
+  TG_TRY(launch_gemm_fp8(qg, sg, qb, sb, 1, da, TG_DTYPE_BF16, M, K, N, st, true));    // dX = g . b.T
+  TG_TRY(launch_quant_cols(a, M, K, qat, sat, st, true));
+  return launch_gemm_fp8(qat, sat, qgt, sgt, 1, db, TG_DTYPE_BF16, K, N, M, st, true);  // dW = a.T . g
 }
 
 

@@ -54,11 +54,14 @@ __device__ __forceinline__ void load_chunk(const void* __restrict__ x, int64_t c
 
 // RELU2: the values quantized are bf16(relu(x)^2) (model.py:72's activation
 // as bf16 tensor ops: relu exact, the square rounded once), for bf16 x.
+// skm_rows > 0: scales stored K-block-major, s[kb * skm_rows + row] (nkb
+// blocks per row), instead of the reference's (rows, nkb) row-major layout.
 template <bool F32_IN, int UNROLL, bool RELU2 = false>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const void* __restrict__ x,
                                                          uint2* __restrict__ q,
                                                          float* __restrict__ s,
-                                                         int64_t nchunks) {
+                                                         int64_t nchunks, int64_t skm_rows = 0,
+                                                         int nkb = 1) {
   const int64_t base = (int64_t)blockIdx.x * (256 * UNROLL) + threadIdx.x;
   float v[UNROLL][8];
 #pragma unroll
@@ -74,23 +77,28 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const void* __restrict_
     float sc = F32_IN ? block_scale(m) : block_scale_bf16(m);
     if (c < nchunks) {
       q[c] = quant8<!F32_IN>(v[u], sc);
-      if ((threadIdx.x & 15) == 0) s[c >> 4] = sc;
+      if ((threadIdx.x & 15) == 0) {
+        const int64_t b = c >> 4;
+        s[skm_rows > 0 ? (b % nkb) * skm_rows + b / nkb : b] = sc;
+      }
     }
   }
 }
 
 int launch_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, uint8_t* q,
-                      float* s, hipStream_t st) {
+                      float* s, hipStream_t st, bool skm) {
   const int64_t nchunks = rows * cols / 8;
   if (nchunks == 0) return TG_OK;
   constexpr int UNROLL = 4;
   const int64_t grid = (nchunks + 256 * UNROLL - 1) / (256 * UNROLL);
+  const int64_t skm_rows = skm ? rows : 0;
+  const int nkb = (int)(cols / 128);
   if (x_dtype == TG_DTYPE_F32)
     hipLaunchKernelGGL((quant_rows_kernel<true, UNROLL>), dim3((unsigned)grid), dim3(256), 0, st, x,
-                       reinterpret_cast<uint2*>(q), s, nchunks);
+                       reinterpret_cast<uint2*>(q), s, nchunks, skm_rows, nkb);
   else
     hipLaunchKernelGGL((quant_rows_kernel<false, UNROLL>), dim3((unsigned)grid), dim3(256), 0, st,
-                       x, reinterpret_cast<uint2*>(q), s, nchunks);
+                       x, reinterpret_cast<uint2*>(q), s, nchunks, skm_rows, nkb);
   return check_launch("quant_rows");
 }
 
@@ -119,7 +127,7 @@ template <bool VEC>
 __global__ __launch_bounds__(256) void quant_cols_kernel(const uint16_t* __restrict__ x,
                                                          int64_t rows, int64_t cols,
                                                          uint8_t* __restrict__ qt,
-                                                         float* __restrict__ st) {
+                                                         float* __restrict__ st, bool skm = false) {
   __shared__ uint32_t tile[128 * 34];
   __shared__ uint32_t tq[64 * 36];
   const int tid = threadIdx.x;
@@ -174,7 +182,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(const uint16_t* __restr
     tq[n * 36 + 4 * i + j] = w;
   }
   const bool col_ok = (c0 + n) < cols;
-  if (j == 0 && col_ok) st[(c0 + n) * (rows >> 7) + blockIdx.y] = sc;
+  if (j == 0 && col_ok) st[skm ? (int64_t)blockIdx.y * cols + c0 + n : (c0 + n) * (rows >> 7) + blockIdx.y] = sc;
   __syncthreads();
   if (col_ok) {
     const uint4* src = reinterpret_cast<const uint4*>(&tq[n * 36 + 8 * j]);
@@ -222,6 +230,7 @@ struct DualJob {
   uint8_t* qt;
   float* st;
   int gx, gy, xcd_blocks;
+  int skm;   // scales K-block-major: s[kb * rows + row], st[kb * cols + col]
 };
 struct DualJobs {
   DualJob job[2];
@@ -271,7 +280,10 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
       f[4] = bf16lo(v[u].z); f[5] = bf16hi(v[u].z); f[6] = bf16lo(v[u].w); f[7] = bf16hi(v[u].w);
       const float sc = block_scale_bf16(row16_max_u32(absmax8(f)));
       q[(r0 + row) * cchunks + (c0 >> 3) + ch] = quant8<true>(f, sc);
-      if (ch == 0) s[(r0 + row) * (cols >> 7) + tx] = sc;
+      if (ch == 0) {
+        if (J.skm) s[(int64_t)tx * rows + r0 + row] = sc;
+        else s[(r0 + row) * (cols >> 7) + tx] = sc;
+      }
     }
     *reinterpret_cast<uint4*>(&tile[row * 68 + ch * 4]) = v[u];
   }
@@ -312,7 +324,10 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
       }
       tq[n * 36 + 4 * i + j] = w;
     }
-    if (j == 0 && (!GUARD || c0 + n < cols)) st[(c0 + n) * (rows >> 7) + ty] = sc;
+    if (j == 0 && (!GUARD || c0 + n < cols)) {
+      if (J.skm) st[(int64_t)ty * cols + c0 + n] = sc;
+      else st[(c0 + n) * (rows >> 7) + ty] = sc;
+    }
   };
   col_words(f0, sc0, 2 * cp);
   col_words(f1, sc1, 2 * cp + 1);
@@ -338,7 +353,7 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
 constexpr int64_t kDualMaxTiles = int64_t(1) << 23;   // slots fit one 1-D grid of 256-thread groups
 
 static int dual_job(DualJob& j, const char* who, const void* x, int64_t rows, int64_t cols, uint8_t* q,
-                    float* s, uint8_t* q_t, float* s_t, bool xcd_ok) {
+                    float* s, uint8_t* q_t, float* s_t, bool xcd_ok, bool skm) {
   const int64_t gx = (cols + 127) / 128, gy = rows / 128;
   if (gx * gy > kDualMaxTiles) {
     char msg[160];
@@ -356,17 +371,18 @@ static int dual_job(DualJob& j, const char* who, const void* x, int64_t rows, in
   j.gx = (int)gx;
   j.gy = (int)gy;
   j.xcd_blocks = xcd_ok && gx % 32 == 0 && gy % 16 == 0 && (gx * gy / 8) % 512 == 0;
+  j.skm = skm ? 1 : 0;
   return TG_OK;
 }
 
 int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, float* s_t,
-                      hipStream_t st) {
+                      hipStream_t st, bool skm) {
   if (rows == 0 || cols == 0) return TG_OK;
   if (rows / 128 > 65535) return einval("quantize_cols: rows / 128 must be <= 65535");
   if (cols % 8 == 0 && aligned(x, 16)) {
     // 128 x 128 tiles: column pairs per LDS read, 64-byte contiguous stores
     DualJobs jobs{};
-    TG_TRY(dual_job(jobs.job[0], "quantize_cols", x, rows, cols, nullptr, nullptr, q_t, s_t, false));
+    TG_TRY(dual_job(jobs.job[0], "quantize_cols", x, rows, cols, nullptr, nullptr, q_t, s_t, false, skm));
     jobs.nblk0 = jobs.job[0].gx * jobs.job[0].gy;
     const dim3 grid((unsigned)jobs.nblk0);
     if (cols % 128 == 0)
@@ -378,16 +394,16 @@ int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, f
   // rows not 16-byte aligned: the element-load kernel
   const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)(rows / 128));
   hipLaunchKernelGGL(quant_cols_kernel<false>, grid, dim3(256), 0, st,
-                     reinterpret_cast<const uint16_t*>(x), rows, cols, q_t, s_t);
+                     reinterpret_cast<const uint16_t*>(x), rows, cols, q_t, s_t, skm);
   return check_launch("quant_cols");
 }
 
 int launch_quant_dual(const void* x, int64_t rows, int64_t cols, uint8_t* q, float* s, uint8_t* q_t,
-                      float* s_t, hipStream_t st) {
+                      float* s_t, hipStream_t st, bool skm) {
   if (rows == 0 || cols == 0) return TG_OK;
   if (rows % 128 || cols % 128) return einval("quantize_dual: rows and cols must be multiples of 128");
   DualJobs jobs{};
-  TG_TRY(dual_job(jobs.job[0], "quantize_dual", x, rows, cols, q, s, q_t, s_t, true));
+  TG_TRY(dual_job(jobs.job[0], "quantize_dual", x, rows, cols, q, s, q_t, s_t, true, skm));
   jobs.nblk0 = jobs.job[0].gx * jobs.job[0].gy;
   hipLaunchKernelGGL((quant_dual_kernel<true, false>), dim3((unsigned)jobs.nblk0), dim3(256), 0, st,
                      jobs);
@@ -396,18 +412,18 @@ int launch_quant_dual(const void* x, int64_t rows, int64_t cols, uint8_t* q, flo
 
 int launch_quant_dual_pair(const void* x0, int64_t rows0, int64_t cols0, uint8_t* q0, float* s0,
                            uint8_t* qt0, float* st0, const void* x1, int64_t rows1, int64_t cols1,
-                           uint8_t* q1, float* s1, uint8_t* qt1, float* st1, hipStream_t st) {
+                           uint8_t* q1, float* s1, uint8_t* qt1, float* st1, hipStream_t st, bool skm) {
   const bool e0 = rows0 == 0 || cols0 == 0, e1 = rows1 == 0 || cols1 == 0;
   if (e0 && e1) return TG_OK;
-  if (e0) return launch_quant_dual(x1, rows1, cols1, q1, s1, qt1, st1, st);
-  if (e1) return launch_quant_dual(x0, rows0, cols0, q0, s0, qt0, st0, st);
+  if (e0) return launch_quant_dual(x1, rows1, cols1, q1, s1, qt1, st1, st, skm);
+  if (e1) return launch_quant_dual(x0, rows0, cols0, q0, s0, qt0, st0, st, skm);
   if (rows0 % 128 || cols0 % 128 || rows1 % 128 || cols1 % 128)
     return einval("quantize_dual_pair: rows and cols must be multiples of 128");
   DualJobs jobs{};
-  TG_TRY(dual_job(jobs.job[0], "quantize_dual_pair", x0, rows0, cols0, q0, s0, qt0, st0, true));
+  TG_TRY(dual_job(jobs.job[0], "quantize_dual_pair", x0, rows0, cols0, q0, s0, qt0, st0, true, skm));
   jobs.nblk0 = jobs.job[0].gx * jobs.job[0].gy;
   TG_TRY(dual_job(jobs.job[1], "quantize_dual_pair", x1, rows1, cols1, q1, s1, qt1, st1,
-                  jobs.nblk0 % 8 == 0));
+                  jobs.nblk0 % 8 == 0, skm));
   const int64_t total = (int64_t)jobs.nblk0 + (int64_t)jobs.job[1].gx * jobs.job[1].gy;
   if (total > kDualMaxTiles) return einval("quantize_dual_pair: too many 128 x 128 tiles");
   hipLaunchKernelGGL((quant_dual_kernel<true, false>), dim3((unsigned)total), dim3(256), 0, st, jobs);
@@ -610,21 +626,29 @@ extern "C" int tg_selftest_divide(uint64_t* counts, void* stream) {
   return check_launch("selftest_divide");
 }
 
-extern "C" int tg_quantize_dual(const void* x, int64_t rows, int64_t cols, int block_k, uint8_t* q,
-                                float* s, uint8_t* q_t, float* s_t, void* stream) {
+static int quantize_dual_entry(const void* x, int64_t rows, int64_t cols, int block_k, uint8_t* q,
+                               float* s, uint8_t* q_t, float* s_t, void* stream, bool skm) {
   if (block_k != 128) return einval("quantize_dual: block_k must be 128");
   if (rows < 0 || cols < 0) return einval("quantize_dual: bad shape");
   if (rows == 0 || cols == 0) return TG_OK;
   if (!x || !q || !s || !q_t || !s_t) return einval("quantize_dual: null pointer");
   if (!aligned(x, 16) || !aligned(q, 8) || !aligned(q_t, 16))
     return einval("quantize_dual: x and q_t must be 16-byte, q 8-byte aligned");
-  return launch_quant_dual(x, rows, cols, q, s, q_t, s_t, as_stream(stream));
+  return launch_quant_dual(x, rows, cols, q, s, q_t, s_t, as_stream(stream), skm);
+}
+extern "C" int tg_quantize_dual(const void* x, int64_t rows, int64_t cols, int block_k, uint8_t* q,
+                                float* s, uint8_t* q_t, float* s_t, void* stream) {
+  return quantize_dual_entry(x, rows, cols, block_k, q, s, q_t, s_t, stream, false);
+}
+extern "C" int tg_quantize_dual_km(const void* x, int64_t rows, int64_t cols, int block_k, uint8_t* q,
+                                   float* s_km, uint8_t* q_t, float* s_t_km, void* stream) {
+  return quantize_dual_entry(x, rows, cols, block_k, q, s_km, q_t, s_t_km, stream, true);
 }
 
-extern "C" int tg_quantize_dual_pair(const void* x0, int64_t rows0, int64_t cols0, uint8_t* q0,
-                                     float* s0, uint8_t* q_t0, float* s_t0, const void* x1,
-                                     int64_t rows1, int64_t cols1, uint8_t* q1, float* s1,
-                                     uint8_t* q_t1, float* s_t1, int block_k, void* stream) {
+static int quantize_dual_pair_entry(const void* x0, int64_t rows0, int64_t cols0, uint8_t* q0,
+                                    float* s0, uint8_t* q_t0, float* s_t0, const void* x1,
+                                    int64_t rows1, int64_t cols1, uint8_t* q1, float* s1,
+                                    uint8_t* q_t1, float* s_t1, int block_k, void* stream, bool skm) {
   if (block_k != 128) return einval("quantize_dual_pair: block_k must be 128");
   if (rows0 < 0 || cols0 < 0 || rows1 < 0 || cols1 < 0) return einval("quantize_dual_pair: bad shape");
   const bool u0 = rows0 > 0 && cols0 > 0, u1 = rows1 > 0 && cols1 > 0;
@@ -634,5 +658,19 @@ extern "C" int tg_quantize_dual_pair(const void* x0, int64_t rows0, int64_t cols
       (u1 && (!aligned(x1, 16) || !aligned(q1, 8) || !aligned(q_t1, 16))))
     return einval("quantize_dual_pair: x and q_t must be 16-byte, q 8-byte aligned");
   return launch_quant_dual_pair(x0, rows0, cols0, q0, s0, q_t0, s_t0, x1, rows1, cols1, q1, s1, q_t1,
-                                s_t1, as_stream(stream));
+                                s_t1, as_stream(stream), skm);
+}
+extern "C" int tg_quantize_dual_pair(const void* x0, int64_t rows0, int64_t cols0, uint8_t* q0,
+                                     float* s0, uint8_t* q_t0, float* s_t0, const void* x1,
+                                     int64_t rows1, int64_t cols1, uint8_t* q1, float* s1,
+                                     uint8_t* q_t1, float* s_t1, int block_k, void* stream) {
+  return quantize_dual_pair_entry(x0, rows0, cols0, q0, s0, q_t0, s_t0, x1, rows1, cols1, q1, s1, q_t1,
+                                  s_t1, block_k, stream, false);
+}
+extern "C" int tg_quantize_dual_pair_km(const void* x0, int64_t rows0, int64_t cols0, uint8_t* q0,
+                                        float* s0_km, uint8_t* q_t0, float* s_t0_km, const void* x1,
+                                        int64_t rows1, int64_t cols1, uint8_t* q1, float* s1_km,
+                                        uint8_t* q_t1, float* s_t1_km, int block_k, void* stream) {
+  return quantize_dual_pair_entry(x0, rows0, cols0, q0, s0_km, q_t0, s_t0_km, x1, rows1, cols1, q1, s1_km,
+                                  q_t1, s_t1_km, block_k, stream, true);
 }

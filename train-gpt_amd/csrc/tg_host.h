@@ -52,20 +52,23 @@ inline int device_cus() {
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 // Kernel launchers shared between translation units.
+// skm: scales stored K-block-major ((cols / 128, rows) for a row quantization,
+// (rows / 128, cols) for the transposed one) instead of the reference's
+// row-major (rows, cols / 128); the GEMM's *_km entry points read that layout.
 int launch_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, uint8_t* q,
-                      float* s, hipStream_t st);
+                      float* s, hipStream_t st, bool skm = false);
 int launch_quant_rows_relu2(const void* x, int64_t rows, int64_t cols, uint8_t* q, float* s,
                             hipStream_t st);
 int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, float* s_t,
-                      hipStream_t st);
+                      hipStream_t st, bool skm = false);
 int launch_quant_dual(const void* x, int64_t rows, int64_t cols, uint8_t* q, float* s, uint8_t* q_t,
-                      float* s_t, hipStream_t st);
+                      float* s_t, hipStream_t st, bool skm = false);
 int launch_quant_dual_pair(const void* x0, int64_t rows0, int64_t cols0, uint8_t* q0, float* s0,
                            uint8_t* qt0, float* st0, const void* x1, int64_t rows1, int64_t cols1,
-                           uint8_t* q1, float* s1, uint8_t* qt1, float* st1, hipStream_t st);
+                           uint8_t* q1, float* s1, uint8_t* qt1, float* st1, hipStream_t st, bool skm = false);
 int launch_gemm_fp8(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s,
                     int b_scale_bn, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
-                    hipStream_t st);
+                    hipStream_t st, bool skm = false);
 
 }  // namespace tg
 

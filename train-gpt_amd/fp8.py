@@ -177,6 +177,48 @@ def quantize_fp8_dual_pair(x0: torch.Tensor, x1: torch.Tensor, block_k: int = DE
     return tuple((q.view(e4), s, qt.view(e4), st) for q, s, qt, st in outs)
 
 
+def _quantize_dual_km(x: torch.Tensor, block_k: int):
+    """quantize_fp8_dual with K-block-major scales (tg_quantize_dual_km): the
+    bytes of quantize_fp8_dual, scales stored transposed, (C/bk, R) and (R/bk, C)."""
+    R, C = x.shape
+    u8, f32 = torch.uint8, torch.float32
+    q = torch.empty((R, C), dtype=u8, device=x.device)
+    s = torch.empty((C // block_k, R), dtype=f32, device=x.device)
+    qt = torch.empty((C, R), dtype=u8, device=x.device)
+    st = torch.empty((R // block_k, C), dtype=f32, device=x.device)
+    _L.check(_L.lib().tg_quantize_dual_km(_L.ptr(x), R, C, block_k, _L.ptr(q), _L.ptr(s), _L.ptr(qt),
+                                          _L.ptr(st), _L.stream_of(x)))
+    return q, s, qt, st
+
+
+def _quantize_dual_pair_km(x0: torch.Tensor, x1: torch.Tensor, block_k: int):
+    """quantize_fp8_dual_pair with K-block-major scales (tg_quantize_dual_pair_km)."""
+    outs, args = [], []
+    u8, f32 = torch.uint8, torch.float32
+    for x in (x0, x1):
+        R, C = x.shape
+        o = (torch.empty((R, C), dtype=u8, device=x.device),
+             torch.empty((C // block_k, R), dtype=f32, device=x.device),
+             torch.empty((C, R), dtype=u8, device=x.device),
+             torch.empty((R // block_k, C), dtype=f32, device=x.device))
+        outs.append(o)
+        args += [_L.ptr(x), R, C] + [_L.ptr(v) for v in o]
+    _L.check(_L.lib().tg_quantize_dual_pair_km(*args, block_k, _L.stream_of(x0)))
+    return outs
+
+
+def _scaled_matmul_km(a_q, a_s_km, b_q, b_s_km):
+    """scaled_matmul on K-block-major scales (tg_gemm_fp8_nt_km), bf16 out; the
+    same bits as scaled_matmul on the transposed scales."""
+    M, K = a_q.shape
+    N = b_q.shape[0]
+    c = torch.empty((M, N), dtype=torch.bfloat16, device=a_q.device)
+    _L.check(_L.lib().tg_gemm_fp8_nt_km(_L.ptr(a_q), _L.ptr(a_s_km), _L.ptr(b_q), _L.ptr(b_s_km), 1,
+                                        _L.ptr(c), _L.TG_DTYPE_BF16, M, N, K, DEFAULT_BLOCK_K,
+                                        _L.stream_of(a_q)))
+    return c
+
+
 def scaled_matmul(a_q, a_s, b_q, b_s, b_scale_bn: int = 1, out_dtype=torch.bfloat16):
     """The scaled GEMM of fp8.py:70-76 on already-quantized operands ("NT"):
     a_q (M, K), b_q (N, K) e4m3fn; a_s (M, K/128), b_s (N or ceil(N/128), K/128) f32.
@@ -315,15 +357,21 @@ def _fp8_forward_quantized_residuals(a, b, block_k, need_da, need_db):
     (a.T bytes, a.T scales) or None, (b bytes, b scales) or None): a.T along M
     for db = fwd(a.T, g), b along N for da = fwd(g, b.T) -- the operands
     _fp8_backward would quantize from a and b (fp8.py:66,68 on those inputs).
+    When both are kept, their scales are K-block-major and each tuple carries a
+    third element "km" (the layout tg_gemm_fp8_nt_km reads); the bytes and the
+    scale values are the same either way.
     """
     leading, K, N = _validate(a, b, block_k)
     a_2d = a.reshape(-1, K)
     if need_db and need_da:
-        # a along K + a.T along M, and b along N + b.T along K: one launch
-        (qa, sa, qat, sat), (qb, sb, qbt, sbt) = quantize_fp8_dual_pair(a_2d, b, block_k)
-        u8 = torch.uint8
-        out = scaled_matmul(qa.view(u8), sa, qbt.view(u8), sbt)     # fp8.py:70-78
-        return out.reshape(*leading, N), (qat, sat), (qb, sb)
+        # a along K + a.T along M, and b along N + b.T along K: one launch, the
+        # scales K-block-major (the residuals' scales too; the backward reads
+        # them with the same GEMM), so the returned residuals are tagged "km"
+        (qa, sa, qat, sat), (qb, sb, qbt, sbt) = _quantize_dual_pair_km(a_2d.contiguous(), b.contiguous(),
+                                                                         block_k)
+        out = _scaled_matmul_km(qa, sa, qbt, sbt)                   # fp8.py:70-78
+        e4 = torch.float8_e4m3fn
+        return out.reshape(*leading, N), (qat.view(e4), sat, "km"), (qb.view(e4), sb, "km")
     if need_db:
         qa, sa, qat, sat = quantize_fp8_dual(a_2d, block_k)    # a along K, a.T along M
         res_a = (qat, sat)
@@ -345,6 +393,19 @@ def _fp8_backward_quantized(block_k, res_a, res_b, g, a_shape, a_dtype, b_dtype)
     N = g.shape[-1]
     g_2d = g.reshape(-1, N)
     u8 = torch.uint8
+    km = res_a is not None and len(res_a) == 3
+    if km and g_2d.dtype == torch.bfloat16:
+        # K-block-major scales throughout: g along N and g.T along M from one read
+        qg, sg, qgt, sgt = _quantize_dual_km(g_2d.contiguous(), block_k)
+        (qat, sat, _), (qb, sb, _) = res_a, res_b
+        da = _scaled_matmul_km(qg, sg, qb.view(u8), sb).reshape(a_shape).to(a_dtype)
+        db = _scaled_matmul_km(qat.view(u8), sat, qgt, sgt).to(b_dtype)
+        return da, db
+    if km:
+        # a non-bf16 gradient: its scales come in the reference layout, so the
+        # residuals' scales are transposed back to it
+        res_a = (res_a[0], res_a[1].t().contiguous())
+        res_b = (res_b[0], res_b[1].t().contiguous())
     if g_2d.dtype == torch.bfloat16 and res_a is not None and res_b is not None:
         qg, sg, qgt, sgt = quantize_fp8_dual(g_2d, block_k)      # g along N and g.T along M
     else:
@@ -378,7 +439,8 @@ class _BlockScaledMatmul(torch.autograd.Function):
                                                                      need_db)
                 ctx.quantized = True
                 ctx.has_a, ctx.has_b = res_a is not None, res_b is not None
-                ctx.save_for_backward(*(res_a or ()), *(res_b or ()))
+                ctx.km = res_a is not None and len(res_a) == 3      # K-block-major residual scales
+                ctx.save_for_backward(*(res_a[:2] if res_a else ()), *(res_b[:2] if res_b else ()))
                 ctx.a_shape, ctx.a_dtype, ctx.b_dtype = a.shape, a.dtype, b.dtype
                 return out
         out, (ra, rb) = _fp8_forward_with_residuals(a, b, block_k)
@@ -392,8 +454,9 @@ class _BlockScaledMatmul(torch.autograd.Function):
                 raise RuntimeError("BACKWARD_MODE changed between forward and backward: this "
                                    "graph kept FP8 residuals for the 'fp8' backward")
             saved = list(ctx.saved_tensors)
-            res_a = (saved.pop(0), saved.pop(0)) if ctx.has_a else None
-            res_b = (saved.pop(0), saved.pop(0)) if ctx.has_b else None
+            tag = ("km",) if ctx.km else ()
+            res_a = (saved.pop(0), saved.pop(0), *tag) if ctx.has_a else None
+            res_b = (saved.pop(0), saved.pop(0), *tag) if ctx.has_b else None
             da, db = _fp8_backward_quantized(ctx.block_k, res_a, res_b, g, ctx.a_shape,
                                              ctx.a_dtype, ctx.b_dtype)
             return da, db, None
