@@ -286,10 +286,13 @@ struct W32Ctx {
   uint32_t row8;              // 8 rows of A / B in bytes (8 * K)
   int wave, nkb;
   // LDS byte addresses of this lane's fragment chunks [K half][chunk] and
-  // scales in stage 0 (lds_addr of the stage-0 object included)
-  uint32_t fa[2][2], fb[2][2];
-  uint32_t fsa;                  // A-row scale of m-tile 0
-  uint32_t fsb;                  // B-column scales (this lane's quad share) of n-tile 0
+  // scales (lds_addr of the object included): B in stage 0 (stage 1 is within
+  // the 16-bit DS offset of it); A and the scales per stage [S], since their
+  // stage-1 objects lie past 64 KiB and an address add per read would cost
+  // VALU issue slots
+  uint32_t fa[2][2][2], fb[2][2];
+  uint32_t fsa[2];               // A-row scale of m-tile 0
+  uint32_t fsb[2];               // B-column scales (this lane's quad share) of n-tile 0
 };
 
 // The carried promotion state: the MFMA result of the previous tile and the
@@ -311,7 +314,8 @@ __device__ __forceinline__ uint32_t lds_addr(const T* p) {
 // derives from objS itself, so the compiler's per-object alias scopes still
 // tell these reads apart from the copies landing in the other stage (a read
 // based on the stage-0 object would wait for every copy in flight), while
-// the address stays one register plus an immediate offset.
+// the address stays one register plus an immediate offset.  w32_at(o, o, a)
+// is address a of object o, as a pointer derived from o.
 template <typename T>
 __device__ __forceinline__ lds_cu8* w32_at(const T* obj0, const T* objS, uint32_t a0) {
   return (lds_cu8*)objS + (a0 - lds_addr(obj0));
@@ -321,8 +325,8 @@ __device__ __forceinline__ u32x4_t lds_ld16(lds_cu8* p) {
 }
 template <int S>
 __device__ __forceinline__ v8i w32_frag_a(const W32Ctx& c, int i, int h) {
-  return as_v8i(lds_ld16(w32_at(g256_za0, g256_a<S>(), c.fa[h][0]) + i * 4096),
-                lds_ld16(w32_at(g256_za0, g256_a<S>(), c.fa[h][1]) + i * 4096));
+  return as_v8i(lds_ld16(w32_at(g256_a<S>(), g256_a<S>(), c.fa[S][h][0]) + i * 4096),
+                lds_ld16(w32_at(g256_a<S>(), g256_a<S>(), c.fa[S][h][1]) + i * 4096));
 }
 template <int S>
 __device__ __forceinline__ v8i w32_frag_b(const W32Ctx& c, int j, int h) {
@@ -331,12 +335,12 @@ __device__ __forceinline__ v8i w32_frag_b(const W32Ctx& c, int j, int h) {
 }
 template <int S>
 __device__ __forceinline__ float4 w32_sb(const W32Ctx& c, int j) {
-  const u32x4_t v = lds_ld16(w32_at(g256_s0, g256_s<S>(), c.fsb) + j * 128);
+  const u32x4_t v = lds_ld16(w32_at(g256_s<S>(), g256_s<S>(), c.fsb[S]) + j * 128);
   return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
 }
 template <int S>
 __device__ __forceinline__ float w32_sa(const W32Ctx& c, int i) {
-  return __uint_as_float(*(const __attribute__((address_space(3))) uint32_t*)(w32_at(g256_s0, g256_s<S>(), c.fsa) + i * 128));
+  return __uint_as_float(*(const __attribute__((address_space(3))) uint32_t*)(w32_at(g256_s<S>(), g256_s<S>(), c.fsa[S]) + i * 128));
 }
 
 __device__ __forceinline__ void w32_issue_part(const W32Ctx& c, uint8_t* la, uint8_t* lb, float* ls,
@@ -626,16 +630,22 @@ __global__ __launch_bounds__(512, 1) void gemm_fp8_nt_256_kernel(
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const uint32_t pat = (uint32_t)cl * 128u + (uint32_t)(((4 * h + 2 * g + e) ^ g256_swz(cl)) * 16);
-      c.fa[h][e] = lds_addr(g256_za0) + (uint32_t)(wm * 64) * 128u + pat;
+      c.fa[0][h][e] = lds_addr(g256_za0) + (uint32_t)(wm * 64) * 128u + pat;
+      c.fa[1][h][e] = lds_addr(g256_za1) + (uint32_t)(wm * 64) * 128u + pat;
       c.fb[h][e] = lds_addr(g256_b0) + (uint32_t)(wn * 128) * 128u + pat;
     }
-  c.fsa = lds_addr(g256_s0) + (uint32_t)(wm * 64 + cl) * 4u;                             // A-row scale of row cl
-  c.fsb = lds_addr(g256_s0) + (uint32_t)(256 + wn * 128 + (g * 4 + (lane & 3)) * 4) * 4u;   // B-column scales
+  const uint32_t sa_ofs = (uint32_t)(wm * 64 + cl) * 4u;                                 // A-row scale of row cl
+  const uint32_t sb_ofs = (uint32_t)(256 + wn * 128 + (g * 4 + (lane & 3)) * 4) * 4u;       // B-column scales
+  c.fsa[0] = lds_addr(g256_s0) + sa_ofs;
+  c.fsa[1] = lds_addr(g256_s1) + sa_ofs;
+  c.fsb[0] = lds_addr(g256_s0) + sb_ofs;
+  c.fsb[1] = lds_addr(g256_s1) + sb_ofs;
   // opaque from here on: the compiler would otherwise cancel the stage-0 base
   // against w32_at's subtraction and re-add the (large) object address per read
-  asm volatile("" : "+v"(c.fa[0][0]), "+v"(c.fa[0][1]), "+v"(c.fa[1][0]), "+v"(c.fa[1][1]));
+  asm volatile("" : "+v"(c.fa[0][0][0]), "+v"(c.fa[0][0][1]), "+v"(c.fa[0][1][0]), "+v"(c.fa[0][1][1]));
+  asm volatile("" : "+v"(c.fa[1][0][0]), "+v"(c.fa[1][0][1]), "+v"(c.fa[1][1][0]), "+v"(c.fa[1][1][1]));
   asm volatile("" : "+v"(c.fb[0][0]), "+v"(c.fb[0][1]), "+v"(c.fb[1][0]), "+v"(c.fb[1][1]));
-  asm volatile("" : "+v"(c.fsa), "+v"(c.fsb));
+  asm volatile("" : "+v"(c.fsa[0]), "+v"(c.fsb[0]), "+v"(c.fsa[1]), "+v"(c.fsb[1]));
 
   v16f acc[2][4];
 #pragma unroll
