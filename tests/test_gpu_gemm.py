@@ -248,6 +248,25 @@ def test_fp8_backward(dev, M, N, K):
     assert same_scales(sat.cpu().numpy(), ops["a_cols"][1])
 
 
+def test_prequant_backward_ragged_same_bits(dev):
+    """block_scaled_matmul_prequant (left operand quantized by the caller, e.g.
+    by rms_norm_fp8) shares block_scaled_matmul's backward, ragged M and N
+    included: the same output and gradient bits."""
+    rng = np.random.default_rng(77)
+    a_u = ob.randn_bf16(rng, (200, 256))
+    b_u = ob.randn_bf16(rng, (256, 200), std=0.02)
+    g = to_dev(ob.randn_bf16(rng, (200, 200), std=1e-3), dev)
+    a1, b1 = to_dev(a_u, dev).requires_grad_(True), to_dev(b_u, dev).requires_grad_(True)
+    a2, b2 = to_dev(a_u, dev).requires_grad_(True), to_dev(b_u, dev).requires_grad_(True)
+    y1 = fp8.block_scaled_matmul(a1, b1)
+    aq, as_ = fp8.quantize_fp8(a2.detach())
+    y2 = fp8.block_scaled_matmul_prequant(a2, aq, as_, b2)
+    y1.backward(g)
+    y2.backward(g)
+    assert torch.equal(y1, y2)
+    assert torch.equal(a1.grad, a2.grad) and torch.equal(b1.grad, b2.grad)
+
+
 @pytest.mark.parametrize("lead,K,N", [((200,), 256, 200), ((256,), 384, 200), ((200,), 128, 384),
                                       ((3,), 128, 8), ((2, 100), 256, 128)])
 def test_fp8_backward_ragged(dev, lead, K, N):
