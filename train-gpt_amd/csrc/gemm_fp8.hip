@@ -822,22 +822,28 @@ template <int S> __device__ __forceinline__ uint8_t* gemv_stage() {
 }
 
 
-template <int MT, int BNS>
+// NS: stages in flight (three per workgroup, one workgroup per CU; or two, and
+// two workgroups per CU).  Workgroup b takes the balanced share of the 8-row
+// groups: groups [b G / grid, (b + 1) G / grid), at most kGemvGroups.
+template <int MT, int BNS, int NS>
 __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict__ XQ,
                                                        const float* __restrict__ XS,
                                                        const uint8_t* __restrict__ WQ,
                                                        const float* __restrict__ WS,
                                                        __bf16* __restrict__ out, int M, int N,
-                                                       int K, int R) {
+                                                       int K) {
   constexpr int NW = 8;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 15, fg = lane >> 4;
   const int nkb = K >> 7;
   const int nchunk = (nkb + 31) >> 5;
-  const int n0 = blockIdx.x * R;
-  const int rows = min(R, N - n0);
-  const int ngroups = (rows + 7) >> 3;
+  const int64_t gtot = (N + 7) >> 3;
+  const int g_lo = (int)(((int64_t)blockIdx.x * gtot) / gridDim.x);
+  const int g_hi = (int)(((int64_t)(blockIdx.x + 1) * gtot) / gridDim.x);
+  const int n0 = 8 * g_lo;
+  const int rows = min(8 * g_hi, N) - n0;
+  const int ngroups = g_hi - g_lo;
 
   const uint32_t wbytes = (uint32_t)rows * (uint32_t)K;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(WQ + (int64_t)n0 * K, wbytes);
@@ -849,14 +855,16 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
   const uint32_t xsbytes = (uint32_t)M * (uint32_t)nkb * 4u;
   const __amdgpu_buffer_rsrc_t rxs = make_rsrc(XS, xsbytes);
 
-  u32x4_t wr[3][4];               // this wave's row of three stages in flight (4 x 1 KiB)
-  float wsr[3];                   // its 32 scales (lanes 0..31; lanes 32..63 read zero)
+  u32x4_t wr[NS][4];              // this wave's row of the NS stages in flight (4 x 1 KiB)
+  float wsr[NS];                  // its 32 scales (lanes 0..31; lanes 32..63 read zero)
   u32x4_t xr[4][MT][2];           // x fragments of blocks 4w .. 4w+3 of the chunk
   float sxr[4][MT];
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
-  v4f acc[kGemvGroups][MT];
+  // acc[P]: the pair of 8-row groups 2P (MFMA rows 0..7, lanes fg < 2) and
+  // 2P + 1 (rows 8..15, lanes fg >= 2)
+  v4f acc[kGemvGroups / 2][MT];
 #pragma unroll
-  for (int g = 0; g < kGemvGroups; ++g)
+  for (int g = 0; g < kGemvGroups / 2; ++g)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[g][mt] = zero;
 
@@ -878,8 +886,13 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
     wsr[SL] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, soff, 0, 0));
   };
 
-  // stage (c, G): registers -> LDS buffer SL = G % 3, start the loads of stage
-  // G + 3 into the same registers, barrier, then blocks 4w .. 4w+3 of the 8 rows
+  // stage (c, G): registers -> LDS buffer SL = G % NS, start the loads of stage
+  // G + NS into the same registers, barrier; then, on odd G, blocks 4w .. 4w+3
+  // of the 16 rows of stages G - 1 (MFMA rows 0..7) and G (rows 8..15), both
+  // still in LDS (stage G - 1's buffer is rewritten only after the next
+  // barrier); on the last stage when it is even, its 8 rows alone (rows 8..15
+  // repeat them and are never stored).  One MFMA per pair of stages instead of
+  // one per stage with half its rows repeated.
   auto stage = [&](auto slot, auto grp, int c) {
     constexpr int SL = decltype(slot)::value;
     constexpr int G = decltype(grp)::value;
@@ -889,24 +902,29 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
     for (int p = 0; p < 4; ++p)
       *reinterpret_cast<u32x4_t*>(buf + wave * kGemvPitch + p * 1024 + lane * 16) = wr[SL][p];
     ssw[wave * 64 + lane] = wsr[SL];      // every lane stores: no load sunk into a branch
-    load_w(slot, c, G + 3);
+    load_w(slot, c, G + NS);
     __syncthreads();
+    if (G % 2 == 0 && ngroups != G + 1) return;     // paired with stage G + 1
+    constexpr int SLP = (G + NS - 1) % NS;           // stage G - 1's buffer (odd G)
+    uint8_t* bprev = gemv_stage<SLP>();
+    const uint8_t* ba = G % 2 == 1 && fr < 8 ? bprev : buf;      // this lane's A-fragment row
+    const float* bs = reinterpret_cast<const float*>((G % 2 == 1 && fg < 2 ? bprev : buf) + 8 * kGemvPitch);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int kb = c * 32 + 4 * wave + i;
       if (kb < nkb) {
-        const uint8_t* pa = buf + (fr & 7) * kGemvPitch + (4 * wave + i) * 128 + fg * 16;
+        const uint8_t* pa = ba + (fr & 7) * kGemvPitch + (4 * wave + i) * 128 + fg * 16;
         const v8i wa = as_v8i(*reinterpret_cast<const uint4*>(pa),
                               *reinterpret_cast<const uint4*>(pa + 64));
         float sw[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sw[r] = ssw[((4 * fg + r) & 7) * 64 + 4 * wave + i];
+        for (int r = 0; r < 4; ++r) sw[r] = bs[((4 * fg + r) & 7) * 64 + 4 * wave + i];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const v4f pr = mfma_f8_16x16x128(wa, as_v8i(xr[i][mt][0], xr[i][mt][1]), zero);
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            acc[G][mt][r] = __builtin_fmaf(pr[r], sw[r] * sxr[i][mt], acc[G][mt][r]);
+            acc[G / 2][mt][r] = __builtin_fmaf(pr[r], sw[r] * sxr[i][mt], acc[G / 2][mt][r]);
         }
       }
     }
@@ -929,50 +947,50 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
     }
     load_w(IntC<0>{}, c, 0);
     load_w(IntC<1>{}, c, 1);
-    load_w(IntC<2>{}, c, 2);
+    if constexpr (NS > 2) load_w(IntC<2 % NS>{}, c, 2);
     // every path to stage G runs stages 0 .. G-1 first (early exits only), so
     // the compiler's count of the loads in flight at stage G is exact
     do {
-      stage(IntC<0>{}, IntC<0>{}, c);
+      stage(IntC<0 % NS>{}, IntC<0>{}, c);
       if (ngroups <= 1) break;
-      stage(IntC<1>{}, IntC<1>{}, c);
+      stage(IntC<1 % NS>{}, IntC<1>{}, c);
       if (ngroups <= 2) break;
-      stage(IntC<2>{}, IntC<2>{}, c);
+      stage(IntC<2 % NS>{}, IntC<2>{}, c);
       if (ngroups <= 3) break;
-      stage(IntC<0>{}, IntC<3>{}, c);
+      stage(IntC<3 % NS>{}, IntC<3>{}, c);
       if (ngroups <= 4) break;
-      stage(IntC<1>{}, IntC<4>{}, c);
+      stage(IntC<4 % NS>{}, IntC<4>{}, c);
       if (ngroups <= 5) break;
-      stage(IntC<2>{}, IntC<5>{}, c);
+      stage(IntC<5 % NS>{}, IntC<5>{}, c);
       if (ngroups <= 6) break;
-      stage(IntC<0>{}, IntC<6>{}, c);
+      stage(IntC<6 % NS>{}, IntC<6>{}, c);
       if (ngroups <= 7) break;
-      stage(IntC<1>{}, IntC<7>{}, c);
+      stage(IntC<7 % NS>{}, IntC<7>{}, c);
     } while (false);
     __syncthreads();                      // the next chunk rewrites the stage buffers
   }
 
   // wave-ordered sum of the partial tiles through LDS (stage memory reused), one
-  // pass per x-row tile: lanes fg < 2 hold rows 8g + 4fg .. +3, so each wave
-  // stores those 32 lanes of its 8 group tiles (32 KiB for the workgroup), and
-  // wave g then adds group g's partials of the 8 waves in wave order
-  v4f* red = reinterpret_cast<v4f*>(gemv_lds0);   // [NW][8][32]
-  const bool vec = (N & 3) == 0 && (R & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0;
+  // pass per x-row tile: lane (fr, fg) of pair tile P holds rows
+  // 8(2P + fg / 2) + 4(fg % 2) .. +3, so each wave stores its 4 pair tiles (32
+  // KiB for the workgroup), and wave g then adds group g's partials of the 8
+  // waves in wave order
+  v4f* red = reinterpret_cast<v4f*>(gemv_lds0);   // [NW][4][64]
+  const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     if (mt > 0) __syncthreads();          // the previous pass has read red
-    if (fg < 2) {
 #pragma unroll
-      for (int g = 0; g < kGemvGroups; ++g) red[(wave * kGemvGroups + g) * 32 + lane] = acc[g][mt];
-    }
+    for (int pp = 0; pp < kGemvGroups / 2; ++pp) red[(wave * (kGemvGroups / 2) + pp) * 64 + lane] = acc[pp][mt];
     __syncthreads();
     const int g = wave;
     const int m = mt * 16 + fr, lr = 8 * g + 4 * fg;
+    const int src = (g & 1) * 32 + lane;  // the lane of pair tile g / 2 holding these rows
     if (fg < 2 && g < ngroups && m < M && lr < rows) {
-      v4f s = red[g * 32 + lane];
+      v4f s = red[(g >> 1) * 64 + src];
 #pragma unroll
       for (int w2 = 1; w2 < NW; ++w2) {
-        const v4f o = red[(w2 * kGemvGroups + g) * 32 + lane];
+        const v4f o = red[(w2 * (kGemvGroups / 2) + (g >> 1)) * 64 + src];
         s[0] += o[0]; s[1] += o[1]; s[2] += o[2]; s[3] += o[3];
       }
       __bf16* o = out + (int64_t)m * N + n0 + lr;
@@ -1459,20 +1477,28 @@ extern "C" int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, cons
 
 
 // Rows per workgroup: equal rows per CU, a multiple of 8, at most 64.
+// Stages in flight per workgroup of the MFMA GEMV (see gemv_fp8_kernel).
+constexpr int kGemvNS = 3;
+
 template <int MT>
 static int launch_gemv(const uint8_t* x_q, const float* x_s, const uint8_t* w_q, const float* w_s,
                        int bn, __bf16* out, int M, int N, int K, hipStream_t st) {
-  const int cus = device_cus();
-  int R = (int)(((int64_t)N + cus - 1) / cus);
-  R = (R + 7) & ~7;
-  if (R > 8 * kGemvGroups) R = 8 * kGemvGroups;
-  const dim3 grid((unsigned)((N + R - 1) / R));
+  constexpr int NS = kGemvNS;
+  // as many workgroups as fit at once (one per CU with three stages in flight,
+  // two with two), each with a balanced share of the 8-row groups (at most
+  // kGemvGroups: more workgroups than fit when N is large)
+  const int64_t groups = ((int64_t)N + 7) / 8;
+  int64_t nwg = (int64_t)device_cus() * (NS == 2 ? 2 : 1);
+  if (nwg > groups) nwg = groups;
+  const int64_t need = (groups + kGemvGroups - 1) / kGemvGroups;
+  if (nwg < need) nwg = need;
+  const dim3 grid((unsigned)nwg);
   if (bn == 1)
-    hipLaunchKernelGGL((gemv_fp8_kernel<MT, 1>), grid, dim3(512), 0, st, x_q, x_s, w_q, w_s, out, M,
-                       N, K, R);
+    hipLaunchKernelGGL((gemv_fp8_kernel<MT, 1, NS>), grid, dim3(512), 0, st, x_q, x_s, w_q, w_s, out, M,
+                       N, K);
   else
-    hipLaunchKernelGGL((gemv_fp8_kernel<MT, 128>), grid, dim3(512), 0, st, x_q, x_s, w_q, w_s, out,
-                       M, N, K, R);
+    hipLaunchKernelGGL((gemv_fp8_kernel<MT, 128, NS>), grid, dim3(512), 0, st, x_q, x_s, w_q, w_s, out,
+                       M, N, K);
   return check_launch("gemv_fp8");
 }
 
