@@ -154,6 +154,23 @@ def test_gemm_km_same_bits(dev, M, N, K, bn):
                            want.view(torch.int32 if out == torch.float32 else torch.int16))
 
 
+@pytest.mark.parametrize("M,K,N", [(200, 256, 200), (64, 384, 100), (300, 128, 1000), (2048, 768, 3072),
+                                   (8192, 2048, 8192)])
+def test_composite_forward_same_bits_as_reference_layout(dev, M, K, N):
+    """tg_block_scaled_matmul (K-block-major scales in its workspace: the row
+    quantizer, the column quantizer's aligned, ragged and unaligned paths, and
+    both GEMM tile paths) = quantize_fp8 + scaled_matmul in the reference's
+    scale layout, bit for bit."""
+    rng = np.random.default_rng(M + K + N)
+    a = to_dev(ob.randn_bf16(rng, (M, K)), dev)
+    b = to_dev(ob.randn_bf16(rng, (K, N), std=0.02), dev)
+    y = fp8.block_scaled_matmul(a, b)
+    qa, sa = fp8.quantize_fp8(a)
+    qb, sb = fp8.quantize_fp8(b, transpose=True)
+    want = fp8.scaled_matmul(qa.view(torch.uint8), sa, qb.view(torch.uint8), sb)
+    assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+
+
 def test_block_scaled_matmul_c1(dev):
     """Config 1: x [2048, 768] ~N(0,1), W [768, 3072] ~N(0, 0.02^2), seed 0."""
     rng = np.random.default_rng(0)
