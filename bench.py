@@ -19,6 +19,11 @@ roofline     = the GEMM kernel: 2*M*N*K FLOP per launch / its mean launch time
                the stream leaves it idle for ~4.5 us, so the region that
                gives `value` has events only at its two ends) vs MI355X
                dense FP8 MFMA peak 5.0 PFLOP/s
+sustained_clock = after the timed region, the step and then its dX GEMM alone
+               back to back for 3 s each, with amdsmi polled for the engine
+               clock (median) and socket energy (average power) against the cap;
+               the GEMM's rate is also given against the FP8 peak scaled from
+               its 2400 MHz to the clock it sustains (not run under rocprofv3)
 norm_quant   = config 2 fused RMSNorm -> FP8 quantize, bytes per launch
                84,414,464 (x read + y/q/scales written + gamma) / mean launch
                time vs 8 TB/s HBM; input/output sets rotate over > 256 MB so
@@ -84,6 +89,110 @@ def under_counter_collection() -> bool:
     pass had covered besides the C4 block step was the decode workload's
     captured-graph replay, so the decode workload is left out in that mode."""
     return os.environ.get("ROCPROF_COUNTER_COLLECTION", "") == "1"
+
+
+def under_profiler() -> bool:
+    """True inside any rocprofv3 run (its launcher always exports ROCPROF_OUTPUT_PATH)."""
+    return "ROCPROF_OUTPUT_PATH" in os.environ
+
+
+FP8_PEAK_CLOCK_MHZ = 2400.0    # the engine clock the 5.0 PFLOP/s dense FP8 peak is quoted at
+POWER_SECONDS = 3.0            # wall time of each sustained-clock phase
+
+
+class PowerSampler:
+    """Sustained engine clock and socket power while a workload runs back to
+    back.  amdsmi (read-only queries) serves the SMU's metrics, which it
+    refreshes about once a second: a host thread polls every 10 ms and keeps
+    each refresh (a new energy-counter timestamp) with its engine clock and
+    accumulated socket energy.  Refreshes that land inside the phase give the
+    clock (median) and, between the first and the last of them, the average
+    power (energy delta / SMU time delta).  The amdsmi device is the one whose
+    PCI bus matches torch's cuda:0."""
+
+    def __init__(self):
+        self.error = None
+        try:
+            import amdsmi
+            import torch
+            amdsmi.amdsmi_init()
+            props = torch.cuda.get_device_properties(0)
+            handles = amdsmi.amdsmi_get_processor_handles()
+            mine = [h for h in handles
+                    if int(amdsmi.amdsmi_get_gpu_device_bdf(h).split(":")[1], 16) == props.pci_bus_id]
+            if len(mine) != 1:
+                raise RuntimeError(f"{len(mine)} amdsmi devices on PCI bus {props.pci_bus_id}")
+            self.amdsmi, self.h = amdsmi, mine[0]
+            self.cap_w = amdsmi.amdsmi_get_power_cap_info(self.h)["power_cap"] / 1e6
+        except Exception as e:          # no amdsmi, or no access to the metrics table
+            self.error = f"{type(e).__name__}: {e}"
+
+    def run(self, fn, seconds=POWER_SECONDS, sync_every=10):
+        """Calls fn() repeatedly for `seconds` (at least 2.5 s, so that two
+        metrics refreshes fall inside); returns the median clock, the average
+        socket power and the mean wall time per call."""
+        if self.error:
+            return {"unavailable": self.error}
+        import statistics
+        import threading
+        import torch
+        refreshes, stop = [], threading.Event()
+
+        def poll():
+            last = None
+            while not stop.is_set():
+                try:
+                    e = self.amdsmi.amdsmi_get_energy_count(self.h)
+                    if e["timestamp"] != last:
+                        m = self.amdsmi.amdsmi_get_gpu_metrics_info(self.h)
+                        refreshes.append((time.perf_counter(), m["current_gfxclk"],
+                                          e["energy_accumulator"] * e["counter_resolution"] * 1e-6,
+                                          e["timestamp"] * 1e-9))
+                        last = e["timestamp"]
+                except Exception:
+                    pass
+                time.sleep(0.01)
+
+        th = threading.Thread(target=poll, daemon=True)
+        torch.cuda.synchronize()
+        th.start()
+        time.sleep(0.05)                # the thread has seen the current refresh
+        t0, calls = time.perf_counter(), 0
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(sync_every):
+                fn()
+            torch.cuda.synchronize()
+            calls += sync_every
+        wall = time.perf_counter() - t0
+        stop.set()
+        th.join()
+        # refreshes seen after the phase began and before it ended (a refresh
+        # is seen within ~10 ms of happening)
+        inside = [r for r in refreshes if t0 + 0.02 <= r[0] <= t0 + wall and isinstance(r[1], int)]
+        if len(inside) < 2:
+            return {"unavailable": f"{len(inside)} metrics refreshes inside the phase"}
+        a, b = inside[0], inside[-1]
+        return {"gfxclk_mhz": statistics.median(r[1] for r in inside),
+                "socket_power_w": round((b[2] - a[2]) / (b[3] - a[3]), 1),
+                "power_cap_w": round(self.cap_w, 1), "refreshes": len(inside),
+                "seconds": round(wall, 3), "us_per_call": round(wall / calls * 1e6, 2)}
+
+
+def sustained_clock(step, seconds=POWER_SECONDS):
+    """The C3 step and its dX GEMM alone, each back to back for `seconds`: the
+    engine clock and socket power they sustain, and the GEMM's rate against the
+    dense FP8 peak scaled to that clock."""
+    ps = PowerSampler()
+    out = {"step": ps.run(step.run, seconds)}
+    gemm = ps.run(lambda: step._gemm(step.qdy, step.sdy, step.qw, step.sw, step.dx, M3, K3, N3, None),
+                  seconds, sync_every=20)
+    if "us_per_call" in gemm:
+        tflops = GEMM_FLOP / (gemm["us_per_call"] * 1e-6) / 1e12
+        peak = FP8_PEAK_TFLOPS * gemm["gfxclk_mhz"] / FP8_PEAK_CLOCK_MHZ
+        gemm.update({"tflops": round(tflops, 1), "peak_at_clock_tflops": round(peak, 1),
+                     "frac_at_clock": round(tflops / peak, 4)})
+    out["gemm_dx"] = gemm
+    return out
 
 
 def measured_traffic():
@@ -845,6 +954,8 @@ def main():
     gemm_tflops = GEMM_FLOP / (gemm_ms * 1e-3) / 1e12
     value = STEP_FLOP / (ms_step * 1e-3) / 1e12
     accuracy = step_accuracy(step)
+    power = (sustained_clock(step) if not under_profiler() else
+             {"skipped": "not run under rocprofv3 (it would add ~2 s of launches to the trace)"})
     if args.only == "step":
         norm = norm_bwd = gemv = bwd_bf16 = block_step = xent = dec = c1 = None
     else:
@@ -872,6 +983,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic().get("gemm_fp8_nt_256")},
         "accuracy": accuracy,
+        "sustained_clock": power,
         "c1": c1,
         "norm_quant": norm,
         "norm_bwd": norm_bwd,
@@ -883,7 +995,7 @@ def main():
     }
     if args.only == "step":                      # the headline step alone (no secondary workloads)
         out = {k: out[k] for k in ("metric", "value", "unit", "steps", "warmup", "clock_settle", "ms_per_step",
-                                   "gemm_us_per_launch", "roofline", "accuracy")}
+                                   "gemm_us_per_launch", "roofline", "accuracy", "sustained_clock")}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(step.host)
     print(json.dumps(out))

@@ -60,3 +60,17 @@ def test_default_warmup_covers_the_clock_ramp():
     # the settle phase precedes the warm-up steps and is reported in the JSON line
     assert main.index("CLOCK_SETTLE_MS") < main.index("range(args.warmup)")
     assert '"clock_settle"' in main
+
+
+def test_power_sampler_degrades_to_a_reason_without_a_device():
+    """Without a GPU (or without amdsmi access) the sustained-clock phase
+    reports why it is unavailable instead of failing the bench line."""
+    r = bench.PowerSampler().run(lambda: None, 0.01)
+    assert set(r) == {"unavailable"} and r["unavailable"]
+
+
+def test_power_phase_is_skipped_under_rocprofv3(monkeypatch):
+    monkeypatch.delenv("ROCPROF_OUTPUT_PATH", raising=False)
+    assert not bench.under_profiler()
+    monkeypatch.setenv("ROCPROF_OUTPUT_PATH", "/tmp")
+    assert bench.under_profiler()
