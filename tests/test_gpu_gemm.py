@@ -57,7 +57,9 @@ def test_layout_known_answer(dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 8, 128), (17, 40, 256), (130, 200, 384), (256, 256, 512),
-                                   (300, 136, 1024), (2048, 3072, 768),
+                                   # below 128 large tiles: 128 x 96 tiles, and 128 x 128 ones
+                                   # where they load the busiest CU less (2048^2 on 256 CUs)
+                                   (300, 136, 1024), (2048, 3072, 768), (2048, 2048, 256),
                                    # >= 128 tiles of 256 x 256: the large-tile kernel, with ragged
                                    # M / N edges and odd / even numbers of K blocks
                                    (2100, 4000, 384), (4096, 4096, 256), (3000, 2900, 640),

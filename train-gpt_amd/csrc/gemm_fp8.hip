@@ -772,6 +772,21 @@ static int launch_gemm_fp8_layout(const uint8_t* a_q, const float* a_s, const ui
     return f32 ? launch_gemm_256<128, true, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st)
                : launch_gemm_256<128, false, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st);
   }
+  // 128 x 128 or 128 x 96 tiles, whichever leaves the busiest CU the fewer
+  // outputs (tiles per CU, rounded up, times the tile's columns): C1's 2048 x
+  // 3072 is 384 tiles of 128 (two on half the CUs) or 512 of 96 (two on
+  // every CU), 10% faster
+  const int64_t cus = device_cus() > 0 ? device_cus() : 1;
+  const int64_t tm = (m + 127) / 128;
+  const int64_t load128 = (tm * ((n + 127) / 128) + cus - 1) / cus * 128;
+  const int64_t load96 = (tm * ((n + 95) / 96) + cus - 1) / cus * 96;
+  if (load96 < load128) {
+    if (b_scale_bn == 1)
+      return f32 ? launch_gemm_cfg<4, 3, 1, true, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st)
+                 : launch_gemm_cfg<4, 3, 1, false, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st);
+    return f32 ? launch_gemm_cfg<4, 3, 128, true, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st)
+               : launch_gemm_cfg<4, 3, 128, false, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st);
+  }
   if (b_scale_bn == 1)
     return f32 ? launch_gemm_cfg<4, 4, 1, true, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st)
                : launch_gemm_cfg<4, 4, 1, false, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st);
