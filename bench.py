@@ -165,7 +165,8 @@ class PowerSampler:
             calls += sync_every
         wall = time.perf_counter() - t0
         stop.set()
-        th.join()
+        th.join(timeout=2.0)            # a metrics query that never returns must not hold the bench line
+        refreshes = list(refreshes)
         # refreshes seen after the phase began and before it ended (a refresh
         # is seen within ~10 ms of happening)
         inside = [r for r in refreshes if t0 + 0.02 <= r[0] <= t0 + wall and isinstance(r[1], int)]
