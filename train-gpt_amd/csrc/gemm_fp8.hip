@@ -1377,8 +1377,14 @@ static int block_scaled_matmul_on(const void* a, const void* b, void* out, int64
   uint8_t* qb = p;                 p += align256((size_t)N * K);
   float* sb = reinterpret_cast<float*>(p);
   // the composite's own workspace: scales K-block-major (the GEMM's cheaper scale reads)
-  TG_TRY(launch_quant_rows(a, TG_DTYPE_BF16, M, K, qa, sa, st, true));     // fp8.py:66
-  TG_TRY(launch_quant_cols(b, K, N, qb, sb, st, true));                     // fp8.py:68
+  if (M % 128 == 0 && N % 128 == 0) {
+    // both quantizations in one launch (fp8.py:66, 68): one kernel's fixed
+    // cost instead of two's, which is most of the time at small shapes
+    TG_TRY(launch_quant_rows_cols(a, M, K, qa, sa, b, N, qb, sb, st, true));
+  } else {
+    TG_TRY(launch_quant_rows(a, TG_DTYPE_BF16, M, K, qa, sa, st, true));     // fp8.py:66
+    TG_TRY(launch_quant_cols(b, K, N, qb, sb, st, true));                     // fp8.py:68
+  }
   return launch_gemm_fp8(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, K, st, true);   // fp8.py:70-78
 }
 

@@ -231,6 +231,7 @@ struct DualJob {
   float* st;
   int gx, gy, xcd_blocks;
   int skm;   // scales K-block-major: s[kb * rows + row], st[kb * cols + col]
+  int part;  // 0: rows and x.T; 1: rows only; 2: x.T only (with ROWS)
 };
 struct DualJobs {
   DualJob job[2];
@@ -267,6 +268,8 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
   const int ch = tid & 15, rr = tid >> 4;
   const int64_t cchunks = cols >> 3;
   const bool ch_ok = !GUARD || (c0 >> 3) + ch < cchunks;
+  // the job's parts (workgroup-uniform)
+  const bool do_rows = ROWS && J.part != 2, do_cols = J.part != 1;
   uint4 v[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u)
@@ -274,7 +277,7 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int row = rr + 16 * u;
-    if (ROWS) {
+    if (do_rows) {
       float f[8];
       f[0] = bf16lo(v[u].x); f[1] = bf16hi(v[u].x); f[2] = bf16lo(v[u].y); f[3] = bf16hi(v[u].y);
       f[4] = bf16lo(v[u].z); f[5] = bf16hi(v[u].z); f[6] = bf16lo(v[u].w); f[7] = bf16hi(v[u].w);
@@ -285,8 +288,9 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
         else s[(r0 + row) * (cols >> 7) + tx] = sc;
       }
     }
-    *reinterpret_cast<uint4*>(&tile[row * 68 + ch * 4]) = v[u];
+    if (do_cols) *reinterpret_cast<uint4*>(&tile[row * 68 + ch * 4]) = v[u];
   }
+  if (!do_cols) return;
   __syncthreads();
 
   // columns: quad (tid >> 2) owns the column pair 2c, 2c + 1 (one 32-bit LDS
@@ -372,6 +376,7 @@ static int dual_job(DualJob& j, const char* who, const void* x, int64_t rows, in
   j.gy = (int)gy;
   j.xcd_blocks = xcd_ok && gx % 32 == 0 && gy % 16 == 0 && (gx * gy / 8) % 512 == 0;
   j.skm = skm ? 1 : 0;
+  j.part = 0;
   return TG_OK;
 }
 
@@ -428,6 +433,26 @@ int launch_quant_dual_pair(const void* x0, int64_t rows0, int64_t cols0, uint8_t
   if (total > kDualMaxTiles) return einval("quantize_dual_pair: too many 128 x 128 tiles");
   hipLaunchKernelGGL((quant_dual_kernel<true, false>), dim3((unsigned)total), dim3(256), 0, st, jobs);
   return check_launch("quant_dual_pair");
+}
+
+// The forward's two quantizations in one launch: a (M, K) along its rows
+// (fp8.py:66) and b (K, N) as b.T along K (fp8.py:68), the bytes and scales of
+// launch_quant_rows and launch_quant_cols.  Every extent a multiple of 128.
+int launch_quant_rows_cols(const void* a, int64_t M, int64_t K, uint8_t* qa, float* sa, const void* b,
+                           int64_t N, uint8_t* qbt, float* sbt, hipStream_t st, bool skm) {
+  if (M % 128 || K % 128 || N % 128) return einval("quantize_rows_cols: M, K and N must be multiples of 128");
+  if (M == 0 || K == 0 || N == 0) return TG_OK;
+  DualJobs jobs{};
+  TG_TRY(dual_job(jobs.job[0], "quantize_rows_cols", a, M, K, qa, sa, nullptr, nullptr, true, skm));
+  jobs.job[0].part = 1;
+  jobs.nblk0 = jobs.job[0].gx * jobs.job[0].gy;
+  TG_TRY(dual_job(jobs.job[1], "quantize_rows_cols", b, K, N, nullptr, nullptr, qbt, sbt, jobs.nblk0 % 8 == 0,
+                  skm));
+  jobs.job[1].part = 2;
+  const int64_t total = (int64_t)jobs.nblk0 + (int64_t)jobs.job[1].gx * jobs.job[1].gy;
+  if (total > kDualMaxTiles) return einval("quantize_rows_cols: too many 128 x 128 tiles");
+  hipLaunchKernelGGL((quant_dual_kernel<true, false>), dim3((unsigned)total), dim3(256), 0, st, jobs);
+  return check_launch("quant_rows_cols");
 }
 
 // ---------------------------------------------------------------------------

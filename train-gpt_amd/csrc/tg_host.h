@@ -63,6 +63,8 @@ int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, f
                       hipStream_t st, bool skm = false);
 int launch_quant_dual(const void* x, int64_t rows, int64_t cols, uint8_t* q, float* s, uint8_t* q_t,
                       float* s_t, hipStream_t st, bool skm = false);
+int launch_quant_rows_cols(const void* a, int64_t M, int64_t K, uint8_t* qa, float* sa, const void* b,
+                           int64_t N, uint8_t* qbt, float* sbt, hipStream_t st, bool skm);
 int launch_quant_dual_pair(const void* x0, int64_t rows0, int64_t cols0, uint8_t* q0, float* s0,
                            uint8_t* qt0, float* st0, const void* x1, int64_t rows1, int64_t cols1,
                            uint8_t* q1, float* s1, uint8_t* qt1, float* st1, hipStream_t st, bool skm = false);
