@@ -248,10 +248,12 @@ int tg_gemv_fp8_rowdot(const uint8_t* x_q, const float* x_s, const uint8_t* w_q,
  * tg_rms_norm_fp8_gemv: h = the FP8 rows (bytes and 1x128 scales) that
  * tg_rms_norm_fp8 (delta == NULL) or tg_add_rms_norm_fp8 (delta != NULL) would
  * produce from x (M, K) bf16, gamma (K,) bf16 and eps, bit for bit; then
- * out (M, N) = h @ W^T as tg_gemv_fp8_rowdot.  With delta, the residual sum
- * bf16(x + delta) is also stored to xout (M, K), which must not overlap x or
- * delta.  M <= 2, K <= 4096, K % 128 == 0; x, delta, gamma, xout 16-byte
- * aligned.  Replaces the norm launch + the GEMV launch of a decode step.
+ * out (M, N) = h @ W^T, as tg_gemv_fp8_rowdot for M <= 2 (K <= 4096) and as
+ * tg_gemv_fp8 (the MFMA GEMV, the same bits) for 3 <= M <= 16 (K <= 2560).
+ * With delta, the residual sum bf16(x + delta) is also stored to xout (M, K),
+ * which must not overlap x or delta.  K % 128 == 0; x, delta, gamma, xout
+ * 16-byte aligned.  Replaces the norm launch + the GEMV launch of a decode
+ * step.
  *
  * tg_relu2_fp8_gemv: h = the FP8 rows tg_quantize_rows_relu2 would produce
  * from u (M, K) bf16 (model.py:72's relu^2), then out = h @ W^T as

@@ -233,16 +233,17 @@ def test_graph_step_matches_eager(dev, B):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B", [1, 2])
+@pytest.mark.parametrize("B", [1, 2, 8, 16])
 def test_fused_step_same_bits(dev, B):
-    """A fused decode step (each norm / relu^2 quantization inside the GEMV that
-    consumes it) gives the same logits, bit for bit, as the step of separate
-    kernels on the same VALU GEMV, eager and replayed from a graph."""
+    """A fused decode step (each norm, and for 1-2 rows the relu^2 quantization,
+    inside the GEMV that consumes it) gives the same logits, bit for bit, as
+    the step of separate kernels on the same GEMV (the VALU one for 1-2 rows,
+    the MFMA one for 8 and 16), eager and replayed from a graph."""
     cfg = TINY
     params = decode.init_params(cfg, dev, seed=16)
-    fused = decode.FP8Decoder(params, cfg, max_batch=B)
+    fused = decode.FP8Decoder(params, cfg, max_batch=B, fused=True)
     plain = decode.FP8Decoder(params, cfg, max_batch=B, fused=False)
-    graph = decode.FP8Decoder(params, cfg, max_batch=B)
+    graph = decode.FP8Decoder(params, cfg, max_batch=B, fused=True)
     assert fused.fused and not plain.fused
     graph.capture_step(B)
     g = torch.Generator(device=dev).manual_seed(17)

@@ -179,7 +179,11 @@ def _bf16_rows(rng, M, K, outliers=True):
 
 
 NORM_FUSED = [(1, 1, 128), (2, 77, 640), (1, 6912, 2304), (2, 2304, 2304), (1, 3000, 4096), (2, 129, 1152),
-              (1, 50257, 2304)]
+              (1, 50257, 2304),
+              # 3-16 rows: the MFMA GEMV with the norm prologue (rows w and w + 8 per wave,
+              # K up to 2560, partial 8-row groups, one scale block, a grid past one wave)
+              (3, 77, 640), (8, 6912, 2304), (16, 2304, 2304), (5, 129, 1152), (16, 1000, 2560),
+              (9, 300, 128), (8, 50257, 2304), (12, 8, 256)]
 
 
 @pytest.mark.parametrize("layout", ["128x1", "128x128"])
@@ -204,6 +208,18 @@ def test_rms_norm_fp8_gemv_same_bits(dev, M, N, K, add, layout):
     ref = qw.matmul_prequant(q, s)          # tg_gemv_fp8_rowdot on the stand-alone bytes
     assert got.shape == (M, N) and got.dtype == torch.bfloat16
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+def test_rms_norm_fp8_gemv_limits(dev):
+    """3-16 rows take K <= 2560 (the FP8 rows and the norm's registers beside
+    the MFMA GEMV's weight stages); more than 16 rows is an error."""
+    rng = np.random.default_rng(5)
+    for M, K, msg in ((4, 2688, "K=2688 too large"), (17, 256, "M must be <= 16")):
+        x = to_dev(_bf16_rows(rng, M, K), dev)
+        gamma = to_dev(ob.randn_bf16(rng, (K,), std=0.1, mean=1.0), dev)
+        qw = fp8.QuantizedWeight.from_weight(to_dev(ob.randn_bf16(rng, (K, 64), std=0.02), dev), "128x128")
+        with pytest.raises(ValueError, match=msg):
+            qw.matmul_rms_norm(x, gamma, 1e-6)
 
 
 def test_rms_norm_fp8_gemv_vs_oracle(dev):
@@ -252,9 +268,8 @@ def test_fused_gemv_errors(dev):
     x3 = torch.zeros((3, 256), dtype=torch.bfloat16, device=dev)
     g2 = torch.ones(256, dtype=torch.bfloat16, device=dev)
     with pytest.raises(ValueError, match="M must be <= 2"):
-        qw2.matmul_rms_norm(x3, g2, 1e-6)
-    with pytest.raises(ValueError, match="M must be <= 2"):
-        qw2.matmul_relu2(x3)
-    x1 = torch.zeros((1, 256), dtype=torch.bfloat16, device=dev)
-    with pytest.raises(ValueError, match="must not overlap"):
-        qw2.matmul_rms_norm(x1, g2, 1e-6, delta=torch.zeros_like(x1), xout=x1)
+        qw2.matmul_relu2(x3)                  # the relu^2 fusion is the VALU GEMV's only
+    for rows in (1, 3):                       # both the VALU and the MFMA path check the overlap
+        xr = torch.zeros((rows, 256), dtype=torch.bfloat16, device=dev)
+        with pytest.raises(ValueError, match="must not overlap"):
+            qw2.matmul_rms_norm(xr, g2, 1e-6, delta=torch.zeros_like(xr), xout=xr)

@@ -837,17 +837,46 @@ template <int S> __device__ __forceinline__ uint8_t* gemv_stage() {
 }
 
 
+// Where a GEMV's activation rows come from (the GEMVs below): PRO_X already
+// quantized x_q / x_s; PRO_NORM / PRO_NORM_ADD rmsnorm of x (after the
+// residual add x + delta) -> FP8 rows, computed by the GEMV's workgroup;
+// PRO_RELU2 bf16(relu(u)^2) -> FP8 rows.
+enum { PRO_X = 0, PRO_NORM = 1, PRO_NORM_ADD = 2, PRO_RELU2 = 3 };
+
+// The norm prologue's inputs (PRO_NORM*): x, delta (M, K) bf16, gamma (K,)
+// bf16; with PRO_NORM_ADD workgroup 0 stores the residual sum bf16(x + delta)
+// to xout (M, K).
+struct GemvNormIn {
+  const uint4* x;
+  const uint4* delta;
+  const uint4* gamma;
+  uint4* xout;
+  float eps;
+};
+
 // NS: stages in flight (three per workgroup, one workgroup per CU; or two, and
 // two workgroups per CU).  Workgroup b takes the balanced share of the 8-row
 // groups: groups [b G / grid, (b + 1) G / grid), at most kGemvGroups.
-template <int MT, int BNS, int NS>
+//
+// PRO_NORM*: before the K loop each workgroup computes the FP8 rows of
+// rms_norm(x [+ delta]) itself -- wave w takes rows w and w + 8, one row per
+// wave as in the norm kernel and with its routine (norm_row: the same bytes
+// and scales as tg_rms_norm_fp8 / tg_add_rms_norm_fp8) -- into dynamic LDS
+// (row pitch K + 16 bytes, so the 16 rows of a fragment read fall on distinct
+// banks), and the x fragments are read from there instead of from HBM.  One
+// launch replaces the norm kernel + the GEMV of a decode step for 3..16 rows;
+// every workgroup repeats the rows' arithmetic (M x K elements, against its
+// W rows' 56 x K bytes of HBM traffic).  J: 16-byte chunks per lane of a row.
+template <int MT, int BNS, int NS, int PRO = PRO_X, int J = 1>
 __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict__ XQ,
                                                        const float* __restrict__ XS,
                                                        const uint8_t* __restrict__ WQ,
                                                        const float* __restrict__ WS,
                                                        __bf16* __restrict__ out, int M, int N,
-                                                       int K) {
+                                                       int K, GemvNormIn nin) {
   constexpr int NW = 8;
+  constexpr bool XLDS = PRO == PRO_NORM || PRO == PRO_NORM_ADD;
+  static_assert(PRO == PRO_X || (XLDS && MT == 1), "the norm prologue takes at most 16 rows");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 15, fg = lane >> 4;
@@ -945,6 +974,68 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
     }
   };
 
+  // PRO_NORM*: the FP8 rows of the norm in LDS (x bytes at pitch K + 16 for
+  // 16 rows, then their scales), from the norm row routine; rows >= M are
+  // never read (their fragments are zero).  The rows' loads go out first, then
+  // the first chunk's weight stages, so the norm's arithmetic runs while the
+  // weight stream is already in flight.
+  extern __shared__ __attribute__((aligned(16))) uint8_t gemv_xl[];
+  const int xpitch = K + 16;
+  float* gemv_xs = reinterpret_cast<float*>(gemv_xl + 16 * xpitch);
+  if constexpr (XLDS) {
+    constexpr bool ADD = PRO == PRO_NORM_ADD;
+    const int nch = K >> 3;
+    // both of a wave's rows are loaded ahead for J <= 5; with J = 8 the
+    // second row's loads wait for the first row's registers (no spills)
+    constexpr int RR = J <= 5 ? 2 : 1;
+    uint4 xv[RR][J], dv[RR][J], gq[J];
+    auto load_row = [&](int rr, int slot) {
+      const int m = wave + NW * rr;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int c = lane + 64 * j;
+        const bool ok = m < M && c < nch;
+        xv[slot][j] = ok ? nin.x[(int64_t)m * nch + c] : make_uint4(0, 0, 0, 0);
+        dv[slot][j] = ADD && ok ? nin.delta[(int64_t)m * nch + c] : make_uint4(0, 0, 0, 0);
+      }
+    };
+#pragma unroll
+    for (int rr = 0; rr < RR; ++rr) load_row(rr, rr);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int c = lane + 64 * j;
+      gq[j] = c < nch ? nin.gamma[c] : make_uint4(0, 0, 0, 0);
+    }
+    load_w(IntC<0>{}, 0, 0);
+    load_w(IntC<1>{}, 0, 1);
+    if constexpr (NS > 2) load_w(IntC<2 % NS>{}, 0, 2);
+    float g[J][8];
+#pragma unroll
+    for (int j = 0; j < J; ++j) unpack8(gq[j], g[j]);
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int m = wave + NW * rr;
+      const int slot = RR == 2 ? rr : 0;
+      if (RR == 1 && rr == 1) load_row(1, 0);
+      if (m < M) {                                 // wave-uniform: the DPP reductions see every lane
+        uint4 yo[J];
+        uint2 qo[J];
+        float so[J];
+        norm_row<J, true, false, ADD>(xv[slot], dv[slot], g, lane, nch, (float)K, nin.eps, yo, qo, so);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          const int c = lane + 64 * j;
+          if (c < nch) {
+            *reinterpret_cast<uint2*>(gemv_xl + m * xpitch + c * 8) = qo[j];
+            if ((c & 15) == 0) gemv_xs[m * nkb + (c >> 4)] = so[j];
+            if (ADD && blockIdx.x == 0) nin.xout[(int64_t)m * nch + c] = xv[slot][j];
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+
   for (int c = 0; c < nchunk; ++c) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -953,16 +1044,26 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
       for (int mt = 0; mt < MT; ++mt) {
         const int m = mt * 16 + fr;
         const bool ok = m < M && kb < nkb;
-        const uint32_t xo = ok ? (uint32_t)m * (uint32_t)K + (uint32_t)kb * 128u + fg * 16u : xbytes;
-        xr[i][mt][0] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
-        xr[i][mt][1] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? xo + 64u : xbytes, 0, 0);
-        const uint32_t so = ok ? ((uint32_t)m * (uint32_t)nkb + (uint32_t)kb) * 4u : xsbytes;
-        sxr[i][mt] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxs, so, 0, 0));
+        if constexpr (XLDS) {
+          const uint8_t* px = gemv_xl + m * xpitch + kb * 128 + fg * 16;
+          const u32x4_t z = {0u, 0u, 0u, 0u};
+          xr[i][mt][0] = ok ? *reinterpret_cast<const u32x4_t*>(px) : z;
+          xr[i][mt][1] = ok ? *reinterpret_cast<const u32x4_t*>(px + 64) : z;
+          sxr[i][mt] = ok ? gemv_xs[m * nkb + kb] : 0.0f;
+        } else {
+          const uint32_t xo = ok ? (uint32_t)m * (uint32_t)K + (uint32_t)kb * 128u + fg * 16u : xbytes;
+          xr[i][mt][0] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+          xr[i][mt][1] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? xo + 64u : xbytes, 0, 0);
+          const uint32_t so = ok ? ((uint32_t)m * (uint32_t)nkb + (uint32_t)kb) * 4u : xsbytes;
+          sxr[i][mt] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxs, so, 0, 0));
+        }
       }
     }
-    load_w(IntC<0>{}, c, 0);
-    load_w(IntC<1>{}, c, 1);
-    if constexpr (NS > 2) load_w(IntC<2 % NS>{}, c, 2);
+    if (!XLDS || c > 0) {                  // XLDS: chunk 0's stages went out before the norm
+      load_w(IntC<0>{}, c, 0);
+      load_w(IntC<1>{}, c, 1);
+      if constexpr (NS > 2) load_w(IntC<2 % NS>{}, c, 2);
+    }
     // every path to stage G runs stages 0 .. G-1 first (early exits only), so
     // the compiler's count of the loads in flight at stage G is exact
     do {
@@ -1069,7 +1170,6 @@ __device__ __forceinline__ float dot16_e4m3(const u32x4_t& w, const uint4& x) {
 
 constexpr int kRowdotMaxK = 16384;   // x of two rows (32 KiB) + scales in LDS
 constexpr int kRowdotNormMaxK = 4096;
-enum { PRO_X = 0, PRO_NORM = 1, PRO_NORM_ADD = 2, PRO_RELU2 = 3 };
 
 struct RowdotIn {
   const uint8_t* xq;      // PRO_X: (M, K) e4m3 bytes
@@ -1514,13 +1614,50 @@ static int launch_gemv(const uint8_t* x_q, const float* x_s, const uint8_t* w_q,
   const int64_t need = (groups + kGemvGroups - 1) / kGemvGroups;
   if (nwg < need) nwg = need;
   const dim3 grid((unsigned)nwg);
+  const GemvNormIn none{};
   if (bn == 1)
     hipLaunchKernelGGL((gemv_fp8_kernel<MT, 1, NS>), grid, dim3(512), 0, st, x_q, x_s, w_q, w_s, out, M,
-                       N, K);
+                       N, K, none);
   else
     hipLaunchKernelGGL((gemv_fp8_kernel<MT, 128, NS>), grid, dim3(512), 0, st, x_q, x_s, w_q, w_s, out,
-                       M, N, K);
+                       M, N, K, none);
   return check_launch("gemv_fp8");
+}
+
+// The norm prologue's LDS (x bytes of 16 rows at pitch K + 16, their scales),
+// beside the three static weight stages (up to K = 3456 would fit).
+static size_t gemv_norm_lds(int64_t K) { return (size_t)16 * (size_t)(K + 16) + (size_t)16 * (size_t)(K / 128) * 4; }
+constexpr size_t kGemvNormMaxLds = (size_t)160 * 1024 - (size_t)3 * kGemvStage;
+
+template <int PRO, int J>
+static int launch_gemv_norm(const GemvNormIn& nin, const uint8_t* w_q, const float* w_s, int bn, __bf16* out,
+                            int M, int N, int K, hipStream_t st) {
+  constexpr int NS = kGemvNS;
+  const int64_t groups = ((int64_t)N + 7) / 8;
+  int64_t nwg = (int64_t)device_cus();
+  if (nwg > groups) nwg = groups;
+  const int64_t need = (groups + kGemvGroups - 1) / kGemvGroups;
+  if (nwg < need) nwg = need;
+  const dim3 grid((unsigned)nwg);
+  const size_t lds = gemv_norm_lds(K);
+  if (bn == 1)
+    hipLaunchKernelGGL((gemv_fp8_kernel<1, 1, NS, PRO, J>), grid, dim3(512), lds, st, nullptr, nullptr, w_q,
+                       w_s, out, M, N, K, nin);
+  else
+    hipLaunchKernelGGL((gemv_fp8_kernel<1, 128, NS, PRO, J>), grid, dim3(512), lds, st, nullptr, nullptr,
+                       w_q, w_s, out, M, N, K, nin);
+  return check_launch("rms_norm_fp8_gemv");
+}
+
+// K <= 2560 (at most 5 chunks per lane of a row: a wider row's registers
+// spill beside the weight stages')
+constexpr int64_t kGemvNormMaxK = 2560;
+template <int PRO>
+static int launch_gemv_norm_k(const GemvNormIn& nin, const uint8_t* w_q, const float* w_s, int bn,
+                              __bf16* out, int M, int N, int K, hipStream_t st) {
+  const int jneed = (K / 8 + 63) / 64;   // 16-byte chunks per lane of a row
+  if (jneed <= 4) return launch_gemv_norm<PRO, 4>(nin, w_q, w_s, bn, out, M, N, K, st);
+  return launch_gemv_norm<PRO, 5>(nin, w_q, w_s, bn, out, M, N, K, st);
 }
 
 extern "C" int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* w_q,
@@ -1646,10 +1783,39 @@ extern "C" int tg_gemv_fp8_rowdot(const uint8_t* x_q, const float* x_s, const ui
   return check_launch("gemv_fp8_rowdot");
 }
 
+// 3..16 rows: the MFMA GEMV with the norm prologue (tg_gemv_fp8's arithmetic).
+static int gemv_norm_checks(int64_t M, int64_t N, int64_t K, int w_scale_bn, const uint8_t* w_q,
+                            const float* w_s, const void* out) {
+  TG_TRY(check_gemm_args("rms_norm_fp8_gemv", M, N, K, 128, w_scale_bn));
+  const char* what = nullptr;
+  char msg[200];
+  if (M > 16) {
+    what = "M must be <= 16 (the norm prologue holds 16 rows)";
+  } else if (K > kGemvNormMaxK || gemv_norm_lds(K) > kGemvNormMaxLds) {
+    snprintf(msg, sizeof(msg), "rms_norm_fp8_gemv: K=%lld too large for 3-16 rows (K <= %lld)", (long long)K,
+             (long long)kGemvNormMaxK);
+    return einval(msg);
+  } else if (N == 0) {
+    return TG_OK;
+  } else if (!w_q || !w_s || !out) {
+    what = "null pointer";
+  } else if (!aligned(w_q, 16)) {
+    what = "operands must be 16-byte aligned";
+  } else if ((uint64_t)N * (uint64_t)(K / 128) * 4u >= (1ull << 32) || (uint64_t)64 * (uint64_t)K >= (1ull << 32)) {
+    what = "operand too large for 32-bit buffer offsets";
+  }
+  if (!what) return TG_OK;
+  snprintf(msg, sizeof(msg), "rms_norm_fp8_gemv: %s", what);
+  return einval(msg);
+}
+
 extern "C" int tg_rms_norm_fp8_gemv(const void* x, const void* delta, const void* gamma, float eps,
                                     void* xout, const uint8_t* w_q, const float* w_s, int w_scale_bn,
                                     void* out, int64_t M, int64_t N, int64_t K, void* stream) {
-  TG_TRY(rowdot_common_checks("rms_norm_fp8_gemv", M, N, K, w_scale_bn, w_q, w_s, out, kRowdotNormMaxK));
+  if (M > 2)
+    TG_TRY(gemv_norm_checks(M, N, K, w_scale_bn, w_q, w_s, out));
+  else
+    TG_TRY(rowdot_common_checks("rms_norm_fp8_gemv", M, N, K, w_scale_bn, w_q, w_s, out, kRowdotNormMaxK));
   if (M == 0 || N == 0) return TG_OK;
   if (!x || !gamma || (delta && !xout)) return einval("rms_norm_fp8_gemv: null pointer");
   if (!aligned(x, 16) || !aligned(gamma, 16) || (delta && (!aligned(delta, 16) || !aligned(xout, 16))))
@@ -1658,15 +1824,25 @@ extern "C" int tg_rms_norm_fp8_gemv(const void* x, const void* delta, const void
   if (delta && (ranges_overlap(xout, x, rb) || ranges_overlap(xout, delta, rb)))
     return einval("rms_norm_fp8_gemv: xout must not overlap x or delta (other workgroups read them "
                   "while workgroup 0 stores xout)");
+  auto o = reinterpret_cast<__bf16*>(out);
+  hipStream_t st = as_stream(stream);
+  const int n = (int)N, k = (int)K;
+  if (M > 2) {
+    GemvNormIn gi{};
+    gi.x = reinterpret_cast<const uint4*>(x);
+    gi.delta = reinterpret_cast<const uint4*>(delta);
+    gi.gamma = reinterpret_cast<const uint4*>(gamma);
+    gi.xout = reinterpret_cast<uint4*>(xout);
+    gi.eps = eps;
+    if (delta) return launch_gemv_norm_k<PRO_NORM_ADD>(gi, w_q, w_s, w_scale_bn, o, (int)M, n, k, st);
+    return launch_gemv_norm_k<PRO_NORM>(gi, w_q, w_s, w_scale_bn, o, (int)M, n, k, st);
+  }
   RowdotIn in{};
   in.x = reinterpret_cast<const uint4*>(x);
   in.delta = reinterpret_cast<const uint4*>(delta);
   in.gamma = reinterpret_cast<const uint4*>(gamma);
   in.xout = reinterpret_cast<uint4*>(xout);
   in.eps = eps;
-  auto o = reinterpret_cast<__bf16*>(out);
-  hipStream_t st = as_stream(stream);
-  const int n = (int)N, k = (int)K;
   if (delta) {
     if (M == 1) TG_TRY((launch_rowdot<1, PRO_NORM_ADD>(in, w_q, w_s, w_scale_bn, o, n, k, st)));
     else TG_TRY((launch_rowdot<2, PRO_NORM_ADD>(in, w_q, w_s, w_scale_bn, o, n, k, st)));

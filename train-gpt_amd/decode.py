@@ -143,10 +143,14 @@ class FP8Decoder:
     exact_gemv: for 1-2 rows use the MFMA GEMV (the GEMM's block arithmetic)
     rather than the faster VALU one (tg_gemv_fp8_rowdot); default: on with
     decode_attn "sdpa" (the bit-exact mode), off with "hip".
-    fused: with the VALU GEMV and at most 2 rows, a decode step runs each norm
-    (or residual add + norm) and the relu^2 quantization inside the GEMV that
-    consumes them (tg_rms_norm_fp8_gemv, tg_relu2_fp8_gemv): 5 kernels per
-    layer instead of 8, the same bits.  Default: on where it applies.
+    fused: a decode step runs each norm (or residual add + norm) inside the
+    GEMV that consumes it (tg_rms_norm_fp8_gemv), and for 1-2 rows also the
+    relu^2 quantization (tg_relu2_fp8_gemv): 5 kernels per layer instead of 8
+    (1-2 rows, VALU GEMV) or 6 (3-16 rows, MFMA GEMV, d_model <= 2560), the
+    same bits.  Default: on for up to 8 rows (measured at the reference
+    config: batch 4 and 8 steps 14% and 11% faster); at 9-16 rows each wave
+    normalises two rows in the GEMV's prologue and the fused step measured 2%
+    slower at 16, so it is off unless asked for.
     """
 
     def __init__(self, params, cfg: Config, layout: str = "128x128", max_batch: int = 1,
@@ -156,10 +160,12 @@ class FP8Decoder:
             raise ValueError("decode_attn must be 'hip' or 'sdpa'")
         self.decode_attn = decode_attn
         self.exact_gemv = decode_attn == "sdpa" if exact_gemv is None else bool(exact_gemv)
-        can_fuse = not self.exact_gemv and max_batch <= 2 and cfg.d_model <= 4096
+        can_fuse = ((max_batch <= 2 and not self.exact_gemv and cfg.d_model <= 4096)
+                    or (3 <= max_batch <= 16 and cfg.d_model <= 2560))
         if fused and not can_fuse:
-            raise ValueError("fused decode steps need exact_gemv=False, max_batch <= 2 and d_model <= 4096")
-        self.fused = can_fuse if fused is None else bool(fused)
+            raise ValueError("fused decode steps need max_batch <= 2 with exact_gemv=False and d_model <= 4096, "
+                             "or 3 <= max_batch <= 16 and d_model <= 2560")
+        self.fused = (can_fuse and max_batch <= 8) if fused is None else bool(fused)
         if not 1 <= max_batch <= 64:
             raise ValueError("max_batch must be in [1, 64] (decode rows per GEMV)")
         self.cfg = cfg
@@ -299,7 +305,10 @@ class FP8Decoder:
                 a = lp["wo"].matmul(self._sdpa_step(li, qkv, int(t.item())))
             # x = x + a (model.py:75), norm2, w_up (model.py:71-72)
             u = lp["w_up"].matmul_rms_norm(xa, lp["norm2"], eps, delta=a, xout=xb)
-            m = lp["w_down"].matmul_relu2(u)                                # model.py:72-73
+            if B <= 2:
+                m = lp["w_down"].matmul_relu2(u)                            # model.py:72-73
+            else:
+                m = lp["w_down"].matmul_prequant(*fp8.quantize_relu2(u))
             # x = x + m (model.py:76), then the next layer's norm1 and q|k|v, or
             # the final norm and the unembedding (model.py:93-96)
             last = li + 1 == len(self.layers)

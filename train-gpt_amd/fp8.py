@@ -645,12 +645,13 @@ class QuantizedWeight:
 
     def matmul_rms_norm(self, x: torch.Tensor, gamma: torch.Tensor, eps: float,
                         delta: torch.Tensor = None, xout: torch.Tensor = None) -> torch.Tensor:
-        """The norm that feeds this weight, fused with the GEMV, for 1-2 rows
+        """The norm that feeds this weight, fused with the GEMV, for 1-16 rows
         (tg_rms_norm_fp8_gemv): out (M, N) bf16 = the FP8 rows of
         rms_norm(x [+ delta]) (kernels.py:30-33, fp8.py:39-47) times the kept W.
         With delta, xout (M, K) receives the residual sum bf16(x + delta); it
         must not overlap x or delta.  Same bits as kernels.rms_norm_fp8 /
-        add_rms_norm_fp8 followed by matmul_prequant (the VALU GEMV)."""
+        add_rms_norm_fp8 followed by matmul_prequant (the VALU GEMV for 1-2
+        rows, K <= 4096; the MFMA GEMV for 3-16 rows, K <= 2560)."""
         K, N = self.shape
         if x.dim() != 2 or x.shape[1] != K or x.dtype != torch.bfloat16:
             raise ValueError(f"matmul_rms_norm: x must be bf16 (M, {K})")
