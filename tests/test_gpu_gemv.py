@@ -45,7 +45,11 @@ def test_gemv_c5(dev, weight, layout, M):
 # 20480), waves without K blocks (K = 256), scale rows straddling a 128-row
 # group, and every M bucket (<= 16, <= 32, <= 64).
 RAGGED = [(3, 40, 256), (16, 100, 384), (64, 72, 512), (5, 16, 4096), (1, 14338, 4096),
-          (20, 1001, 1280), (33, 130, 8192), (17, 515, 20480), (64, 3000, 2048), (2, 257, 128)]
+          (20, 1001, 1280), (33, 130, 8192), (17, 515, 20480), (64, 3000, 2048), (2, 257, 128),
+          # the direct kernel (<= 8 or 17-32 rows, <= 512 row blocks or N > 16384): 12 K blocks
+          # per wave with the 16-chunk x copy, two x-row tiles, a grid walking many row
+          # blocks per workgroup, 12 K blocks with the 4-chunk copy, more than 512 x scales
+          (8, 2304, 9216), (32, 2304, 2304), (4, 50257, 2304), (1, 777, 12288), (24, 130, 4096)]
 
 
 @pytest.mark.parametrize("layout", ["128x1", "128x128"])
@@ -59,6 +63,8 @@ def test_gemv_ragged(dev, M, N, K, layout):
     qx, sx = fp8_ref.quantize_fp8(ob.bf16_to_f32(x))
     ref = fp8_ref.gemv_prequant(qx, sx, u8(wq), ws.cpu().numpy(), bn)
     assert maxabs_rel(out, ref) <= 1e-2
+    # elementwise: one bf16 rounding of an f32 sum (a mis-placed scale or row fails this)
+    assert _rowdot_close(out, ref)
 
 
 def _rowdot_close(out, ref) -> bool:

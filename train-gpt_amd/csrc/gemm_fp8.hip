@@ -1122,6 +1122,214 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
 }
 
 // ---------------------------------------------------------------------------
+// Decode GEMV, direct form (M <= 16 MT rows): the weight's MFMA fragments go
+// from HBM straight into registers.
+//   * A row block is 16 weight rows, the MFMA's A operand.  Workgroup b takes
+//     row blocks b, b + grid, ...; its 8 waves split K: wave w takes the
+//     contiguous K blocks [w kpw, (w + 1) kpw).  Lane (r, g) loads row r's
+//     16-byte pieces g and 4 + g of each of its K blocks (each load
+//     instruction reads 64 contiguous bytes of 16 rows), all of a row block
+//     at once: one memory round trip per row block, and the next row block's
+//     loads go out before this one's reduction.
+//   * The x rows (bytes and scales) sit in LDS at pitch K + 16 (the 16 rows of
+//     a fragment read fall on distinct banks): copied from x_q / x_s (PRO_X,
+//     their loads issued before the weight's) or computed by the norm
+//     prologue (PRO_NORM*, M <= 8: wave w normalises row w with the norm
+//     kernel's row routine; the rows' loads, then the weight's, then the
+//     norm's arithmetic).
+//   * acc = fma(P, w_s * x_s, acc) per K block; the 8 waves' partial tiles are
+//     added in wave order through LDS, so the result is deterministic and the
+//     same for every prologue.
+// Against the staged kernel above (4 KiB-contiguous reads through LDS, K walked
+// in 4 KiB chunks) this has no staging and no serial chunk walk: on the
+// reference decode weights (5-21 MB) the staged kernel's fixed cost and its
+// chunk walk over the 9 KiB w_down rows dominated.
+// KPW: K blocks per wave (at least ceil(K / 1024)); XC: 16-byte x chunks per
+// thread of the PRO_X copy; J: 16-byte chunks per lane of a norm row.
+// ---------------------------------------------------------------------------
+template <int MT, int BNS, int KPW, int PRO, int XC, int J>
+__global__ __launch_bounds__(512) void gemv_direct_kernel(const uint8_t* __restrict__ XQ,
+                                                          const float* __restrict__ XS,
+                                                          const uint8_t* __restrict__ WQ,
+                                                          const float* __restrict__ WS,
+                                                          __bf16* __restrict__ out, int M, int N, int K,
+                                                          GemvNormIn nin) {
+  constexpr int NW = 8;
+  constexpr bool XNORM = PRO == PRO_NORM || PRO == PRO_NORM_ADD;
+  static_assert(PRO == PRO_X || (XNORM && MT == 1), "the norm prologue takes at most 8 rows");
+  extern __shared__ __attribute__((aligned(16))) uint8_t gdx[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 15, fg = lane >> 4;
+  const int nkb = K >> 7;
+  const int xpitch = K + 16;
+  float* xsl = reinterpret_cast<float*>(gdx + M * xpitch);                            // (M, nkb)
+  v4f* red = reinterpret_cast<v4f*>(gdx + ((M * xpitch + M * nkb * 4 + 15) & ~15));   // [NW][MT][64]
+  const int nrb = (N + 15) >> 4;
+  const int kpw = (nkb + NW - 1) / NW;        // <= KPW (host)
+  const int kb0 = wave * kpw;
+
+  // ---- x rows: loads first (PRO_X into registers; PRO_NORM* the norm rows) ----
+  u32x4_t xc[PRO == PRO_X ? XC : 1];
+  float xsc = 0.0f;
+  const int xchunks = M * (K >> 4);
+  uint4 nxv[XNORM ? J : 1], ndv[XNORM ? J : 1], ngq[XNORM ? J : 1];
+  const int nch = K >> 3;
+  if constexpr (PRO == PRO_X) {
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(XQ, (uint32_t)M * (uint32_t)K);
+    const __amdgpu_buffer_rsrc_t rxs = make_rsrc(XS, (uint32_t)M * (uint32_t)nkb * 4u);
+#pragma unroll
+    for (int j = 0; j < XC; ++j)           // chunk tid + 512 j of the (M, K) bytes; past them: zero
+      xc[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(tid + 512 * j) * 16u, 0, 0);
+    xsc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxs, (uint32_t)tid * 4u, 0, 0));
+  } else {
+    constexpr bool ADD = PRO == PRO_NORM_ADD;
+    const int m = wave;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int c = lane + 64 * j;
+      const bool ok = m < M && c < nch;
+      nxv[j] = ok ? nin.x[(int64_t)m * nch + c] : make_uint4(0, 0, 0, 0);
+      ndv[j] = ADD && ok ? nin.delta[(int64_t)m * nch + c] : make_uint4(0, 0, 0, 0);
+      ngq[j] = c < nch ? nin.gamma[c] : make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  // ---- the first row block's weight fragments and scales ----
+  const uint32_t wbytes = (uint32_t)N * (uint32_t)K;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(WQ, wbytes);
+  const int srows = BNS == 1 ? N : (N + BNS - 1) / BNS;
+  const uint32_t sbytes = (uint32_t)srows * (uint32_t)nkb * 4u;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(WS, sbytes);
+  constexpr int NSC = BNS == 1 ? 4 : 1;      // W scales per lane and K block
+  struct Frag {
+    u32x4_t w[KPW][2];
+    float s[KPW][NSC];
+  };
+  auto load_rb = [&](Frag& F, int rb) {
+    const int row = rb * 16 + fr;
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      const int kb = kb0 + i;
+      const bool kok = i < kpw && kb < nkb;
+      const bool ok = kok && row < N;
+      const uint32_t off = ok ? (uint32_t)row * (uint32_t)K + (uint32_t)kb * 128u + fg * 16u : wbytes;
+      F.w[i][0] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kAuxNT);
+      F.w[i][1] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? off + 64u : wbytes, 0, kAuxNT);
+#pragma unroll
+      for (int r = 0; r < NSC; ++r) {
+        const int srow = BNS == 1 ? rb * 16 + 4 * fg + r : (rb * 16) / BNS;
+        const bool sok = kok && srow < srows;
+        const uint32_t so = sok ? ((uint32_t)srow * (uint32_t)nkb + (uint32_t)kb) * 4u : sbytes;
+        F.s[i][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0));
+      }
+    }
+  };
+  // one register set, refilled with the next row block's fragments before each
+  // reduction (a second set, to keep two row blocks in flight, measured slower:
+  // the registers cost a workgroup per CU)
+  Frag FA;
+  const int G = (int)gridDim.x;
+  load_rb(FA, blockIdx.x);                    // the host launches at most nrb workgroups
+
+  // ---- x rows into LDS ----
+  if constexpr (PRO == PRO_X) {
+    const int kc = K >> 4;                    // 16-byte chunks per row
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+      const int c = tid + 512 * j;
+      if (c < xchunks) {
+        const int m = c / kc, k16 = c - m * kc;
+        *reinterpret_cast<u32x4_t*>(gdx + m * xpitch + k16 * 16) = xc[j];
+      }
+    }
+    if (tid < M * nkb) xsl[tid] = xsc;
+    for (int c = tid + 512; c < M * nkb; c += 512) xsl[c] = XS[c];   // more than 512 scales: rare
+  } else {
+    constexpr bool ADD = PRO == PRO_NORM_ADD;
+    const int m = wave;
+    if (m < M) {                              // wave-uniform: the DPP reductions see every lane
+      float g[J][8];
+#pragma unroll
+      for (int j = 0; j < J; ++j) unpack8(ngq[j], g[j]);
+      uint4 yo[J];
+      uint2 qo[J];
+      float so[J];
+      norm_row<J, true, false, ADD>(nxv, ndv, g, lane, nch, (float)K, nin.eps, yo, qo, so);
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nch) {
+          *reinterpret_cast<uint2*>(gdx + m * xpitch + c * 8) = qo[j];
+          if ((c & 15) == 0) xsl[m * nkb + (c >> 4)] = so[j];
+          if (ADD && blockIdx.x == 0) nin.xout[(int64_t)m * nch + c] = nxv[j];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0;
+  // one row block from register set F: MFMAs, then (refill) the 8 waves'
+  // partial tiles added in wave order through LDS and stored
+  auto process = [&](Frag& F, int rb, int refill_rb) {
+    v4f acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      const int kb = kb0 + i;
+      if (i < kpw && kb < nkb) {              // wave-uniform
+        const v8i a = as_v8i(F.w[i][0], F.w[i][1]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int m = mt * 16 + fr;
+          const bool mok = m < M;
+          const int mc = mok ? m : M - 1;     // rows past M read row M - 1 and are zeroed
+          const uint8_t* px = gdx + mc * xpitch + kb * 128 + fg * 16;
+          u32x4_t b0 = *reinterpret_cast<const u32x4_t*>(px);
+          u32x4_t b1 = *reinterpret_cast<const u32x4_t*>(px + 64);
+          const u32x4_t z = {0u, 0u, 0u, 0u};
+          b0 = mok ? b0 : z;
+          b1 = mok ? b1 : z;
+          const float sx = mok ? xsl[mc * nkb + kb] : 0.0f;
+          const v4f pr = mfma_f8_16x16x128(a, as_v8i(b0, b1), v4f{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[mt][r] = __builtin_fmaf(pr[r], F.s[i][BNS == 1 ? r : 0] * sx, acc[mt][r]);
+        }
+      }
+    }
+    if (refill_rb < nrb) load_rb(F, refill_rb);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) red[(wave * MT + mt) * 64 + lane] = acc[mt];
+    __syncthreads();
+    if (wave < MT) {
+      const int mt = wave;
+      v4f sm = red[mt * 64 + lane];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) {
+        const v4f o = red[(w2 * MT + mt) * 64 + lane];
+        sm[0] += o[0]; sm[1] += o[1]; sm[2] += o[2]; sm[3] += o[3];
+      }
+      const int m = mt * 16 + fr, n = rb * 16 + 4 * fg;
+      if (m < M && n < N) {
+        __bf16* o = out + (int64_t)m * N + n;
+        if (vec) {
+          *reinterpret_cast<uint2*>(o) = make_uint2(pack_bf16x2(sm[0], sm[1]), pack_bf16x2(sm[2], sm[3]));
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < N) o[r] = (__bf16)sm[r];
+        }
+      }
+    }
+    __syncthreads();                          // red is rewritten by the next row block
+  };
+  for (int rb = blockIdx.x; rb < nrb; rb += G) process(FA, rb, rb + G);
+}
+
+// ---------------------------------------------------------------------------
 // GEMV for one or two activation rows on the VALU (no MFMA, no LDS staging of
 // W).  With M <= 2 the MFMA kernel above spends its time moving each weight
 // row through LDS so that 8 rows can feed one 16-row MFMA fragment; here each
@@ -1660,6 +1868,110 @@ static int launch_gemv_norm_k(const GemvNormIn& nin, const uint8_t* w_q, const f
   return launch_gemv_norm<PRO, 5>(nin, w_q, w_s, bn, out, M, N, K, st);
 }
 
+// ---- the direct GEMV (gemv_direct_kernel) ----
+// LDS: x rows at pitch K + 16, their scales, the 8 waves' partial tiles.
+static size_t gemv_direct_lds(int64_t M, int64_t K, int mt) {
+  const size_t x = (size_t)M * (size_t)(K + 16) + (size_t)M * (size_t)(K / 128) * 4;
+  return ((x + 15) & ~(size_t)15) + (size_t)8 * mt * 64 * 16;
+}
+// Whether the direct kernel takes (M, N, K).  Shape: at most 8 or 17-32 rows
+// (9-16 rows stay on the staged kernel, whose norm prologue takes them, so
+// that tg_rms_norm_fp8_gemv and tg_gemv_fp8 keep one summation order per
+// shape), K blocks of a wave in registers (K <= 12288, and <= 4096 past 16
+// rows), the x copy in one round of 16 chunks per thread, and the LDS above
+// within a CU's 160 KiB.  Speed (same-box A/B at the reference decode shapes
+// and C5): direct wins while every 16-row block has a workgroup at once (<=
+// 512 blocks: the decode wo, w_down and q|k|v weights) and past N = 16384
+// (the 50257-row unembedding, where the staged kernel runs several rounds of
+// workgroups); in between (C5's 14336 rows, w_up's 9216) the staged kernel's
+// 4 KiB-contiguous row reads stream better than 64 bytes of 16 rows per load.
+static bool gemv_direct_fits(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || M > 32 || (M > 8 && M <= 16)) return false;
+  const int64_t nrb = (N + 15) / 16;
+  if (nrb > 512 && N <= 16384) return false;
+  const int mt = M <= 16 ? 1 : 2;
+  const int64_t kpw = (K / 128 + 7) / 8;
+  if (kpw > (mt == 1 ? 12 : 4)) return false;
+  if ((M * K / 16 + 511) / 512 > 16) return false;
+  return gemv_direct_lds(M, K, mt) <= (size_t)160 * 1024;
+}
+
+template <int MT, int BNS, int KPW, int PRO, int XC, int J>
+static int launch_gemv_direct_t(const uint8_t* x_q, const float* x_s, const GemvNormIn& nin, const uint8_t* w_q,
+                                const float* w_s, __bf16* out, int M, int N, int K, hipStream_t st) {
+  auto kern = gemv_direct_kernel<MT, BNS, KPW, PRO, XC, J>;
+  // workgroups resident at once: registers (once per instantiation), LDS per launch
+  static const int occ_regs = [] {
+    int v = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_direct_kernel<MT, BNS, KPW, PRO, XC, J>, 512, 0) !=
+            hipSuccess || v <= 0)
+      v = 1;
+    return v;
+  }();
+  const size_t lds = gemv_direct_lds(M, K, MT);
+  int per_cu = occ_regs;
+  const int by_lds = (int)(((size_t)160 * 1024) / lds);
+  if (by_lds < per_cu) per_cu = by_lds < 1 ? 1 : by_lds;
+  const int64_t nrb = ((int64_t)N + 15) / 16, cap = (int64_t)per_cu * (device_cus() > 0 ? device_cus() : 1);
+  const int grid = (int)(nrb < cap ? nrb : cap);
+  if (lds > 64 * 1024) {
+    // the dynamic-LDS limit is a per-device function attribute (set once per device)
+    constexpr int kMaxDev = 64;
+    static std::once_flag once[kMaxDev];
+    static hipError_t attr_rc[kMaxDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) dev = 0;
+    std::call_once(once[dev], [&] {
+      attr_rc[dev] = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    });
+    if (attr_rc[dev] != hipSuccess) {
+      set_error("gemv_fp8 (set LDS size): %s", hipGetErrorString(attr_rc[dev]));
+      return TG_EHIP;
+    }
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(512), lds, st, x_q, x_s, w_q, w_s, out, M, N, K, nin);
+  return check_launch("gemv_fp8 (direct)");
+}
+
+template <int MT, int BNS>
+static int launch_gemv_direct_x(const uint8_t* x_q, const float* x_s, const uint8_t* w_q, const float* w_s,
+                                __bf16* out, int M, int N, int K, hipStream_t st) {
+  const GemvNormIn none{};
+  const int kpw = (K / 128 + 7) / 8;
+  const int xc = (M * (K / 16) + 511) / 512;
+  if constexpr (MT == 2) {
+    return launch_gemv_direct_t<2, BNS, 4, PRO_X, 16, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
+  } else {
+    if (xc <= 4) {
+      if (kpw <= 4) return launch_gemv_direct_t<1, BNS, 4, PRO_X, 4, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
+      if (kpw <= 8) return launch_gemv_direct_t<1, BNS, 8, PRO_X, 4, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
+      return launch_gemv_direct_t<1, BNS, 12, PRO_X, 4, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
+    }
+    if (kpw <= 4) return launch_gemv_direct_t<1, BNS, 4, PRO_X, 16, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
+    if (kpw <= 8) return launch_gemv_direct_t<1, BNS, 8, PRO_X, 16, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
+    return launch_gemv_direct_t<1, BNS, 12, PRO_X, 16, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
+  }
+}
+
+static int launch_gemv_direct(const uint8_t* x_q, const float* x_s, const uint8_t* w_q, const float* w_s, int bn,
+                              __bf16* out, int M, int N, int K, hipStream_t st) {
+  if (M <= 16)
+    return bn == 1 ? launch_gemv_direct_x<1, 1>(x_q, x_s, w_q, w_s, out, M, N, K, st)
+                   : launch_gemv_direct_x<1, 128>(x_q, x_s, w_q, w_s, out, M, N, K, st);
+  return bn == 1 ? launch_gemv_direct_x<2, 1>(x_q, x_s, w_q, w_s, out, M, N, K, st)
+                 : launch_gemv_direct_x<2, 128>(x_q, x_s, w_q, w_s, out, M, N, K, st);
+}
+
+// The norm prologue in the direct GEMV: at most 8 rows, K <= 2560 (one K
+// block group of <= 4 per wave; 5 chunks per lane of a norm row).
+template <int PRO>
+static int launch_gemv_direct_norm(const GemvNormIn& nin, const uint8_t* w_q, const float* w_s, int bn,
+                                   __bf16* out, int M, int N, int K, hipStream_t st) {
+  return bn == 1 ? launch_gemv_direct_t<1, 1, 4, PRO, 1, 5>(nullptr, nullptr, nin, w_q, w_s, out, M, N, K, st)
+                 : launch_gemv_direct_t<1, 128, 4, PRO, 1, 5>(nullptr, nullptr, nin, w_q, w_s, out, M, N, K, st);
+}
+
 extern "C" int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* w_q,
                            const float* w_s, int w_scale_bn, void* out, int64_t M, int64_t N,
                            int64_t K, int block_k, void* stream) {
@@ -1674,6 +1986,7 @@ extern "C" int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* 
   hipStream_t st = as_stream(stream);
   const int m = (int)M, n = (int)N, k = (int)K;
   auto o = reinterpret_cast<__bf16*>(out);
+  if (gemv_direct_fits(M, N, K)) return launch_gemv_direct(x_q, x_s, w_q, w_s, w_scale_bn, o, m, n, k, st);
   if (M <= 16) return launch_gemv<1>(x_q, x_s, w_q, w_s, w_scale_bn, o, m, n, k, st);
   if (M <= 32) return launch_gemv<2>(x_q, x_s, w_q, w_s, w_scale_bn, o, m, n, k, st);
   // 33 <= M <= 64: activation rows 0..31 and 32..M-1 in two passes over W
@@ -1834,6 +2147,10 @@ extern "C" int tg_rms_norm_fp8_gemv(const void* x, const void* delta, const void
     gi.gamma = reinterpret_cast<const uint4*>(gamma);
     gi.xout = reinterpret_cast<uint4*>(xout);
     gi.eps = eps;
+    if (M <= 8 && gemv_direct_fits(M, N, K)) {   // the rows tg_gemv_fp8 would take directly
+      if (delta) return launch_gemv_direct_norm<PRO_NORM_ADD>(gi, w_q, w_s, w_scale_bn, o, (int)M, n, k, st);
+      return launch_gemv_direct_norm<PRO_NORM>(gi, w_q, w_s, w_scale_bn, o, (int)M, n, k, st);
+    }
     if (delta) return launch_gemv_norm_k<PRO_NORM_ADD>(gi, w_q, w_s, w_scale_bn, o, (int)M, n, k, st);
     return launch_gemv_norm_k<PRO_NORM>(gi, w_q, w_s, w_scale_bn, o, (int)M, n, k, st);
   }
