@@ -1171,7 +1171,7 @@ __global__ __launch_bounds__(512) void gemv_direct_kernel(const uint8_t* __restr
 
   // ---- x rows: loads first (PRO_X into registers; PRO_NORM* the norm rows) ----
   u32x4_t xc[PRO == PRO_X ? XC : 1];
-  float xsc = 0.0f;
+  float xsc[2] = {0.0f, 0.0f};
   const int xchunks = M * (K >> 4);
   uint4 nxv[XNORM ? J : 1], ndv[XNORM ? J : 1], ngq[XNORM ? J : 1];
   const int nch = K >> 3;
@@ -1181,7 +1181,11 @@ __global__ __launch_bounds__(512) void gemv_direct_kernel(const uint8_t* __restr
 #pragma unroll
     for (int j = 0; j < XC; ++j)           // chunk tid + 512 j of the (M, K) bytes; past them: zero
       xc[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(tid + 512 * j) * 16u, 0, 0);
-    xsc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxs, (uint32_t)tid * 4u, 0, 0));
+    // M * nkb <= 1024 (the host keeps M * K <= 131072): two scales per thread, no drain before the barrier
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      xsc[j] = __builtin_bit_cast(float,
+                                  __builtin_amdgcn_raw_buffer_load_b32(rxs, (uint32_t)(tid + 512 * j) * 4u, 0, 0));
   } else {
     constexpr bool ADD = PRO == PRO_NORM_ADD;
     const int m = wave;
@@ -1214,8 +1218,10 @@ __global__ __launch_bounds__(512) void gemv_direct_kernel(const uint8_t* __restr
       const bool kok = i < kpw && kb < nkb;
       const bool ok = kok && row < N;
       const uint32_t off = ok ? (uint32_t)row * (uint32_t)K + (uint32_t)kb * 128u + fg * 16u : wbytes;
-      F.w[i][0] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kAuxNT);
-      F.w[i][1] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? off + 64u : wbytes, 0, kAuxNT);
+      // cached loads: the two 64-byte halves of a weight line come from two instructions, and the
+      // second one hits in L2 (non-temporal, each half was fetched on its own: 10-13% slower)
+      F.w[i][0] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
+      F.w[i][1] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? off + 64u : wbytes, 0, 0);
 #pragma unroll
       for (int r = 0; r < NSC; ++r) {
         const int srow = BNS == 1 ? rb * 16 + 4 * fg + r : (rb * 16) / BNS;
@@ -1243,8 +1249,8 @@ __global__ __launch_bounds__(512) void gemv_direct_kernel(const uint8_t* __restr
         *reinterpret_cast<u32x4_t*>(gdx + m * xpitch + k16 * 16) = xc[j];
       }
     }
-    if (tid < M * nkb) xsl[tid] = xsc;
-    for (int c = tid + 512; c < M * nkb; c += 512) xsl[c] = XS[c];   // more than 512 scales: rare
+    if (tid < M * nkb) xsl[tid] = xsc[0];
+    if (tid + 512 < M * nkb) xsl[tid + 512] = xsc[1];
   } else {
     constexpr bool ADD = PRO == PRO_NORM_ADD;
     const int m = wave;
@@ -1377,6 +1383,7 @@ __device__ __forceinline__ float dot16_e4m3(const u32x4_t& w, const uint4& x) {
 }
 
 constexpr int kRowdotMaxK = 16384;   // x of two rows (32 KiB) + scales in LDS
+constexpr int kRowdotProWaves = 8;  // waves per workgroup of the norm / relu^2 prologue variants
 constexpr int kRowdotNormMaxK = 4096;
 
 struct RowdotIn {
@@ -1428,13 +1435,18 @@ __device__ __forceinline__ void rowdot_compute(const RowdotUnit& U, const uint8_
 }
 
 // XL: 4 KiB pieces of x staged by PRO_X (NX * K <= 4096 * XL), or 16-byte
-// chunks of u per thread for PRO_RELU2 (NX * K <= 2048 * XL); J: chunks per
-// lane of the norm row (K <= 512 * J).
-template <int NX, int PRO, int XL, int J>
-__global__ __launch_bounds__(256) void gemv_rowdot_kernel(RowdotIn in, const uint8_t* __restrict__ WQ,
+// chunks of u per thread for PRO_RELU2 (NX * K <= 8 * 64 * WPG * XL); J:
+// chunks per lane of the norm row (K <= 512 * J); WPG: waves per workgroup
+// (4 for PRO_X; 8 for the computing prologues, whose bf16 row loads every
+// workgroup repeats: 8 waves measured best of 4, 8 and 16 at the decode
+// shapes).
+template <int NX, int PRO, int XL, int J, int WPG>
+__global__ __launch_bounds__(64 * WPG) void gemv_rowdot_kernel(RowdotIn in, const uint8_t* __restrict__ WQ,
                                                           const float* __restrict__ WS, int bns,
                                                           __bf16* __restrict__ out, int N, int K,
                                                           int sx_off) {
+  static_assert(PRO != PRO_X || WPG == 4, "the x copy is laid out for 256 threads");
+  constexpr int NT = 64 * WPG;
   extern __shared__ __attribute__((aligned(16))) uint8_t rowdot_lds[];   // x bytes, then x scales
   uint8_t* xl = rowdot_lds;
   float* sxs = reinterpret_cast<float*>(rowdot_lds + sx_off);
@@ -1444,7 +1456,7 @@ __global__ __launch_bounds__(256) void gemv_rowdot_kernel(RowdotIn in, const uin
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(WQ, (uint32_t)N * (uint32_t)K);
   const int srows = bns == 1 ? N : (N + 127) >> 7;
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(WS, (uint32_t)srows * (uint32_t)nkb * 4u);
-  const int nw = gridDim.x * 4, gw = blockIdx.x * 4 + wave;
+  const int nw = gridDim.x * WPG, gw = blockIdx.x * WPG + wave;
   const int G = (K + 4095) >> 12;                      // units per row
   const int nrows = gw < N ? (N - 1 - gw) / nw + 1 : 0;
   const int nu = nrows * G;
@@ -1453,7 +1465,7 @@ __global__ __launch_bounds__(256) void gemv_rowdot_kernel(RowdotIn in, const uin
   u32x4_t xr[PRO == PRO_X ? XL : 1];
   float xsr = 0.f;
   uint4 nx[J], nd[J];
-  constexpr int CI = PRO == PRO_NORM || PRO == PRO_NORM_ADD ? (NX * J * 64 + 255) / 256 : 1;   // chunks per thread
+  constexpr int CI = PRO == PRO_NORM || PRO == PRO_NORM_ADD ? (NX * J * 64 + NT - 1) / NT : 1;   // chunks per thread
   uint4 ng[CI];
   uint4 rv[PRO == PRO_RELU2 ? XL : 1];
   if (PRO == PRO_X) {
@@ -1487,7 +1499,7 @@ __global__ __launch_bounds__(256) void gemv_rowdot_kernel(RowdotIn in, const uin
     // flattened (NX, K) rows uses gamma chunk c mod nch)
 #pragma unroll
     for (int i = 0; i < CI; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NT * i;
       const uint32_t go = c < NX * nch ? (uint32_t)(c % nch) * 16u : (uint32_t)K * 2u;
       const u32x4_t vg = __builtin_amdgcn_raw_buffer_load_b128(rg, go, 0, 0);
       ng[i] = make_uint4(vg.x, vg.y, vg.z, vg.w);
@@ -1496,7 +1508,7 @@ __global__ __launch_bounds__(256) void gemv_rowdot_kernel(RowdotIn in, const uin
     const __amdgpu_buffer_rsrc_t ru = make_rsrc(in.x, (uint32_t)(NX * K) * 2u);
 #pragma unroll
     for (int r = 0; r < XL; ++r) {   // past NX * K: out of range, reads zero
-      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(ru, (uint32_t)(tid + 256 * r) * 16u, 0, 0);
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(ru, (uint32_t)(tid + NT * r) * 16u, 0, 0);
       rv[r] = make_uint4(v.x, v.y, v.z, v.w);
     }
   }
@@ -1518,7 +1530,7 @@ __global__ __launch_bounds__(256) void gemv_rowdot_kernel(RowdotIn in, const uin
   } else if (PRO == PRO_NORM || PRO == PRO_NORM_ADD) {
     // phase 1: wave m < NX takes row m's statistics (the norm kernel's own
     // routine and lane layout, so the same f64 sum) and parks the residual
-    // sums (bf16) and r in LDS; phase 2: the 256 threads norm and quantize
+    // sums (bf16) and r in LDS; phase 2: all threads norm and quantize
     // 8-element chunks, 16 consecutive chunks (one scale block) per DPP row
     uint4* sums = reinterpret_cast<uint4*>(rowdot_lds + ((sx_off + NX * nkb * 4 + 15) & ~15));
     float* rbs = reinterpret_cast<float*>(sums + NX * nch);
@@ -1537,7 +1549,7 @@ __global__ __launch_bounds__(256) void gemv_rowdot_kernel(RowdotIn in, const uin
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < CI; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NT * i;
       const bool valid = c < NX * nch;
       const int m = valid ? c / nch : 0;
       const uint4 xc = valid ? sums[c] : make_uint4(0, 0, 0, 0);
@@ -1555,7 +1567,7 @@ __global__ __launch_bounds__(256) void gemv_rowdot_kernel(RowdotIn in, const uin
   } else {
 #pragma unroll
     for (int r = 0; r < XL; ++r) {
-      const int c = tid + 256 * r;   // chunk of the flattened (NX, K) rows; 16 chunks = one block
+      const int c = tid + NT * r;   // chunk of the flattened (NX, K) rows; 16 chunks = one block
       float v[8];
       unpack8(rv[r], v);
       relu2_bf16(v);
@@ -1880,15 +1892,16 @@ static size_t gemv_direct_lds(int64_t M, int64_t K, int mt) {
 // shape), K blocks of a wave in registers (K <= 12288, and <= 4096 past 16
 // rows), the x copy in one round of 16 chunks per thread, and the LDS above
 // within a CU's 160 KiB.  Speed (same-box A/B at the reference decode shapes
-// and C5): direct wins while every 16-row block has a workgroup at once (<=
-// 512 blocks: the decode wo, w_down and q|k|v weights) and past N = 16384
-// (the 50257-row unembedding, where the staged kernel runs several rounds of
-// workgroups); in between (C5's 14336 rows, w_up's 9216) the staged kernel's
-// 4 KiB-contiguous row reads stream better than 64 bytes of 16 rows per load.
+// and C5): direct wins up to ~2.5 row blocks per CU (<= 640 blocks: the
+// decode wo, w_down, q|k|v and w_up weights; w_up 6.9 against 8.0 us at 8
+// rows) and past N = 16384 (the 50257-row unembedding, where the staged
+// kernel runs several rounds of workgroups); in between (C5's 14336 rows:
+// 14.8 against 13.1 us) the staged kernel's 4 KiB-contiguous row reads
+// stream better than 64 bytes of 16 rows per load.
 static bool gemv_direct_fits(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || M > 32 || (M > 8 && M <= 16)) return false;
   const int64_t nrb = (N + 15) / 16;
-  if (nrb > 512 && N <= 16384) return false;
+  if (nrb > 640 && N <= 16384) return false;
   const int mt = M <= 16 ? 1 : 2;
   const int64_t kpw = (K / 128 + 7) / 8;
   if (kpw > (mt == 1 ? 12 : 4)) return false;
@@ -1943,13 +1956,18 @@ static int launch_gemv_direct_x(const uint8_t* x_q, const float* x_s, const uint
   if constexpr (MT == 2) {
     return launch_gemv_direct_t<2, BNS, 4, PRO_X, 16, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
   } else {
+    // K blocks per wave: exact for the decode widths (3 at K = 2304, 9 at 9216), else rounded up
     if (xc <= 4) {
+      if (kpw <= 3) return launch_gemv_direct_t<1, BNS, 3, PRO_X, 4, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
       if (kpw <= 4) return launch_gemv_direct_t<1, BNS, 4, PRO_X, 4, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
       if (kpw <= 8) return launch_gemv_direct_t<1, BNS, 8, PRO_X, 4, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
+      if (kpw <= 9) return launch_gemv_direct_t<1, BNS, 9, PRO_X, 4, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
       return launch_gemv_direct_t<1, BNS, 12, PRO_X, 4, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
     }
+    if (kpw <= 3) return launch_gemv_direct_t<1, BNS, 3, PRO_X, 16, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
     if (kpw <= 4) return launch_gemv_direct_t<1, BNS, 4, PRO_X, 16, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
     if (kpw <= 8) return launch_gemv_direct_t<1, BNS, 8, PRO_X, 16, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
+    if (kpw <= 9) return launch_gemv_direct_t<1, BNS, 9, PRO_X, 16, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
     return launch_gemv_direct_t<1, BNS, 12, PRO_X, 16, 1>(x_q, x_s, none, w_q, w_s, out, M, N, K, st);
   }
 }
@@ -1968,6 +1986,9 @@ static int launch_gemv_direct(const uint8_t* x_q, const float* x_s, const uint8_
 template <int PRO>
 static int launch_gemv_direct_norm(const GemvNormIn& nin, const uint8_t* w_q, const float* w_s, int bn,
                                    __bf16* out, int M, int N, int K, hipStream_t st) {
+  if ((K / 128 + 7) / 8 <= 3)
+    return bn == 1 ? launch_gemv_direct_t<1, 1, 3, PRO, 1, 5>(nullptr, nullptr, nin, w_q, w_s, out, M, N, K, st)
+                   : launch_gemv_direct_t<1, 128, 3, PRO, 1, 5>(nullptr, nullptr, nin, w_q, w_s, out, M, N, K, st);
   return bn == 1 ? launch_gemv_direct_t<1, 1, 4, PRO, 1, 5>(nullptr, nullptr, nin, w_q, w_s, out, M, N, K, st)
                  : launch_gemv_direct_t<1, 128, 4, PRO, 1, 5>(nullptr, nullptr, nin, w_q, w_s, out, M, N, K, st);
 }
@@ -1995,26 +2016,27 @@ extern "C" int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* 
                         n, k, st);
 }
 
-template <int NX, int PRO, int XL, int J>
+template <int NX, int PRO, int XL, int J, int WPG = 4>
 static void launch_rowdot_k(const RowdotIn& in, const uint8_t* w_q, const float* w_s, int bns, __bf16* o,
                             int n, int k, int sx_off, size_t lds, hipStream_t st) {
   // persistent waves, one wave per weight row at a time: as many workgroups
   // as fit on the CUs at once (registers: once per instantiation; LDS: 160 KiB
-  // per CU), at most 8 per CU, so that no workgroup waits for a free slot
-  // (a function-local static: its initializer runs once, thread-safely)
+  // per CU), at most 32 waves per CU, so that no workgroup waits for a free
+  // slot (a function-local static: its initializer runs once, thread-safely)
   static const int occ_regs = [] {
     int v = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_rowdot_kernel<NX, PRO, XL, J>, 256, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_rowdot_kernel<NX, PRO, XL, J, WPG>, 64 * WPG, 0) !=
             hipSuccess || v <= 0)
-      v = 4;
+      v = 16 / WPG;
     return v;
   }();
-  int per_cu = occ_regs < 8 ? occ_regs : 8;
+  constexpr int kMaxPerCu = 32 / WPG;
+  int per_cu = occ_regs < kMaxPerCu ? occ_regs : kMaxPerCu;
   const int by_lds = (int)((160 * 1024) / (lds > 0 ? lds : 1));
   if (by_lds < per_cu) per_cu = by_lds < 1 ? 1 : by_lds;
-  const int64_t wgs = ((int64_t)n + 3) / 4, cap = (int64_t)per_cu * device_cus();
-  hipLaunchKernelGGL((gemv_rowdot_kernel<NX, PRO, XL, J>), dim3((unsigned)(wgs < cap ? wgs : cap)), dim3(256),
-                     lds, st, in, w_q, w_s, bns, o, n, k, sx_off);
+  const int64_t wgs = ((int64_t)n + WPG - 1) / WPG, cap = (int64_t)per_cu * device_cus();
+  hipLaunchKernelGGL((gemv_rowdot_kernel<NX, PRO, XL, J, WPG>), dim3((unsigned)(wgs < cap ? wgs : cap)),
+                     dim3(64 * WPG), lds, st, in, w_q, w_s, bns, o, n, k, sx_off);
 }
 
 // PRO_X: XL 4 KiB pieces of x; PRO_RELU2: XL 16-byte chunks of u per thread;
@@ -2037,20 +2059,21 @@ static int launch_rowdot(const RowdotIn& in, const uint8_t* w_q, const float* w_
                            ? (size_t)sx_off + (size_t)NX * (k / 128) * 4
                            : (((size_t)sx_off + (size_t)NX * (k / 128) * 4 + 15) & ~(size_t)15) +
                                  (size_t)NX * k * 2 + 16;
+    constexpr int W = kRowdotProWaves;
     if constexpr (PRO == PRO_RELU2) {
-      const int need = (NX * k + 2047) / 2048;
-      if (need <= 1) launch_rowdot_k<NX, PRO, 1, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (need <= 2) launch_rowdot_k<NX, PRO, 2, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (need <= 4) launch_rowdot_k<NX, PRO, 4, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (need <= 8) launch_rowdot_k<NX, PRO, 8, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else launch_rowdot_k<NX, PRO, 16, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      const int need = (NX * k / 8 + 64 * W - 1) / (64 * W);   // 16-byte chunks of u per thread
+      if (need <= 1) launch_rowdot_k<NX, PRO, 1, 1, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (need <= 2) launch_rowdot_k<NX, PRO, 2, 1, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (need <= 4) launch_rowdot_k<NX, PRO, 4, 1, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (need <= 8) launch_rowdot_k<NX, PRO, 8, 1, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else launch_rowdot_k<NX, PRO, 16, 1, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
     } else {
       const int jneed = (k / 8 + 63) / 64;
-      if (jneed <= 1) launch_rowdot_k<NX, PRO, 1, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (jneed <= 2) launch_rowdot_k<NX, PRO, 1, 2>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (jneed <= 4) launch_rowdot_k<NX, PRO, 1, 4>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (jneed <= 5) launch_rowdot_k<NX, PRO, 1, 5>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else launch_rowdot_k<NX, PRO, 1, 8>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      if (jneed <= 1) launch_rowdot_k<NX, PRO, 1, 1, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (jneed <= 2) launch_rowdot_k<NX, PRO, 1, 2, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (jneed <= 4) launch_rowdot_k<NX, PRO, 1, 4, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (jneed <= 5) launch_rowdot_k<NX, PRO, 1, 5, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else launch_rowdot_k<NX, PRO, 1, 8, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
     }
   }
   return TG_OK;
