@@ -50,11 +50,15 @@ decode       = KV-cached decode (decode.py) of the reference model config:
 io_floor     = (--only) config 2's bytes moved by csrc/probe/io_floor.hip with
                the fused norm kernel's access pattern and no arithmetic: the
                attainable rate of that read / write mix, beside the real kernel
+gemv_floor   = (--only) the reference decode weights at 8 rows: the direct
+               GEMV's loads moved by csrc/probe/gemv_stream.hip with no
+               arithmetic (with and without the x rows, cached and
+               non-temporal), beside tg_gemv_fp8 on the same weights
 cpu_baseline = the CPU oracle (numpy + C) on a row sample of the same step
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                       [--only step|norm_quant|norm_bwd|gemv|bwd_bf16|block_step|xent|decode|
-                              vendor_gemm|c1|io_floor]
+                              vendor_gemm|c1|io_floor|gemv_floor]
 """
 import argparse
 import json
@@ -218,7 +222,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--norm-iters", type=int, default=200)
     p.add_argument("--only", choices=["step", "norm_quant", "norm_bwd", "gemv", "bwd_bf16",
-                                      "block_step", "xent", "decode", "vendor_gemm", "c1", "io_floor"],
+                                      "block_step", "xent", "decode", "vendor_gemm", "c1", "io_floor",
+                                      "gemv_floor"],
                    help="run one secondary workload alone and print its JSON object")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (calibrates the FETCH_SIZE / "
@@ -439,6 +444,77 @@ def bench_io_floor(dev, iters):
     mix = [r for r in out["modes"] if r["mode"] == 2][0]
     best = max(mix[k]["GB/s"] for k in mix if k.startswith("rows_per_wave"))
     out["norm_vs_best_mix_floor"] = round(out["rms_norm_fp8_same_run"]["GB/s"] / best, 4)
+    return out
+
+
+def bench_gemv_floor(dev, iters):
+    """The streaming floor of the direct decode GEMV at the reference decode
+    weights (8 activation rows): libtg_probe.so's gemv_stream_kernel issues
+    the same weight loads on the same grid with no arithmetic, with and
+    without every workgroup's read of the x rows, with cached and with
+    non-temporal loads; tg_gemv_fp8 runs beside it on the same weights.
+    Weight copies rotate over > 800 MB, so HBM serves them."""
+    import ctypes
+    import torch
+    import _tglib as L
+    import build as tg_build
+    lib = L.lib()
+    if not os.path.exists(tg_build.PROBE_LIB):
+        raise RuntimeError(f"{tg_build.PROBE_LIB} is missing: run python train-gpt_amd/build.py")
+    probe = ctypes.CDLL(tg_build.PROBE_LIB)
+    probe.tg_probe_gemv_stream.restype = ctypes.c_int
+    probe.tg_probe_gemv_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                           ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_void_p]
+    M = 8
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    out = {"workload": "reference decode weights (d 2304, d_ff 9216) at 8 rows: the direct GEMV's loads without "
+                       "arithmetic (csrc/probe/gemv_stream.hip) beside tg_gemv_fp8", "cus": cus, "shapes": []}
+    # clock settle: ~50 ms of launches before the first timed one
+    wz = torch.zeros((6912, 2304), dtype=torch.uint8, device=dev)
+    sz = torch.empty(432 * 512, dtype=torch.int32, device=dev)
+    t_settle = time.perf_counter()
+    while (time.perf_counter() - t_settle) < 0.05:
+        for _ in range(20):
+            L.check(probe.tg_probe_gemv_stream(L.ptr(wz), 6912, 2304, None, 0, L.ptr(sz), 432, 1,
+                                               L.stream_of(wz)))
+        torch.cuda.synchronize()
+    del wz, sz
+    for name, N, K in (("wo", 2304, 2304), ("qkv", 6912, 2304), ("w_up", 9216, 2304), ("w_down", 2304, 9216)):
+        nset = int(800e6 // (N * K)) + 1
+        ws = [torch.randint(0, 126, (N, K), generator=g, device=dev, dtype=torch.uint8) for _ in range(nset)]
+        wsc = [torch.rand((N + 127) // 128, K // 128, generator=g, device=dev) * 1e-2 for _ in range(nset)]
+        xq = torch.randint(0, 126, (M, K), generator=g, device=dev, dtype=torch.uint8)
+        xs = torch.rand(M, K // 128, generator=g, device=dev)
+        o = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        nrb = (N + 15) // 16
+        grid = min(nrb, 2 * cus)
+        sink = torch.empty(grid * 512, dtype=torch.int32, device=dev)
+        st = L.stream_of(o)
+        wbytes = N * K
+        row = {"weight": name, "N": N, "K": K, "weight_bytes": wbytes, "grid": grid}
+
+        def rate(us):
+            return {"us_per_launch": round(us, 3), "weight_GB/s": round(wbytes / (us * 1e-6) / 1e9, 1)}
+
+        def gemv(i):
+            L.check(lib.tg_gemv_fp8(L.ptr(xq), L.ptr(xs), L.ptr(ws[i % nset]), L.ptr(wsc[i % nset]), 128, L.ptr(o),
+                                    M, N, K, 128, st))
+        # two passes over the four launches; the second pass is reported (the
+        # first pass over freshly allocated copies runs slower)
+        for _ in range(2):
+            for label, xb, cached in (("loads_cached", 0, 1), ("loads_cached_with_x", M * K, 1),
+                                      ("loads_nontemporal_with_x", M * K, 0)):
+                def launch(i, xb=xb, cached=cached):
+                    L.check(probe.tg_probe_gemv_stream(L.ptr(ws[i % nset]), N, K, L.ptr(xq), xb, L.ptr(sink),
+                                                       grid, cached, st))
+                row[label] = rate(_mean_launch_us(launch, iters))
+            row["tg_gemv_fp8"] = rate(_mean_launch_us(gemv, iters))
+        out["shapes"].append(row)
+        del ws, wsc
+        torch.cuda.empty_cache()
     return out
 
 
@@ -914,7 +990,7 @@ def main():
               "block_step": lambda d, _: bench_block(d), "xent": bench_xent,
               "decode": lambda d, _: bench_decode(d),
               "vendor_gemm": lambda d, _: bench_vendor_gemm(d, 20),
-              "c1": bench_c1, "io_floor": bench_io_floor}[args.only]
+              "c1": bench_c1, "io_floor": bench_io_floor, "gemv_floor": bench_gemv_floor}[args.only]
         print(json.dumps({args.only: fn(dev, args.norm_iters)}))
         return
     step = Step(dev)

@@ -54,16 +54,17 @@ def build_library(verbose: bool = False) -> str:
     return LIB
 
 
-PROBE_SRC = os.path.join(CSRC, "probe", "io_floor.hip")
+PROBE_SRCS = [os.path.join(CSRC, "probe", f) for f in ("io_floor.hip", "gemv_stream.hip")]
 PROBE_LIB = os.path.join(HERE, "libtg_probe.so")
 
 
 def build_probe(verbose: bool = False) -> str:
-    """Compile bench.py's I/O-floor probe (csrc/probe/io_floor.hip) into
+    """Compile bench.py's floor probes (csrc/probe/io_floor.hip: the fused norm's
+    I/O; csrc/probe/gemv_stream.hip: the direct decode GEMV's loads) into
     libtg_probe.so, linked against libtg_fp8.so for its error reporting.  It is
     measurement tooling: nothing in the package loads it."""
     tmp = PROBE_LIB + ".tmp"
-    cmd = [HIPCC, *FLAGS, "-shared", PROBE_SRC, "-L", HERE, "-ltg_fp8", "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    cmd = [HIPCC, *FLAGS, "-shared", *PROBE_SRCS, "-L", HERE, "-ltg_fp8", "-Wl,-rpath,$ORIGIN", "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"probe build failed:\n{r.stdout}\n{r.stderr}")
