@@ -11,8 +11,14 @@
  *
  * Layouts are row-major and contiguous.  bf16 is passed as uint16_t bits,
  * e4m3fn bytes as uint8_t (OCP float8_e4m3fn, the gfx950 FP8 format).
- * block_k must be 128 (the reference's DEFAULT_BLOCK_K, fp8.py:27, and the K
- * depth of one gfx950 FP8 MFMA).
+ * block_k: the reference's block_scaled_matmul takes any block_k dividing K
+ * (fp8.py:30-36, 55-56; DEFAULT_BLOCK_K = 128, fp8.py:27).  tg_quantize_rows,
+ * tg_quantize_cols, tg_gemm_fp8_nt, tg_block_scaled_matmul and
+ * tg_block_scaled_matmul_bwd_fp8 accept every block_k >= 1 that divides the
+ * contracted extent: 128 runs the tuned kernels (two FP8 MFMA K steps per
+ * scale block), any other size the general kernels (the same numeric
+ * contract, bytes and scales bit for bit; not tuned).  Every other entry
+ * point is a fused kernel of this library and takes block_k == 128 only.
  *
  * Reference citations are /root/reference/<file>:<line>.
  */
@@ -88,10 +94,12 @@ int tg_quantize_dual_pair_km(const void* x0, int64_t rows0, int64_t cols0, uint8
 
 /* jax.nn.scaled_matmul + bf16 cast as called at fp8.py:70-78 ("NT" layout):
  * c[m, n] = sum_kb a_s[m, kb] * b_s[n / b_scale_bn, kb] * sum_{k in kb} a_q[m, k] * b_q[n, k]
- * a_q: (M, K) e4m3fn, a_s: (M, K/128) f32; b_q: (N, K) e4m3fn;
- * b_s: (N, K/128) f32 when b_scale_bn == 1 (fp8.py:68's per-column scales) or
- *      (ceil(N/128), K/128) when b_scale_bn == 128 (128x128 weight tiles).
- * c: (M, N) bf16 (RNE, fp8.py:78) or f32 (c_dtype).  f32 accumulation. */
+ * a_q: (M, K) e4m3fn, a_s: (M, K/block_k) f32; b_q: (N, K) e4m3fn;
+ * b_s: (N, K/block_k) f32 when b_scale_bn == 1 (fp8.py:68's per-column scales)
+ *      or (ceil(N/128), K/block_k) when b_scale_bn == 128 (128x128 weight tiles
+ *      at block_k 128).
+ * c: (M, N) bf16 (RNE, fp8.py:78) or f32 (c_dtype).  f32 accumulation.
+ * block_k: any divisor of K (128: the tuned MFMA kernels). */
 int tg_gemm_fp8_nt(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s,
                    int b_scale_bn, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
                    int block_k, void* stream);
@@ -108,7 +116,7 @@ int tg_gemm_fp8_nt_km(const uint8_t* a_q, const float* a_s_km, const uint8_t* b_
 size_t tg_block_scaled_matmul_workspace(int64_t M, int64_t N, int64_t K, int block_k);
 
 /* _fp8_forward (fp8.py:50-78) in one call: quantize a (M, K) and b.T (b is (K, N)),
- * then the scaled GEMM into out (M, N) bf16.  a and b are bf16.
+ * then the scaled GEMM into out (M, N) bf16.  a and b are bf16; block_k any divisor of K.
  * workspace: >= tg_block_scaled_matmul_workspace(M, N, K, block_k) bytes, 256-B aligned. */
 int tg_block_scaled_matmul(const void* a, const void* b, void* out, int64_t M, int64_t N,
                            int64_t K, int block_k, void* workspace, size_t workspace_bytes,
@@ -124,7 +132,7 @@ int tg_block_scaled_matmul(const void* a, const void* b, void* out, int64_t M, i
  * C3's forward (8192 x 2048 x 8192) needs 34.6 MB.  Output bits equal
  * tg_block_scaled_matmul's.  All calls on one device share the array: calls
  * that overlap on one device (different streams, or host threads) race;
- * serialize them.  a, b 16-byte aligned. */
+ * serialize them.  a, b 16-byte aligned; block_k 128. */
 #define TG_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 int tg_block_scaled_matmul_noalloc(const void* a, const void* b, void* out, int64_t M, int64_t N,
                                    int64_t K, int block_k, void* stream);
@@ -137,7 +145,9 @@ size_t tg_block_scaled_matmul_bwd_workspace(int64_t M, int64_t N, int64_t K, int
  * gradients; fp8.py:85-98 itself is the bf16 straight-through rule):
  *   da (M, K) = fwd(g, b.T):  g row-quantized along N, b row-quantized along N
  *   db (K, N) = fwd(a.T, g):  a.T and g.T quantized along M
- * a: (M, K), b: (K, N), g: (M, N), all bf16; da, db bf16.  M % 128 == 0. */
+ * a: (M, K), b: (K, N), g: (M, N), all bf16; da, db bf16.  block_k any
+ * divisor of K; M and N multiples of block_k (a caller pads a ragged last
+ * block with zeros, which change neither amax nor any product). */
 int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, const void* g, void* da,
                                    void* db, int64_t M, int64_t N, int64_t K, int block_k,
                                    void* workspace, size_t workspace_bytes, void* stream);

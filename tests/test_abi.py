@@ -28,8 +28,20 @@ def test_library_exports_every_declared_symbol():
 def test_invalid_arguments_return_einval_without_launch():
     lib = L.lib()
     nul = ctypes.c_void_p(0)
-    assert lib.tg_quantize_rows(nul, 0, 4, 256, 64, nul, nul, nul) == L.TG_EINVAL
+    assert lib.tg_quantize_rows(nul, 0, 4, 256, 0, nul, nul, nul) == L.TG_EINVAL
     assert b"block_k" in lib.tg_last_error()
+    # any block_k dividing the extent is accepted (the general path); 96 does not divide 256
+    assert lib.tg_quantize_rows(nul, 0, 4, 256, 64, nul, nul, nul) == L.TG_EINVAL
+    assert b"null pointer" in lib.tg_last_error()
+    assert lib.tg_quantize_rows(nul, 0, 4, 256, 96, nul, nul, nul) == L.TG_EINVAL
+    assert b"not divisible" in lib.tg_last_error()
+    assert lib.tg_gemm_fp8_nt(nul, nul, nul, nul, 1, nul, 0, 4, 4, 256, 0, nul) == L.TG_EINVAL
+    assert b"block_k" in lib.tg_last_error()
+    # the pre-quantized-weight GEMV and the K-block-major GEMM are block_k = 128 only
+    assert lib.tg_gemv_fp8(nul, nul, nul, nul, 1, nul, 1, 4, 256, 64, nul) == L.TG_EINVAL
+    assert b"block_k must be 128" in lib.tg_last_error()
+    assert lib.tg_gemm_fp8_nt_km(nul, nul, nul, nul, 1, nul, 0, 4, 4, 256, 64, nul) == L.TG_EINVAL
+    assert b"block_k must be 128" in lib.tg_last_error()
     assert lib.tg_quantize_rows(nul, 0, 4, 200, 128, nul, nul, nul) == L.TG_EINVAL
     assert b"not divisible" in lib.tg_last_error()
     assert lib.tg_quantize_rows(nul, 5, 4, 256, 128, nul, nul, nul) == L.TG_EINVAL

@@ -230,8 +230,8 @@ def test_errors(dev):
     x = torch.zeros((4, 200), dtype=torch.bfloat16, device=dev)
     with pytest.raises(ValueError, match="not divisible by block_k"):
         fp8.quantize_fp8(x)
-    with pytest.raises(NotImplementedError):
-        fp8.quantize_fp8(torch.zeros((4, 256), dtype=torch.bfloat16, device=dev), block_k=64)
+    with pytest.raises(NotImplementedError):   # the fused dual quantizer is block_k = 128 only
+        fp8.quantize_fp8_dual(torch.zeros((256, 256), dtype=torch.bfloat16, device=dev), block_k=64)
     q, s = fp8.quantize_fp8(torch.zeros((0, 256), dtype=torch.bfloat16, device=dev))
     assert q.shape == (0, 256) and s.shape == (0, 2)
     assert bf16_bits is not None

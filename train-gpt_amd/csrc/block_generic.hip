@@ -1,0 +1,194 @@
+// Block-scaled FP8 for any block_k that divides the contracted extent: the
+// reference's block_scaled_matmul takes block_k as an argument
+// (/root/reference/fp8.py:30-36, 55-56), while the tuned kernels of this
+// library fix it at 128 (one scale block per FP8 MFMA K step pair).  These
+// kernels are the general path the C ABI takes for every other block size.
+// They follow the same numeric contract as the 128 path, written per element:
+//   scale = max(amax / 448, 1e-30)  (IEEE divide; amax NaN-propagating)
+//   q     = e4m3fn(x / scale)       (IEEE divide, RNE; the non-finite-scale
+//                                    rule of e4m3_nonfinite_scale)
+// so a block's bytes and scale are those the 128 kernels give for the same
+// block, and the GEMM adds each block's exact-in-f32 partial dot product as
+// acc = fma(P, sa * sb, acc) in block order (fp8.py:70-76), in f32 on the VALU.
+// They are correct for every block size, not tuned: one thread per block in
+// the quantizers, a 64 x 64 LDS-tiled VALU GEMM.
+#include "tg_device.h"
+#include "tg_host.h"
+
+namespace tg {
+
+__device__ __forceinline__ float gb_load(const void* x, int64_t i, bool f32) {
+  return f32 ? reinterpret_cast<const float*>(x)[i]
+             : __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(x)[i] << 16);
+}
+
+// e4m3fn byte of x / s
+__device__ __forceinline__ uint8_t gb_quant1(float x, float s, bool finite_scale) {
+  return (uint8_t)(finite_scale ? (e4m3x4(x / s, 0.0f, 0.0f, 0.0f) & 0xFFu) : e4m3_nonfinite_scale(x, s));
+}
+
+__device__ __forceinline__ bool gb_finite(float s) { return (__float_as_uint(s) & 0x7F800000u) != 0x7F800000u; }
+
+// one thread per (row, block): q (rows, cols), s (rows, cols / bk)
+template <bool F32_IN>
+__global__ __launch_bounds__(256) void quant_rows_gb_kernel(const void* __restrict__ x, int64_t rows,
+                                                            int64_t cols, int bk, uint8_t* __restrict__ q,
+                                                            float* __restrict__ s) {
+  const int64_t nb = cols / bk;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * nb) return;
+  const int64_t r = i / nb, b = i - r * nb;
+  const int64_t base = r * cols + b * bk;
+  uint32_t m = 0;
+  for (int k = 0; k < bk; ++k) m = max(m, __float_as_uint(gb_load(x, base + k, F32_IN)) & 0x7FFFFFFFu);
+  const float sc = block_scale(m);
+  s[i] = sc;
+  const bool fin = gb_finite(sc);
+  for (int k = 0; k < bk; ++k) q[base + k] = gb_quant1(gb_load(x, base + k, F32_IN), sc, fin);
+}
+
+// x (R, C) bf16 -> the quantization of x.T along R: q_t (C, R), s_t (C, R / bk);
+// one thread per (row block, column), columns fastest (coalesced reads of x)
+__global__ __launch_bounds__(256) void quant_cols_gb_kernel(const uint16_t* __restrict__ x, int64_t R, int64_t C,
+                                                            int bk, uint8_t* __restrict__ qt,
+                                                            float* __restrict__ st) {
+  const int64_t nb = R / bk;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nb * C) return;
+  const int64_t b = i / C, c = i - b * C;
+  const int64_t r0 = b * bk;
+  uint32_t m = 0;
+  for (int k = 0; k < bk; ++k) m = max(m, ((uint32_t)x[(r0 + k) * C + c] << 16) & 0x7FFFFFFFu);
+  const float sc = block_scale(m);
+  st[c * nb + b] = sc;
+  const bool fin = gb_finite(sc);
+  for (int k = 0; k < bk; ++k)
+    qt[c * R + r0 + k] = gb_quant1(__uint_as_float((uint32_t)x[(r0 + k) * C + c] << 16), sc, fin);
+}
+
+// C (M, N) = sum over K blocks b of (A_b . B_b^T) * sa[m][b] * sb[n / bn][b];
+// A (M, K), B (N, K) e4m3fn bytes.  Workgroup tile 64 x 64, thread (tx, ty)
+// owns rows 4 ty .. +3 and columns 4 tx .. +3.  K walks in 32-byte chunks
+// staged through LDS transposed ([k][row], so a thread's 4 rows at one k are
+// one 32-bit read); the block's partial sums P run in k order and are folded
+// into the accumulator at each block end.
+constexpr int kGbTile = 64, kGbKc = 32, kGbPitch = kGbTile + 4;
+
+template <bool OUT_F32>
+__global__ __launch_bounds__(256) void gemm_gb_kernel(const uint8_t* __restrict__ A, const float* __restrict__ SA,
+                                                      const uint8_t* __restrict__ B, const float* __restrict__ SB,
+                                                      int bn, void* __restrict__ Cout, int M, int N, int K,
+                                                      int bk) {
+  __shared__ __attribute__((aligned(16))) uint8_t at[kGbKc][kGbPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t bt[kGbKc][kGbPitch];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int m0 = blockIdx.y * kGbTile, n0 = blockIdx.x * kGbTile;
+  const int nb = K / bk;
+  const int nsb_rows = (N + bn - 1) / bn;
+  // chunk loader: thread t copies 8 bytes of row t / 4 (bytes 8 (t % 4) ..)
+  const int lr = tid >> 2, lk = (tid & 3) * 8;
+  float acc[4][4], P[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = P[i][j] = 0.0f;
+  int kin = 0, blk = 0;   // position inside the current K block, its index
+  for (int k0 = 0; k0 < K; k0 += kGbKc) {
+    __syncthreads();   // the previous chunk is read by every thread
+    {
+      const int ma = m0 + lr, nbr = n0 + lr;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int k = k0 + lk + e;
+        at[lk + e][lr] = (ma < M && k < K) ? A[(int64_t)ma * K + k] : (uint8_t)0;
+        bt[lk + e][lr] = (nbr < N && k < K) ? B[(int64_t)nbr * K + k] : (uint8_t)0;
+      }
+    }
+    __syncthreads();
+    const int kn = K - k0 < kGbKc ? K - k0 : kGbKc;
+    for (int kk = 0; kk < kn; ++kk) {
+      const uint32_t a4 = *reinterpret_cast<const uint32_t*>(&at[kk][ty * 4]);
+      const uint32_t b4 = *reinterpret_cast<const uint32_t*>(&bt[kk][tx * 4]);
+      typedef float v2f_t __attribute__((ext_vector_type(2)));
+      const v2f_t a01 = __builtin_amdgcn_cvt_pk_f32_fp8(a4, false), a23 = __builtin_amdgcn_cvt_pk_f32_fp8(a4, true);
+      const v2f_t b01 = __builtin_amdgcn_cvt_pk_f32_fp8(b4, false), b23 = __builtin_amdgcn_cvt_pk_f32_fp8(b4, true);
+      const float av[4] = {a01.x, a01.y, a23.x, a23.y}, bv[4] = {b01.x, b01.y, b23.x, b23.y};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) P[i][j] = __builtin_fmaf(av[i], bv[j], P[i][j]);
+      if (++kin == bk) {   // block end (uniform over the workgroup)
+        float sa[4], sb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = m0 + ty * 4 + i;
+          sa[i] = m < M ? SA[(int64_t)m * nb + blk] : 0.0f;
+          const int n = n0 + tx * 4 + i;
+          const int sr = n < N ? n / bn : 0;
+          sb[i] = n < N && sr < nsb_rows ? SB[(int64_t)sr * nb + blk] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[i][j] = __builtin_fmaf(P[i][j], sa[i] * sb[j], acc[i][j]);
+            P[i][j] = 0.0f;
+          }
+        kin = 0;
+        ++blk;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + ty * 4 + i;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + tx * 4 + j;
+      if (n >= N) continue;
+      if (OUT_F32) reinterpret_cast<float*>(Cout)[(int64_t)m * N + n] = acc[i][j];
+      else reinterpret_cast<uint16_t*>(Cout)[(int64_t)m * N + n] = (uint16_t)pack_bf16x2(acc[i][j], 0.0f);
+    }
+  }
+}
+
+static unsigned gb_grid(int64_t threads) { return (unsigned)((threads + 255) / 256); }
+
+int launch_quant_rows_gb(const void* x, int x_dtype, int64_t rows, int64_t cols, int bk, uint8_t* q, float* s,
+                         hipStream_t st) {
+  const int64_t n = rows * (cols / bk);
+  if (n == 0) return TG_OK;
+  if (n / 256 >= 0x7FFFFFFF) return einval("quantize_rows: too many blocks");
+  if (x_dtype == TG_DTYPE_F32)
+    hipLaunchKernelGGL(quant_rows_gb_kernel<true>, dim3(gb_grid(n)), dim3(256), 0, st, x, rows, cols, bk, q, s);
+  else
+    hipLaunchKernelGGL(quant_rows_gb_kernel<false>, dim3(gb_grid(n)), dim3(256), 0, st, x, rows, cols, bk, q, s);
+  return check_launch("quantize_rows (block_k != 128)");
+}
+
+int launch_quant_cols_gb(const void* x, int64_t rows, int64_t cols, int bk, uint8_t* q_t, float* s_t,
+                         hipStream_t st) {
+  const int64_t n = (rows / bk) * cols;
+  if (n == 0) return TG_OK;
+  if (n / 256 >= 0x7FFFFFFF) return einval("quantize_cols: too many blocks");
+  hipLaunchKernelGGL(quant_cols_gb_kernel, dim3(gb_grid(n)), dim3(256), 0, st,
+                     reinterpret_cast<const uint16_t*>(x), rows, cols, bk, q_t, s_t);
+  return check_launch("quantize_cols (block_k != 128)");
+}
+
+int launch_gemm_gb(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s, int bn, void* c,
+                   int c_dtype, int64_t M, int64_t N, int64_t K, int bk, hipStream_t st) {
+  if (M == 0 || N == 0) return TG_OK;
+  if ((M + kGbTile - 1) / kGbTile > 65535) return einval("gemm_fp8_nt (block_k != 128): M too large");
+  const dim3 grid((unsigned)((N + kGbTile - 1) / kGbTile), (unsigned)((M + kGbTile - 1) / kGbTile));
+  if (c_dtype == TG_DTYPE_F32)
+    hipLaunchKernelGGL(gemm_gb_kernel<true>, grid, dim3(256), 0, st, a_q, a_s, b_q, b_s, bn, c, (int)M, (int)N,
+                       (int)K, bk);
+  else
+    hipLaunchKernelGGL(gemm_gb_kernel<false>, grid, dim3(256), 0, st, a_q, a_s, b_q, b_s, bn, c, (int)M, (int)N,
+                       (int)K, bk);
+  return check_launch("gemm_fp8_nt (block_k != 128)");
+}
+
+}  // namespace tg

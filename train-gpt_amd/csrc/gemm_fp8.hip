@@ -1643,8 +1643,11 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rowdot_kernel(RowdotIn in, cons
 
 using namespace tg;
 
-static int check_gemm_args(const char* who, int64_t M, int64_t N, int64_t K, int block_k, int bns) {
-  if (block_k != 128) return einval("block_k must be 128");
+// any_block: the entry has the general path for block_k != 128 (block_generic.hip)
+static int check_gemm_args(const char* who, int64_t M, int64_t N, int64_t K, int block_k, int bns,
+                           bool any_block = false) {
+  if (any_block ? block_k <= 0 : block_k != 128)
+    return einval(any_block ? "block_k must be positive" : "block_k must be 128");
   if (M < 0 || N < 0 || K <= 0) return einval("bad GEMM shape");
   if (K % block_k) return einval("K not divisible by block_k");
   if (M > 0x7FFFFFFF || N > 0x7FFFFFFF || K > 0x7FFFFFFF) return einval("GEMM dimension too large");
@@ -1656,10 +1659,12 @@ static int check_gemm_args(const char* who, int64_t M, int64_t N, int64_t K, int
 static int gemm_fp8_nt_entry(const char* who, const uint8_t* a_q, const float* a_s, const uint8_t* b_q,
                              const float* b_s, int b_scale_bn, void* c, int c_dtype, int64_t M,
                              int64_t N, int64_t K, int block_k, void* stream, bool skm) {
-  TG_TRY(check_gemm_args(who, M, N, K, block_k, b_scale_bn));
+  TG_TRY(check_gemm_args(who, M, N, K, block_k, b_scale_bn, !skm));
   if (c_dtype != TG_DTYPE_BF16 && c_dtype != TG_DTYPE_F32) return einval("gemm_fp8_nt: bad c_dtype");
   if (M == 0 || N == 0) return TG_OK;
   if (!a_q || !a_s || !b_q || !b_s || !c) return einval("gemm_fp8_nt: null pointer");
+  if (block_k != 128)
+    return launch_gemm_gb(a_q, a_s, b_q, b_s, b_scale_bn, c, c_dtype, M, N, K, block_k, as_stream(stream));
   if (!aligned(a_q, 16) || !aligned(b_q, 16)) return einval("gemm_fp8_nt: operands must be 16-byte aligned");
   return launch_gemm_fp8(a_q, a_s, b_q, b_s, b_scale_bn, c, c_dtype, M, N, K, as_stream(stream), skm);
 }
@@ -1708,14 +1713,33 @@ static int block_scaled_matmul_on(const void* a, const void* b, void* out, int64
   return launch_gemm_fp8(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, K, st, true);   // fp8.py:70-78
 }
 
+// The forward composite for block_k != 128: row-major scales, the general kernels.
+static int block_scaled_matmul_gb(const void* a, const void* b, void* out, int64_t M, int64_t N, int64_t K,
+                                  int bk, void* workspace, hipStream_t st) {
+  const int64_t nkb = K / bk;
+  uint8_t* p = reinterpret_cast<uint8_t*>(workspace);
+  uint8_t* qa = p;                 p += align256((size_t)M * K);
+  float* sa = reinterpret_cast<float*>(p);   p += align256((size_t)M * nkb * 4);
+  uint8_t* qb = p;                 p += align256((size_t)N * K);
+  float* sb = reinterpret_cast<float*>(p);
+  TG_TRY(launch_quant_rows_gb(a, TG_DTYPE_BF16, M, K, bk, qa, sa, st));     // fp8.py:66
+  TG_TRY(launch_quant_cols_gb(b, K, N, bk, qb, sb, st));                     // fp8.py:68
+  return launch_gemm_gb(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, K, bk, st);   // fp8.py:70-78
+}
+
 extern "C" int tg_block_scaled_matmul(const void* a, const void* b, void* out, int64_t M,
                                       int64_t N, int64_t K, int block_k, void* workspace,
                                       size_t workspace_bytes, void* stream) {
-  TG_TRY(check_gemm_args("block_scaled_matmul", M, N, K, block_k, 1));
+  TG_TRY(check_gemm_args("block_scaled_matmul", M, N, K, block_k, 1, true));
   if (M == 0 || N == 0) return TG_OK;
   if (!a || !b || !out || !workspace) return einval("block_scaled_matmul: null pointer");
   if (workspace_bytes < tg_block_scaled_matmul_workspace(M, N, K, block_k))
     return einval("block_scaled_matmul: workspace too small");
+  if (block_k != 128) {
+    if (!aligned(workspace, 256) || !aligned(a, 2) || !aligned(b, 2))
+      return einval("block_scaled_matmul: a, b must be 2-byte and workspace 256-byte aligned");
+    return block_scaled_matmul_gb(a, b, out, M, N, K, block_k, workspace, as_stream(stream));
+  }
   if (!aligned(workspace, 256) || !aligned(a, 16) || !aligned(b, 16))
     return einval("block_scaled_matmul: a, b must be 16-byte and workspace 256-byte aligned");
   return block_scaled_matmul_on(a, b, out, M, N, K, workspace, as_stream(stream));
@@ -1788,12 +1812,36 @@ extern "C" int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, cons
                                               void* da, void* db, int64_t M, int64_t N, int64_t K,
                                               int block_k, void* workspace,
                                               size_t workspace_bytes, void* stream) {
-  TG_TRY(check_gemm_args("block_scaled_matmul_bwd_fp8", M, N, K, block_k, 1));
-  if (M % 128 || N % 128) return einval("block_scaled_matmul_bwd_fp8: M and N must be multiples of 128");
+  TG_TRY(check_gemm_args("block_scaled_matmul_bwd_fp8", M, N, K, block_k, 1, true));
+  if (M % block_k || N % block_k)
+    return einval("block_scaled_matmul_bwd_fp8: M and N must be multiples of block_k");
   if (M == 0 || N == 0) return TG_OK;
   if (!a || !b || !g || !da || !db || !workspace) return einval("block_scaled_matmul_bwd_fp8: null pointer");
   if (workspace_bytes < tg_block_scaled_matmul_bwd_workspace(M, N, K, block_k))
     return einval("block_scaled_matmul_bwd_fp8: workspace too small");
+  if (block_k != 128) {
+    // the general kernels, row-major scales: g along N, b along N, a.T along M, g.T along M
+    if (!aligned(workspace, 256) || !aligned(a, 2) || !aligned(b, 2) || !aligned(g, 2))
+      return einval("block_scaled_matmul_bwd_fp8: inputs must be 2-byte and workspace 256-byte aligned");
+    hipStream_t st = as_stream(stream);
+    const int bk = block_k;
+    const int64_t mkb = M / bk, nkb = N / bk;
+    uint8_t* p = reinterpret_cast<uint8_t*>(workspace);
+    uint8_t* qg = p;    p += align256((size_t)M * N);
+    float* sg = reinterpret_cast<float*>(p);    p += align256((size_t)M * nkb * 4);
+    uint8_t* qb = p;    p += align256((size_t)K * N);
+    float* sb = reinterpret_cast<float*>(p);    p += align256((size_t)K * nkb * 4);
+    uint8_t* qat = p;   p += align256((size_t)K * M);
+    float* sat = reinterpret_cast<float*>(p);   p += align256((size_t)K * mkb * 4);
+    uint8_t* qgt = p;   p += align256((size_t)N * M);
+    float* sgt = reinterpret_cast<float*>(p);
+    TG_TRY(launch_quant_rows_gb(g, TG_DTYPE_BF16, M, N, bk, qg, sg, st));
+    TG_TRY(launch_quant_rows_gb(b, TG_DTYPE_BF16, K, N, bk, qb, sb, st));
+    TG_TRY(launch_gemm_gb(qg, sg, qb, sb, 1, da, TG_DTYPE_BF16, M, K, N, bk, st));      // dX = g . b.T
+    TG_TRY(launch_quant_cols_gb(a, M, K, bk, qat, sat, st));
+    TG_TRY(launch_quant_cols_gb(g, M, N, bk, qgt, sgt, st));
+    return launch_gemm_gb(qat, sat, qgt, sgt, 1, db, TG_DTYPE_BF16, K, N, M, bk, st);   // dW = a.T . g
+  }
   if (!aligned(workspace, 256) || !aligned(a, 16) || !aligned(b, 16) || !aligned(g, 16))
     return einval("block_scaled_matmul_bwd_fp8: inputs must be 16-byte and workspace 256-byte aligned");
   hipStream_t st = as_stream(stream);

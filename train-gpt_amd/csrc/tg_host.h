@@ -71,6 +71,14 @@ int launch_quant_dual_pair(const void* x0, int64_t rows0, int64_t cols0, uint8_t
 int launch_gemm_fp8(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s,
                     int b_scale_bn, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
                     hipStream_t st, bool skm = false);
+// The general path for block_k != 128 (block_generic.hip): row-major scales,
+// any block_k >= 1 dividing the contracted extent.
+int launch_quant_rows_gb(const void* x, int x_dtype, int64_t rows, int64_t cols, int bk, uint8_t* q, float* s,
+                         hipStream_t st);
+int launch_quant_cols_gb(const void* x, int64_t rows, int64_t cols, int bk, uint8_t* q_t, float* s_t,
+                         hipStream_t st);
+int launch_gemm_gb(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s, int bn, void* c,
+                   int c_dtype, int64_t M, int64_t N, int64_t K, int bk, hipStream_t st);
 
 }  // namespace tg
 

@@ -36,14 +36,24 @@ E4M3_MAX = 448.0          # fp8.py:26
 DEFAULT_BLOCK_K = 128     # fp8.py:27
 BACKWARD_MODE = "fp8"
 
-_SUPPORTED_BLOCK_K = (128,)
+# block_k = 128 runs the tuned kernels (one scale block per pair of FP8 MFMA K
+# steps); any other block size dividing K runs the library's general
+# block-size kernels (correct for every block size, not tuned).  The fused
+# paths that exist only for 128 (the one-read dual quantizers, the kept FP8
+# residuals, relu^2 quantization) are taken only at 128.
+TUNED_BLOCK_K = 128
 
 
 def _check_block_k(block_k: int) -> None:
-    if block_k not in _SUPPORTED_BLOCK_K:
-        raise NotImplementedError(
-            f"block_k={block_k}: the gfx950 kernels implement block_k=128 "
-            "(one FP8 MFMA K step per scale block)")
+    if not isinstance(block_k, int) or block_k < 1:
+        raise ValueError(f"block_k must be a positive integer, got {block_k!r}")
+
+
+def _check_block_k_tuned(block_k: int, what: str) -> None:
+    _check_block_k(block_k)
+    if block_k != TUNED_BLOCK_K:
+        raise NotImplementedError(f"{what}: block_k={block_k}: this fused kernel exists for block_k=128 only "
+                                  "(quantize_fp8 takes any block_k)")
 
 
 def block_scaled_matmul(a: torch.Tensor, b: torch.Tensor, block_k: int = DEFAULT_BLOCK_K) -> torch.Tensor:
@@ -101,7 +111,7 @@ def quantize_relu2(x: torch.Tensor, block_k: int = DEFAULT_BLOCK_K):
     """_quantize_to_fp8 of bf16(relu(x)^2) along the last axis (model.py:72's
     activation fused with the quantization feeding the next matmul); x bf16."""
     _L.require_gpu(x)
-    _check_block_k(block_k)
+    _check_block_k_tuned(block_k, "quantize_relu2")
     if x.dtype != torch.bfloat16:
         raise TypeError("quantize_relu2: x must be bfloat16")
     K = x.shape[-1]
@@ -132,7 +142,7 @@ def quantize_fp8_dual(x: torch.Tensor, block_k: int = DEFAULT_BLOCK_K):
     bit to quantize_fp8(x) and quantize_fp8(x, transpose=True).  R and C must
     be multiples of block_k (the FP8 backward's dY)."""
     _L.require_gpu(x)
-    _check_block_k(block_k)
+    _check_block_k_tuned(block_k, "quantize_fp8_dual")
     if x.dim() != 2 or x.dtype != torch.bfloat16:
         raise ValueError("quantize_fp8_dual needs a 2-D bfloat16 tensor")
     R, C = x.shape
@@ -155,7 +165,7 @@ def quantize_fp8_dual_pair(x0: torch.Tensor, x1: torch.Tensor, block_k: int = DE
     fp8.py:66,68, with the backward's forms from the same reads): returns the
     two 4-tuples, bit for bit those of quantize_fp8_dual on each tensor."""
     _L.require_gpu(x0, x1)
-    _check_block_k(block_k)
+    _check_block_k_tuned(block_k, "quantize_fp8_dual_pair")
     xs, outs, args = [], [], []
     for x in (x0, x1):
         if x.dim() != 2 or x.dtype != torch.bfloat16:
@@ -221,19 +231,25 @@ def _scaled_matmul_km(a_q, a_s_km, b_q, b_s_km):
 
 def scaled_matmul(a_q, a_s, b_q, b_s, b_scale_bn: int = 1, out_dtype=torch.bfloat16):
     """The scaled GEMM of fp8.py:70-76 on already-quantized operands ("NT"):
-    a_q (M, K), b_q (N, K) e4m3fn; a_s (M, K/128), b_s (N or ceil(N/128), K/128) f32.
-    Returns (M, N) in out_dtype (bf16 by RNE, or f32)."""
+    a_q (M, K), b_q (N, K) e4m3fn; a_s (M, K/bk), b_s (N or ceil(N/128), K/bk)
+    f32, where the block size bk = K / a_s.shape[1] (128 unless the operands
+    were quantized with another block_k).  Returns (M, N) in out_dtype (bf16 by
+    RNE, or f32)."""
     _L.require_gpu(a_q, b_q)
     M, K = a_q.shape
     N = b_q.shape[0]
     if b_q.shape[1] != K:
         raise ValueError(f"contracted-dim mismatch: a K={K}, b K={b_q.shape[1]}")
+    nkb = a_s.shape[1] if a_s.dim() == 2 else 0
+    if nkb < 1 or K % nkb or b_s.shape[-1] != nkb:
+        raise ValueError(f"scales do not tile K={K}: a_s {tuple(a_s.shape)}, b_s {tuple(b_s.shape)}")
+    block_k = K // nkb
     c = torch.empty((M, N), dtype=out_dtype, device=a_q.device)
     code = _L.TG_DTYPE_F32 if out_dtype == torch.float32 else _L.TG_DTYPE_BF16
     a_q, b_q = a_q.contiguous(), b_q.contiguous()
     a_s, b_s = a_s.contiguous().float(), b_s.contiguous().float()
     _L.check(_L.lib().tg_gemm_fp8_nt(_L.ptr(a_q), _L.ptr(a_s), _L.ptr(b_q), _L.ptr(b_s),
-                                     b_scale_bn, _L.ptr(c), code, M, N, K, DEFAULT_BLOCK_K,
+                                     b_scale_bn, _L.ptr(c), code, M, N, K, block_k,
                                      _L.stream_of(a_q)))
     return c
 
@@ -316,7 +332,7 @@ def _fp8_backward(block_k, residuals, g):
             _L.ptr(ws), ws_bytes, _L.stream_of(a_2d)))
     else:
         u8 = torch.uint8
-        if g_2d.dtype == bf:
+        if g_2d.dtype == bf and block_k == TUNED_BLOCK_K:
             qg, sg, qgt, sgt = quantize_fp8_dual(g_2d, block_k)    # g along N and g.T along M
         else:
             qg, sg = quantize_fp8(g_2d, block_k)                   # g along N
@@ -434,7 +450,7 @@ class _BlockScaledMatmul(torch.autograd.Function):
             leading, K, N = _validate(a, b, block_k)
             _check_block_k(block_k)
             M = a.numel() // K if K else 0
-            if M > 0 and N > 0 and M % block_k == 0 and N % block_k == 0:
+            if block_k == TUNED_BLOCK_K and M > 0 and N > 0 and M % block_k == 0 and N % block_k == 0:
                 out, res_a, res_b = _fp8_forward_quantized_residuals(a, b, block_k, need_da,
                                                                      need_db)
                 ctx.quantized = True
@@ -583,7 +599,7 @@ class QuantizedWeight:
                  block_k: int = DEFAULT_BLOCK_K):
         if bn not in (1, 128):
             raise ValueError("bn must be 1 or 128")
-        _check_block_k(block_k)
+        _check_block_k_tuned(block_k, "QuantizedWeight")
         if q.dim() != 2 or scales.dim() != 2:
             raise ValueError("q and scales must be 2-D")
         N, K = q.shape
@@ -734,7 +750,7 @@ def fp8_gemv(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, w_scale_bn: 
     pre-quantized weight (w_q (N, K), w_s) -> (..., N) bf16.  For 1-2 rows the
     VALU kernel is used unless exact (see _gemv_prequant)."""
     _L.require_gpu(x, w_q)
-    _check_block_k(block_k)
+    _check_block_k_tuned(block_k, "fp8_gemv")
     *lead, K = x.shape
     N = w_q.shape[0]
     if w_q.shape[1] != K:
