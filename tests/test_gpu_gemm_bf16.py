@@ -169,6 +169,24 @@ def test_bf16_backward_matches_oracle(dev, lead, K, N):
         assert _within_bound(got.float().cpu().numpy(), ref, s, k)
 
 
+@pytest.mark.parametrize("M,K,N", [(100, 256, 200), (1, 128, 8), (515, 1152, 520), (2048, 768, 3072)])
+def test_bf16_backward_tn_same_bits_as_packed(dev, M, K, N):
+    """db = a.T . g from the contraction-major kernel (bf16 a and g, read in
+    place through transposed LDS reads) equals, bit for bit, db from the NT
+    kernel on the packed transposes (the same a passed as f32, which forces
+    the packing): the same products in the same MFMA order.  Ragged output
+    tiles (K, N not multiples of 256) and contraction (M not a multiple of 32)."""
+    rng = np.random.default_rng(M + K + N)
+    a = ob.randn_bf16(rng, (M, K))
+    b = ob.randn_bf16(rng, (K, N), std=0.02)
+    g = ob.randn_bf16(rng, (M, N), std=1e-3)
+    _, db_tn = _bf16_bwd(to_dev(a, dev), to_dev(b, dev), to_dev(g, dev))
+    a32 = torch.from_numpy(ob.bf16_to_f32(a)).to(dev)
+    _, db_packed = _bf16_bwd(a32, to_dev(b, dev), to_dev(g, dev))
+    assert db_tn.dtype == db_packed.dtype == torch.bfloat16
+    np.testing.assert_array_equal(bf16_bits(db_tn), bf16_bits(db_packed))
+
+
 def test_bf16_backward_f32_operands(dev):
     """f32 a / b: the operands are rounded to bf16 first (fp8.py:92-94) and the
     gradients come back as f32 holding bf16 values (fp8.py:95-96)."""

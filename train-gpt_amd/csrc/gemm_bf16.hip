@@ -73,25 +73,70 @@ template <int S> __device__ __forceinline__ uint8_t* q4_b() {
 
 struct Q4Ctx {
   __amdgpu_buffer_rsrc_t ra, rb;
-  uint32_t voa, vob;       // loader lane's byte offsets of slice 0, part 0
-  uint32_t row16;          // 16 rows in bytes
+  uint32_t voa, vob;       // NT: loader lane's byte offsets of slice 0, part 0
+  uint32_t row16;          // NT: 16 rows in bytes
   int wave, nks;
-  uint32_t fa, fb;         // LDS byte offsets of this lane's fragment chunk (tile 0)
+  uint32_t fa, fb;         // NT: LDS byte offsets of this lane's fragment chunk (tile 0)
+  // TN (operands contraction-major, see gemm_bf16_tn_q4_kernel)
+  uint32_t voa4[4], vob4[4];   // loader lane's byte offsets of slice 0, part p
+  uint32_t sla, slb;           // bytes of one 32-row slice of A and of B
+  uint32_t tro[2];             // LDS byte offset of the row of this lane's transpose read h
+  uint32_t trx[2];             // chunk XOR of that row
+  uint32_t tca, tcb, tin;      // logical chunk of this lane's columns in subtile 0 of A / B, byte within it
 };
 
-// slice ks into the stage at (la, lb): loader wave w fills rows 64w .. 64w+63
-// of A and of B, 16 rows per instruction
-template <bool LOADER>
+// TN stage layout: 32 contraction rows of 512 bytes (the tile's 256 output
+// indices); 16-byte chunk c of row r sits at chunk c ^ tn_swz(r).  The XOR
+// moves whole 32-byte pieces (a transposed fragment read's 4 lanes of one row)
+// and differs over the 8 rows that 32 lanes of one read touch.
+__device__ __forceinline__ uint32_t tn_swz(uint32_t r) { return ((r & 3u) | (((r >> 3) & 1u) << 2)) << 1; }
+
+// slice ks into the stage at (la, lb).  NT: loader wave w fills rows
+// 64w .. 64w+63 of A and of B, 16 rows per instruction; TN: contraction rows
+// 8w .. 8w+7, 2 rows per instruction.
+template <bool LOADER, bool TN>
 __device__ __forceinline__ void q4_issue(const Q4Ctx& c, uint8_t* la, uint8_t* lb, int ks) {
   if (!LOADER) return;
-  const uint32_t so = ks < c.nks ? (uint32_t)ks * 64u : 0x80000000u;   // out of range: zeros
+  if constexpr (TN) {
+    const bool in = ks < c.nks;
+    const uint32_t soa = in ? (uint32_t)ks * c.sla : 0x80000000u;   // out of range: zeros
+    const uint32_t sob = in ? (uint32_t)ks * c.slb : 0x80000000u;
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.ra, la + c.wave * 4096 + p * 1024, 16, c.voa,
-                                             so + p * c.row16, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rb, lb + c.wave * 4096 + p * 1024, 16, c.vob,
-                                             so + p * c.row16, 0, 0);
+    for (int p = 0; p < 4; ++p) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(c.ra, la + c.wave * 4096 + p * 1024, 16, c.voa4[p], soa, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rb, lb + c.wave * 4096 + p * 1024, 16, c.vob4[p], sob, 0, 0);
+    }
+  } else {
+    const uint32_t so = ks < c.nks ? (uint32_t)ks * 64u : 0x80000000u;   // out of range: zeros
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(c.ra, la + c.wave * 4096 + p * 1024, 16, c.voa,
+                                               so + p * c.row16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rb, lb + c.wave * 4096 + p * 1024, 16, c.vob,
+                                               so + p * c.row16, 0, 0);
+    }
   }
+}
+
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
+
+// TN fragment of subtile t (16 output indices at column chunk base cb + 2t):
+// lane (fr, fg) gets contraction rows 8 fg .. 8 fg + 7 of output index
+// (subtile start) + fr, as the NT fragment holds them, from two transposed
+// reads (ds_read_b64_tr_b16: in each 16-lane group, lane i receives element
+// i % 4 of the 8-byte pieces lanes 4j + i / 4 read, j = 0..3); lane 4j + q
+// of a group reads row 8 fg + j (+4) at columns 4q .. 4q+3 of the subtile.
+__device__ __forceinline__ uint4 tn_frag(const uint8_t* l, const Q4Ctx& c, uint32_t cb, int t) {
+  const uint32_t ch = cb + 2u * (uint32_t)t;
+  const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4s_t*)(l + c.tro[0] + ((ch ^ c.trx[0]) << 4) + c.tin));
+  const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4s_t*)(l + c.tro[1] + ((ch ^ c.trx[1]) << 4) + c.tin));
+  return make_uint4(((uint32_t)(uint16_t)lo[0]) | ((uint32_t)(uint16_t)lo[1] << 16),
+                    ((uint32_t)(uint16_t)lo[2]) | ((uint32_t)(uint16_t)lo[3] << 16),
+                    ((uint32_t)(uint16_t)hi[0]) | ((uint32_t)(uint16_t)hi[1] << 16),
+                    ((uint32_t)(uint16_t)hi[2]) | ((uint32_t)(uint16_t)hi[3] << 16));
 }
 
 // s_waitcnt vmcnt(16) as the builtin (gfx9 encoding: vmcnt bits 15:14 = 1,
@@ -99,44 +144,90 @@ __device__ __forceinline__ void q4_issue(const Q4Ctx& c, uint8_t* la, uint8_t* l
 // takes into account; an inline-asm wait is opaque to it.
 constexpr int kWaitVm16 = (1 << 14) | (0xF << 8) | (0x7 << 4);
 
-template <int S, bool LOADER>
+template <int S, bool LOADER, bool TN>
 __device__ __forceinline__ void q4_step(const Q4Ctx& c, int ks, v4f (&acc)[4][8]) {
   if (LOADER) __builtin_amdgcn_s_waitcnt(kWaitVm16);
   __builtin_amdgcn_s_barrier();
   constexpr int kRefill = (S + 3) & 3;   // the stage slice ks - 1 occupied
-  q4_issue<LOADER>(c, q4_a<kRefill>(), q4_b<kRefill>(), ks + 3);
+  q4_issue<LOADER, TN>(c, q4_a<kRefill>(), q4_b<kRefill>(), ks + 3);
   const uint8_t* la = q4_a<S>();
   const uint8_t* lb = q4_b<S>();
   uint4 af[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const uint4*>(la + c.fa + i * 1024);
-  uint4 bn = *reinterpret_cast<const uint4*>(lb + c.fb);
+  for (int i = 0; i < 4; ++i)
+    af[i] = TN ? tn_frag(la, c, c.tca, i) : *reinterpret_cast<const uint4*>(la + c.fa + i * 1024);
+  uint4 bn = TN ? tn_frag(lb, c, c.tcb, 0) : *reinterpret_cast<const uint4*>(lb + c.fb);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const uint4 bf = bn;
-    if (j + 1 < 8) bn = *reinterpret_cast<const uint4*>(lb + c.fb + (j + 1) * 1024);
+    if (j + 1 < 8)
+      bn = TN ? tn_frag(lb, c, c.tcb, j + 1) : *reinterpret_cast<const uint4*>(lb + c.fb + (j + 1) * 1024);
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i][j] = mfma_bf16_16x16x32(bf, af[i], acc[i][j]);
   }
 }
 
-template <bool LOADER>
+template <bool LOADER, bool TN>
 __device__ __forceinline__ void q4_main_loop(const Q4Ctx& c, v4f (&acc)[4][8]) {
-  q4_issue<LOADER>(c, q4_a0, q4_b0, 0);
-  q4_issue<LOADER>(c, q4_a1, q4_b1, 1);
-  q4_issue<LOADER>(c, q4_a2, q4_b2, 2);
+  q4_issue<LOADER, TN>(c, q4_a0, q4_b0, 0);
+  q4_issue<LOADER, TN>(c, q4_a1, q4_b1, 1);
+  q4_issue<LOADER, TN>(c, q4_a2, q4_b2, 2);
   int ks = 0;
   for (; ks + 4 <= c.nks; ks += 4) {
-    q4_step<0, LOADER>(c, ks, acc);
-    q4_step<1, LOADER>(c, ks + 1, acc);
-    q4_step<2, LOADER>(c, ks + 2, acc);
-    q4_step<3, LOADER>(c, ks + 3, acc);
+    q4_step<0, LOADER, TN>(c, ks, acc);
+    q4_step<1, LOADER, TN>(c, ks + 1, acc);
+    q4_step<2, LOADER, TN>(c, ks + 2, acc);
+    q4_step<3, LOADER, TN>(c, ks + 3, acc);
   }
   if (ks < c.nks) {
-    q4_step<0, LOADER>(c, ks, acc);
+    q4_step<0, LOADER, TN>(c, ks, acc);
     if (ks + 1 < c.nks) {
-      q4_step<1, LOADER>(c, ks + 1, acc);
-      if (ks + 2 < c.nks) q4_step<2, LOADER>(c, ks + 2, acc);
+      q4_step<1, LOADER, TN>(c, ks + 1, acc);
+      if (ks + 2 < c.nks) q4_step<2, LOADER, TN>(c, ks + 2, acc);
+    }
+  }
+}
+
+// Epilogue of the 256 x 256 bf16 kernels: lane (fr, fg) holds row i * 16 + fr
+// and columns j * 16 + 4 fg .. +3 of the wave tile; stage it in this wave's
+// 16 KiB (256-byte rows, chunk c of row r at c ^ (r & 15)), then 16 lanes
+// store each row's 256 bytes.
+__device__ __forceinline__ void q4_store_tile(const v4f (&acc)[4][8], __bf16* __restrict__ C, int M, int N, int m0,
+                                              int n0, int wm, int wn, int wave, int lane) {
+  const int fr = lane & 15, fg = lane >> 4;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  uint8_t* wbuf = wave == 0 ? q4_a0 : wave == 1 ? q4_b0 : wave == 2 ? q4_a1 : wave == 3 ? q4_b1
+                : wave == 4 ? q4_a2 : wave == 5 ? q4_b2 : wave == 6 ? q4_a3 : q4_b3;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = i * 16 + fr;
+      const int chunk = (j * 2 + (fg >> 1)) ^ (r & 15);
+      const v4f v = acc[i][j];
+      *reinterpret_cast<uint2*>(wbuf + r * 256 + chunk * 16 + (fg & 1) * 8) =
+          make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  const bool vec_ok = (N % 8) == 0;
+  const int k = lane & 15;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int r = q * 4 + (lane >> 4);
+    const int m = m0 + wm * 64 + r;
+    const int n = n0 + wn * 128 + k * 8;
+    const uint4 v = *reinterpret_cast<const uint4*>(wbuf + r * 256 + ((k ^ (r & 15)) * 16));
+    if (m < M && n < N) {
+      __bf16* dst = C + (int64_t)m * N + n;
+      if (vec_ok) {
+        *reinterpret_cast<uint4*>(dst) = v;
+      } else {
+        const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          if (n + t < N) reinterpret_cast<uint16_t*>(dst)[t] = e[t];
+      }
     }
   }
 }
@@ -176,47 +267,71 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_nt_q4_kernel(const __bf16* _
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  if (c.wave < 4) q4_main_loop<true>(c, acc);
-  else q4_main_loop<false>(c, acc);
+  if (c.wave < 4) q4_main_loop<true, false>(c, acc);
+  else q4_main_loop<false, false>(c, acc);
 
-  // epilogue: lane (fr, fg) holds row i * 16 + fr and columns j * 16 + 4 fg ..
-  // +3 of the wave tile; stage it in this wave's 16 KiB (256-byte rows,
-  // chunk c of row r at c ^ (r & 15)), then 16 lanes store each row's 256 bytes
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  uint8_t* wbuf = c.wave == 0 ? q4_a0 : c.wave == 1 ? q4_b0 : c.wave == 2 ? q4_a1 : c.wave == 3 ? q4_b1
-                : c.wave == 4 ? q4_a2 : c.wave == 5 ? q4_b2 : c.wave == 6 ? q4_a3 : q4_b3;
+  q4_store_tile(acc, C, M, N, m0, n0, wm, wn, c.wave, lane);
+}
+
+// C (M, N) = A^T B on contraction-major operands: A (Kc, M) and B (Kc, N)
+// row-major with row pitches lda and ldb elements, C[m][n] = sum_c A[c][m] B[c][n].
+// This is the straight-through backward's db = a.T @ g (fp8.py:96) read
+// straight from a and g, with no transposed copies.  The pipeline, tiles and
+// epilogue are the NT kernel's; a stage holds 32 contraction rows of the
+// tile's 256 m (A) or n (B) indices, 512 bytes each (stored with tn_swz), and
+// the MFMA fragments come from transposed LDS reads (tn_frag).  Contraction
+// rows past Kc read zero; tile columns past M or N read neighbouring memory
+// that only reaches discarded outputs.
+__global__ __launch_bounds__(512, 1) void gemm_bf16_tn_q4_kernel(const __bf16* __restrict__ A,
+                                                                 const __bf16* __restrict__ B,
+                                                                 __bf16* __restrict__ C, int M, int N, int Kc,
+                                                                 int lda, int ldb, int tiles_m, int tiles_n) {
+  Q4Ctx c;
+  const int tid = threadIdx.x, lane = tid & 63;
+  c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  c.nks = (Kc + 31) >> 5;
+  const int fr = lane & 15, fg = lane >> 4;
+  const int wm = c.wave >> 1, wn = c.wave & 1;
+  int tmi, tni;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tmi, tni);
+  const int m0 = tmi * 256, n0 = tni * 256;
+  const uint32_t pa = 2u * (uint32_t)lda, pb = 2u * (uint32_t)ldb;
+  c.ra = make_rsrc(A, (uint32_t)Kc * pa);
+  c.rb = make_rsrc(B, (uint32_t)Kc * pb);
+  c.sla = 32u * pa;
+  c.slb = 32u * pb;
+  // DMA: instruction p of loader wave w fills slice rows r = 8w + 2p + L / 32;
+  // lane L lands at physical chunk L % 32 of row r, which holds logical chunk
+  // (L % 32) ^ tn_swz(r)
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t r = (uint32_t)(8 * c.wave + 2 * p + (lane >> 5));
+    const uint32_t lc = (uint32_t)(lane & 31) ^ tn_swz(r);
+    c.voa4[p] = r * pa + (uint32_t)m0 * 2u + lc * 16u;
+    c.vob4[p] = r * pb + (uint32_t)n0 * 2u + lc * 16u;
+  }
+  // transposed reads: lane (fr, fg) reads row 8 fg + fr / 4 (+ 4) at columns
+  // 4 (fr % 4) .. +3 of a subtile: chunk (fr % 4) / 2 of it, byte 8 (fr % 2)
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t r = (uint32_t)(8 * fg + 4 * h + (fr >> 2));
+    c.tro[h] = r * 512u;
+    c.trx[h] = tn_swz(r);
+  }
+  c.tca = (uint32_t)(wm * 8 + ((fr & 3) >> 1));
+  c.tcb = (uint32_t)(wn * 16 + ((fr & 3) >> 1));
+  c.tin = 8u * (uint32_t)(fr & 1);
+
+  v4f acc[4][8];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int r = i * 16 + fr;
-      const int chunk = (j * 2 + (fg >> 1)) ^ (r & 15);
-      const v4f v = acc[i][j];
-      *reinterpret_cast<uint2*>(wbuf + r * 256 + chunk * 16 + (fg & 1) * 8) =
-          make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-    }
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  const bool vec_ok = (N % 8) == 0;
-  const int k = lane & 15;
-#pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    const int r = q * 4 + (lane >> 4);
-    const int m = m0 + wm * 64 + r;
-    const int n = n0 + wn * 128 + k * 8;
-    const uint4 v = *reinterpret_cast<const uint4*>(wbuf + r * 256 + ((k ^ (r & 15)) * 16));
-    if (m < M && n < N) {
-      __bf16* dst = C + (int64_t)m * N + n;
-      if (vec_ok) {
-        *reinterpret_cast<uint4*>(dst) = v;
-      } else {
-        const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
-#pragma unroll
-        for (int t = 0; t < 8; ++t)
-          if (n + t < N) reinterpret_cast<uint16_t*>(dst)[t] = e[t];
-      }
-    }
-  }
+    for (int j = 0; j < 8; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  if (c.wave < 4) q4_main_loop<true, true>(c, acc);
+  else q4_main_loop<false, true>(c, acc);
+
+  q4_store_tile(acc, C, M, N, m0, n0, wm, wn, c.wave, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -369,6 +484,16 @@ int launch_fill_zero_bf16(void* p, int64_t n, hipStream_t st) {
   return check_launch("fill_zero_bf16");
 }
 
+// C (M, N) = A^T B, A (Kc, M) pitch lda, B (Kc, N) pitch ldb (gemm_bf16_tn_q4_kernel)
+int launch_gemm_bf16_tn(const __bf16* a, int64_t lda, const __bf16* b, int64_t ldb, __bf16* c, int64_t M,
+                        int64_t N, int64_t Kc, hipStream_t st) {
+  if (M == 0 || N == 0) return TG_OK;
+  const int tiles_m = (int)((M + 255) / 256), tiles_n = (int)((N + 255) / 256);
+  hipLaunchKernelGGL(gemm_bf16_tn_q4_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, st, a, b, c,
+                     (int)M, (int)N, (int)Kc, (int)lda, (int)ldb, tiles_m, tiles_n);
+  return check_launch("gemm_bf16_tn_256");
+}
+
 int launch_gemm_bf16(const __bf16* a, const __bf16* b, __bf16* c, int64_t M, int64_t N, int64_t K,
                      hipStream_t st) {
   if (M == 0 || N == 0) return TG_OK;
@@ -463,6 +588,11 @@ extern "C" int tg_block_scaled_matmul_bwd_bf16(const void* a, int a_dtype, const
     bx = bp;
   }
   TG_TRY(launch_gemm_bf16(gx, bx, reinterpret_cast<__bf16*>(da), M, K, np, st));   // fp8.py:95
+  if (a_dtype == TG_DTYPE_BF16 && g_dtype == TG_DTYPE_BF16 && K % 8 == 0 && N % 8 == 0 && aligned(a, 16) &&
+      aligned(g, 16))
+    // db = a.T . g read straight from a and g (contraction-major operands)
+    return launch_gemm_bf16_tn(reinterpret_cast<const __bf16*>(a), K, reinterpret_cast<const __bf16*>(g), N,
+                               reinterpret_cast<__bf16*>(db), K, N, M, st);                // fp8.py:96
   TG_TRY(launch_pack_bf16(a, a_dtype, M, K, 1, at, mp, st));
   TG_TRY(launch_pack_bf16(g, g_dtype, M, N, 1, gt, mp, st));
   return launch_gemm_bf16(at, gt, reinterpret_cast<__bf16*>(db), K, N, mp, st);      // fp8.py:96
