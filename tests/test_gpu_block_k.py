@@ -155,6 +155,27 @@ def test_fp8_backward(dev, block_k, M, K, N):
     assert maxabs_rel(bd.grad, dw) <= TOL
 
 
+@pytest.mark.parametrize("block_k", [64, 256])
+def test_c1_shape(dev, block_k):
+    """Config 1's shape (x 2048 x 768, W 768 x 3072) through the general path:
+    the quantized operands bit-exact, the f32 GEMM within F32_TOL and the bf16
+    composite within the north star's 1e-2 of the float64 oracle."""
+    rng = np.random.default_rng(block_k)
+    x = ob.randn_bf16(rng, (2048, 768))
+    w = ob.randn_bf16(rng, (768, 3072), std=0.02)
+    xd, wd = to_dev(x, dev), to_dev(w, dev)
+    y = fp8.block_scaled_matmul(xd, wd, block_k=block_k)
+    _, ref, (qa, sa), (qb, sb) = fp8_ref.fp8_forward(x, w, block_k)
+    assert maxabs_rel(y, ref) <= TOL
+    q1, s1 = fp8.quantize_fp8(xd, block_k)
+    q2, s2 = fp8.quantize_fp8(wd, block_k, transpose=True)
+    np.testing.assert_array_equal(u8(q1), qa)
+    np.testing.assert_array_equal(u8(q2), qb)
+    assert same_scales(s1.cpu().numpy(), sa) and same_scales(s2.cpu().numpy(), sb)
+    c32 = fp8.scaled_matmul(q1.view(torch.uint8), s1, q2.view(torch.uint8), s2, out_dtype=torch.float32)
+    assert maxabs_rel(c32, ref) <= F32_TOL
+
+
 def test_errors(dev):
     a = torch.zeros((4, 96), dtype=torch.bfloat16, device=dev)
     b = torch.zeros((96, 8), dtype=torch.bfloat16, device=dev)
