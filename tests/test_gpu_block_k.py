@@ -13,9 +13,11 @@ Bars:
     same bytes (its block sums are f32 fma chains), exactly equal on
     power-of-two known answers with row-, column- and block-dependent scales,
     and its bf16 output the RNE of its f32 output;
-  * the forward composite equal bit for bit to quantize_fp8 + scaled_matmul,
-    and within the north star's 1e-2 of the float64 oracle; the FP8 backward
-    within 1e-2 of fp8_ref.fp8_backward_fp8, ragged M / N included.
+  * the forward composite equal bit for bit to quantize_fp8 + scaled_matmul
+    (block_k a multiple of 128: the composites run the tuned GEMM on the block
+    scales repeated per 128 columns, and the check does too), and within the
+    north star's 1e-2 of the float64 oracle; the FP8 backward within 1e-2 of
+    fp8_ref.fp8_backward_fp8, ragged M / N included.
 """
 import numpy as np
 import pytest
@@ -126,15 +128,18 @@ def test_forward_composite(dev, block_k, lead, K, N):
     _, ref, _, _ = fp8_ref.fp8_forward(a, b, block_k)
     assert y.shape == (*lead, N) and y.dtype == torch.bfloat16
     assert maxabs_rel(y.reshape(-1, N), ref) <= TOL
-    # the composite (tg_block_scaled_matmul) = quantize_fp8 + scaled_matmul, bit for bit
+    # the composite (tg_block_scaled_matmul) = quantize_fp8 + scaled_matmul, bit for bit; a multiple
+    # of 128 runs the tuned GEMM on the block scales repeated per 128 columns, so the check does too
     qa, sa = fp8.quantize_fp8(ad.reshape(-1, K), block_k)
     qb, sb = fp8.quantize_fp8(bd, block_k, transpose=True)
+    if block_k % 128 == 0:
+        sa, sb = sa.repeat_interleave(block_k // 128, dim=1), sb.repeat_interleave(block_k // 128, dim=1)
     y2 = fp8.scaled_matmul(qa.view(torch.uint8), sa, qb.view(torch.uint8), sb)
     assert torch.equal(y.reshape(-1, N).view(torch.int16), y2.view(torch.int16))
 
 
-@pytest.mark.parametrize("block_k", [32, 64])
-@pytest.mark.parametrize("M,K,N", [(128, 256, 192), (100, 256, 70)])
+@pytest.mark.parametrize("block_k", [32, 64, 256])
+@pytest.mark.parametrize("M,K,N", [(128, 256, 192), (100, 256, 70), (512, 512, 768)])
 def test_fp8_backward(dev, block_k, M, K, N):
     """BACKWARD_MODE "fp8" through autograd; ragged M / N (not multiples of
     block_k) take the zero-padded last block."""

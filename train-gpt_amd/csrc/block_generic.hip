@@ -29,11 +29,13 @@ __device__ __forceinline__ uint8_t gb_quant1(float x, float s, bool finite_scale
 
 __device__ __forceinline__ bool gb_finite(float s) { return (__float_as_uint(s) & 0x7F800000u) != 0x7F800000u; }
 
-// one thread per (row, block): q (rows, cols), s (rows, cols / bk)
+// one thread per (row, block): q (rows, cols), s (rows, cols / bk * srep),
+// each block's scale written srep times (srep = bk / 128 gives the 128-wide
+// scale layout of the tuned GEMM, whose blocks then share their scale)
 template <bool F32_IN>
 __global__ __launch_bounds__(256) void quant_rows_gb_kernel(const void* __restrict__ x, int64_t rows,
                                                             int64_t cols, int bk, uint8_t* __restrict__ q,
-                                                            float* __restrict__ s) {
+                                                            float* __restrict__ s, int srep) {
   const int64_t nb = cols / bk;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= rows * nb) return;
@@ -42,7 +44,7 @@ __global__ __launch_bounds__(256) void quant_rows_gb_kernel(const void* __restri
   uint32_t m = 0;
   for (int k = 0; k < bk; ++k) m = max(m, __float_as_uint(gb_load(x, base + k, F32_IN)) & 0x7FFFFFFFu);
   const float sc = block_scale(m);
-  s[i] = sc;
+  for (int t = 0; t < srep; ++t) s[i * srep + t] = sc;
   const bool fin = gb_finite(sc);
   for (int k = 0; k < bk; ++k) q[base + k] = gb_quant1(gb_load(x, base + k, F32_IN), sc, fin);
 }
@@ -51,7 +53,7 @@ __global__ __launch_bounds__(256) void quant_rows_gb_kernel(const void* __restri
 // one thread per (row block, column), columns fastest (coalesced reads of x)
 __global__ __launch_bounds__(256) void quant_cols_gb_kernel(const uint16_t* __restrict__ x, int64_t R, int64_t C,
                                                             int bk, uint8_t* __restrict__ qt,
-                                                            float* __restrict__ st) {
+                                                            float* __restrict__ st, int srep) {
   const int64_t nb = R / bk;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= nb * C) return;
@@ -60,7 +62,7 @@ __global__ __launch_bounds__(256) void quant_cols_gb_kernel(const uint16_t* __re
   uint32_t m = 0;
   for (int k = 0; k < bk; ++k) m = max(m, ((uint32_t)x[(r0 + k) * C + c] << 16) & 0x7FFFFFFFu);
   const float sc = block_scale(m);
-  st[c * nb + b] = sc;
+  for (int t = 0; t < srep; ++t) st[(c * nb + b) * srep + t] = sc;
   const bool fin = gb_finite(sc);
   for (int k = 0; k < bk; ++k)
     qt[c * R + r0 + k] = gb_quant1(__uint_as_float((uint32_t)x[(r0 + k) * C + c] << 16), sc, fin);
@@ -156,24 +158,26 @@ __global__ __launch_bounds__(256) void gemm_gb_kernel(const uint8_t* __restrict_
 static unsigned gb_grid(int64_t threads) { return (unsigned)((threads + 255) / 256); }
 
 int launch_quant_rows_gb(const void* x, int x_dtype, int64_t rows, int64_t cols, int bk, uint8_t* q, float* s,
-                         hipStream_t st) {
+                         hipStream_t st, int srep) {
   const int64_t n = rows * (cols / bk);
   if (n == 0) return TG_OK;
   if (n / 256 >= 0x7FFFFFFF) return einval("quantize_rows: too many blocks");
   if (x_dtype == TG_DTYPE_F32)
-    hipLaunchKernelGGL(quant_rows_gb_kernel<true>, dim3(gb_grid(n)), dim3(256), 0, st, x, rows, cols, bk, q, s);
+    hipLaunchKernelGGL(quant_rows_gb_kernel<true>, dim3(gb_grid(n)), dim3(256), 0, st, x, rows, cols, bk, q, s,
+                       srep);
   else
-    hipLaunchKernelGGL(quant_rows_gb_kernel<false>, dim3(gb_grid(n)), dim3(256), 0, st, x, rows, cols, bk, q, s);
+    hipLaunchKernelGGL(quant_rows_gb_kernel<false>, dim3(gb_grid(n)), dim3(256), 0, st, x, rows, cols, bk, q, s,
+                       srep);
   return check_launch("quantize_rows (block_k != 128)");
 }
 
 int launch_quant_cols_gb(const void* x, int64_t rows, int64_t cols, int bk, uint8_t* q_t, float* s_t,
-                         hipStream_t st) {
+                         hipStream_t st, int srep) {
   const int64_t n = (rows / bk) * cols;
   if (n == 0) return TG_OK;
   if (n / 256 >= 0x7FFFFFFF) return einval("quantize_cols: too many blocks");
   hipLaunchKernelGGL(quant_cols_gb_kernel, dim3(gb_grid(n)), dim3(256), 0, st,
-                     reinterpret_cast<const uint16_t*>(x), rows, cols, bk, q_t, s_t);
+                     reinterpret_cast<const uint16_t*>(x), rows, cols, bk, q_t, s_t, srep);
   return check_launch("quantize_cols (block_k != 128)");
 }
 

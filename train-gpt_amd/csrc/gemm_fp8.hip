@@ -1685,9 +1685,16 @@ extern "C" int tg_gemm_fp8_nt_km(const uint8_t* a_q, const float* a_s_km, const 
 
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Scale entries per row for a contraction of `extent` in blocks of block_k:
+// multiples of 128 keep one scale per 128 (each block's scale repeated), so
+// that the tuned GEMM runs on them.
+static inline size_t scale_cols(int64_t extent, int block_k) {
+  return (size_t)(block_k % 128 == 0 ? extent / 128 : extent / block_k);
+}
+
 extern "C" size_t tg_block_scaled_matmul_workspace(int64_t M, int64_t N, int64_t K, int block_k) {
   if (block_k <= 0 || M < 0 || N < 0 || K < 0) return 0;
-  const size_t nkb = (size_t)(K / block_k);
+  const size_t nkb = scale_cols(K, block_k);
   return align256((size_t)M * K) + align256((size_t)M * nkb * 4) + align256((size_t)N * K) +
          align256((size_t)N * nkb * 4);
 }
@@ -1713,17 +1720,22 @@ static int block_scaled_matmul_on(const void* a, const void* b, void* out, int64
   return launch_gemm_fp8(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, K, st, true);   // fp8.py:70-78
 }
 
-// The forward composite for block_k != 128: row-major scales, the general kernels.
+// The forward composite for block_k != 128: row-major scales, the general
+// quantizers; a multiple of 128 then runs the tuned GEMM on its scales
+// repeated per 128-wide sub-block (the same sum: a block's sub-blocks share
+// the scale), any other block size the general GEMM.
 static int block_scaled_matmul_gb(const void* a, const void* b, void* out, int64_t M, int64_t N, int64_t K,
                                   int bk, void* workspace, hipStream_t st) {
-  const int64_t nkb = K / bk;
+  const int64_t nkb = (int64_t)scale_cols(K, bk);
+  const int srep = bk % 128 == 0 ? bk / 128 : 1;
   uint8_t* p = reinterpret_cast<uint8_t*>(workspace);
   uint8_t* qa = p;                 p += align256((size_t)M * K);
   float* sa = reinterpret_cast<float*>(p);   p += align256((size_t)M * nkb * 4);
   uint8_t* qb = p;                 p += align256((size_t)N * K);
   float* sb = reinterpret_cast<float*>(p);
-  TG_TRY(launch_quant_rows_gb(a, TG_DTYPE_BF16, M, K, bk, qa, sa, st));     // fp8.py:66
-  TG_TRY(launch_quant_cols_gb(b, K, N, bk, qb, sb, st));                     // fp8.py:68
+  TG_TRY(launch_quant_rows_gb(a, TG_DTYPE_BF16, M, K, bk, qa, sa, st, srep));     // fp8.py:66
+  TG_TRY(launch_quant_cols_gb(b, K, N, bk, qb, sb, st, srep));                     // fp8.py:68
+  if (srep > 1) return launch_gemm_fp8(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, K, st, false);
   return launch_gemm_gb(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, K, bk, st);   // fp8.py:70-78
 }
 
@@ -1801,7 +1813,7 @@ extern "C" int tg_block_scaled_matmul_noalloc(const void* a, const void* b, void
 
 extern "C" size_t tg_block_scaled_matmul_bwd_workspace(int64_t M, int64_t N, int64_t K, int block_k) {
   if (block_k <= 0 || M < 0 || N < 0 || K < 0) return 0;
-  const size_t mkb = (size_t)(M / block_k), nkb = (size_t)(N / block_k);
+  const size_t mkb = scale_cols(M, block_k), nkb = scale_cols(N, block_k);
   return align256((size_t)M * N) + align256((size_t)M * nkb * 4) +   // g along N
          align256((size_t)K * N) + align256((size_t)K * nkb * 4) +   // b along N
          align256((size_t)K * M) + align256((size_t)K * mkb * 4) +   // a.T along M
@@ -1825,7 +1837,8 @@ extern "C" int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, cons
       return einval("block_scaled_matmul_bwd_fp8: inputs must be 2-byte and workspace 256-byte aligned");
     hipStream_t st = as_stream(stream);
     const int bk = block_k;
-    const int64_t mkb = M / bk, nkb = N / bk;
+    const int64_t mkb = (int64_t)scale_cols(M, bk), nkb = (int64_t)scale_cols(N, bk);
+    const int srep = bk % 128 == 0 ? bk / 128 : 1;   // multiples of 128: the tuned GEMM (see block_scaled_matmul_gb)
     uint8_t* p = reinterpret_cast<uint8_t*>(workspace);
     uint8_t* qg = p;    p += align256((size_t)M * N);
     float* sg = reinterpret_cast<float*>(p);    p += align256((size_t)M * nkb * 4);
@@ -1835,11 +1848,13 @@ extern "C" int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, cons
     float* sat = reinterpret_cast<float*>(p);   p += align256((size_t)K * mkb * 4);
     uint8_t* qgt = p;   p += align256((size_t)N * M);
     float* sgt = reinterpret_cast<float*>(p);
-    TG_TRY(launch_quant_rows_gb(g, TG_DTYPE_BF16, M, N, bk, qg, sg, st));
-    TG_TRY(launch_quant_rows_gb(b, TG_DTYPE_BF16, K, N, bk, qb, sb, st));
-    TG_TRY(launch_gemm_gb(qg, sg, qb, sb, 1, da, TG_DTYPE_BF16, M, K, N, bk, st));      // dX = g . b.T
-    TG_TRY(launch_quant_cols_gb(a, M, K, bk, qat, sat, st));
-    TG_TRY(launch_quant_cols_gb(g, M, N, bk, qgt, sgt, st));
+    TG_TRY(launch_quant_rows_gb(g, TG_DTYPE_BF16, M, N, bk, qg, sg, st, srep));
+    TG_TRY(launch_quant_rows_gb(b, TG_DTYPE_BF16, K, N, bk, qb, sb, st, srep));
+    if (srep > 1) TG_TRY(launch_gemm_fp8(qg, sg, qb, sb, 1, da, TG_DTYPE_BF16, M, K, N, st, false));
+    else TG_TRY(launch_gemm_gb(qg, sg, qb, sb, 1, da, TG_DTYPE_BF16, M, K, N, bk, st));      // dX = g . b.T
+    TG_TRY(launch_quant_cols_gb(a, M, K, bk, qat, sat, st, srep));
+    TG_TRY(launch_quant_cols_gb(g, M, N, bk, qgt, sgt, st, srep));
+    if (srep > 1) return launch_gemm_fp8(qat, sat, qgt, sgt, 1, db, TG_DTYPE_BF16, K, N, M, st, false);
     return launch_gemm_gb(qat, sat, qgt, sgt, 1, db, TG_DTYPE_BF16, K, N, M, bk, st);   // dW = a.T . g
   }
   if (!aligned(workspace, 256) || !aligned(a, 16) || !aligned(b, 16) || !aligned(g, 16))

@@ -73,10 +73,11 @@ int launch_gemm_fp8(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, co
                     hipStream_t st, bool skm = false);
 // The general path for block_k != 128 (block_generic.hip): row-major scales,
 // any block_k >= 1 dividing the contracted extent.
+// srep: each block's scale written srep times (bk / 128: the tuned GEMM's 128-wide scale layout).
 int launch_quant_rows_gb(const void* x, int x_dtype, int64_t rows, int64_t cols, int bk, uint8_t* q, float* s,
-                         hipStream_t st);
+                         hipStream_t st, int srep = 1);
 int launch_quant_cols_gb(const void* x, int64_t rows, int64_t cols, int bk, uint8_t* q_t, float* s_t,
-                         hipStream_t st);
+                         hipStream_t st, int srep = 1);
 int launch_gemm_gb(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s, int bn, void* c,
                    int c_dtype, int64_t M, int64_t N, int64_t K, int bk, hipStream_t st);
 
