@@ -14,8 +14,9 @@ Bars:
     power-of-two known answers with row-, column- and block-dependent scales,
     and its bf16 output the RNE of its f32 output;
   * the forward composite equal bit for bit to quantize_fp8 + scaled_matmul
-    (block_k a multiple of 128: the composites run the tuned GEMM on the block
-    scales repeated per 128 columns, and the check does too), and within the
+    in the layout the composites give the tuned GEMM (block_k a multiple of
+    128: each block's scale repeated per 128 columns; a divisor of 128: each
+    block in a zero-filled 128-byte slot), and within the
     north star's 1e-2 of the float64 oracle; the FP8 backward within 1e-2 of
     fp8_ref.fp8_backward_fp8, ragged M / N included.
 """
@@ -128,13 +129,22 @@ def test_forward_composite(dev, block_k, lead, K, N):
     _, ref, _, _ = fp8_ref.fp8_forward(a, b, block_k)
     assert y.shape == (*lead, N) and y.dtype == torch.bfloat16
     assert maxabs_rel(y.reshape(-1, N), ref) <= TOL
-    # the composite (tg_block_scaled_matmul) = quantize_fp8 + scaled_matmul, bit for bit; a multiple
-    # of 128 runs the tuned GEMM on the block scales repeated per 128 columns, so the check does too
+    # the composite (tg_block_scaled_matmul) = quantize_fp8 + scaled_matmul, bit for bit, in the
+    # layout the composite feeds the tuned GEMM: a multiple of 128 repeats each block's scale per
+    # 128 columns; a divisor of 128 puts each block at the start of a zero-filled 128-byte slot
     qa, sa = fp8.quantize_fp8(ad.reshape(-1, K), block_k)
     qb, sb = fp8.quantize_fp8(bd, block_k, transpose=True)
+    qa, qb = qa.view(torch.uint8), qb.view(torch.uint8)
     if block_k % 128 == 0:
         sa, sb = sa.repeat_interleave(block_k // 128, dim=1), sb.repeat_interleave(block_k // 128, dim=1)
-    y2 = fp8.scaled_matmul(qa.view(torch.uint8), sa, qb.view(torch.uint8), sb)
+    else:
+        def slots(q):
+            r = q.shape[0]
+            z = torch.zeros((r, K // block_k, 128), dtype=torch.uint8, device=dev)
+            z[:, :, :block_k] = q.reshape(r, K // block_k, block_k)
+            return z.reshape(r, -1)
+        qa, qb = slots(qa), slots(qb)
+    y2 = fp8.scaled_matmul(qa, sa, qb, sb)
     assert torch.equal(y.reshape(-1, N).view(torch.int16), y2.view(torch.int16))
 
 

@@ -29,13 +29,15 @@ __device__ __forceinline__ uint8_t gb_quant1(float x, float s, bool finite_scale
 
 __device__ __forceinline__ bool gb_finite(float s) { return (__float_as_uint(s) & 0x7F800000u) != 0x7F800000u; }
 
-// one thread per (row, block): q (rows, cols), s (rows, cols / bk * srep),
-// each block's scale written srep times (srep = bk / 128 gives the 128-wide
-// scale layout of the tuned GEMM, whose blocks then share their scale)
+// one thread per (row, block): q (rows, cols * pf), s (rows, cols / bk * srep).
+// Two layouts for the tuned GEMM: each block's scale written srep times
+// (srep = bk / 128: 128-wide blocks that share their scale), or each block's
+// bytes at the start of a 128-byte slot followed by zeros (pf = 128 / bk: one
+// block per 128-wide block, the zeros adding nothing to any product).
 template <bool F32_IN>
 __global__ __launch_bounds__(256) void quant_rows_gb_kernel(const void* __restrict__ x, int64_t rows,
                                                             int64_t cols, int bk, uint8_t* __restrict__ q,
-                                                            float* __restrict__ s, int srep) {
+                                                            float* __restrict__ s, int srep, int pf) {
   const int64_t nb = cols / bk;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= rows * nb) return;
@@ -46,14 +48,16 @@ __global__ __launch_bounds__(256) void quant_rows_gb_kernel(const void* __restri
   const float sc = block_scale(m);
   for (int t = 0; t < srep; ++t) s[i * srep + t] = sc;
   const bool fin = gb_finite(sc);
-  for (int k = 0; k < bk; ++k) q[base + k] = gb_quant1(gb_load(x, base + k, F32_IN), sc, fin);
+  uint8_t* qo = q + base * pf;
+  for (int k = 0; k < bk; ++k) qo[k] = gb_quant1(gb_load(x, base + k, F32_IN), sc, fin);
+  for (int k = bk; k < bk * pf; ++k) qo[k] = 0;
 }
 
 // x (R, C) bf16 -> the quantization of x.T along R: q_t (C, R), s_t (C, R / bk);
 // one thread per (row block, column), columns fastest (coalesced reads of x)
 __global__ __launch_bounds__(256) void quant_cols_gb_kernel(const uint16_t* __restrict__ x, int64_t R, int64_t C,
                                                             int bk, uint8_t* __restrict__ qt,
-                                                            float* __restrict__ st, int srep) {
+                                                            float* __restrict__ st, int srep, int pf) {
   const int64_t nb = R / bk;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= nb * C) return;
@@ -64,8 +68,10 @@ __global__ __launch_bounds__(256) void quant_cols_gb_kernel(const uint16_t* __re
   const float sc = block_scale(m);
   for (int t = 0; t < srep; ++t) st[(c * nb + b) * srep + t] = sc;
   const bool fin = gb_finite(sc);
+  uint8_t* qo = qt + (c * R + r0) * pf;
   for (int k = 0; k < bk; ++k)
-    qt[c * R + r0 + k] = gb_quant1(__uint_as_float((uint32_t)x[(r0 + k) * C + c] << 16), sc, fin);
+    qo[k] = gb_quant1(__uint_as_float((uint32_t)x[(r0 + k) * C + c] << 16), sc, fin);
+  for (int k = bk; k < bk * pf; ++k) qo[k] = 0;
 }
 
 // C (M, N) = sum over K blocks b of (A_b . B_b^T) * sa[m][b] * sb[n / bn][b];
@@ -158,26 +164,26 @@ __global__ __launch_bounds__(256) void gemm_gb_kernel(const uint8_t* __restrict_
 static unsigned gb_grid(int64_t threads) { return (unsigned)((threads + 255) / 256); }
 
 int launch_quant_rows_gb(const void* x, int x_dtype, int64_t rows, int64_t cols, int bk, uint8_t* q, float* s,
-                         hipStream_t st, int srep) {
+                         hipStream_t st, int srep, int pf) {
   const int64_t n = rows * (cols / bk);
   if (n == 0) return TG_OK;
   if (n / 256 >= 0x7FFFFFFF) return einval("quantize_rows: too many blocks");
   if (x_dtype == TG_DTYPE_F32)
     hipLaunchKernelGGL(quant_rows_gb_kernel<true>, dim3(gb_grid(n)), dim3(256), 0, st, x, rows, cols, bk, q, s,
-                       srep);
+                       srep, pf);
   else
     hipLaunchKernelGGL(quant_rows_gb_kernel<false>, dim3(gb_grid(n)), dim3(256), 0, st, x, rows, cols, bk, q, s,
-                       srep);
+                       srep, pf);
   return check_launch("quantize_rows (block_k != 128)");
 }
 
 int launch_quant_cols_gb(const void* x, int64_t rows, int64_t cols, int bk, uint8_t* q_t, float* s_t,
-                         hipStream_t st, int srep) {
+                         hipStream_t st, int srep, int pf) {
   const int64_t n = (rows / bk) * cols;
   if (n == 0) return TG_OK;
   if (n / 256 >= 0x7FFFFFFF) return einval("quantize_cols: too many blocks");
   hipLaunchKernelGGL(quant_cols_gb_kernel, dim3(gb_grid(n)), dim3(256), 0, st,
-                     reinterpret_cast<const uint16_t*>(x), rows, cols, bk, q_t, s_t, srep);
+                     reinterpret_cast<const uint16_t*>(x), rows, cols, bk, q_t, s_t, srep, pf);
   return check_launch("quantize_cols (block_k != 128)");
 }
 

@@ -1685,17 +1685,23 @@ extern "C" int tg_gemm_fp8_nt_km(const uint8_t* a_q, const float* a_s_km, const 
 
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Scale entries per row for a contraction of `extent` in blocks of block_k:
-// multiples of 128 keep one scale per 128 (each block's scale repeated), so
-// that the tuned GEMM runs on them.
+// How the composites feed a block_k != 128 to the tuned GEMM (128-wide scale
+// blocks): a multiple of 128 repeats each block's scale per 128 columns
+// (srep); a divisor of 128 down to 16 puts each block in a zero-filled
+// 128-byte slot (pf, the contraction grows pf-fold); other sizes run the
+// general GEMM.
+static inline int gb_srep(int block_k) { return block_k % 128 == 0 ? block_k / 128 : 1; }
+static inline int gb_pf(int block_k) { return block_k < 128 && block_k >= 16 && 128 % block_k == 0 ? 128 / block_k : 1; }
+static inline bool gb_tuned(int block_k) { return gb_srep(block_k) > 1 || gb_pf(block_k) > 1; }
+// scale entries per row for a contraction of `extent`
 static inline size_t scale_cols(int64_t extent, int block_k) {
   return (size_t)(block_k % 128 == 0 ? extent / 128 : extent / block_k);
 }
 
 extern "C" size_t tg_block_scaled_matmul_workspace(int64_t M, int64_t N, int64_t K, int block_k) {
   if (block_k <= 0 || M < 0 || N < 0 || K < 0) return 0;
-  const size_t nkb = scale_cols(K, block_k);
-  return align256((size_t)M * K) + align256((size_t)M * nkb * 4) + align256((size_t)N * K) +
+  const size_t nkb = scale_cols(K, block_k), kq = (size_t)K * (size_t)gb_pf(block_k);
+  return align256((size_t)M * kq) + align256((size_t)M * nkb * 4) + align256((size_t)N * kq) +
          align256((size_t)N * nkb * 4);
 }
 
@@ -1727,15 +1733,16 @@ static int block_scaled_matmul_on(const void* a, const void* b, void* out, int64
 static int block_scaled_matmul_gb(const void* a, const void* b, void* out, int64_t M, int64_t N, int64_t K,
                                   int bk, void* workspace, hipStream_t st) {
   const int64_t nkb = (int64_t)scale_cols(K, bk);
-  const int srep = bk % 128 == 0 ? bk / 128 : 1;
+  const int srep = gb_srep(bk), pf = gb_pf(bk);
+  const int64_t kq = K * pf;
   uint8_t* p = reinterpret_cast<uint8_t*>(workspace);
-  uint8_t* qa = p;                 p += align256((size_t)M * K);
+  uint8_t* qa = p;                 p += align256((size_t)M * kq);
   float* sa = reinterpret_cast<float*>(p);   p += align256((size_t)M * nkb * 4);
-  uint8_t* qb = p;                 p += align256((size_t)N * K);
+  uint8_t* qb = p;                 p += align256((size_t)N * kq);
   float* sb = reinterpret_cast<float*>(p);
-  TG_TRY(launch_quant_rows_gb(a, TG_DTYPE_BF16, M, K, bk, qa, sa, st, srep));     // fp8.py:66
-  TG_TRY(launch_quant_cols_gb(b, K, N, bk, qb, sb, st, srep));                     // fp8.py:68
-  if (srep > 1) return launch_gemm_fp8(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, K, st, false);
+  TG_TRY(launch_quant_rows_gb(a, TG_DTYPE_BF16, M, K, bk, qa, sa, st, srep, pf));     // fp8.py:66
+  TG_TRY(launch_quant_cols_gb(b, K, N, bk, qb, sb, st, srep, pf));                     // fp8.py:68
+  if (gb_tuned(bk)) return launch_gemm_fp8(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, kq, st, false);
   return launch_gemm_gb(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, K, bk, st);   // fp8.py:70-78
 }
 
@@ -1813,11 +1820,11 @@ extern "C" int tg_block_scaled_matmul_noalloc(const void* a, const void* b, void
 
 extern "C" size_t tg_block_scaled_matmul_bwd_workspace(int64_t M, int64_t N, int64_t K, int block_k) {
   if (block_k <= 0 || M < 0 || N < 0 || K < 0) return 0;
-  const size_t mkb = scale_cols(M, block_k), nkb = scale_cols(N, block_k);
-  return align256((size_t)M * N) + align256((size_t)M * nkb * 4) +   // g along N
-         align256((size_t)K * N) + align256((size_t)K * nkb * 4) +   // b along N
-         align256((size_t)K * M) + align256((size_t)K * mkb * 4) +   // a.T along M
-         align256((size_t)N * M) + align256((size_t)N * mkb * 4);    // g.T along M
+  const size_t mkb = scale_cols(M, block_k), nkb = scale_cols(N, block_k), pf = (size_t)gb_pf(block_k);
+  return align256((size_t)M * N * pf) + align256((size_t)M * nkb * 4) +   // g along N
+         align256((size_t)K * N * pf) + align256((size_t)K * nkb * 4) +   // b along N
+         align256((size_t)K * M * pf) + align256((size_t)K * mkb * 4) +   // a.T along M
+         align256((size_t)N * M * pf) + align256((size_t)N * mkb * 4);    // g.T along M
 }
 
 extern "C" int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, const void* g,
@@ -1838,23 +1845,25 @@ extern "C" int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, cons
     hipStream_t st = as_stream(stream);
     const int bk = block_k;
     const int64_t mkb = (int64_t)scale_cols(M, bk), nkb = (int64_t)scale_cols(N, bk);
-    const int srep = bk % 128 == 0 ? bk / 128 : 1;   // multiples of 128: the tuned GEMM (see block_scaled_matmul_gb)
+    const int srep = gb_srep(bk), pf = gb_pf(bk);   // the tuned GEMM's layouts (see block_scaled_matmul_gb)
+    const bool tuned = gb_tuned(bk);
+    const int64_t nq = N * pf, mq = M * pf;
     uint8_t* p = reinterpret_cast<uint8_t*>(workspace);
-    uint8_t* qg = p;    p += align256((size_t)M * N);
+    uint8_t* qg = p;    p += align256((size_t)M * nq);
     float* sg = reinterpret_cast<float*>(p);    p += align256((size_t)M * nkb * 4);
-    uint8_t* qb = p;    p += align256((size_t)K * N);
+    uint8_t* qb = p;    p += align256((size_t)K * nq);
     float* sb = reinterpret_cast<float*>(p);    p += align256((size_t)K * nkb * 4);
-    uint8_t* qat = p;   p += align256((size_t)K * M);
+    uint8_t* qat = p;   p += align256((size_t)K * mq);
     float* sat = reinterpret_cast<float*>(p);   p += align256((size_t)K * mkb * 4);
-    uint8_t* qgt = p;   p += align256((size_t)N * M);
+    uint8_t* qgt = p;   p += align256((size_t)N * mq);
     float* sgt = reinterpret_cast<float*>(p);
-    TG_TRY(launch_quant_rows_gb(g, TG_DTYPE_BF16, M, N, bk, qg, sg, st, srep));
-    TG_TRY(launch_quant_rows_gb(b, TG_DTYPE_BF16, K, N, bk, qb, sb, st, srep));
-    if (srep > 1) TG_TRY(launch_gemm_fp8(qg, sg, qb, sb, 1, da, TG_DTYPE_BF16, M, K, N, st, false));
+    TG_TRY(launch_quant_rows_gb(g, TG_DTYPE_BF16, M, N, bk, qg, sg, st, srep, pf));
+    TG_TRY(launch_quant_rows_gb(b, TG_DTYPE_BF16, K, N, bk, qb, sb, st, srep, pf));
+    if (tuned) TG_TRY(launch_gemm_fp8(qg, sg, qb, sb, 1, da, TG_DTYPE_BF16, M, K, nq, st, false));
     else TG_TRY(launch_gemm_gb(qg, sg, qb, sb, 1, da, TG_DTYPE_BF16, M, K, N, bk, st));      // dX = g . b.T
-    TG_TRY(launch_quant_cols_gb(a, M, K, bk, qat, sat, st, srep));
-    TG_TRY(launch_quant_cols_gb(g, M, N, bk, qgt, sgt, st, srep));
-    if (srep > 1) return launch_gemm_fp8(qat, sat, qgt, sgt, 1, db, TG_DTYPE_BF16, K, N, M, st, false);
+    TG_TRY(launch_quant_cols_gb(a, M, K, bk, qat, sat, st, srep, pf));
+    TG_TRY(launch_quant_cols_gb(g, M, N, bk, qgt, sgt, st, srep, pf));
+    if (tuned) return launch_gemm_fp8(qat, sat, qgt, sgt, 1, db, TG_DTYPE_BF16, K, N, mq, st, false);
     return launch_gemm_gb(qat, sat, qgt, sgt, 1, db, TG_DTYPE_BF16, K, N, M, bk, st);   // dW = a.T . g
   }
   if (!aligned(workspace, 256) || !aligned(a, 16) || !aligned(b, 16) || !aligned(g, 16))

@@ -73,11 +73,13 @@ int launch_gemm_fp8(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, co
                     hipStream_t st, bool skm = false);
 // The general path for block_k != 128 (block_generic.hip): row-major scales,
 // any block_k >= 1 dividing the contracted extent.
-// srep: each block's scale written srep times (bk / 128: the tuned GEMM's 128-wide scale layout).
+// For the tuned GEMM: srep = bk / 128 writes each block's scale srep times;
+// pf = 128 / bk puts each block at the start of a zero-filled 128-byte slot
+// (q rows of cols * pf bytes).
 int launch_quant_rows_gb(const void* x, int x_dtype, int64_t rows, int64_t cols, int bk, uint8_t* q, float* s,
-                         hipStream_t st, int srep = 1);
+                         hipStream_t st, int srep = 1, int pf = 1);
 int launch_quant_cols_gb(const void* x, int64_t rows, int64_t cols, int bk, uint8_t* q_t, float* s_t,
-                         hipStream_t st, int srep = 1);
+                         hipStream_t st, int srep = 1, int pf = 1);
 int launch_gemm_gb(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s, int bn, void* c,
                    int c_dtype, int64_t M, int64_t N, int64_t K, int bk, hipStream_t st);
 
