@@ -11,7 +11,8 @@
 // block, and the GEMM adds each block's exact-in-f32 partial dot product as
 // acc = fma(P, sa * sb, acc) in block order (fp8.py:70-76), in f32 on the VALU.
 // They are correct for every block size, not tuned: one thread per block in
-// the quantizers, a 64 x 64 LDS-tiled VALU GEMM.
+// the quantizers (16-byte loads / stores where bk % 16 == 0), a 64 x 64
+// LDS-tiled VALU GEMM.
 #include "tg_device.h"
 #include "tg_host.h"
 
@@ -53,8 +54,50 @@ __global__ __launch_bounds__(256) void quant_rows_gb_kernel(const void* __restri
   for (int k = bk; k < bk * pf; ++k) qo[k] = 0;
 }
 
+// four e4m3fn bytes of (a, b, c, d) / s, packed little-endian
+__device__ __forceinline__ uint32_t gb_quant4(float a, float b, float c, float d, float s, bool finite_scale) {
+  if (finite_scale) return e4m3x4(a / s, b / s, c / s, d / s);
+  return e4m3_nonfinite_scale(a, s) | (e4m3_nonfinite_scale(b, s) << 8) | (e4m3_nonfinite_scale(c, s) << 16) |
+         (e4m3_nonfinite_scale(d, s) << 24);
+}
+__device__ __forceinline__ uint32_t gb_quant4_bf16(uint32_t lo, uint32_t hi, float s, bool fin) {
+  return gb_quant4(bf16lo(lo), bf16hi(lo), bf16lo(hi), bf16hi(hi), s, fin);
+}
+__device__ __forceinline__ uint32_t bf16_amax2(uint32_t w) {
+  return max((w << 16) & 0x7FFFFFFFu, w & 0x7FFF0000u);
+}
+
+// The same for bf16 x, bk % 16 == 0, x and q 16-byte aligned: 16-byte loads
+// and stores (a thread's block is contiguous in x and in q).
+__global__ __launch_bounds__(256) void quant_rows_gb16_kernel(const uint16_t* __restrict__ x, int64_t rows,
+                                                              int64_t cols, int bk, uint8_t* __restrict__ q,
+                                                              float* __restrict__ s, int srep, int pf) {
+  const int64_t nb = cols / bk;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * nb) return;
+  const int64_t r = i / nb, b = i - r * nb;
+  const int64_t base = r * cols + b * bk;
+  const uint4* xv = reinterpret_cast<const uint4*>(x + base);
+  uint32_t m = 0;
+  for (int k = 0; k < bk / 8; ++k) {
+    const uint4 v = xv[k];
+    m = max(max(max(m, bf16_amax2(v.x)), bf16_amax2(v.y)), max(bf16_amax2(v.z), bf16_amax2(v.w)));
+  }
+  const float sc = block_scale(m);
+  for (int t = 0; t < srep; ++t) s[i * srep + t] = sc;
+  const bool fin = gb_finite(sc);
+  uint4* qo = reinterpret_cast<uint4*>(q + base * pf);
+  for (int k = 0; k < bk / 16; ++k) {
+    const uint4 u = xv[2 * k], v = xv[2 * k + 1];
+    qo[k] = make_uint4(gb_quant4_bf16(u.x, u.y, sc, fin), gb_quant4_bf16(u.z, u.w, sc, fin),
+                       gb_quant4_bf16(v.x, v.y, sc, fin), gb_quant4_bf16(v.z, v.w, sc, fin));
+  }
+  for (int k = bk / 16; k < bk * pf / 16; ++k) qo[k] = make_uint4(0u, 0u, 0u, 0u);
+}
+
 // x (R, C) bf16 -> the quantization of x.T along R: q_t (C, R), s_t (C, R / bk);
 // one thread per (row block, column), columns fastest (coalesced reads of x)
+template <bool VEC>
 __global__ __launch_bounds__(256) void quant_cols_gb_kernel(const uint16_t* __restrict__ x, int64_t R, int64_t C,
                                                             int bk, uint8_t* __restrict__ qt,
                                                             float* __restrict__ st, int srep, int pf) {
@@ -69,8 +112,20 @@ __global__ __launch_bounds__(256) void quant_cols_gb_kernel(const uint16_t* __re
   for (int t = 0; t < srep; ++t) st[(c * nb + b) * srep + t] = sc;
   const bool fin = gb_finite(sc);
   uint8_t* qo = qt + (c * R + r0) * pf;
-  for (int k = 0; k < bk; ++k)
-    qo[k] = gb_quant1(__uint_as_float((uint32_t)x[(r0 + k) * C + c] << 16), sc, fin);
+  auto xf = [&](int k) { return __uint_as_float((uint32_t)x[(r0 + k) * C + c] << 16); };
+  if (VEC) {   // bk % 16 == 0, q_t 16-byte aligned: a thread's bytes in 16-byte stores
+    uint4* qv = reinterpret_cast<uint4*>(qo);
+    for (int k = 0; k < bk; k += 16) {
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        w[j] = gb_quant4(xf(k + 4 * j), xf(k + 4 * j + 1), xf(k + 4 * j + 2), xf(k + 4 * j + 3), sc, fin);
+      qv[k / 16] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    for (int k = bk / 16; k < bk * pf / 16; ++k) qv[k] = make_uint4(0u, 0u, 0u, 0u);
+    return;
+  }
+  for (int k = 0; k < bk; ++k) qo[k] = gb_quant1(xf(k), sc, fin);
   for (int k = bk; k < bk * pf; ++k) qo[k] = 0;
 }
 
@@ -168,7 +223,11 @@ int launch_quant_rows_gb(const void* x, int x_dtype, int64_t rows, int64_t cols,
   const int64_t n = rows * (cols / bk);
   if (n == 0) return TG_OK;
   if (n / 256 >= 0x7FFFFFFF) return einval("quantize_rows: too many blocks");
-  if (x_dtype == TG_DTYPE_F32)
+  const bool vec = bk % 16 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 15) == 0;
+  if (x_dtype != TG_DTYPE_F32 && vec)
+    hipLaunchKernelGGL(quant_rows_gb16_kernel, dim3(gb_grid(n)), dim3(256), 0, st,
+                       reinterpret_cast<const uint16_t*>(x), rows, cols, bk, q, s, srep, pf);
+  else if (x_dtype == TG_DTYPE_F32)
     hipLaunchKernelGGL(quant_rows_gb_kernel<true>, dim3(gb_grid(n)), dim3(256), 0, st, x, rows, cols, bk, q, s,
                        srep, pf);
   else
@@ -182,8 +241,12 @@ int launch_quant_cols_gb(const void* x, int64_t rows, int64_t cols, int bk, uint
   const int64_t n = (rows / bk) * cols;
   if (n == 0) return TG_OK;
   if (n / 256 >= 0x7FFFFFFF) return einval("quantize_cols: too many blocks");
-  hipLaunchKernelGGL(quant_cols_gb_kernel, dim3(gb_grid(n)), dim3(256), 0, st,
-                     reinterpret_cast<const uint16_t*>(x), rows, cols, bk, q_t, s_t, srep, pf);
+  if (bk % 16 == 0 && ((uintptr_t)q_t & 15) == 0)
+    hipLaunchKernelGGL(quant_cols_gb_kernel<true>, dim3(gb_grid(n)), dim3(256), 0, st,
+                       reinterpret_cast<const uint16_t*>(x), rows, cols, bk, q_t, s_t, srep, pf);
+  else
+    hipLaunchKernelGGL(quant_cols_gb_kernel<false>, dim3(gb_grid(n)), dim3(256), 0, st,
+                       reinterpret_cast<const uint16_t*>(x), rows, cols, bk, q_t, s_t, srep, pf);
   return check_launch("quantize_cols (block_k != 128)");
 }
 
