@@ -47,6 +47,9 @@ xent         = config 4's head: fused logit cap + cross entropy (losses.py) on
 decode       = KV-cached decode (decode.py) of the reference model config:
                ms per decode step at batch 1 and 8, and the kept FP8 weights +
                KV cache read per step against 8 TB/s
+block_k_sizes = config 3's forward (tg_block_scaled_matmul) at block_k 128,
+               64 (zero-filled 128-byte slots) and 256 (repeated scales):
+               mean time per call, quantization included
 io_floor     = (--only) config 2's bytes moved by csrc/probe/io_floor.hip with
                the fused norm kernel's access pattern and no arithmetic: the
                attainable rate of that read / write mix, beside the real kernel
@@ -58,7 +61,7 @@ cpu_baseline = the CPU oracle (numpy + C) on a row sample of the same step
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                       [--only step|norm_quant|norm_bwd|gemv|bwd_bf16|block_step|xent|decode|
-                              vendor_gemm|c1|io_floor|gemv_floor]
+                              vendor_gemm|c1|block_k|io_floor|gemv_floor]
 """
 import argparse
 import json
@@ -222,7 +225,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--norm-iters", type=int, default=200)
     p.add_argument("--only", choices=["step", "norm_quant", "norm_bwd", "gemv", "bwd_bf16",
-                                      "block_step", "xent", "decode", "vendor_gemm", "c1", "io_floor",
+                                      "block_step", "xent", "decode", "vendor_gemm", "c1", "block_k", "io_floor",
                                       "gemv_floor"],
                    help="run one secondary workload alone and print its JSON object")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -774,6 +777,35 @@ def step_accuracy(step, rows=256):
     return out
 
 
+def bench_block_k(dev, iters):
+    """The C3 forward (tg_block_scaled_matmul, x[8192,2048] . W[2048,8192]
+    with both quantizations) at block sizes other than 128 (fp8.py:30-36 takes
+    any block_k dividing K): 256 runs the tuned GEMM on repeated scales, 64 on
+    zero-filled 128-byte slots (twice the MFMA work)."""
+    import torch
+    import _tglib as L
+    lib = L.lib()
+    M, K, N = 8192, 2048, 8192
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    x = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn((K, N), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    st = L.stream_of(x)
+    out = {"workload": "C3 block_scaled_matmul forward, x[8192,2048] W[2048,8192] bf16, quantization included"}
+    for bk in (128, 64, 256):
+        ws_bytes = lib.tg_block_scaled_matmul_workspace(M, N, K, bk)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+
+        def fwd(i, bk=bk, ws=ws, ws_bytes=ws_bytes):
+            L.check(lib.tg_block_scaled_matmul(L.ptr(x), L.ptr(w), L.ptr(y), M, N, K, bk, L.ptr(ws),
+                                               ws_bytes, st))
+        us = _mean_launch_us(fwd, iters)
+        out[f"block_k_{bk}"] = {"us_per_call": round(us, 2), "tflops": round(2.0 * M * N * K / (us * 1e-6) / 1e12, 1)}
+        del ws
+    return out
+
+
 def bench_c1(dev, iters):
     """Config 1: the forward block_scaled_matmul at x[2048,768] . W[768,3072]
     (tg_block_scaled_matmul: both quantizations + the GEMM), and the GEMM alone
@@ -990,7 +1022,7 @@ def main():
               "block_step": lambda d, _: bench_block(d), "xent": bench_xent,
               "decode": lambda d, _: bench_decode(d),
               "vendor_gemm": lambda d, _: bench_vendor_gemm(d, 20),
-              "c1": bench_c1, "io_floor": bench_io_floor, "gemv_floor": bench_gemv_floor}[args.only]
+              "c1": bench_c1, "block_k": bench_block_k, "io_floor": bench_io_floor, "gemv_floor": bench_gemv_floor}[args.only]
         print(json.dumps({args.only: fn(dev, args.norm_iters)}))
         return
     step = Step(dev)
@@ -1034,9 +1066,10 @@ def main():
     power = (sustained_clock(step) if not under_profiler() else
              {"skipped": "not run under rocprofv3 (it would add ~2 s of launches to the trace)"})
     if args.only == "step":
-        norm = norm_bwd = gemv = bwd_bf16 = block_step = xent = dec = c1 = None
+        norm = norm_bwd = gemv = bwd_bf16 = block_step = xent = dec = c1 = bks = None
     else:
         c1 = bench_c1(dev, args.norm_iters)
+        bks = bench_block_k(dev, args.norm_iters)
         norm = bench_norm(dev, args.norm_iters)
         norm_bwd = bench_norm_bwd(dev, args.norm_iters)
         gemv = bench_gemv(dev, args.norm_iters)
@@ -1062,6 +1095,7 @@ def main():
         "accuracy": accuracy,
         "sustained_clock": power,
         "c1": c1,
+        "block_k_sizes": bks,
         "norm_quant": norm,
         "norm_bwd": norm_bwd,
         "gemv": gemv,
