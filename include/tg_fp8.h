@@ -16,9 +16,15 @@
  * tg_quantize_cols, tg_gemm_fp8_nt, tg_block_scaled_matmul and
  * tg_block_scaled_matmul_bwd_fp8 accept every block_k >= 1 that divides the
  * contracted extent: 128 runs the tuned kernels (two FP8 MFMA K steps per
- * scale block), any other size the general kernels (the same numeric
- * contract, bytes and scales bit for bit; not tuned).  Every other entry
- * point is a fused kernel of this library and takes block_k == 128 only.
+ * scale block); other sizes quantize with the general kernels (bytes and
+ * scales bit for bit those of the 128 path's contract).  The composites
+ * (tg_block_scaled_matmul, tg_block_scaled_matmul_bwd_fp8) then run the
+ * tuned GEMM for 16, 32, 64 (each block in a zero-filled 128-wide slot) and
+ * multiples of 128 (the block's scale repeated per 128-wide sub-block, so the
+ * f32 sum is folded once per sub-block and can differ from tg_gemm_fp8_nt at
+ * the same block_k in the last bits), and the general GEMM (one P per block,
+ * folded once) for every other size.  Every other entry point is a fused
+ * kernel of this library and takes block_k == 128 only.
  *
  * Reference citations are /root/reference/<file>:<line>.
  */
@@ -51,10 +57,13 @@ int tg_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, int
 int tg_quantize_rows_relu2(const void* x, int64_t rows, int64_t cols, int block_k, uint8_t* q,
                            float* scales, void* stream);
 
-/* _quantize_to_fp8 of x.T (fp8.py:68 applies it to b.T): quantizes the columns
- * of x (rows, cols) bf16 and writes them transposed:
- * q_t: (cols, rows) e4m3fn; scales_t: (cols, rows/block_k) f32.  rows % block_k == 0;
- * any cols (16-byte loads when cols % 8 == 0 and x is 16-byte aligned). */
+/* _quantize_to_fp8 of x.T (fp8.py:68 applies it to b.T, whatever b's float
+ * dtype, after astype(f32)): quantizes the columns of x (rows, cols) and writes
+ * them transposed: q_t: (cols, rows) e4m3fn; scales_t: (cols, rows/block_k)
+ * f32.  x_dtype TG_DTYPE_BF16 or TG_DTYPE_F32; rows % block_k == 0; any cols.
+ * bf16 with block_k == 128 runs the tuned tile kernel (16-byte loads when
+ * cols % 8 == 0 and x is 16-byte aligned); f32 and other block sizes the
+ * general one-thread-per-block kernel. */
 int tg_quantize_cols(const void* x, int x_dtype, int64_t rows, int64_t cols, int block_k,
                      uint8_t* q_t, float* scales_t, void* stream);
 

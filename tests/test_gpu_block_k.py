@@ -66,6 +66,20 @@ def test_quantize_rows_f32_bit_exact(dev, block_k):
     assert same_scales(s.cpu().numpy(), so)
 
 
+@pytest.mark.parametrize("block_k", [16, 96, 128, 768])
+def test_quantize_transposed_f32_bit_exact(dev, block_k):
+    """f32 input to the transposed quantizer (fp8.py:68 quantizes b.T after
+    astype(f32), whatever b's dtype): the general kernel at every block_k."""
+    rng = np.random.default_rng(31 + block_k)
+    x = (rng.standard_normal((768, 24)) * np.exp2(rng.integers(-20, 20, (1, 24)))).astype(np.float32)
+    x[:4, 0] = [np.nan, np.inf, -np.inf, 1e-42]
+    x[:, 3] = 0.0
+    q, s = fp8.quantize_fp8(torch.from_numpy(x).to(dev), block_k, transpose=True)
+    qo, so = fp8_ref.quantize_fp8(np.ascontiguousarray(x.T), block_k)
+    np.testing.assert_array_equal(u8(q), qo)
+    assert same_scales(s.cpu().numpy(), so)
+
+
 @pytest.mark.parametrize("block_k", BLOCKS)
 def test_quantize_transposed_bit_exact(dev, block_k):
     rng = np.random.default_rng(100 + block_k)
@@ -118,13 +132,34 @@ def test_scaled_gemm_known_answer(dev, block_k, bn):
     np.testing.assert_array_equal(c32, want.astype(np.float32))
 
 
-@pytest.mark.parametrize("block_k", [32, 64, 256])
-@pytest.mark.parametrize("lead,K,N", [((96,), 512, 160), ((3, 50), 768, 96)])
-def test_forward_composite(dev, block_k, lead, K, N):
+def _unaligned_bf16(x_u16: np.ndarray, dev) -> torch.Tensor:
+    """x on the device at a 2-byte (not 16-byte) aligned address: a contiguous
+    view one element into a larger buffer, so the scalar quantizer runs."""
+    flat = torch.zeros(x_u16.size + 8, dtype=torch.bfloat16, device=dev)
+    v = flat[1:1 + x_u16.size].view(x_u16.shape)
+    v.copy_(to_dev(x_u16, dev))
+    assert v.data_ptr() % 16 != 0 and v.is_contiguous()
+    return v
+
+
+COMPOSITE_CASES = [(bk, (96,), 512, 160) for bk in (16, 32, 64, 256)] + \
+    [(bk, (3, 50), 768, 96) for bk in (16, 32, 64, 96, 256, 384)]
+
+
+@pytest.mark.parametrize("unaligned", [False, True])
+@pytest.mark.parametrize("block_k,lead,K,N", COMPOSITE_CASES)
+def test_forward_composite(dev, block_k, lead, K, N, unaligned):
+    """Random data through tg_block_scaled_matmul at every kind of block size:
+    16 (eight zero slots per 128, one 16-byte vector per block), 32, 64, the
+    untuned 96 (the general GEMM), 256 and 384 (scales repeated 2 and 3
+    times); unaligned=True feeds a 2-byte aligned a (the scalar quantizer)."""
+    if unaligned and block_k not in (16, 96, 384):
+        pytest.skip("the unaligned input is exercised at one size of each kind")
     rng = np.random.default_rng(K + N + block_k)
     a = ob.randn_bf16(rng, (*lead, K))
     b = ob.randn_bf16(rng, (K, N), std=0.02)
-    ad, bd = to_dev(a, dev), to_dev(b, dev)
+    ad = _unaligned_bf16(a, dev) if unaligned else to_dev(a, dev)
+    bd = to_dev(b, dev)
     y = fp8.block_scaled_matmul(ad, bd, block_k=block_k)
     _, ref, _, _ = fp8_ref.fp8_forward(a, b, block_k)
     assert y.shape == (*lead, N) and y.dtype == torch.bfloat16
@@ -135,7 +170,9 @@ def test_forward_composite(dev, block_k, lead, K, N):
     qa, sa = fp8.quantize_fp8(ad.reshape(-1, K), block_k)
     qb, sb = fp8.quantize_fp8(bd, block_k, transpose=True)
     qa, qb = qa.view(torch.uint8), qb.view(torch.uint8)
-    if block_k % 128 == 0:
+    if block_k % 128 != 0 and 128 % block_k != 0:
+        pass                                  # untuned: the composite runs the general GEMM itself
+    elif block_k % 128 == 0:
         sa, sb = sa.repeat_interleave(block_k // 128, dim=1), sb.repeat_interleave(block_k // 128, dim=1)
     else:
         def slots(q):
@@ -148,8 +185,12 @@ def test_forward_composite(dev, block_k, lead, K, N):
     assert torch.equal(y.reshape(-1, N).view(torch.int16), y2.view(torch.int16))
 
 
-@pytest.mark.parametrize("block_k", [32, 64, 256])
-@pytest.mark.parametrize("M,K,N", [(128, 256, 192), (100, 256, 70), (512, 512, 768)])
+BWD_CASES = [(bk, M, K, N) for bk in (16, 32, 64, 256)
+             for (M, K, N) in ((128, 256, 192), (100, 256, 70), (512, 512, 768))] + \
+    [(bk, M, K, N) for bk in (96, 384) for (M, K, N) in ((200, 768, 300), (768, 384, 96))]
+
+
+@pytest.mark.parametrize("block_k,M,K,N", BWD_CASES)
 def test_fp8_backward(dev, block_k, M, K, N):
     """BACKWARD_MODE "fp8" through autograd; ragged M / N (not multiples of
     block_k) take the zero-padded last block."""

@@ -40,6 +40,22 @@ def test_gemv_c5(dev, weight, layout, M):
     assert maxabs_rel(out, ref) <= 1e-2
 
 
+@pytest.mark.parametrize("layout", ["128x1", "128x128"])
+def test_gemv_c5_rowdot_m1(dev, weight, layout):
+    """Config 5 at M = 1 on the kernel the default fp8_gemv (and bench.py's
+    C5 M = 1 line) runs, tg_gemv_fp8_rowdot, against the float64 oracle: the
+    1e-2 bar and the elementwise one-bf16-rounding bar."""
+    w_u, w_d = weight
+    rng = np.random.default_rng(101)
+    x = ob.randn_bf16(rng, (1, 4096))
+    wq, ws, bn = fp8.quantize_weight(w_d, layout=layout)
+    out = fp8.fp8_gemv(to_dev(x, dev), wq, ws, w_scale_bn=bn)
+    assert out.shape == (1, 14336) and out.dtype == torch.bfloat16
+    qx, sx = fp8_ref.quantize_fp8(ob.bf16_to_f32(x))
+    ref = fp8_ref.gemv_prequant(qx, sx, u8(wq), ws.cpu().numpy(), bn)
+    assert maxabs_rel(out, ref) <= 1e-2 and _rowdot_close(out, ref)
+
+
 # Ragged shapes: rows per workgroup not a multiple of 16, N not a multiple of 4
 # (scalar output stores), K spanning several rounds of the 8 waves (K = 8192,
 # 20480), waves without K blocks (K = 256), scale rows straddling a 128-row
@@ -75,7 +91,8 @@ def _rowdot_close(out, ref) -> bool:
 # N = 1 (one wave busy), N not a multiple of 4, K = 128 (one block, lanes past
 # the row) up to K = 16384 (the LDS limit), rows beyond one sweep of the grid
 # (N > 8 workgroups x 4 waves x CUs), both M.
-ROWDOT = [(1, 1, 128), (2, 1, 128), (1, 3, 256), (2, 130, 1152), (1, 1001, 4096), (2, 14336, 4096),
+ROWDOT = [(1, 1, 128), (2, 1, 128), (1, 3, 256), (2, 130, 1152), (1, 1001, 4096), (1, 14336, 4096),
+          (2, 14336, 4096),
           (1, 4096, 14336), (2, 2304, 9216), (1, 50257, 2304), (2, 77, 16384), (1, 9000, 640)]
 
 

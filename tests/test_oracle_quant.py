@@ -10,6 +10,7 @@ an e4m3 step; NaN/inf propagate; the C and numpy restatements agree.
 from fractions import Fraction
 
 import numpy as np
+import torch
 
 from oracle import bf16 as ob
 from oracle import cbind, fp8_ref
@@ -107,6 +108,46 @@ def test_weight_128x128_tiles():
     assert s[1, 1] == np.float32(np.max(np.abs(w_t[128:, 128:]))) / np.float32(448)
     deq = fp8_ref.e4m3fn_decode(q) * np.repeat(np.repeat(s, 128, 0)[:200], 128, 1)
     assert np.max(np.abs(deq - w_t)) <= np.max(np.abs(w_t)) * 2.0 ** -4
+
+
+def test_weight_128x128_every_tile_exact():
+    """Every tile of a non-square, ragged grid: (300, 512) -> 3 x 4 tiles, the
+    last row block 44 rows deep.  Each tile gets its own magnitude (a factor
+    2^(row block) * 3^(col block)), so a transposed or shifted tile index picks
+    a scale that is off by a factor >= 1.5 and fails.  Tile (1, 2) is all zero
+    (scale floor 1e-30, bytes 0x00); one element of tile (2, 3) is -0.0.  The
+    expected scale is the exact rational amax / 448 rounded once to f32 by
+    _round_f32 (Fraction arithmetic, no numpy division), floored at
+    fl32(1e-30); the expected bytes are torch's float8_e4m3fn cast of the IEEE
+    f32 quotient, and the tile's amax element encodes to +-448."""
+    rng = np.random.default_rng(11)
+    N, K = 300, 512
+    w = rng.standard_normal((N, K)).astype(np.float32)
+    for tr in range(3):
+        for tc in range(4):
+            w[128 * tr:128 * (tr + 1), 128 * tc:128 * (tc + 1)] *= np.float32(2.0 ** tr * 3.0 ** tc)
+    w[128:256, 256:384] = 0.0
+    w[299, 511] = -0.0
+    q, s = fp8_ref.quantize_weight_128x128(w)
+    assert q.shape == (N, K) and s.shape == (3, 4)
+    floor = np.float32(1e-30)
+    for tr in range(3):
+        rows = slice(128 * tr, min(128 * (tr + 1), N))
+        for tc in range(4):
+            cols = slice(128 * tc, 128 * (tc + 1))
+            tile = w[rows, cols]
+            amax = max(abs(float(v)) for v in tile.ravel())
+            want = max(_round_f32(Fraction(amax) / 448), floor) if amax > 0 else floor
+            assert s[tr, tc] == want, (tr, tc, s[tr, tc], want)
+            quot = (tile / np.float32(want)).astype(np.float32)
+            got = q[rows, cols]
+            exp = torch.from_numpy(np.ascontiguousarray(quot)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+            np.testing.assert_array_equal(got, exp, err_msg=f"tile ({tr}, {tc})")
+            if amax > 0:
+                r, c = np.unravel_index(np.argmax(np.abs(tile)), tile.shape)
+                assert got[r, c] in (0x7E, 0xFE), (tr, tc, hex(int(got[r, c])))
+    assert s[1, 2] == floor and np.all(q[128:256, 256:384] == 0)
+    assert q[299, 511] == 0x80
 
 
 def test_partial_trailing_block_is_its_valid_elements():

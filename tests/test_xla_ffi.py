@@ -58,3 +58,33 @@ def test_build_step_skips_without_jax(capsys):
         assert "skipping the XLA FFI handlers" in capsys.readouterr().out
     else:  # jaxlib present: the handlers must build
         assert os.path.exists(build.build_xla_ffi())
+
+
+def test_handler_dtypes_are_accepted_by_their_c_abi():
+    """Every handler that maps an operand's bf16 / f32 element type onto a
+    dtype code forwards it to a C-ABI entry point, which must accept both
+    codes: called with null pointers on a non-empty shape, each entry point
+    gets past its dtype check and stops at the pointer check (no launch)."""
+    import ctypes
+    lib = L.lib()
+    nul = ctypes.c_void_p(0)
+    code = _code(SRC)
+    # the handlers forwarding dtype codes, and the entry points they call with them
+    assert re.search(r"tg_quantize_cols\(b\.untyped_data\(\), cb,", code)
+    assert re.search(r"tg_quantize_rows\(a\.untyped_data\(\), ca,", code)
+    calls = {
+        "tg_quantize_rows": lambda d: lib.tg_quantize_rows(nul, d, 4, 256, 128, nul, nul, nul),
+        "tg_quantize_cols": lambda d: lib.tg_quantize_cols(nul, d, 256, 4, 128, nul, nul, nul),
+        "tg_quantize_cols (block_k 64)": lambda d: lib.tg_quantize_cols(nul, d, 256, 4, 64, nul, nul, nul),
+        "tg_rms_norm_ex": lambda d: lib.tg_rms_norm_ex(nul, d, nul, d, nul, 4, 256, ctypes.c_float(1e-6), nul),
+        "tg_rms_norm_bwd_ex": lambda d: lib.tg_rms_norm_bwd_ex(nul, d, nul, d, nul, d, nul, nul, 4, 256,
+                                                               ctypes.c_float(1e-6), nul, 0, nul),
+        "tg_block_scaled_matmul_bwd_bf16": lambda d: lib.tg_block_scaled_matmul_bwd_bf16(
+            nul, d, nul, d, nul, d, nul, nul, 128, 128, 128, nul, 0, nul),
+    }
+    for name, call in calls.items():
+        for d in (L.TG_DTYPE_BF16, L.TG_DTYPE_F32):
+            assert call(d) == L.TG_EINVAL, (name, d)
+            msg = lib.tg_last_error().decode()
+            assert "dtype" not in msg, (name, d, msg)
+        assert call(9) == L.TG_EINVAL and "dtype" in lib.tg_last_error().decode(), name

@@ -8,8 +8,10 @@
 //   q     = e4m3fn(x / scale)       (IEEE divide, RNE; the non-finite-scale
 //                                    rule of e4m3_nonfinite_scale)
 // so a block's bytes and scale are those the 128 kernels give for the same
-// block, and the GEMM adds each block's exact-in-f32 partial dot product as
-// acc = fma(P, sa * sb, acc) in block order (fp8.py:70-76), in f32 on the VALU.
+// block, and the GEMM forms each block's partial dot product P as an f32 fma
+// chain in k order (which rounds once the block's products span more than
+// f32's 24 bits) and adds it as acc = fma(P, sa * sb, acc) in block order
+// (fp8.py:70-76), in f32 on the VALU.
 // They are correct for every block size, not tuned: one thread per block in
 // the quantizers (16-byte loads / stores where bk % 16 == 0), a 64 x 64
 // LDS-tiled VALU GEMM.
@@ -95,10 +97,11 @@ __global__ __launch_bounds__(256) void quant_rows_gb16_kernel(const uint16_t* __
   for (int k = bk / 16; k < bk * pf / 16; ++k) qo[k] = make_uint4(0u, 0u, 0u, 0u);
 }
 
-// x (R, C) bf16 -> the quantization of x.T along R: q_t (C, R), s_t (C, R / bk);
-// one thread per (row block, column), columns fastest (coalesced reads of x)
-template <bool VEC>
-__global__ __launch_bounds__(256) void quant_cols_gb_kernel(const uint16_t* __restrict__ x, int64_t R, int64_t C,
+// x (R, C) bf16 or f32 -> the quantization of x.T along R: q_t (C, R),
+// s_t (C, R / bk); one thread per (row block, column), columns fastest
+// (coalesced reads of x)
+template <bool VEC, bool F32_IN>
+__global__ __launch_bounds__(256) void quant_cols_gb_kernel(const void* __restrict__ x, int64_t R, int64_t C,
                                                             int bk, uint8_t* __restrict__ qt,
                                                             float* __restrict__ st, int srep, int pf) {
   const int64_t nb = R / bk;
@@ -106,13 +109,13 @@ __global__ __launch_bounds__(256) void quant_cols_gb_kernel(const uint16_t* __re
   if (i >= nb * C) return;
   const int64_t b = i / C, c = i - b * C;
   const int64_t r0 = b * bk;
+  auto xf = [&](int k) { return gb_load(x, (r0 + k) * C + c, F32_IN); };
   uint32_t m = 0;
-  for (int k = 0; k < bk; ++k) m = max(m, ((uint32_t)x[(r0 + k) * C + c] << 16) & 0x7FFFFFFFu);
+  for (int k = 0; k < bk; ++k) m = max(m, __float_as_uint(xf(k)) & 0x7FFFFFFFu);
   const float sc = block_scale(m);
   for (int t = 0; t < srep; ++t) st[(c * nb + b) * srep + t] = sc;
   const bool fin = gb_finite(sc);
   uint8_t* qo = qt + (c * R + r0) * pf;
-  auto xf = [&](int k) { return __uint_as_float((uint32_t)x[(r0 + k) * C + c] << 16); };
   if (VEC) {   // bk % 16 == 0, q_t 16-byte aligned: a thread's bytes in 16-byte stores
     uint4* qv = reinterpret_cast<uint4*>(qo);
     for (int k = 0; k < bk; k += 16) {
@@ -236,18 +239,21 @@ int launch_quant_rows_gb(const void* x, int x_dtype, int64_t rows, int64_t cols,
   return check_launch("quantize_rows (block_k != 128)");
 }
 
-int launch_quant_cols_gb(const void* x, int64_t rows, int64_t cols, int bk, uint8_t* q_t, float* s_t,
-                         hipStream_t st, int srep, int pf) {
+int launch_quant_cols_gb(const void* x, bool x_f32, int64_t rows, int64_t cols, int bk, uint8_t* q_t,
+                         float* s_t, hipStream_t st, int srep, int pf) {
   const int64_t n = (rows / bk) * cols;
   if (n == 0) return TG_OK;
   if (n / 256 >= 0x7FFFFFFF) return einval("quantize_cols: too many blocks");
-  if (bk % 16 == 0 && ((uintptr_t)q_t & 15) == 0)
-    hipLaunchKernelGGL(quant_cols_gb_kernel<true>, dim3(gb_grid(n)), dim3(256), 0, st,
-                       reinterpret_cast<const uint16_t*>(x), rows, cols, bk, q_t, s_t, srep, pf);
-  else
-    hipLaunchKernelGGL(quant_cols_gb_kernel<false>, dim3(gb_grid(n)), dim3(256), 0, st,
-                       reinterpret_cast<const uint16_t*>(x), rows, cols, bk, q_t, s_t, srep, pf);
-  return check_launch("quantize_cols (block_k != 128)");
+  const bool vec = bk % 16 == 0 && ((uintptr_t)q_t & 15) == 0;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(gb_grid(n)), dim3(256), 0, st, x, rows, cols, bk, q_t, s_t, srep, pf);
+  };
+  if (x_f32) {
+    if (vec) go(quant_cols_gb_kernel<true, true>); else go(quant_cols_gb_kernel<false, true>);
+  } else {
+    if (vec) go(quant_cols_gb_kernel<true, false>); else go(quant_cols_gb_kernel<false, false>);
+  }
+  return check_launch("quantize_cols (general)");
 }
 
 int launch_gemm_gb(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s, int bn, void* c,

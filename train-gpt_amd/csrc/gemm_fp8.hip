@@ -1728,12 +1728,19 @@ static int block_scaled_matmul_on(const void* a, const void* b, void* out, int64
 
 // The forward composite for block_k != 128: row-major scales, the general
 // quantizers; a multiple of 128 then runs the tuned GEMM on its scales
-// repeated per 128-wide sub-block (the same sum: a block's sub-blocks share
-// the scale), any other block size the general GEMM.
+// repeated per 128-wide sub-block.  The bytes and scales are the block's; the
+// f32 sum is the same in exact arithmetic but rounds differently: the tuned
+// GEMM folds acc = fma(P_128, sa * sb, acc) once per 128-wide sub-block,
+// where tg_gemm_fp8_nt at the same block_k (the general GEMM) forms one P per
+// block and folds it once, so the two agree to f32 rounding, not bit for bit.
+// Any other block size runs the general GEMM.
 static int block_scaled_matmul_gb(const void* a, const void* b, void* out, int64_t M, int64_t N, int64_t K,
                                   int bk, void* workspace, hipStream_t st) {
   const int64_t nkb = (int64_t)scale_cols(K, bk);
-  const int srep = gb_srep(bk), pf = gb_pf(bk);
+  // the tuned GEMM takes a 32-bit contraction extent: a zero-slot layout that
+  // would grow K past it runs the general kernels instead
+  const bool tuned = gb_tuned(bk) && K * gb_pf(bk) <= 0x7FFFFFFF;
+  const int srep = tuned ? gb_srep(bk) : 1, pf = tuned ? gb_pf(bk) : 1;
   const int64_t kq = K * pf;
   uint8_t* p = reinterpret_cast<uint8_t*>(workspace);
   uint8_t* qa = p;                 p += align256((size_t)M * kq);
@@ -1741,8 +1748,8 @@ static int block_scaled_matmul_gb(const void* a, const void* b, void* out, int64
   uint8_t* qb = p;                 p += align256((size_t)N * kq);
   float* sb = reinterpret_cast<float*>(p);
   TG_TRY(launch_quant_rows_gb(a, TG_DTYPE_BF16, M, K, bk, qa, sa, st, srep, pf));     // fp8.py:66
-  TG_TRY(launch_quant_cols_gb(b, K, N, bk, qb, sb, st, srep, pf));                     // fp8.py:68
-  if (gb_tuned(bk)) return launch_gemm_fp8(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, kq, st, false);
+  TG_TRY(launch_quant_cols_gb(b, false, K, N, bk, qb, sb, st, srep, pf));                     // fp8.py:68
+  if (tuned) return launch_gemm_fp8(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, kq, st, false);
   return launch_gemm_gb(qa, sa, qb, sb, 1, out, TG_DTYPE_BF16, M, N, K, bk, st);   // fp8.py:70-78
 }
 
@@ -1845,8 +1852,10 @@ extern "C" int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, cons
     hipStream_t st = as_stream(stream);
     const int bk = block_k;
     const int64_t mkb = (int64_t)scale_cols(M, bk), nkb = (int64_t)scale_cols(N, bk);
-    const int srep = gb_srep(bk), pf = gb_pf(bk);   // the tuned GEMM's layouts (see block_scaled_matmul_gb)
-    const bool tuned = gb_tuned(bk);
+    // the tuned GEMM's layouts (see block_scaled_matmul_gb), while the grown
+    // contraction extents (N * pf for dX, M * pf for dW) stay 32-bit
+    const bool tuned = gb_tuned(bk) && N * gb_pf(bk) <= 0x7FFFFFFF && M * gb_pf(bk) <= 0x7FFFFFFF;
+    const int srep = tuned ? gb_srep(bk) : 1, pf = tuned ? gb_pf(bk) : 1;
     const int64_t nq = N * pf, mq = M * pf;
     uint8_t* p = reinterpret_cast<uint8_t*>(workspace);
     uint8_t* qg = p;    p += align256((size_t)M * nq);
@@ -1861,8 +1870,8 @@ extern "C" int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, cons
     TG_TRY(launch_quant_rows_gb(b, TG_DTYPE_BF16, K, N, bk, qb, sb, st, srep, pf));
     if (tuned) TG_TRY(launch_gemm_fp8(qg, sg, qb, sb, 1, da, TG_DTYPE_BF16, M, K, nq, st, false));
     else TG_TRY(launch_gemm_gb(qg, sg, qb, sb, 1, da, TG_DTYPE_BF16, M, K, N, bk, st));      // dX = g . b.T
-    TG_TRY(launch_quant_cols_gb(a, M, K, bk, qat, sat, st, srep, pf));
-    TG_TRY(launch_quant_cols_gb(g, M, N, bk, qgt, sgt, st, srep, pf));
+    TG_TRY(launch_quant_cols_gb(a, false, M, K, bk, qat, sat, st, srep, pf));
+    TG_TRY(launch_quant_cols_gb(g, false, M, N, bk, qgt, sgt, st, srep, pf));
     if (tuned) return launch_gemm_fp8(qat, sat, qgt, sgt, 1, db, TG_DTYPE_BF16, K, N, mq, st, false);
     return launch_gemm_gb(qat, sat, qgt, sgt, 1, db, TG_DTYPE_BF16, K, N, M, bk, st);   // dW = a.T . g
   }

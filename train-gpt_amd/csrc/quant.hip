@@ -617,14 +617,18 @@ extern "C" int tg_quantize_rows_relu2(const void* x, int64_t rows, int64_t cols,
 extern "C" int tg_quantize_cols(const void* x, int x_dtype, int64_t rows, int64_t cols,
                                 int block_k, uint8_t* q_t, float* scales_t, void* stream) {
   if (block_k <= 0) return einval("quantize_cols: block_k must be positive");
-  if (x_dtype != TG_DTYPE_BF16) return einval("quantize_cols: x_dtype must be TG_DTYPE_BF16");
+  if (x_dtype != TG_DTYPE_BF16 && x_dtype != TG_DTYPE_F32)
+    return einval("quantize_cols: x_dtype must be TG_DTYPE_BF16 or TG_DTYPE_F32");
   if (rows < 0 || cols < 0) return einval("quantize_cols: negative shape");
   if (rows % block_k) return einval("quantize_cols: rows not divisible by block_k");
   if (rows * cols == 0) return TG_OK;
   if (!x || !q_t || !scales_t) return einval("quantize_cols: null pointer");
-  if (block_k != 128) {
-    if (!aligned(x, 2) || !aligned(scales_t, 4)) return einval("quantize_cols: x and scales_t must be aligned");
-    return launch_quant_cols_gb(x, rows, cols, block_k, q_t, scales_t, as_stream(stream));
+  // f32 input (any block_k) and block_k != 128 take the general kernel
+  if (block_k != 128 || x_dtype == TG_DTYPE_F32) {
+    if (!aligned(x, x_dtype == TG_DTYPE_F32 ? 4 : 2) || !aligned(scales_t, 4))
+      return einval("quantize_cols: x and scales_t must be aligned");
+    return launch_quant_cols_gb(x, x_dtype == TG_DTYPE_F32, rows, cols, block_k, q_t, scales_t,
+                                as_stream(stream));
   }
   if (!aligned(x, 2) || !aligned(q_t, 16)) return einval("quantize_cols: q_t must be 16-byte aligned");
   return launch_quant_cols(x, rows, cols, q_t, scales_t, as_stream(stream));

@@ -78,8 +78,8 @@ int launch_gemm_fp8(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, co
 // (q rows of cols * pf bytes).
 int launch_quant_rows_gb(const void* x, int x_dtype, int64_t rows, int64_t cols, int bk, uint8_t* q, float* s,
                          hipStream_t st, int srep = 1, int pf = 1);
-int launch_quant_cols_gb(const void* x, int64_t rows, int64_t cols, int bk, uint8_t* q_t, float* s_t,
-                         hipStream_t st, int srep = 1, int pf = 1);
+int launch_quant_cols_gb(const void* x, bool x_f32, int64_t rows, int64_t cols, int bk, uint8_t* q_t,
+                         float* s_t, hipStream_t st, int srep = 1, int pf = 1);
 int launch_gemm_gb(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s, int bn, void* c,
                    int c_dtype, int64_t M, int64_t N, int64_t K, int bk, hipStream_t st);
 

@@ -84,13 +84,12 @@ def quantize_fp8(x: torch.Tensor, block_k: int = DEFAULT_BLOCK_K, transpose: boo
         R, C = x.shape
         if R % block_k != 0:
             raise ValueError(f"K={R} not divisible by block_k={block_k}")
-        if x.dtype != torch.bfloat16:
-            # the transposing kernel reads bf16; other dtypes go through a row quantize of x.T
-            return quantize_fp8(x.t().contiguous(), block_k)
+        if x.dtype not in (torch.bfloat16, torch.float32):
+            x = x.to(torch.float32)
         x = x.contiguous()
         q = torch.empty((C, R), dtype=torch.uint8, device=x.device)
         s = torch.empty((C, R // block_k), dtype=torch.float32, device=x.device)
-        _L.check(_L.lib().tg_quantize_cols(_L.ptr(x), _L.TG_DTYPE_BF16, R, C, block_k,
+        _L.check(_L.lib().tg_quantize_cols(_L.ptr(x), _L.dtype_code(x), R, C, block_k,
                                            _L.ptr(q), _L.ptr(s), _L.stream_of(x)))
         return q.view(torch.float8_e4m3fn), s
     *lead, K = x.shape
