@@ -53,6 +53,9 @@ block_k_sizes = config 3's forward (tg_block_scaled_matmul) at block_k 128,
 io_floor     = (--only) config 2's bytes moved by csrc/probe/io_floor.hip with
                the fused norm kernel's access pattern and no arithmetic: the
                attainable rate of that read / write mix, beside the real kernel
+quant_floor  = (--only) config 3's dual quantizers beside the same kernel with
+               its arithmetic taken out (csrc/probe/quant_floor.hip): the I/O
+               floor of their access pattern, with and without the scales
 gemv_floor   = (--only) the reference decode weights at 8 rows: the direct
                GEMV's loads moved by csrc/probe/gemv_stream.hip with no
                arithmetic (with and without the x rows, cached and
@@ -61,7 +64,7 @@ cpu_baseline = the CPU oracle (numpy + C) on a row sample of the same step
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                       [--only step|norm_quant|norm_bwd|gemv|bwd_bf16|block_step|xent|decode|
-                              vendor_gemm|c1|block_k|io_floor|gemv_floor]
+                              vendor_gemm|c1|block_k|io_floor|quant_floor|gemv_floor]
 """
 import argparse
 import json
@@ -225,7 +228,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--norm-iters", type=int, default=200)
     p.add_argument("--only", choices=["step", "norm_quant", "norm_bwd", "gemv", "bwd_bf16",
-                                      "block_step", "xent", "decode", "vendor_gemm", "c1", "block_k", "io_floor",
+                                      "block_step", "xent", "decode", "vendor_gemm", "c1", "block_k", "io_floor", "quant_floor",
                                       "gemv_floor"],
                    help="run one secondary workload alone and print its JSON object")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -447,6 +450,99 @@ def bench_io_floor(dev, iters):
     mix = [r for r in out["modes"] if r["mode"] == 2][0]
     best = max(mix[k]["GB/s"] for k in mix if k.startswith("rows_per_wave"))
     out["norm_vs_best_mix_floor"] = round(out["rms_norm_fp8_same_run"]["GB/s"] / best, 4)
+    return out
+
+
+def bench_quant_floor(dev, iters):
+    """The I/O floor of config 3's dual quantizers: libtg_probe.so's
+    quant_floor (csrc/probe/quant_floor.hip) runs the product's
+    quant_dual_kernel with its arithmetic taken out -- the same loads, LDS
+    traffic and stores on the same grid and tile order -- with and without the
+    K-block-major scale stores, timed beside tg_quantize_dual_km (dY 8192 x
+    8192) and tg_quantize_dual_pair_km (x 8192 x 2048 + W 2048 x 8192) on the
+    step's buffers (three rotating input sets, one output set, as the step
+    rewrites its quantized operands), interleaved, median of 7 rounds."""
+    import ctypes
+    import statistics
+    import torch
+    import _tglib as L
+    import build as tg_build
+    lib = L.lib()
+    if not os.path.exists(tg_build.PROBE_LIB):
+        raise RuntimeError(f"{tg_build.PROBE_LIB} is missing: run python train-gpt_amd/build.py")
+    probe = ctypes.CDLL(tg_build.PROBE_LIB)
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    probe.tg_probe_quant_floor.restype = ctypes.c_int
+    probe.tg_probe_quant_floor.argtypes = [ctypes.c_int, vp, i64, i64, vp, vp, vp, vp, vp, i64, i64, vp, vp,
+                                           vp, vp, vp]
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    nsets = 3                                    # 3 x 134 MB of dY > 256 MB Infinity Cache
+
+    def outs(r, c):
+        return (torch.empty((r, c), dtype=torch.uint8, device=dev),
+                torch.empty((c // 128, r), dtype=torch.float32, device=dev),
+                torch.empty((c, r), dtype=torch.uint8, device=dev),
+                torch.empty((r // 128, c), dtype=torch.float32, device=dev))
+    dys = [(torch.randn((M3, N3), generator=g, device=dev) * 1e-3).to(torch.bfloat16) for _ in range(nsets)]
+    xs = [torch.randn((M3, K3), generator=g, device=dev).to(torch.bfloat16) for _ in range(nsets)]
+    ws = [(torch.randn((K3, N3), generator=g, device=dev) * 0.02).to(torch.bfloat16) for _ in range(nsets)]
+    # one output set, as in the C3 step (the step rewrites the same quantized
+    # operands every step; only the inputs are new)
+    ody, ox, ow = [outs(M3, N3)] * nsets, [outs(M3, K3)] * nsets, [outs(K3, N3)] * nsets
+    st = L.stream_of(dys[0])
+    P = L.ptr
+
+    def per_elem(r, c):          # 2 B read + (1 + 4/128) B written twice
+        return r * c * 2 + 2 * (r * c + r * c // 128 * 4)
+    dy_bytes, pair_bytes = per_elem(M3, N3), per_elem(M3, K3) + per_elem(K3, N3)
+
+    def dy_prod(i):
+        k = i % nsets
+        L.check(lib.tg_quantize_dual_km(P(dys[k]), M3, N3, 128, *[P(t) for t in ody[k]], st))
+
+    def dy_probe(mode):
+        def f(i):
+            k = i % nsets
+            L.check(probe.tg_probe_quant_floor(mode, P(dys[k]), M3, N3, *[P(t) for t in ody[k]],
+                                               None, 0, 0, None, None, None, None, st))
+        return f
+
+    def pair_prod(i):
+        k = i % nsets
+        L.check(lib.tg_quantize_dual_pair_km(P(xs[k]), M3, K3, *[P(t) for t in ox[k]], P(ws[k]), K3, N3,
+                                             *[P(t) for t in ow[k]], 128, st))
+
+    def pair_probe(mode):
+        def f(i):
+            k = i % nsets
+            L.check(probe.tg_probe_quant_floor(mode, P(xs[k]), M3, K3, *[P(t) for t in ox[k]], P(ws[k]), K3, N3,
+                                               *[P(t) for t in ow[k]], st))
+        return f
+    cases = {"dY 8192 x 8192": (dy_bytes, {"product tg_quantize_dual_km": dy_prod, "io_floor_with_scales":
+                                           dy_probe(0), "io_floor_no_scales": dy_probe(1)}),
+             "x 8192 x 2048 + W 2048 x 8192": (pair_bytes, {"product tg_quantize_dual_pair_km": pair_prod,
+                                                            "io_floor_with_scales": pair_probe(0),
+                                                            "io_floor_no_scales": pair_probe(1)})}
+    res = {}
+    for rnd in range(7):
+        for cname, (byts, fns) in cases.items():
+            for name, f in fns.items():
+                res.setdefault((cname, name), []).append(_mean_launch_us(f, iters, warm=3))
+    out = {"workload": "config 3's dual quantizers (dY; x + W pair) beside the same kernel without arithmetic "
+                       "(csrc/probe/quant_floor.hip), 3 rotating input sets and one output set (as in the "
+                       "C3 step), median of 7 interleaved rounds", "cases": []}
+    for cname, (byts, fns) in cases.items():
+        row = {"case": cname, "bytes_per_launch": byts}
+        for name in fns:
+            us = statistics.median(res[(cname, name)])
+            gbps = byts / (us * 1e-6) / 1e9
+            row[name] = {"us_per_launch": round(us, 2), "GB/s": round(gbps, 1),
+                         "frac_of_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4)}
+        prod = [v for k, v in row.items() if k.startswith("product")][0]
+        row["product_vs_floor_with_scales"] = round(row["io_floor_with_scales"]["us_per_launch"] /
+                                                    prod["us_per_launch"], 4)
+        out["cases"].append(row)
     return out
 
 
@@ -1022,7 +1118,8 @@ def main():
               "block_step": lambda d, _: bench_block(d), "xent": bench_xent,
               "decode": lambda d, _: bench_decode(d),
               "vendor_gemm": lambda d, _: bench_vendor_gemm(d, 20),
-              "c1": bench_c1, "block_k": bench_block_k, "io_floor": bench_io_floor, "gemv_floor": bench_gemv_floor}[args.only]
+              "c1": bench_c1, "block_k": bench_block_k, "io_floor": bench_io_floor, "gemv_floor": bench_gemv_floor,
+              "quant_floor": bench_quant_floor}[args.only]
         print(json.dumps({args.only: fn(dev, args.norm_iters)}))
         return
     step = Step(dev)

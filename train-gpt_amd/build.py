@@ -54,7 +54,7 @@ def build_library(verbose: bool = False) -> str:
     return LIB
 
 
-PROBE_SRCS = [os.path.join(CSRC, "probe", f) for f in ("io_floor.hip", "gemv_stream.hip")]
+PROBE_SRCS = [os.path.join(CSRC, "probe", f) for f in ("io_floor.hip", "gemv_stream.hip", "quant_floor.hip")]
 PROBE_LIB = os.path.join(HERE, "libtg_probe.so")
 
 

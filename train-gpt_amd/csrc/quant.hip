@@ -13,6 +13,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include "quant_dual.h"
 #include "row_ops.h"
 #include "tg_device.h"
 #include "tg_host.h"
@@ -193,192 +194,8 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(const uint16_t* __restr
 }
 
 
-// ---------------------------------------------------------------------------
-// Dual quantization: _quantize_to_fp8 of x along its rows AND of x.T (the two
-// operands the FP8 backward needs from dY, fp8.py:39-47) from one read of x.
-// Tile = 128 x 128 bf16.  Lanes 16r .. 16r+15 of a wave hold one 128-element
-// row block (as in quant_rows_kernel), quantize it and keep the raw tile in
-// LDS (row pitch 272 B); then quads of lanes own whole columns (as in
-// quant_cols_kernel), quantize them and store 128 contiguous bytes per
-// column.  The bytes and scales equal those of the two separate kernels.
-// ---------------------------------------------------------------------------
-// ROWS = false gives the column quantization alone (tg_quantize_cols for
-// 16-byte-aligned rows); GUARD handles a last tile narrower than 128 columns.
-//
-// Tile order.  Launch slots go round-robin to the 8 XCDs (slot % 8), each
-// with its own L2.  A line of row scales (32 tiles along x) and a line of
-// column scales (32 tiles along y) are each written 4 bytes at a time by 32
-// workgroups; on one XCD the pieces merge in its L2, spread over eight they
-// leave as partial-line writes.  The identity order keeps the column-scale
-// lines on one XCD (the XCD of a slot is tx % 8 when gridDim.x % 8 == 0) and
-// spreads the row-scale lines over all eight.  With xcd_blocks the tiles are
-// dealt to XCDs in blocks of 32 x 16 (each XCD a contiguous run of whole
-// blocks), which keeps a row-scale line on one XCD and a column-scale line on
-// two.  The host sets it when gridDim.x % 32 == 0, gridDim.y % 16 == 0 and
-// each XCD's share is a multiple of 512 tiles.
-//
-// One launch may carry two tensors (DualJobs): slots [0, nblk0) take the tiles
-// of job 0 and the rest those of job 1, each in its own row-major tile order
-// (gx tiles along x).  Two 1024-tile tensors (C3's x and W) then fill the
-// machine twice over and the second tensor's loads overlap the first one's
-// stores, where two launches each run one wave of workgroups.
-struct DualJob {
-  const uint4* x;
-  int64_t rows, cols;
-  uint2* q;
-  float* s;
-  uint8_t* qt;
-  float* st;
-  int gx, gy, xcd_blocks;
-  int skm;   // scales K-block-major: s[kb * rows + row], st[kb * cols + col]
-  int part;  // 0: rows and x.T; 1: rows only; 2: x.T only (with ROWS)
-};
-struct DualJobs {
-  DualJob job[2];
-  int nblk0;   // tiles of job 0; gridDim.x - nblk0 are job 1's
-};
-
-template <bool ROWS, bool GUARD>
-__global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
-  // the raw tile (row pitch 272 B); once every column is in registers the
-  // same memory stages the transposed bytes (column pitch 144 B)
-  __shared__ uint32_t tile[128 * 68];
-  uint32_t* tq = tile;
-  const int tid = threadIdx.x;
-  const bool second = (int)blockIdx.x >= jobs.nblk0;
-  const DualJob& J = second ? jobs.job[1] : jobs.job[0];
-  const uint4* __restrict__ x = J.x;
-  const int64_t rows = J.rows, cols = J.cols;
-  uint2* __restrict__ q = J.q;
-  float* __restrict__ s = J.s;
-  uint8_t* __restrict__ qt = J.qt;
-  float* __restrict__ st = J.st;
-  const int slot = (int)blockIdx.x - (second ? jobs.nblk0 : 0);
-  int tx = slot % J.gx, ty = slot / J.gx;
-  if (J.xcd_blocks) {
-    // slot % 8 is the XCD: the host sets xcd_blocks only on a job that
-    // starts at a multiple of 8
-    const int per_xcd = J.gx * J.gy / 8;
-    const int t = (slot & 7) * per_xcd + (slot >> 3);     // position in XCD-contiguous order
-    const int blk = t >> 9, w = t & 511;
-    tx = (blk % (J.gx / 32)) * 32 + (w & 31);
-    ty = (blk / (J.gx / 32)) * 16 + (w >> 5);
-  }
-  const int64_t c0 = (int64_t)tx * 128, r0 = (int64_t)ty * 128;
-  const int ch = tid & 15, rr = tid >> 4;
-  const int64_t cchunks = cols >> 3;
-  const bool ch_ok = !GUARD || (c0 >> 3) + ch < cchunks;
-  // the job's parts (workgroup-uniform)
-  const bool do_rows = ROWS && J.part != 2, do_cols = J.part != 1;
-  uint4 v[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u)
-    v[u] = ch_ok ? ldg_stream(x + (r0 + rr + 16 * u) * cchunks + (c0 >> 3) + ch) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int row = rr + 16 * u;
-    if (do_rows) {
-      float f[8];
-      f[0] = bf16lo(v[u].x); f[1] = bf16hi(v[u].x); f[2] = bf16lo(v[u].y); f[3] = bf16hi(v[u].y);
-      f[4] = bf16lo(v[u].z); f[5] = bf16hi(v[u].z); f[6] = bf16lo(v[u].w); f[7] = bf16hi(v[u].w);
-      const float sc = block_scale_bf16(row16_max_u32(absmax8(f)));
-      q[(r0 + row) * cchunks + (c0 >> 3) + ch] = quant8<true>(f, sc);
-      if (ch == 0) {
-        if (J.skm) s[(int64_t)tx * rows + r0 + row] = sc;
-        else s[(r0 + row) * (cols >> 7) + tx] = sc;
-      }
-    }
-    if (do_cols) *reinterpret_cast<uint4*>(&tile[row * 68 + ch * 4]) = v[u];
-  }
-  if (!do_cols) return;
-  __syncthreads();
-
-  // columns: quad (tid >> 2) owns the column pair 2c, 2c + 1 (one 32-bit LDS
-  // word per row); lane j of the quad holds rows 16i + 4j + r
-  const int j = tid & 3, cp = tid >> 2;
-  float f0[32], f1[32];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const uint32_t w = tile[(16 * i + 4 * j + r) * 68 + cp];
-      f0[i * 4 + r] = __uint_as_float(w << 16);
-      f1[i * 4 + r] = __uint_as_float(w & 0xFFFF0000u);
-    }
-  uint32_t m0 = 0, m1 = 0;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    m0 = max(m0, __float_as_uint(f0[i]) & 0x7FFFFFFFu);
-    m1 = max(m1, __float_as_uint(f1[i]) & 0x7FFFFFFFu);
-  }
-  const float sc0 = block_scale_bf16(quad_max_u32(m0));
-  const float sc1 = block_scale_bf16(quad_max_u32(m1));
-  __syncthreads();   // every lane has read its columns: the tile becomes tq
-  auto col_words = [&](const float (&f)[32], float sc, int n) {
-    Divider d(sc);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint32_t w;
-      if (d.fast) {
-        w = e4m3x4(d.div(f[4 * i]), d.div(f[4 * i + 1]), d.div(f[4 * i + 2]), d.div(f[4 * i + 3]));
-      } else {
-        w = e4m3_nonfinite_scale(f[4 * i], sc) | (e4m3_nonfinite_scale(f[4 * i + 1], sc) << 8) |
-            (e4m3_nonfinite_scale(f[4 * i + 2], sc) << 16) |
-            (e4m3_nonfinite_scale(f[4 * i + 3], sc) << 24);
-      }
-      tq[n * 36 + 4 * i + j] = w;
-    }
-    if (j == 0 && (!GUARD || c0 + n < cols)) {
-      if (J.skm) st[(int64_t)ty * cols + c0 + n] = sc;
-      else st[(c0 + n) * (rows >> 7) + ty] = sc;
-    }
-  };
-  col_words(f0, sc0, 2 * cp);
-  col_words(f1, sc1, 2 * cp + 1);
-  __syncthreads();
-  // eight lanes per column, lane k writing bytes 16k .. 16k + 15: each store
-  // instruction writes eight whole 128-byte columns (full lines).  Ordinary
-  // (not non-temporal) stores: the transposed operands are read by the next
-  // GEMMs (W.T by the forward's, x.T and dY.T by dW), and written around the
-  // Infinity Cache they came back from HBM with each dY.T panel read by one
-  // XCD only, which left dW ~15% slower than dX inside the C3 step.
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int n = (tid >> 3) + 32 * p, k = tid & 7;
-    if (GUARD && c0 + n >= cols) continue;
-    const uint4 val = *reinterpret_cast<const uint4*>(&tq[n * 36 + 4 * k]);
-    *(reinterpret_cast<uint4*>(qt + (c0 + n) * rows + r0) + k) = val;
-  }
-}
-
-// One DualJob over x (rows, cols) in 128 x 128 tiles (a narrower last tile
-// along cols).  xcd_ok: the job's first slot is a multiple of 8, so the
-// XCD-blocked order may be used (when the tile grid has its shape).
-constexpr int64_t kDualMaxTiles = int64_t(1) << 23;   // slots fit one 1-D grid of 256-thread groups
-
-static int dual_job(DualJob& j, const char* who, const void* x, int64_t rows, int64_t cols, uint8_t* q,
-                    float* s, uint8_t* q_t, float* s_t, bool xcd_ok, bool skm) {
-  const int64_t gx = (cols + 127) / 128, gy = rows / 128;
-  if (gx * gy > kDualMaxTiles) {
-    char msg[160];
-    snprintf(msg, sizeof msg, "%s: (rows / 128) x (cols / 128) must be <= %lld tiles", who,
-             (long long)kDualMaxTiles);
-    return einval(msg);
-  }
-  j.x = reinterpret_cast<const uint4*>(x);
-  j.rows = rows;
-  j.cols = cols;
-  j.q = reinterpret_cast<uint2*>(q);
-  j.s = s;
-  j.qt = q_t;
-  j.st = s_t;
-  j.gx = (int)gx;
-  j.gy = (int)gy;
-  j.xcd_blocks = xcd_ok && gx % 32 == 0 && gy % 16 == 0 && (gx * gy / 8) % 512 == 0;
-  j.skm = skm ? 1 : 0;
-  j.part = 0;
-  return TG_OK;
-}
+// The dual kernel (rows and / or x.T from one read) lives in quant_dual.h,
+// shared with the I/O-floor probe csrc/probe/quant_floor.hip.
 
 int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, float* s_t,
                       hipStream_t st, bool skm) {
