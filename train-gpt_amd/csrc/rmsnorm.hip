@@ -148,9 +148,9 @@ static int launch_rmsnorm(const void* x, const void* gamma, void* y, uint8_t* q,
 // wave per row, lane l owns 16-byte chunks l + 64j): x and dy are read once,
 // dx written once.  The dscale column sums stay in registers across all rows
 // a wave visits; the four waves of a workgroup add theirs into LDS in wave
-// order and the workgroup writes one partial row, which rmsnorm_bwd_reduce
-// adds up in workgroup order.  Both orders are fixed, so dscale is the same
-// on every run.
+// order and the workgroup writes one partial row (slice-major, see
+// kNormBwdSlice), which rmsnorm_bwd_reduce_sm adds up in a fixed order.
+// Both orders are fixed, so dscale is the same on every run.
 // GREG: gamma in registers (J <= 4); PF: prefetch the next row (J <= 4).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float (&f)[8]) {
@@ -158,7 +158,18 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float (&f)[8]) {
   f[4] = bf16lo(v.z); f[5] = bf16hi(v.z); f[6] = bf16lo(v.w); f[7] = bf16hi(v.w);
 }
 
-constexpr int kNormBwdMaxGrid = 512;
+#ifndef TG_NBWD_GRID
+#define TG_NBWD_GRID 256
+#endif
+#ifndef TG_NBWD_SLICE
+#define TG_NBWD_SLICE 32
+#endif
+constexpr int kNormBwdMaxGrid = TG_NBWD_GRID;
+// The row kernel's partial dscale rows are stored slice-major: slice k holds
+// columns 32k .. 32k + 31 of every partial row, one 128-byte line per row,
+// the rows of a slice contiguous, so that the reduction of a slice reads one
+// contiguous run.
+constexpr int kNormBwdSlice = TG_NBWD_SLICE;
 
 template <int J, bool FULL>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint4* __restrict__ x,
@@ -268,8 +279,12 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint4* __restric
     }
     __syncthreads();
   }
+  // slice-major: the partial rows' columns c .. c + kNormBwdSlice - 1 are
+  // contiguous across workgroups (see rmsnorm_bwd_reduce_sm)
   const int dim = nch * 8;
-  for (int i = threadIdx.x; i < dim; i += 256) partial[(int64_t)blockIdx.x * dim + i] = colsum[i];
+  for (int i = threadIdx.x; i < dim; i += 256)
+    partial[((int64_t)(i / kNormBwdSlice) * gridDim.x + blockIdx.x) * kNormBwdSlice + i % kNormBwdSlice] =
+        colsum[i];
 }
 
 // ---------------------------------------------------------------------------
@@ -410,8 +425,49 @@ __global__ __launch_bounds__(1024) void rmsnorm_bwd_reduce(const float* __restri
   }
 }
 
+// dscale[c] = bf16(sum over b of the slice-major partial rows) with f64
+// accumulation in a fixed order: one workgroup per slice of kNormBwdSlice
+// columns; thread (pg, cl) adds partial rows pg, pg + PG, ... of column cl
+// (16 loads in flight), then the PG group sums are added in group order.  A
+// wave's load covers 64 / kNormBwdSlice consecutive partial rows of the slice,
+// i.e. one contiguous 256-byte piece.
+#ifndef TG_NBWD_RTHREADS
+#define TG_NBWD_RTHREADS 1024
+#endif
+template <typename OT, int U>
+__global__ __launch_bounds__(TG_NBWD_RTHREADS) void rmsnorm_bwd_reduce_sm(const float* __restrict__ partial,
+                                                                          int nparts, int dim,
+                                                                          OT* __restrict__ dscale) {
+  constexpr int SW = kNormBwdSlice, PG = TG_NBWD_RTHREADS / SW;
+  __shared__ double gsum[PG][SW];
+  const int cl = threadIdx.x % SW, pg = threadIdx.x / SW;
+  const int c = blockIdx.x * SW + cl;
+  const float* __restrict__ base = partial + (int64_t)blockIdx.x * nparts * SW + cl;
+  double acc = 0.0;
+  int b = pg;
+  for (; b + (U - 1) * PG < nparts; b += U * PG) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = base[(int64_t)(b + u * PG) * SW];
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc += (double)v[u];
+  }
+  for (; b < nparts; b += PG) acc += (double)base[(int64_t)b * SW];
+  gsum[pg][cl] = acc;
+  __syncthreads();
+  if (pg == 0 && c < dim) {
+    double t = 0.0;
+#pragma unroll
+    for (int g = 0; g < PG; ++g) t += gsum[g][cl];
+    st_f32(dscale, c, (float)t);
+  }
+}
+
+static int64_t norm_bwd_slices(int64_t dim) { return (dim + kNormBwdSlice - 1) / kNormBwdSlice; }
+
 static int64_t norm_bwd_grid(int64_t rows) {
-  // about four rows per wave, at most two workgroups per CU
+  // about four rows per wave, at most one workgroup per CU (256 partial rows
+  // at C2's 8192: 0.5 us less than 512 over both kernels, measured)
   int64_t g = (rows + 15) / 16;
   if (g > kNormBwdMaxGrid) g = kNormBwdMaxGrid;
   return g;
@@ -449,8 +505,17 @@ static int launch_rmsnorm_bwd(const void* x, const void* gamma, const void* dy, 
     if (!launched) return einval("rms_norm_bwd: dim must be <= 4096");
     TG_TRY(check_launch("rmsnorm_bwd"));
   }
-  hipLaunchKernelGGL(rmsnorm_bwd_reduce<uint16_t>, dim3((unsigned)((dim + 63) / 64)), dim3(1024), 0, st,
-                     partial, (int)grid, (int)dim, reinterpret_cast<uint16_t*>(dscale));
+  // no rows: no partial rows, and the reduction writes dscale = 0
+  // U: partial rows per thread in flight at once (every one of them at C2's 512)
+  constexpr int kPG = TG_NBWD_RTHREADS / kNormBwdSlice;
+  const dim3 rgrid((unsigned)norm_bwd_slices(dim)), rblock(TG_NBWD_RTHREADS);
+  auto ds = reinterpret_cast<uint16_t*>(dscale);
+  if (grid >= 16 * kPG)
+    hipLaunchKernelGGL((rmsnorm_bwd_reduce_sm<uint16_t, 16>), rgrid, rblock, 0, st, partial, (int)grid, (int)dim, ds);
+  else if (grid >= 8 * kPG)
+    hipLaunchKernelGGL((rmsnorm_bwd_reduce_sm<uint16_t, 8>), rgrid, rblock, 0, st, partial, (int)grid, (int)dim, ds);
+  else
+    hipLaunchKernelGGL((rmsnorm_bwd_reduce_sm<uint16_t, 4>), rgrid, rblock, 0, st, partial, (int)grid, (int)dim, ds);
   return check_launch("rmsnorm_bwd_reduce");
 }
 
@@ -558,7 +623,7 @@ extern "C" int tg_add_rms_norm_fp8(const void* x, const void* delta, const void*
 
 extern "C" size_t tg_rms_norm_bwd_workspace(int64_t rows, int64_t dim) {
   if (rows < 0 || dim <= 0) return 0;
-  const size_t fast = (size_t)norm_bwd_grid(rows) * (size_t)dim * 4;
+  const size_t fast = (size_t)norm_bwd_grid(rows) * (size_t)norm_bwd_slices(dim) * kNormBwdSlice * 4;
   const size_t gen = gen_bwd_workspace(rows, dim);
   return fast > gen ? fast : gen;
 }
