@@ -450,6 +450,27 @@ def bench_io_floor(dev, iters):
     mix = [r for r in out["modes"] if r["mode"] == 2][0]
     best = max(mix[k]["GB/s"] for k in mix if k.startswith("rows_per_wave"))
     out["norm_vs_best_mix_floor"] = round(out["rms_norm_fp8_same_run"]["GB/s"] / best, 4)
+    # A different access pattern for the same bytes (csrc/probe/io_floor.hip's
+    # io_stream_kernel): x as a plain stream of 16-byte units in address order,
+    # y / q / scale stores per unit, no rows; grid and loads in flight swept.
+    probe.tg_probe_io_stream.restype = ctypes.c_int
+    probe.tg_probe_io_stream.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                         ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    units = C2_ROWS * C2_D // 8
+    stream_rows = []
+    for grid in (256, 512, 1024, 2048, 4096, 8192):
+        for unroll in (2, 4, 8):
+            def launch(i, grid=grid, unroll=unroll):
+                k = i % nsets
+                L.check(probe.tg_probe_io_stream(L.ptr(xs[k]), L.ptr(ys[k]), L.ptr(qs[k]), L.ptr(ss[k]), units,
+                                                 grid, unroll, st))
+            r = rate(_mean_launch_us(launch, iters), 2 * xb + qb + sb)
+            r.update({"grid": grid, "units_in_flight_per_lane": unroll})
+            stream_rows.append(r)
+    out["stream_pattern_same_bytes"] = stream_rows
+    best_stream = max(r["GB/s"] for r in stream_rows)
+    out["best_stream_vs_best_row_pattern"] = round(best_stream / best, 4)
+    out["norm_vs_best_of_both_patterns"] = round(out["rms_norm_fp8_same_run"]["GB/s"] / max(best, best_stream), 4)
     return out
 
 

@@ -85,3 +85,57 @@ extern "C" int tg_probe_io_floor(int mode, const void* x, void* y, void* q, floa
   }
   return check_launch("io_floor");
 }
+
+// A different access pattern for the same bytes: no rows at all.  x is a
+// stream of 16-byte units (8 bf16); unit i is read once (non-temporal) and
+// gives a 16-byte y store, an 8-byte q store and, every 16th unit, one 4-byte
+// scale -- config 2's byte mix (2 B read, 2 + 1 + 4/128 B written per element)
+// in address order.  Thread t of a grid of G workgroups x 256 threads takes
+// units t, t + 256 G, ... with U of them loaded before the first is stored,
+// so U x 16 B per lane are in flight; G and U are swept by bench.py.
+namespace tg {
+
+template <int U>
+__global__ __launch_bounds__(256) void io_stream_kernel(const uint4* __restrict__ x, uint4* __restrict__ y,
+                                                        uint2* __restrict__ q, float* __restrict__ s,
+                                                        int64_t units) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t base = (int64_t)blockIdx.x * 256 + threadIdx.x; base < units; base += stride * U) {
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = base + u * stride;
+      v[u] = i < units ? ldg_stream(x + i) : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = base + u * stride;
+      if (i < units) {
+        stg_stream(&y[i], v[u]);
+        stg_stream(&q[i], make_uint2(v[u].x ^ v[u].z, v[u].y ^ v[u].w));
+        if ((i & 15) == 0) s[i >> 4] = __uint_as_float(v[u].x);
+      }
+    }
+  }
+}
+
+}  // namespace tg
+
+// units 16-byte units of x (units % 16 == 0), grid workgroups of 256 threads,
+// unroll 2, 4 or 8 units in flight per thread.
+extern "C" int tg_probe_io_stream(const void* x, void* y, void* q, float* s, int64_t units, int grid,
+                                  int unroll, void* stream) {
+  using namespace tg;
+  if (units <= 0 || units % 16 || grid <= 0 || (unroll != 2 && unroll != 4 && unroll != 8))
+    return einval("tg_probe_io_stream: bad arguments");
+  if (!x || !y || !q || !s) return einval("tg_probe_io_stream: null pointer");
+  auto st = static_cast<hipStream_t>(stream);
+  auto X = reinterpret_cast<const uint4*>(x);
+  auto Y = reinterpret_cast<uint4*>(y);
+  auto Q = reinterpret_cast<uint2*>(q);
+  const dim3 g((unsigned)grid), b(256);
+  if (unroll == 2) hipLaunchKernelGGL(io_stream_kernel<2>, g, b, 0, st, X, Y, Q, s, units);
+  else if (unroll == 4) hipLaunchKernelGGL(io_stream_kernel<4>, g, b, 0, st, X, Y, Q, s, units);
+  else hipLaunchKernelGGL(io_stream_kernel<8>, g, b, 0, st, X, Y, Q, s, units);
+  return check_launch("io_stream");
+}
