@@ -841,7 +841,10 @@ template <int S> __device__ __forceinline__ uint8_t* gemv_stage() {
 // quantized x_q / x_s; PRO_NORM / PRO_NORM_ADD rmsnorm of x (after the
 // residual add x + delta) -> FP8 rows, computed by the GEMV's workgroup;
 // PRO_RELU2 bf16(relu(u)^2) -> FP8 rows.
-enum { PRO_X = 0, PRO_NORM = 1, PRO_NORM_ADD = 2, PRO_RELU2 = 3 };
+// PRO_XCOPY: x_q / x_s already quantized, at most 8 rows, copied into LDS by
+// the workgroup with whole-row loads before the K loop (the fragment loads
+// from x_q would each touch 16 rows' 64-byte pieces; see gemv_fp8_kernel).
+enum { PRO_X = 0, PRO_NORM = 1, PRO_NORM_ADD = 2, PRO_RELU2 = 3, PRO_XCOPY = 4 };
 
 // The norm prologue's inputs (PRO_NORM*): x, delta (M, K) bf16, gamma (K,)
 // bf16; with PRO_NORM_ADD workgroup 0 stores the residual sum bf16(x + delta)
@@ -875,8 +878,10 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
                                                        __bf16* __restrict__ out, int M, int N,
                                                        int K, GemvNormIn nin) {
   constexpr int NW = 8;
-  constexpr bool XLDS = PRO == PRO_NORM || PRO == PRO_NORM_ADD;
+  constexpr bool XLDS = PRO == PRO_NORM || PRO == PRO_NORM_ADD || PRO == PRO_XCOPY;
   static_assert(PRO == PRO_X || (XLDS && MT == 1), "the norm prologue takes at most 16 rows");
+  // rows of x held in LDS: 16 for the norm prologue, 8 for the copy
+  constexpr int XROWS = PRO == PRO_XCOPY ? 8 : 16;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 15, fg = lane >> 4;
@@ -981,8 +986,43 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
   // weight stream is already in flight.
   extern __shared__ __attribute__((aligned(16))) uint8_t gemv_xl[];
   const int xpitch = K + 16;
-  float* gemv_xs = reinterpret_cast<float*>(gemv_xl + 16 * xpitch);
-  if constexpr (XLDS) {
+  float* gemv_xs = reinterpret_cast<float*>(gemv_xl + XROWS * xpitch);
+  if constexpr (PRO == PRO_XCOPY) {
+    // x rows (M <= 8) into LDS at pitch K + 16: 16-byte loads, consecutive
+    // threads on consecutive bytes of a row (whole lines), then the scales;
+    // the loads go out before the first chunk's weight stages, whose loads
+    // then overlap this copy's round trip
+    const int nch = K >> 4;                        // 16-byte chunks per row
+    const int tot = M * nch;
+    constexpr int XU = 8;                          // chunks per thread in flight (8 rows x 4 KiB / 512 threads)
+    u32x4_t xv[XU];
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
+      const int e = tid + u * 512;
+      const uint32_t off = e < tot ? (uint32_t)(e / nch) * (uint32_t)K + (uint32_t)(e % nch) * 16u : xbytes;
+      xv[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+    }
+    const int nsc = M * nkb;
+    const float sv = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(rxs, tid < nsc ? (uint32_t)tid * 4u : xsbytes, 0, 0));
+    load_w(IntC<0>{}, 0, 0);
+    load_w(IntC<1>{}, 0, 1);
+    if constexpr (NS > 2) load_w(IntC<2 % NS>{}, 0, 2);
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
+      const int e = tid + u * 512;
+      if (e < tot) *reinterpret_cast<u32x4_t*>(gemv_xl + (e / nch) * xpitch + (e % nch) * 16) = xv[u];
+    }
+    // rows beyond K / 16 * XU chunks per thread: a tail loop (K > 4096)
+    for (int e = tid + XU * 512; e < tot; e += 512)
+      *reinterpret_cast<u32x4_t*>(gemv_xl + (e / nch) * xpitch + (e % nch) * 16) =
+          __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(e / nch) * (uint32_t)K + (uint32_t)(e % nch) * 16u, 0, 0);
+    if (tid < nsc) gemv_xs[tid] = sv;
+    for (int e = tid + 512; e < nsc; e += 512)
+      gemv_xs[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxs, (uint32_t)e * 4u, 0, 0));
+    __syncthreads();
+  }
+  if constexpr (PRO == PRO_NORM || PRO == PRO_NORM_ADD) {
     constexpr bool ADD = PRO == PRO_NORM_ADD;
     const int nch = K >> 3;
     // both of a wave's rows are loaded ahead for J <= 5; with J = 8 the
@@ -1916,6 +1956,18 @@ static int launch_gemv(const uint8_t* x_q, const float* x_s, const uint8_t* w_q,
   if (nwg < need) nwg = need;
   const dim3 grid((unsigned)nwg);
   const GemvNormIn none{};
+  // up to 8 rows: x copied into LDS with whole-row loads (PRO_XCOPY), when it
+  // fits beside the three weight stages
+  const size_t xlds = (size_t)8 * (size_t)(K + 16) + (size_t)8 * (size_t)(K / 128) * 4;
+  if (MT == 1 && M <= 8 && xlds <= (size_t)160 * 1024 - (size_t)NS * kGemvStage) {
+    if (bn == 1)
+      hipLaunchKernelGGL((gemv_fp8_kernel<1, 1, NS, PRO_XCOPY>), grid, dim3(512), xlds, st, x_q, x_s, w_q, w_s,
+                         out, M, N, K, none);
+    else
+      hipLaunchKernelGGL((gemv_fp8_kernel<1, 128, NS, PRO_XCOPY>), grid, dim3(512), xlds, st, x_q, x_s, w_q,
+                         w_s, out, M, N, K, none);
+    return check_launch("gemv_fp8");
+  }
   if (bn == 1)
     hipLaunchKernelGGL((gemv_fp8_kernel<MT, 1, NS>), grid, dim3(512), 0, st, x_q, x_s, w_q, w_s, out, M,
                        N, K, none);
