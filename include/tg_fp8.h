@@ -39,7 +39,9 @@ extern "C" {
 #endif
 
 enum { TG_OK = 0, TG_EINVAL = 1, TG_EHIP = 2 };
-enum { TG_DTYPE_BF16 = 0, TG_DTYPE_F32 = 1 };
+/* Element types of untyped operands.  TG_DTYPE_F16 is taken by tg_rms_norm_ex
+ * and tg_rms_norm_bwd_ex only; every other entry point refuses it. */
+enum { TG_DTYPE_BF16 = 0, TG_DTYPE_F32 = 1, TG_DTYPE_F16 = 2 };
 
 /* Message for the calling thread's last non-zero return. */
 const char* tg_last_error(void);
@@ -198,8 +200,9 @@ int tg_rms_norm(const void* x, const void* scale, void* y, int64_t rows, int64_t
                 void* stream);
 
 /* _rms_norm_pure (kernels.py:30-33) for any float dtypes: x (rows, dim) and
- * scale (dim,) each bf16 or f32 (x_dtype / scale_dtype); y (rows, dim) is f32
- * when either is f32, else bf16 (jnp's promotion of x_n * scale).
+ * scale (dim,) each bf16, f16 or f32 (x_dtype / scale_dtype); y (rows, dim) is
+ * in their common dtype when they agree, else f32 (jnp's promotion of
+ * x_n * scale: bf16 with f16 gives f32).
  * r = rsqrt(mean(x^2) + eps) rounded to x's dtype, x_n = x * r rounded to
  * x's dtype, y = x_n * scale.  Any dim; bf16/bf16 takes tg_rms_norm's kernel. */
 int tg_rms_norm_ex(const void* x, int x_dtype, const void* scale, int scale_dtype, void* y,
@@ -234,7 +237,7 @@ int tg_rms_norm_bwd(const void* x, const void* scale, const void* dy, void* dx, 
                     int64_t rows, int64_t dim, float eps, void* workspace, size_t workspace_bytes,
                     void* stream);
 
-/* The same backward for any float dtypes: x, scale, dy each bf16 or f32 (their
+/* The same backward for any float dtypes: x, scale, dy each bf16, f16 or f32 (their
  * *_dtype codes); dx is written in x's dtype, dscale in scale's (the
  * .astype(x.dtype) / .astype(scale.dtype) of kernels.py:115-117); any dim.
  * Workspace as tg_rms_norm_bwd_workspace. */

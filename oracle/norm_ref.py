@@ -50,13 +50,25 @@ def rms_norm_pure(x_bf16: np.ndarray, g_bf16: np.ndarray, eps: float) -> np.ndar
     return y
 
 
-def rms_norm_pure_any(x_f32, x_is_bf16: bool, g_f32, eps):
+def _round_to(v, dtype):
+    """v (f32) rounded to dtype's precision (RNE), returned as f32."""
+    if dtype == "bf16":
+        return bf16_to_f32(f32_to_bf16(v))
+    if dtype == "f16":
+        return np.asarray(v, dtype=np.float32).astype(np.float16).astype(np.float32)
+    if dtype == "f32":
+        return np.asarray(v, dtype=np.float32)
+    raise ValueError(f"unknown dtype {dtype!r}")
+
+
+def rms_norm_pure_any(x_f32, x_dtype: str, g_f32, eps):
     """``_rms_norm_pure`` (kernels.py:30-33) for any float dtypes, on values.
 
-    x_f32 holds x's values (bf16-representable when x_is_bf16), g_f32 the
-    scale's.  r = rsqrt(var + eps) and x_n = x * r are rounded to x's dtype;
-    y = x_n * scale in f32 (the caller rounds to bf16 when both are bf16).
-    Returns y as f32 values.
+    x_f32 holds x's values (representable in x_dtype: "bf16", "f16" or "f32"),
+    g_f32 the scale's.  r = rsqrt(var + eps) and x_n = x * r are rounded to x's
+    dtype; y = x_n * scale in f32 (the caller rounds to bf16 / f16 when both
+    operands have that dtype: the product of two such values is exact in f32,
+    so one rounding of it is the dtype's own multiply).  Returns y as f32 values.
     """
     x = np.asarray(x_f32, dtype=np.float32)
     g = np.asarray(g_f32, dtype=np.float32)
@@ -67,11 +79,8 @@ def rms_norm_pure_any(x_f32, x_is_bf16: bool, g_f32, eps):
         var = (ssum / np.float32(D)).astype(np.float32)
         v = (var + np.float32(eps)).astype(np.float32)
         r = (1.0 / np.sqrt(v.astype(np.float64))).astype(np.float32)[..., None]
-        if x_is_bf16:
-            r = bf16_to_f32(f32_to_bf16(r))
-        t = (x * r).astype(np.float32)
-        if x_is_bf16:
-            t = bf16_to_f32(f32_to_bf16(t))
+        r = _round_to(r, x_dtype)
+        t = _round_to((x * r).astype(np.float32), x_dtype)
         return (t * g).astype(np.float32)
 
 

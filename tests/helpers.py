@@ -35,3 +35,14 @@ def same_scales(got: np.ndarray, ref: np.ndarray) -> bool:
     r = np.asarray(ref, dtype=np.float32)
     both_nan = np.isnan(g) & np.isnan(r)
     return bool(np.all(both_nan | (g.view(np.uint32) == r.view(np.uint32))))
+
+
+def as_dtype_values(v: np.ndarray, dt) -> np.ndarray:
+    """f32 values rounded (RNE) to torch dtype dt's precision: what a tensor of dtype dt holds."""
+    from oracle import bf16 as ob
+    v = np.asarray(v, dtype=np.float32)
+    if dt == torch.bfloat16:
+        return ob.bf16_to_f32(ob.f32_to_bf16(v))
+    if dt == torch.float16:
+        return v.astype(np.float16).astype(np.float32)
+    return v

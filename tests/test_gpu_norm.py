@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import kernels
-from helpers import bf16_bits, f32_bits, maxabs_rel, same_scales, to_dev, u8
+from helpers import as_dtype_values, bf16_bits, f32_bits, maxabs_rel, same_scales, to_dev, u8
 from oracle import bf16 as ob
 from oracle import cbind, norm_ref
 
@@ -90,8 +90,10 @@ def test_rms_norm_errors(dev):
     with pytest.raises(ValueError, match="not divisible by block_k"):
         kernels.rms_norm_fp8(torch.zeros((2, 200), dtype=torch.bfloat16, device=dev),
                              torch.ones(200, dtype=torch.bfloat16, device=dev), 1e-6)
+    with pytest.raises(TypeError, match="bfloat16, float16 or float32"):
+        kernels.rms_norm(x.double(), g, 1e-6)
     with pytest.raises(TypeError):
-        kernels.rms_norm(x.half(), g, 1e-6)
+        kernels.rms_norm_fp8(x.half(), g, 1e-6)
     with pytest.raises(TypeError):
         kernels.rms_norm_fp8(x.float(), g, 1e-6)
     with pytest.raises(ValueError, match="scale must have shape"):
@@ -132,27 +134,35 @@ def test_add_rms_norm_fp8_without_y(dev):
     assert same_scales(s.cpu().numpy(), s_o)
 
 
+_ORACLE_DT = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
+
+
 @pytest.mark.parametrize("x_dt,g_dt,D", [(torch.float32, torch.float32, 2048), (torch.float32, torch.bfloat16, 1000),
                                         (torch.bfloat16, torch.float32, 2304), (torch.bfloat16, torch.bfloat16, 20000),
-                                        (torch.bfloat16, torch.bfloat16, 100)])
+                                        (torch.bfloat16, torch.bfloat16, 100), (torch.float16, torch.float16, 2048),
+                                        (torch.float16, torch.float16, 100), (torch.float16, torch.bfloat16, 1000),
+                                        (torch.bfloat16, torch.float16, 512), (torch.float16, torch.float32, 768)])
 def test_rms_norm_any_dtype_and_width(dev, x_dt, g_dt, D):
     """_rms_norm_pure (kernels.py:30-33) keeps x's dtype for r and x * r and returns
-    the promoted dtype (f32 when either operand is f32); bit-exact against
-    norm_ref.rms_norm_pure_any, including a width the bf16 kernel does not take."""
+    the promoted dtype (the common dtype, else f32: bf16 with f16 promotes to
+    f32); bit-exact against norm_ref.rms_norm_pure_any, including widths the
+    bf16 kernel does not take and f16 rows whose x * r is subnormal."""
     rng = np.random.default_rng(D)
     x = (rng.standard_normal((37, D)) * np.where(rng.random((37, D)) < 1e-3, 50, 1)).astype(np.float32)
+    if x_dt == torch.float16:
+        x[:4] *= 1e-3
+        x[:4, 3] = 2000.0                      # x * r in f16's subnormal range for the rest of these rows
     g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
-    if x_dt == torch.bfloat16:
-        x = ob.bf16_to_f32(ob.f32_to_bf16(x))
-    if g_dt == torch.bfloat16:
-        g = ob.bf16_to_f32(ob.f32_to_bf16(g))
+    x, g = as_dtype_values(x, x_dt), as_dtype_values(g, g_dt)
     xt = torch.from_numpy(x).to(dev).to(x_dt)
     gt = torch.from_numpy(g).to(dev).to(g_dt)
     y = kernels._rms_norm_pure(xt, gt, 1e-6)
-    want = norm_ref.rms_norm_pure_any(x, x_dt == torch.bfloat16, g, 1e-6)
-    out_dt = torch.float32 if torch.float32 in (x_dt, g_dt) else torch.bfloat16
+    want = norm_ref.rms_norm_pure_any(x, _ORACLE_DT[x_dt], g, 1e-6)
+    out_dt = x_dt if x_dt == g_dt else torch.float32
     assert y.dtype == out_dt and y.shape == xt.shape
     if out_dt == torch.bfloat16:
         np.testing.assert_array_equal(bf16_bits(y), ob.f32_to_bf16(want))
+    elif out_dt == torch.float16:
+        np.testing.assert_array_equal(y.cpu().numpy().view(np.uint16), want.astype(np.float16).view(np.uint16))
     else:
         np.testing.assert_array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 import kernels
-from helpers import bf16_bits, maxabs_rel, to_dev
+from helpers import as_dtype_values, bf16_bits, maxabs_rel, to_dev
 from oracle import bf16 as ob
 from oracle import norm_ref
 
@@ -86,7 +86,8 @@ def test_rms_norm_bwd_constant_rows(dev):
 
 @pytest.mark.parametrize("x_dt,g_dt,D", [(torch.float32, torch.float32, 2048), (torch.float32, torch.bfloat16, 1000),
                                         (torch.bfloat16, torch.float32, 512), (torch.bfloat16, torch.bfloat16, 8192),
-                                        (torch.bfloat16, torch.bfloat16, 100)])
+                                        (torch.bfloat16, torch.bfloat16, 100), (torch.float16, torch.float16, 2048),
+                                        (torch.float16, torch.bfloat16, 1000), (torch.float32, torch.float16, 300)])
 def test_rms_norm_bwd_any_dtype_and_width(dev, x_dt, g_dt, D):
     """kernels.py:104-118 for f32 / mixed operands and a width above the bf16
     kernel's 4096: dx in x's dtype, dscale in scale's, against the float64 VJP;
@@ -94,23 +95,19 @@ def test_rms_norm_bwd_any_dtype_and_width(dev, x_dt, g_dt, D):
     rng = np.random.default_rng(D + 1)
     x = rng.standard_normal((300, D)).astype(np.float32)
     g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
-    if x_dt == torch.bfloat16:
-        x = ob.bf16_to_f32(ob.f32_to_bf16(x))
-    if g_dt == torch.bfloat16:
-        g = ob.bf16_to_f32(ob.f32_to_bf16(g))
-    out_dt = torch.float32 if torch.float32 in (x_dt, g_dt) else torch.bfloat16
-    dy = (rng.standard_normal((300, D)) * 1e-2).astype(np.float32)
-    if out_dt == torch.bfloat16:
-        dy = ob.bf16_to_f32(ob.f32_to_bf16(dy))
+    x, g = as_dtype_values(x, x_dt), as_dtype_values(g, g_dt)
+    out_dt = x_dt if x_dt == g_dt else torch.float32
+    dy = as_dtype_values((rng.standard_normal((300, D)) * 1e-2).astype(np.float32), out_dt)
     xt = torch.from_numpy(x).to(dev).to(x_dt).requires_grad_(True)
     gt = torch.from_numpy(g).to(dev).to(g_dt).requires_grad_(True)
     y = kernels.rms_norm(xt, gt, 1e-6)
     y.backward(torch.from_numpy(dy).to(dev).to(out_dt))
     gx, gg = norm_ref.rms_norm_vjp_vals(x, g, 1e-6, dy)
     assert xt.grad.dtype == x_dt and gt.grad.dtype == g_dt
-    tol = TOL if torch.bfloat16 in (x_dt, g_dt) else 1e-5
-    assert maxabs_rel(xt.grad, gx) <= (TOL if x_dt == torch.bfloat16 else tol)
-    assert maxabs_rel(gt.grad, gg) <= (TOL if g_dt == torch.bfloat16 else 1e-4)
+    # the output's rounding: bf16 (TOL), f16 (11 significand bits), f32
+    tol = {torch.bfloat16: TOL, torch.float16: 2e-3, torch.float32: 1e-5}
+    assert maxabs_rel(xt.grad, gx) <= tol[x_dt]
+    assert maxabs_rel(gt.grad, gg) <= max(tol[g_dt], 1e-4)
     first = gt.grad.clone()
     gt.grad = None
     kernels.rms_norm(xt, gt, 1e-6).backward(torch.from_numpy(dy).to(dev).to(out_dt))

@@ -53,15 +53,45 @@ def test_any_dtype_path_matches_torch_and_the_bf16_path():
     var = (np.sum((x32 * x32).astype(np.float64), axis=-1).astype(np.float32) / np.float32(1024)).astype(np.float32)
     r = (1.0 / np.sqrt((var + np.float32(1e-6)).astype(np.float64))).astype(np.float32)
     want = ((torch.from_numpy(x32) * torch.from_numpy(r)[:, None]) * torch.from_numpy(g32)).numpy()
-    np.testing.assert_array_equal(norm_ref.rms_norm_pure_any(x32, False, g32, 1e-6), want)
+    np.testing.assert_array_equal(norm_ref.rms_norm_pure_any(x32, "f32", g32, 1e-6), want)
     # bf16 x, f32 scale: x_n in bf16, then an f32 product
     _, rb = norm_ref.row_inv_rms(xb, 1e-6)
     xn = _t(xb) * _t(ob.f32_to_bf16(rb))[:, None]                    # bf16 x bf16 -> bf16
     want = (xn.float() * torch.from_numpy(g32)).numpy()
-    np.testing.assert_array_equal(norm_ref.rms_norm_pure_any(ob.bf16_to_f32(xb), True, g32, 1e-6), want)
+    np.testing.assert_array_equal(norm_ref.rms_norm_pure_any(ob.bf16_to_f32(xb), "bf16", g32, 1e-6), want)
     # both bf16
-    y = norm_ref.rms_norm_pure_any(ob.bf16_to_f32(xb), True, ob.bf16_to_f32(gb), 1e-6)
+    y = norm_ref.rms_norm_pure_any(ob.bf16_to_f32(xb), "bf16", ob.bf16_to_f32(gb), 1e-6)
     np.testing.assert_array_equal(ob.f32_to_bf16(y), norm_ref.rms_norm_pure(xb, gb, 1e-6))
+
+
+def test_any_dtype_path_f16_matches_torch():
+    """rms_norm_pure_any with f16 x: r and x * r rounded to f16, against torch's
+    f16 CPU arithmetic on the oracle's rsqrt; f16 scale (an f16 product) and
+    bf16 / f32 scales (f16 x bf16 promotes to f32 in jnp and torch alike).
+    Rows with one large element put x * r into f16's subnormal range, where the
+    rounding step is 2^-24."""
+    rng = np.random.default_rng(16)
+    x = (rng.standard_normal((24, 768)) * 3).astype(np.float16)
+    x[:6] = (rng.standard_normal((6, 768)) * 1e-3).astype(np.float16)
+    x[:6, 5] = 2000.0                                 # x * r ~ 1e-3 * 0.014: subnormal f16
+    x32 = x.astype(np.float32)
+    var = (np.sum((x32 * x32).astype(np.float64), axis=-1).astype(np.float32) / np.float32(768)).astype(np.float32)
+    r = (1.0 / np.sqrt((var + np.float32(1e-6)).astype(np.float64))).astype(np.float32)
+    xn = torch.from_numpy(x) * torch.from_numpy(r.astype(np.float16))[:, None]      # f16 x f16 -> f16
+    assert (xn[:6].abs() < 6.1e-5).float().mean() > 0.9                             # mostly subnormal
+    g16 = (1 + 0.1 * rng.standard_normal(768)).astype(np.float16)
+    want = (xn * torch.from_numpy(g16)).numpy()                                     # f16 product
+    got = norm_ref.rms_norm_pure_any(x32, "f16", g16.astype(np.float32), 1e-6)
+    np.testing.assert_array_equal(got.astype(np.float16).view(np.uint16), want.view(np.uint16))
+    gb = ob.f32_to_bf16((1 + 0.1 * rng.standard_normal(768)).astype(np.float32))
+    want = (xn * _t(gb)).numpy()                                                   # promotes to f32
+    assert want.dtype == np.float32
+    got = norm_ref.rms_norm_pure_any(x32, "f16", ob.bf16_to_f32(gb), 1e-6)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    g32 = (1 + 0.1 * rng.standard_normal(768)).astype(np.float32)
+    want = (xn * torch.from_numpy(g32)).numpy()
+    got = norm_ref.rms_norm_pure_any(x32, "f16", g32, 1e-6)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 def test_variance_and_rsqrt_exact():

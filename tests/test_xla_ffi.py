@@ -83,8 +83,13 @@ def test_handler_dtypes_are_accepted_by_their_c_abi():
             nul, d, nul, d, nul, d, nul, nul, 128, 128, 128, nul, 0, nul),
     }
     for name, call in calls.items():
-        for d in (L.TG_DTYPE_BF16, L.TG_DTYPE_F32):
+        norm = name.startswith("tg_rms_norm")
+        for d in (L.TG_DTYPE_BF16, L.TG_DTYPE_F32) + ((L.TG_DTYPE_F16,) if norm else ()):
             assert call(d) == L.TG_EINVAL, (name, d)
             msg = lib.tg_last_error().decode()
             assert "dtype" not in msg, (name, d, msg)
+        # f16 is a norm-only code: the FFI maps it (norm_dtype_code) for the norm handlers only
+        if not norm:
+            assert call(L.TG_DTYPE_F16) == L.TG_EINVAL and "dtype" in lib.tg_last_error().decode(), name
         assert call(9) == L.TG_EINVAL and "dtype" in lib.tg_last_error().decode(), name
+    assert re.search(r"norm_dtype_code\(t, code\)|DataType::F16\) \{ \*code = TG_DTYPE_F16", code)

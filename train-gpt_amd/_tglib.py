@@ -15,7 +15,7 @@ HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "tg_fp8.h")
 
 TG_OK, TG_EINVAL, TG_EHIP = 0, 1, 2
 TG_NOALLOC_SCRATCH_BYTES = 64 << 20     # include/tg_fp8.h
-TG_DTYPE_BF16, TG_DTYPE_F32 = 0, 1
+TG_DTYPE_BF16, TG_DTYPE_F32, TG_DTYPE_F16 = 0, 1, 2
 
 _vp, _i64, _int, _f32, _sz = (ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
                               ctypes.c_float, ctypes.c_size_t)
@@ -118,3 +118,11 @@ def dtype_code(t: torch.Tensor) -> int:
     if t.dtype == torch.float32:
         return TG_DTYPE_F32
     raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def norm_dtype_code(t: torch.Tensor) -> int:
+    """dtype_code plus float16, which the norm entry points (tg_rms_norm_ex,
+    tg_rms_norm_bwd_ex) take and no other entry point does."""
+    if t.dtype == torch.float16:
+        return TG_DTYPE_F16
+    return dtype_code(t)

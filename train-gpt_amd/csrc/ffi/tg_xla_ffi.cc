@@ -39,6 +39,12 @@ bool dtype_code(ffi::DataType t, int* code) {
   return false;
 }
 
+// The norm entry points also take f16.
+bool norm_dtype_code(ffi::DataType t, int* code) {
+  if (t == ffi::DataType::F16) { *code = TG_DTYPE_F16; return true; }
+  return dtype_code(t, code);
+}
+
 template <typename Dims>
 int64_t last_dim(const Dims& d) { return d.empty() ? 1 : d.back(); }
 int64_t rows_of(int64_t count, int64_t last) { return last == 0 ? 0 : count / last; }
@@ -150,16 +156,15 @@ ffi::Error BlockScaledMatmulBwdBf16(hipStream_t stream, ffi::ScratchAllocator sc
                                                 db->untyped_data(), M, N, K, ws, ws_bytes, stream));
 }
 
-// _rms_norm_pure (kernels.py:30-33): x (..., D), scale (D,), each bf16 or f32
-// -> y (..., D) in their promoted dtype (f32 if either is f32).
+// _rms_norm_pure (kernels.py:30-33): x (..., D), scale (D,), each bf16, f16 or
+// f32 -> y (..., D) in their promoted dtype (the common one, else f32).
 ffi::Error RmsNorm(hipStream_t stream, ffi::AnyBuffer x, ffi::AnyBuffer scale,
                    ffi::Result<ffi::AnyBuffer> y, float eps) {
   int cx, cs, cy;
-  if (!dtype_code(x.element_type(), &cx) || !dtype_code(scale.element_type(), &cs) ||
-      !dtype_code(y->element_type(), &cy) ||
-      cy != ((cx == TG_DTYPE_F32 || cs == TG_DTYPE_F32) ? TG_DTYPE_F32 : TG_DTYPE_BF16))
+  if (!norm_dtype_code(x.element_type(), &cx) || !norm_dtype_code(scale.element_type(), &cs) ||
+      !norm_dtype_code(y->element_type(), &cy) || cy != (cx == cs ? cx : TG_DTYPE_F32))
     return ffi::Error(ffi::ErrorCode::kInvalidArgument,
-                      "rms_norm: x, scale bf16 or f32; y in their promoted dtype");
+                      "rms_norm: x, scale bf16, f16 or f32; y in their promoted dtype");
   const int64_t D = last_dim(x.dimensions());
   return status(tg_rms_norm_ex(x.untyped_data(), cx, scale.untyped_data(), cs, y->untyped_data(),
                                rows_of(x.element_count(), D), D, eps, stream));
@@ -176,17 +181,17 @@ ffi::Error RmsNormFp8(hipStream_t stream, ffi::Buffer<ffi::BF16> x, ffi::Buffer<
                                 rows_of(x.element_count(), D), D, eps, (int)block_k, stream));
 }
 
-// The norm's _bwd (kernels.py:104-118): x, scale, dy bf16 or f32 -> dx in
-// x's dtype, dscale in scale's.
+// The norm's _bwd (kernels.py:104-118): x, scale, dy bf16, f16 or f32 -> dx
+// in x's dtype, dscale in scale's.
 ffi::Error RmsNormBwd(hipStream_t stream, ffi::ScratchAllocator scratch, ffi::AnyBuffer x,
                       ffi::AnyBuffer scale, ffi::AnyBuffer dy, ffi::Result<ffi::AnyBuffer> dx,
                       ffi::Result<ffi::AnyBuffer> dscale, float eps) {
   int cx, cs, cd, cdx, cds;
-  if (!dtype_code(x.element_type(), &cx) || !dtype_code(scale.element_type(), &cs) ||
-      !dtype_code(dy.element_type(), &cd) || !dtype_code(dx->element_type(), &cdx) ||
-      !dtype_code(dscale->element_type(), &cds) || cdx != cx || cds != cs)
+  if (!norm_dtype_code(x.element_type(), &cx) || !norm_dtype_code(scale.element_type(), &cs) ||
+      !norm_dtype_code(dy.element_type(), &cd) || !norm_dtype_code(dx->element_type(), &cdx) ||
+      !norm_dtype_code(dscale->element_type(), &cds) || cdx != cx || cds != cs)
     return ffi::Error(ffi::ErrorCode::kInvalidArgument,
-                      "rms_norm backward: bf16 / f32 operands; dx in x's dtype, dscale in scale's");
+                      "rms_norm backward: bf16 / f16 / f32 operands; dx in x's dtype, dscale in scale's");
   const int64_t D = last_dim(x.dimensions()), rows = rows_of(x.element_count(), D);
   ffi::Error err = ffi::Error::Success();
   const size_t ws_bytes = tg_rms_norm_bwd_workspace(rows, D);

@@ -14,6 +14,8 @@
 // 128-element scale block is one 16-lane DPP row.  gamma stays in registers
 // while the wave walks rows with a grid stride.  x is read once; y, q and the
 // scales are written once.
+#include <type_traits>
+
 #include "row_ops.h"
 #include "tg_device.h"
 #include "tg_host.h"
@@ -288,7 +290,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint4* __restric
 }
 
 // ---------------------------------------------------------------------------
-// General path: any width and either dtype (bf16 or f32) for x, scale and the
+// General path: any width and any of bf16, f16, f32 for x, scale and the
 // gradients, with _rms_norm_pure's op-by-op rounding in x's dtype
 // (kernels.py:30-33: r = rsqrt(var + eps).astype(x.dtype), x_n = x * r in
 // x.dtype, y = x_n * scale in the promoted dtype).  Rows are walked by one
@@ -306,7 +308,17 @@ template <> __device__ __forceinline__ void st_f32<uint16_t>(uint16_t* p, int64_
   p[i] = __builtin_bit_cast(uint16_t, (__bf16)v);   // RNE
 }
 template <> __device__ __forceinline__ void st_f32<float>(float* p, int64_t i, float v) { p[i] = v; }
-template <typename T> constexpr bool is_bf16() { return sizeof(T) == 2; }
+template <> __device__ __forceinline__ float ld_f32<_Float16>(const _Float16* p, int64_t i) { return (float)p[i]; }
+template <> __device__ __forceinline__ void st_f32<_Float16>(_Float16* p, int64_t i, float v) {
+  p[i] = (_Float16)v;   // RNE, f16 subnormals kept
+}
+template <typename T> constexpr bool is_bf16() { return std::is_same<T, uint16_t>::value; }
+// v rounded to T's precision (the .astype(x.dtype) of kernels.py:32), as f32.
+template <typename T> __device__ __forceinline__ float round_to(float v) {
+  if constexpr (std::is_same<T, uint16_t>::value) return round_bf16(v);
+  else if constexpr (std::is_same<T, _Float16>::value) return (float)(_Float16)v;
+  else return v;
+}
 
 // var = fl32(sum fl32(x)^2) / D (f64 accumulation), rnorm = fl32(1 / sqrt(var + eps)).
 template <typename XT>
@@ -330,11 +342,9 @@ __global__ __launch_bounds__(256) void rmsnorm_gen_kernel(const XT* __restrict__
   for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows;
        row += (int64_t)gridDim.x * 4) {
     const XT* xr = x + row * dim;
-    float r = row_rnorm(xr, dim, lane, eps);
-    if (is_bf16<XT>()) r = round_bf16(r);                              // .astype(x.dtype)
+    const float r = round_to<XT>(row_rnorm(xr, dim, lane, eps));      // .astype(x.dtype)
     for (int c = lane; c < dim; c += 64) {
-      float t = ld_f32(xr, c) * r;                                      // x * r in x.dtype
-      if (is_bf16<XT>()) t = round_bf16(t);
+      const float t = round_to<XT>(ld_f32(xr, c) * r);                  // x * r in x.dtype
       st_f32(y + row * dim, c, t * ld_f32(gamma, c));                   // x_n * scale
     }
   }
@@ -531,18 +541,29 @@ static unsigned row_grid(int64_t rows) {
   return (unsigned)(g < 1 ? 1 : g > 16384 ? 16384 : g);
 }
 
+// Calls f(T{}) with T the element type of dtype code d: bf16 as its uint16_t
+// bits, _Float16, float.  Codes are validated by the entry points.
+template <typename F> static int with_dtype(int d, F&& f) {
+  switch (d) {
+    case TG_DTYPE_BF16: return f(uint16_t{});
+    case TG_DTYPE_F16: return f(_Float16{});
+    default: return f(float{});
+  }
+}
+
+static bool valid_float_dtype(int d) { return d == TG_DTYPE_BF16 || d == TG_DTYPE_F16 || d == TG_DTYPE_F32; }
+
 template <typename XT, typename GT>
-static int launch_gen_fwd(const void* x, const void* g, void* y, bool y_f32, int64_t rows, int64_t dim,
+static int launch_gen_fwd(const void* x, const void* g, void* y, int y_dtype, int64_t rows, int64_t dim,
                           float eps, hipStream_t st) {
   auto X = reinterpret_cast<const XT*>(x);
   auto G = reinterpret_cast<const GT*>(g);
-  if (y_f32)
-    hipLaunchKernelGGL((rmsnorm_gen_kernel<XT, GT, float>), dim3(row_grid(rows)), dim3(256), 0, st, X, G,
-                       reinterpret_cast<float*>(y), rows, (int)dim, eps);
-  else
-    hipLaunchKernelGGL((rmsnorm_gen_kernel<XT, GT, uint16_t>), dim3(row_grid(rows)), dim3(256), 0, st, X,
-                       G, reinterpret_cast<uint16_t*>(y), rows, (int)dim, eps);
-  return check_launch("rmsnorm_gen");
+  return with_dtype(y_dtype, [&](auto yt) {
+    using YT = decltype(yt);
+    hipLaunchKernelGGL((rmsnorm_gen_kernel<XT, GT, YT>), dim3(row_grid(rows)), dim3(256), 0, st, X, G,
+                       reinterpret_cast<YT*>(y), rows, (int)dim, eps);
+    return check_launch("rmsnorm_gen");
+  });
 }
 
 template <typename XT, typename GT, typename DT>
@@ -571,12 +592,8 @@ static int launch_gen_bwd(const void* x, const void* g, const void* dy, void* dx
                        (int)dim, 1);
     TG_TRY(check_launch("rmsnorm_gen_bwd"));
   }
-  if (is_bf16<GT>())
-    hipLaunchKernelGGL(rmsnorm_bwd_reduce<uint16_t>, dim3((unsigned)((dim + 63) / 64)), dim3(1024), 0, st,
-                       partial, (int)groups, (int)dim, reinterpret_cast<uint16_t*>(dscale));
-  else
-    hipLaunchKernelGGL(rmsnorm_bwd_reduce<float>, dim3((unsigned)((dim + 63) / 64)), dim3(1024), 0, st,
-                       partial, (int)groups, (int)dim, reinterpret_cast<float*>(dscale));
+  hipLaunchKernelGGL(rmsnorm_bwd_reduce<GT>, dim3((unsigned)((dim + 63) / 64)), dim3(1024), 0, st, partial,
+                     (int)groups, (int)dim, reinterpret_cast<GT*>(dscale));
   return check_launch("rmsnorm_bwd_reduce");
 }
 
@@ -648,21 +665,21 @@ extern "C" int tg_rms_norm_bwd(const void* x, const void* scale, const void* dy,
 extern "C" int tg_rms_norm_ex(const void* x, int x_dtype, const void* scale, int scale_dtype, void* y,
                               int64_t rows, int64_t dim, float eps, void* stream) {
   if (rows < 0 || dim <= 0 || dim > 0x7FFFFFFF) return einval("rms_norm_ex: bad shape");
-  if ((x_dtype != TG_DTYPE_BF16 && x_dtype != TG_DTYPE_F32) ||
-      (scale_dtype != TG_DTYPE_BF16 && scale_dtype != TG_DTYPE_F32))
-    return einval("rms_norm_ex: dtypes must be TG_DTYPE_BF16 or TG_DTYPE_F32");
+  if (!valid_float_dtype(x_dtype) || !valid_float_dtype(scale_dtype))
+    return einval("rms_norm_ex: dtypes must be TG_DTYPE_BF16, TG_DTYPE_F16 or TG_DTYPE_F32");
   if (rows == 0) return TG_OK;
   if (!x || !scale || !y) return einval("rms_norm_ex: null pointer");
   hipStream_t st = as_stream(stream);
   if (x_dtype == TG_DTYPE_BF16 && scale_dtype == TG_DTYPE_BF16 && dim % 8 == 0 && dim <= 16384 &&
       aligned(x, 16) && aligned(scale, 16) && aligned(y, 16))
     return launch_rmsnorm<false>(x, scale, y, nullptr, nullptr, rows, dim, eps, st);
-  const bool y_f32 = x_dtype == TG_DTYPE_F32 || scale_dtype == TG_DTYPE_F32;
-  if (x_dtype == TG_DTYPE_BF16)
-    return scale_dtype == TG_DTYPE_BF16 ? launch_gen_fwd<uint16_t, uint16_t>(x, scale, y, y_f32, rows, dim, eps, st)
-                                        : launch_gen_fwd<uint16_t, float>(x, scale, y, y_f32, rows, dim, eps, st);
-  return scale_dtype == TG_DTYPE_BF16 ? launch_gen_fwd<float, uint16_t>(x, scale, y, y_f32, rows, dim, eps, st)
-                                      : launch_gen_fwd<float, float>(x, scale, y, y_f32, rows, dim, eps, st);
+  // jnp's promotion of x_n * scale: the common dtype, else f32 (bf16 with f16 included)
+  const int y_dtype = x_dtype == scale_dtype ? x_dtype : TG_DTYPE_F32;
+  return with_dtype(x_dtype, [&](auto xt) {
+    return with_dtype(scale_dtype, [&](auto gt) {
+      return launch_gen_fwd<decltype(xt), decltype(gt)>(x, scale, y, y_dtype, rows, dim, eps, st);
+    });
+  });
 }
 
 extern "C" int tg_rms_norm_bwd_ex(const void* x, int x_dtype, const void* scale, int scale_dtype,
@@ -671,8 +688,8 @@ extern "C" int tg_rms_norm_bwd_ex(const void* x, int x_dtype, const void* scale,
                                   void* stream) {
   if (rows < 0 || dim <= 0 || dim > 0x7FFFFFFF) return einval("rms_norm_bwd_ex: bad shape");
   for (int d : {x_dtype, scale_dtype, dy_dtype})
-    if (d != TG_DTYPE_BF16 && d != TG_DTYPE_F32)
-      return einval("rms_norm_bwd_ex: dtypes must be TG_DTYPE_BF16 or TG_DTYPE_F32");
+    if (!valid_float_dtype(d))
+      return einval("rms_norm_bwd_ex: dtypes must be TG_DTYPE_BF16, TG_DTYPE_F16 or TG_DTYPE_F32");
   if (!scale || !dscale) return einval("rms_norm_bwd_ex: null pointer");
   if (rows > 0 && (!x || !dy || !dx || !workspace)) return einval("rms_norm_bwd_ex: null pointer");
   if (workspace_bytes < tg_rms_norm_bwd_workspace(rows, dim))
@@ -682,15 +699,12 @@ extern "C" int tg_rms_norm_bwd_ex(const void* x, int x_dtype, const void* scale,
   if (all_bf16 && dim % 8 == 0 && aligned(x, 16) && aligned(scale, 16) && aligned(dy, 16) && aligned(dx, 16))
     return tg_rms_norm_bwd(x, scale, dy, dx, dscale, rows, dim, eps, workspace, workspace_bytes, stream);
   hipStream_t st = as_stream(stream);
-  const int key = (x_dtype == TG_DTYPE_F32) * 4 + (scale_dtype == TG_DTYPE_F32) * 2 + (dy_dtype == TG_DTYPE_F32);
-  switch (key) {
-    case 0: return launch_gen_bwd<uint16_t, uint16_t, uint16_t>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
-    case 1: return launch_gen_bwd<uint16_t, uint16_t, float>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
-    case 2: return launch_gen_bwd<uint16_t, float, uint16_t>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
-    case 3: return launch_gen_bwd<uint16_t, float, float>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
-    case 4: return launch_gen_bwd<float, uint16_t, uint16_t>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
-    case 5: return launch_gen_bwd<float, uint16_t, float>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
-    case 6: return launch_gen_bwd<float, float, uint16_t>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
-    default: return launch_gen_bwd<float, float, float>(x, scale, dy, dx, dscale, rows, dim, eps, workspace, st);
-  }
+  return with_dtype(x_dtype, [&](auto xt) {
+    return with_dtype(scale_dtype, [&](auto gt) {
+      return with_dtype(dy_dtype, [&](auto dt) {
+        return launch_gen_bwd<decltype(xt), decltype(gt), decltype(dt)>(x, scale, dy, dx, dscale, rows, dim,
+                                                                          eps, workspace, st);
+      });
+    });
+  });
 }

@@ -129,6 +129,9 @@ def _fp8_backward(block_k, residuals, g):
 block_scaled_matmul.defvjp(_fp8_forward_with_residuals, _fp8_backward)
 
 
+_NORM_FLOATS = (jnp.bfloat16, jnp.float16, jnp.float32)
+
+
 def _norm_out_dtype(x, scale):
     """jnp's promotion of x_n (x.dtype) * scale (kernels.py:33)."""
     return jnp.promote_types(x.dtype, scale.dtype)
@@ -136,8 +139,8 @@ def _norm_out_dtype(x, scale):
 
 def _check_norm(x, scale):
     for t in (x, scale):
-        if t.dtype not in (jnp.bfloat16, jnp.float32):
-            raise TypeError(f"rms_norm: x and scale must be bfloat16 or float32, got {x.dtype}, {scale.dtype}")
+        if t.dtype not in _NORM_FLOATS:
+            raise TypeError(f"rms_norm: x and scale must be bfloat16, float16 or float32, got {x.dtype}, {scale.dtype}")
     D = x.shape[-1]
     if scale.shape != (D,):
         raise ValueError(f"scale must have shape ({D},), got {tuple(scale.shape)}")
@@ -164,7 +167,7 @@ def _rms_norm_fwd(x, scale, eps):
 def _rms_norm_bwd(eps, residuals, g):
     """kernels.py:104-118: (grad_x as x.dtype, grad_scale as scale.dtype)."""
     x, scale = residuals
-    if g.dtype not in (jnp.bfloat16, jnp.float32):
+    if g.dtype not in _NORM_FLOATS:
         g = g.astype(jnp.float32)
     return tuple(_call("tg_rms_norm_bwd",
                        (jax.ShapeDtypeStruct(x.shape, x.dtype), jax.ShapeDtypeStruct(scale.shape, scale.dtype)),

@@ -26,7 +26,7 @@ import torch
 import _tglib as _L
 
 
-_FLOATS = (torch.bfloat16, torch.float32)
+_FLOATS = (torch.bfloat16, torch.float16, torch.float32)
 
 
 def _prep(x: torch.Tensor, scale: torch.Tensor, bf16_only: bool = True):
@@ -34,7 +34,7 @@ def _prep(x: torch.Tensor, scale: torch.Tensor, bf16_only: bool = True):
     if bf16_only and (x.dtype != torch.bfloat16 or scale.dtype != torch.bfloat16):
         raise TypeError("rms_norm_fp8: x and scale must be bfloat16 (the model's dtype)")
     if x.dtype not in _FLOATS or scale.dtype not in _FLOATS:
-        raise TypeError(f"rms_norm: x and scale must be bfloat16 or float32, got {x.dtype}, {scale.dtype}")
+        raise TypeError(f"rms_norm: x and scale must be bfloat16, float16 or float32, got {x.dtype}, {scale.dtype}")
     D = x.shape[-1]
     if scale.shape != (D,):
         raise ValueError(f"scale must have shape ({D},), got {tuple(scale.shape)}")
@@ -42,16 +42,17 @@ def _prep(x: torch.Tensor, scale: torch.Tensor, bf16_only: bool = True):
 
 
 def _out_dtype(x: torch.Tensor, scale: torch.Tensor):
-    """jnp's promotion of x_n (x.dtype) * scale: f32 if either is f32."""
-    return torch.float32 if torch.float32 in (x.dtype, scale.dtype) else torch.bfloat16
+    """jnp's promotion of x_n (x.dtype) * scale: the common dtype, else f32
+    (bf16 with f16 promotes to f32, as in torch)."""
+    return x.dtype if x.dtype == scale.dtype else torch.float32
 
 
 def _rms_norm_pure(x: torch.Tensor, scale: torch.Tensor, eps: float) -> torch.Tensor:
-    """kernels.py:30-33 on the GPU: x (..., D), scale (D,), bf16 or f32 -> (..., D) in the promoted dtype."""
+    """kernels.py:30-33 on the GPU: x (..., D), scale (D,), bf16, f16 or f32 -> (..., D) in the promoted dtype."""
     x2, g, D = _prep(x, scale, bf16_only=False)
     y = torch.empty(x2.shape, dtype=_out_dtype(x, scale), device=x.device)
     # bf16 x and scale with D % 8 == 0 (D <= 16384) take the fast kernel inside
-    _L.check(_L.lib().tg_rms_norm_ex(_L.ptr(x2), _L.dtype_code(x2), _L.ptr(g), _L.dtype_code(g),
+    _L.check(_L.lib().tg_rms_norm_ex(_L.ptr(x2), _L.norm_dtype_code(x2), _L.ptr(g), _L.norm_dtype_code(g),
                                      _L.ptr(y), x2.shape[0], D, float(eps), _L.stream_of(x2)))
     return y.reshape(x.shape)
 
@@ -122,7 +123,7 @@ def _rms_norm_bwd(x: torch.Tensor, scale: torch.Tensor, eps: float, g: torch.Ten
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=x.device)
     # all-bf16 operands with D % 8 == 0 take tg_rms_norm_bwd's kernels inside
     _L.check(_L.lib().tg_rms_norm_bwd_ex(
-        _L.ptr(x2), _L.dtype_code(x2), _L.ptr(sc), _L.dtype_code(sc), _L.ptr(g2), _L.dtype_code(g2),
+        _L.ptr(x2), _L.norm_dtype_code(x2), _L.ptr(sc), _L.norm_dtype_code(sc), _L.ptr(g2), _L.norm_dtype_code(g2),
         _L.ptr(dx), _L.ptr(dscale), R, D, float(eps), _L.ptr(ws), ws_bytes, _L.stream_of(x2)))
     return dx.reshape(x.shape), dscale
 
