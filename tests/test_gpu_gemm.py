@@ -57,9 +57,13 @@ def test_layout_known_answer(dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 8, 128), (17, 40, 256), (130, 200, 384), (256, 256, 512),
-                                   # below 128 large tiles: 128 x 96 tiles, and 128 x 128 ones
-                                   # where they load the busiest CU less (2048^2 on 256 CUs)
-                                   (300, 136, 1024), (2048, 3072, 768), (2048, 2048, 256),
+                                   # below 128 large tiles: the short-K ring kernel with 128 x 192
+                                   # tiles (C1; 1, 5 and 6 K blocks: no tail / a tail of 2 after a
+                                   # round of 3 stages), 128 x 128 (2048^2 on 256 CUs), 128 x 64 (few
+                                   # rows: 1 tile row over many CUs; 5 and 18 K blocks against 6
+                                   # stages) and N % 8 != 0 (element stores instead of staged rows)
+                                   (300, 136, 1024), (2048, 3072, 768), (2048, 3072, 640), (2048, 3072, 128),
+                                   (2048, 2048, 256), (128, 6912, 2304), (640, 768, 640), (257, 1001, 640),
                                    # >= 128 tiles of 256 x 256: the large-tile kernel, with ragged
                                    # M / N edges and odd / even numbers of K blocks
                                    (2100, 4000, 384), (4096, 4096, 256), (3000, 2900, 640),

@@ -30,9 +30,15 @@ FLAGS = [
 ]
 
 
+# Per-source flags.  gemm_fp8.hip: MFMA results in VGPRs even where one wave
+# per SIMD would let the compiler use AGPRs (its short-K kernel promotes every
+# MFMA result with VALU FMAs, which read VGPRs only).
+EXTRA_FLAGS = {"gemm_fp8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
@@ -48,10 +54,21 @@ def build_library(verbose: bool = False) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    _check_stubs(tmp)
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
     return LIB
+
+
+def _check_stubs(lib: str) -> None:
+    """Fail on a kernel whose host launch stub the compiler did not emit: hipcc
+    then links a library with an undefined __device_stub__ symbol that only
+    fails when the library is loaded."""
+    r = subprocess.run(["nm", "-u", lib], capture_output=True, text=True)
+    missing = [ln.split()[-1] for ln in r.stdout.splitlines() if "__device_stub__" in ln]
+    if missing:
+        raise RuntimeError(f"{lib}: {len(missing)} kernel stubs undefined, e.g. {missing[0]}")
 
 
 PROBE_SRCS = [os.path.join(CSRC, "probe", f) for f in ("io_floor.hip", "gemv_stream.hip", "quant_floor.hip")]

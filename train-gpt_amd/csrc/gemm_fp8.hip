@@ -185,6 +185,324 @@ __global__ __launch_bounds__(256, 2) void gemm_fp8_nt_kernel(
     }
 }
 
+template <int V> using IntC = std::integral_constant<int, V>;
+
+// ---------------------------------------------------------------------------
+// Short-K kernel for launches of fewer than 128 tiles of 256 x 256 (C1's
+// 2048 x 3072 x 768 and the decode prefill's GEMMs).  With a few K blocks per
+// tile (6 at K = 768) the time a block's bytes take to arrive, not the MFMAs,
+// is what one block in flight leaves exposed; here NST stages of one K block
+// each ring through LDS, so NST - 1 blocks are in flight while one is computed.
+//   * Workgroup tile 128 x BN (BN = 32 * TN), 2 x WN waves, wave tile
+//     64 x BN / WN on v_mfma_f32_16x16x128_f8f6f4: the same fragments, MFMA
+//     operand order and promotion as gemm_fp8_nt_kernel, so the same bits.
+//   * Copies: HBM -> LDS with buffer_load ... lds (no VGPR staging).  A stage
+//     is 128 + BN rows of 128 B plus the block's scales; the W waves split the
+//     A rows and the B rows evenly, 8 rows (1 KiB) per instruction, and the
+//     64-float scale copies (padded to a multiple of W with copies that read
+//     nothing).  16-byte chunk c of row r sits at c ^ g256_swz(r): the 16 rows
+//     one fragment read touches (two per 256-byte bank line) fall on all 64
+//     banks.  The swizzle is applied to the global offset a lane fetches.  Rows past M / N and blocks past the last fall outside the
+//     buffer range and read as zero; every wave issues the same count per
+//     block, so one vmcnt immediate says "block kb has landed".
+//   * Step kb (stage kb % NST): wait for this wave's copies of block kb, bare
+//     s_barrier (block kb complete; every wave done reading block kb - 1),
+//     issue block kb + NST - 1 into block kb - 1's stage, compute block kb.
+//     The stages are distinct __shared__ objects and the loop is unrolled by
+//     NST, so the compiler tells the copies in flight from the reads.
+//   * bf16 output with N % 8 == 0: each wave stages its result in a private
+//     LDS region and stores whole 16-byte pieces of rows; otherwise element
+//     stores.
+// ---------------------------------------------------------------------------
+template <int TN, int WN> struct LatCfg {
+  static constexpr int TM = 4, BM = 128, BN = 32 * TN, W = 2 * WN;
+  static constexpr int TNW = 2 * TN / WN;                     // 16-column tiles per wave
+  static constexpr int APW = 16 / W, BPW = 4 * TN / W;        // 1 KiB copies per wave: A, B
+  static constexpr int SAC = BM / 64, SBC = (BN + 63) / 64;   // 64-float scale copies of A / B
+  static constexpr int SCW = (SAC + SBC + W - 1) / W;         // scale copies per wave (padded)
+  static constexpr int SREG = W * SCW * 64;                   // scale floats per stage
+  static constexpr int STAGE = (BM + BN) * 128 + SREG * 4;    // bytes per stage
+  static constexpr int NST = 163840 / STAGE > 6 ? 6 : 163840 / STAGE;
+  static constexpr int IPW = APW + BPW + SCW;                 // copy instructions per wave per block
+  static constexpr int RP = 32 * TNW + 16;                    // epilogue row pitch (bytes)
+  static constexpr int RPS = (W + NST - 1) / NST;             // epilogue regions per stage
+  static_assert(16 % W == 0 && (4 * TN) % W == 0 && (2 * TN) % WN == 0, "even split over the waves");
+  static_assert(APW <= 4 && BPW <= 6 && SCW <= 2, "within LatLoad's arrays");
+};
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+__device__ __forceinline__ u32x4_t lat_ld16(const lds_u8* p) {
+  return *(const __attribute__((address_space(3))) u32x4_t*)p;
+}
+__device__ __forceinline__ float lat_ldf(const lds_u8* p) {
+  return *(const __attribute__((address_space(3))) float*)p;
+}
+
+// Loader state of one wave: buffer descriptors and per-lane offsets of its
+// operand and scale copies.
+constexpr int kLatMaxAPW = 4, kLatMaxBPW = 6, kLatMaxSCW = 2;
+struct LatLoad {
+  __amdgpu_buffer_rsrc_t ra, rb, rsa, rsb;
+  uint32_t voa[kLatMaxAPW], vob[kLatMaxBPW], vos[kLatMaxSCW], skb[kLatMaxSCW];
+  bool sb[kLatMaxSCW];        // scale copy u reads B scales (else A scales)
+  int wave, nkb;
+};
+
+// The LDS destination of an LDS-DMA copy, cast explicitly: in a template,
+// the implicit generic -> LDS conversion fails the host pass's instantiation,
+// and a kernel whose host instantiation fails gets no launch stub (the build
+// checks the library for undefined stubs).
+#define TG_LAT_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+// Block kb into the stage at l.  Blocks past the last read zero, at offset
+// 2^31: beyond any buffer here (32-bit sizes), and voa + 2^31 < 2^32.
+template <class Cfg>
+__device__ __forceinline__ void lat_issue(const LatLoad& c, uint8_t* l, int kb) {
+  const bool in = kb < c.nkb;
+  const uint32_t k0 = in ? (uint32_t)kb * 128u : 0x80000000u;
+#pragma unroll
+  for (int p = 0; p < Cfg::APW; ++p)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.ra, TG_LAT_LDS(l + (8 * Cfg::APW * c.wave + 8 * p) * 128), 16, c.voa[p],
+                                             k0, 0, 0);
+#pragma unroll
+  for (int p = 0; p < Cfg::BPW; ++p)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rb, TG_LAT_LDS(l + (Cfg::BM + 8 * Cfg::BPW * c.wave + 8 * p) * 128), 16,
+                                             c.vob[p], k0, 0, 0);
+#pragma unroll
+  for (int u = 0; u < Cfg::SCW; ++u)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.sb[u] ? c.rsb : c.rsa,
+                                             TG_LAT_LDS(l + (Cfg::BM + Cfg::BN) * 128 + (c.wave + Cfg::W * u) * 256), 4,
+                                             c.vos[u], in ? (uint32_t)kb * c.skb[u] : 0x80000000u, 0, 0);
+}
+
+// LDS byte offsets (within a stage) of this lane's fragment chunks and scales
+// for m-tile 0 / n-tile 0.
+struct LatFrag {
+  uint32_t fa0, fa1, fb0, fb1, fsa, fsb;
+};
+
+// Step of block kb: wait for this wave's copies of it, barrier, refill the
+// stage block kb - 1 used with block kb_refill, compute block kb from cur.
+template <class Cfg>
+__device__ __forceinline__ void lat_step(const LatLoad& ld, const LatFrag& f,
+                                         v4f (&acc)[Cfg::TM][Cfg::TNW], const uint8_t* cur, uint8_t* refill,
+                                         int kb_refill) {
+  constexpr int TM = Cfg::TM, TNW = Cfg::TNW;
+  constexpr int kWait = (Cfg::NST - 2) * Cfg::IPW;
+  // s_waitcnt vmcnt(kWait) in the gfx9 encoding (vmcnt low bits 3:0, high
+  // bits 15:14; expcnt and lgkmcnt not waited)
+  constexpr int kWaitImm = (kWait & 15) | ((kWait >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+  __builtin_amdgcn_s_waitcnt(kWaitImm);
+  __builtin_amdgcn_s_barrier();
+  lat_issue<Cfg>(ld, refill, kb_refill);
+  const lds_u8* l = (const lds_u8*)cur;
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  v8i bf[TNW];
+  float sbv[TNW];
+#pragma unroll
+  for (int j = 0; j < TNW; ++j) {
+    bf[j] = as_v8i(lat_ld16(l + f.fb0 + j * 2048), lat_ld16(l + f.fb1 + j * 2048));
+    sbv[j] = lat_ldf(l + f.fsb + j * 64);
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const v8i af = as_v8i(lat_ld16(l + f.fa0 + i * 2048), lat_ld16(l + f.fa1 + i * 2048));
+    const u32x4_t sv = lat_ld16(l + f.fsa + i * 64);
+    const float4 sav = make_float4(__uint_as_float(sv.x), __uint_as_float(sv.y), __uint_as_float(sv.z),
+                                   __uint_as_float(sv.w));
+    // the m-tile's MFMAs first, then their promotions: the VALU work of tile
+    // j runs while the MFMAs after it are in the matrix pipe
+    v4f p[TNW];
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) p[j] = mfma_f8_16x16x128(af, bf[j], zero);
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) {
+      acc[i][j][0] = __builtin_fmaf(p[j][0], sav.x * sbv[j], acc[i][j][0]);
+      acc[i][j][1] = __builtin_fmaf(p[j][1], sav.y * sbv[j], acc[i][j][1]);
+      acc[i][j][2] = __builtin_fmaf(p[j][2], sav.z * sbv[j], acc[i][j][2]);
+      acc[i][j][3] = __builtin_fmaf(p[j][3], sav.w * sbv[j], acc[i][j][3]);
+    }
+  }
+}
+
+template <int S>
+__device__ __forceinline__ uint8_t* lat_pick(uint8_t* s0, uint8_t* s1, uint8_t* s2, uint8_t* s3, uint8_t* s4,
+                                             uint8_t* s5) {
+  return S == 0 ? s0 : S == 1 ? s1 : S == 2 ? s2 : S == 3 ? s3 : S == 4 ? s4 : s5;
+}
+
+// (At one workgroup per CU the compiler would put the MFMA results in AGPRs,
+// each element then copied out for the promotion; this file is built with
+// -amdgpu-mfma-vgpr-form, which keeps them in VGPRs and changes no other
+// kernel here.)
+template <int TN, int WN, int BNS, bool OUT_F32, bool SKM>
+__global__ __launch_bounds__(128 * WN, 1) void gemm_fp8_lat_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ SA, const uint8_t* __restrict__ B,
+    const float* __restrict__ SB, void* __restrict__ C, int M, int N, int K, int tiles_m, int tiles_n,
+    int vec_out) {
+  using Cfg = LatCfg<TN, WN>;
+  constexpr int TM = Cfg::TM, BM = Cfg::BM, BN = Cfg::BN, NST = Cfg::NST, STAGE = Cfg::STAGE;
+  constexpr int TNW = Cfg::TNW, W = Cfg::W;
+  static_assert(NST >= 3, "at least two blocks in flight");
+  static_assert((NST - 2) * Cfg::IPW <= 63, "vmcnt immediate");
+  static_assert(Cfg::RPS * 64 * Cfg::RP <= STAGE, "epilogue regions fit the stages");
+  __shared__ __attribute__((aligned(16))) uint8_t st0[STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t st1[STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t st2[STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t st3[NST > 3 ? STAGE : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t st4[NST > 4 ? STAGE : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t st5[NST > 5 ? STAGE : 16];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  int tmi, tni;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tmi, tni);
+  const int m0 = tmi * BM, n0 = tni * BN;
+  const int nkb = K >> 7;
+  const uint32_t uK = (uint32_t)K;
+
+  // ---- loader state ----
+  LatLoad ld;
+  ld.wave = wave;
+  ld.nkb = nkb;
+  ld.ra = make_rsrc(A, (uint32_t)M * uK);
+  ld.rb = make_rsrc(B, (uint32_t)N * uK);
+  // the lane's slot in copy p holds logical chunk (lane & 7) ^ g256_swz(row),
+  // row = 8 * g + lane / 8 for the copy's 8-row group g: g256_swz(row) =
+  // 4 * (g & 1) + lane / 16
+#pragma unroll
+  for (int p = 0; p < Cfg::APW; ++p) {
+    const int g = Cfg::APW * wave + p;
+    ld.voa[p] = (uint32_t)(m0 + 8 * g + (lane >> 3)) * uK + (uint32_t)((lane & 7) ^ (4 * (g & 1) + (lane >> 4))) * 16u;
+  }
+#pragma unroll
+  for (int p = 0; p < Cfg::BPW; ++p) {
+    const int g = Cfg::BPW * wave + p;
+    ld.vob[p] = (uint32_t)(n0 + 8 * g + (lane >> 3)) * uK + (uint32_t)((lane & 7) ^ (4 * (g & 1) + (lane >> 4))) * 16u;
+  }
+  const int nsb = BNS == 1 ? N : (N + BNS - 1) / BNS;
+  ld.rsa = make_rsrc(SA, (uint32_t)M * (uint32_t)nkb * 4u);
+  ld.rsb = make_rsrc(SB, (uint32_t)nsb * (uint32_t)nkb * 4u);
+#pragma unroll
+  for (int u = 0; u < Cfg::SCW; ++u) {
+    const int c = wave + W * u;                       // scale copy c: floats 64c .. 64c+63 of the region
+    if (c < Cfg::SAC) {
+      const uint32_t m = (uint32_t)(m0 + 64 * c + lane);
+      ld.sb[u] = false;
+      ld.vos[u] = SKM ? m * 4u : m * (uint32_t)nkb * 4u;
+      ld.skb[u] = SKM ? (uint32_t)M * 4u : 4u;
+    } else if (c < Cfg::SAC + Cfg::SBC) {
+      const uint32_t sn = (uint32_t)((n0 + 64 * (c - Cfg::SAC) + lane) / BNS);
+      ld.sb[u] = true;
+      ld.vos[u] = SKM ? sn * 4u : sn * (uint32_t)nkb * 4u;
+      ld.skb[u] = SKM ? (uint32_t)nsb * 4u : 4u;
+    } else {                                          // padding copy: out of range, reads zero
+      ld.sb[u] = false;
+      ld.vos[u] = 0x80000000u;
+      ld.skb[u] = 0u;
+    }
+  }
+
+  // ---- compute state: lane (fr, fg) reads logical chunks 2fg, 2fg + 1 ----
+  const int fr = lane & 15, fg = lane >> 4;
+  const int ra0 = wm * 16 * TM + fr, rb0 = wn * 16 * TNW + fr;      // fragment rows of tile 0
+  // (g256_swz(row + 16 i) == g256_swz(row))
+  LatFrag f;
+  f.fa0 = (uint32_t)ra0 * 128u + (uint32_t)(((2 * fg) ^ g256_swz(ra0)) * 16);
+  f.fa1 = (uint32_t)ra0 * 128u + (uint32_t)(((2 * fg + 1) ^ g256_swz(ra0)) * 16);
+  f.fb0 = (uint32_t)(BM + rb0) * 128u + (uint32_t)(((2 * fg) ^ g256_swz(rb0)) * 16);
+  f.fb1 = (uint32_t)(BM + rb0) * 128u + (uint32_t)(((2 * fg + 1) ^ g256_swz(rb0)) * 16);
+  f.fsa = (uint32_t)(BM + BN) * 128u + (uint32_t)(wm * 16 * TM + 4 * fg) * 4u;
+  f.fsb = (uint32_t)(BM + BN) * 128u + (uint32_t)(Cfg::SAC * 64 + rb0) * 4u;
+
+  v4f acc[TM][TNW];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+#define TG_LAT_STEP(S, KB)                                                                                 \
+  lat_step<Cfg>(ld, f, acc, lat_pick<S>(st0, st1, st2, st3, st4, st5),                                  \
+                lat_pick<((S) + NST - 1) % NST>(st0, st1, st2, st3, st4, st5), (KB) + NST - 1)
+  lat_issue<Cfg>(ld, st0, 0);
+  lat_issue<Cfg>(ld, st1, 1);
+  if constexpr (NST > 3) lat_issue<Cfg>(ld, st2, 2);
+  if constexpr (NST > 4) lat_issue<Cfg>(ld, st3, 3);
+  if constexpr (NST > 5) lat_issue<Cfg>(ld, st4, 4);
+  int kb = 0;
+  for (; kb + NST <= nkb; kb += NST) {
+    TG_LAT_STEP(0, kb);
+    TG_LAT_STEP(1, kb + 1);
+    TG_LAT_STEP(2, kb + 2);
+    if constexpr (NST > 3) TG_LAT_STEP(3, kb + 3);
+    if constexpr (NST > 4) TG_LAT_STEP(4, kb + 4);
+    if constexpr (NST > 5) TG_LAT_STEP(5, kb + 5);
+  }
+  if (kb < nkb) {
+    TG_LAT_STEP(0, kb);
+    if (kb + 1 < nkb) {
+      TG_LAT_STEP(1, kb + 1);
+      if constexpr (NST > 3) if (kb + 2 < nkb) {
+        TG_LAT_STEP(2, kb + 2);
+        if constexpr (NST > 4) if (kb + 3 < nkb) {
+          TG_LAT_STEP(3, kb + 3);
+          if constexpr (NST > 5) if (kb + 4 < nkb) TG_LAT_STEP(4, kb + 4);
+        }
+      }
+    }
+  }
+#undef TG_LAT_STEP
+
+  // ---- epilogue: lane holds rows 4 * fg + r, column fr of each 16 x 16 tile ----
+  const int mw = m0 + wm * 16 * TM, nw = n0 + wn * 16 * TNW;
+  if (!OUT_F32 && vec_out) {
+    // every copy has landed (the last ones read zero) and every wave is done
+    // with the stages before they hold results
+    __builtin_amdgcn_s_waitcnt(0x0070 | 0x0F00);    // vmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    const int so = wave % NST;
+    uint8_t* wb = (so == 0 ? st0 : so == 1 ? st1 : so == 2 ? st2 : so == 3 ? st3 : so == 4 ? st4 : st5) +
+                  (wave / NST) * 64 * Cfg::RP;
+    lds_u8* wl = (lds_u8*)wb;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TNW; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          *(__attribute__((address_space(3))) __bf16*)(wl + (16 * i + 4 * fg + r) * Cfg::RP + (16 * j + fr) * 2) =
+              (__bf16)acc[i][j][r];
+    // a wave reads back only what it wrote; LDS completes a wave's accesses in order
+    constexpr int CPR = 2 * TNW;                    // 16-byte pieces per row
+#pragma unroll
+    for (int u = 0; u < CPR; ++u) {
+      const int idx = lane + 64 * u, row = idx / CPR, ch = idx % CPR;
+      const u32x4_t v = lat_ld16(wl + row * Cfg::RP + ch * 16);
+      const int m = mw + row, n = nw + ch * 8;
+      if (m < M && n < N)
+        *reinterpret_cast<u32x4_t*>(reinterpret_cast<__bf16*>(C) + (int64_t)m * N + n) = v;
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) {
+      const int n = nw + j * 16 + fr;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = mw + i * 16 + 4 * fg + r;
+        if (m < M && n < N) {
+          if (OUT_F32)
+            reinterpret_cast<float*>(C)[(int64_t)m * N + n] = acc[i][j][r];
+          else
+            reinterpret_cast<__bf16*>(C)[(int64_t)m * N + n] = (__bf16)acc[i][j][r];
+        }
+      }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Large-tile kernel: workgroup tile 256 x 256 x 128, 8 waves (4 along M x 2
 // along N), wave tile 64 x 128.  Operands travel HBM -> LDS with
@@ -198,8 +516,6 @@ __global__ __launch_bounds__(256, 2) void gemm_fp8_nt_kernel(
 // one stage from the fragment reads of the other and it puts no wait
 // between them.
 // ---------------------------------------------------------------------------
-template <int V> using IntC = std::integral_constant<int, V>;
-
 // The compiler lays out LDS objects by size, then by name.  A DS read's
 // immediate offset is 16 bits, so reads of an object past 64 KiB cost an
 // address add each; the B stages, read twice as often as the A stages, sort
@@ -761,10 +1077,71 @@ static int launch_gemm_cfg(const uint8_t* a_q, const float* a_s, const uint8_t* 
   return check_launch("gemm_fp8_nt");
 }
 
+#ifndef TG_LAT_WN
+#define TG_LAT_WN 4
+#endif
+template <int TN, bool SKM>
+static int launch_gemm_lat(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s,
+                           int b_scale_bn, void* c, bool f32, int M, int N, int K, hipStream_t st) {
+  constexpr int BM = 128, BN = 32 * TN, WN = TG_LAT_WN;
+  if constexpr ((2 * TN) % WN != 0) {
+    return einval("gemm_fp8_lat: tile width not split over the waves");
+  } else {
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int vec = !f32 && N % 8 == 0 && aligned(c, 16);
+  const dim3 grid((unsigned)(tiles_m * tiles_n));
+#define TG_LAT(BNS, F32)                                                                                    \
+  hipLaunchKernelGGL((gemm_fp8_lat_kernel<TN, WN, BNS, F32, SKM>), grid, dim3(128 * WN), 0, st, a_q, a_s, b_q, \
+                     b_s, c, M, N, K, tiles_m, tiles_n, vec)
+  if (b_scale_bn == 1) {
+    if (f32) TG_LAT(1, true); else TG_LAT(1, false);
+  } else {
+    if (f32) TG_LAT(128, true); else TG_LAT(128, false);
+  }
+#undef TG_LAT
+  return check_launch("gemm_fp8_lat");
+  }
+}
+
+// Build-time choice of the short-K kernel (0: the VGPR-staged 128-row kernel
+// for every launch below 128 tiles of 256).
+#ifndef TG_GEMM_LAT
+#define TG_GEMM_LAT 1
+#endif
+static bool lat_kernel_enabled() { return TG_GEMM_LAT != 0; }
+
+// The short-K kernel's tile width: 192, 128, 96 or 64 columns, whichever
+// leaves the busiest CU the least work, counted as workgroups per CU (one
+// fits a CU) times (columns + 48), the 48 standing for a tile's fixed cost
+// (pipeline fill, epilogue).  C1's 2048 x 3072: 256 tiles of 192, one per CU.
+static int lat_tile_n(int m, int n) {
+  const int64_t cus = device_cus() > 0 ? device_cus() : 1;
+  int best = 6;
+  int64_t best_cost = -1;
+  for (int tn : {6, 4, 3, 2}) {
+    if ((2 * tn) % TG_LAT_WN) continue;               // the wave split needs whole 16-column tiles
+    const int64_t tiles = (int64_t)((m + 127) / 128) * ((n + 32 * tn - 1) / (32 * tn));
+    const int64_t cost = (tiles + cus - 1) / cus * (32 * tn + 48);
+    if (best_cost < 0 || cost < best_cost) {
+      best = tn;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 template <bool SKM>
 static int launch_gemm_fp8_layout(const uint8_t* a_q, const float* a_s, const uint8_t* b_q,
                                   const float* b_s, int b_scale_bn, void* c, bool f32, int m, int n,
-                                  int k, bool big, hipStream_t st) {
+                                  int k, bool big, bool lat, hipStream_t st) {
+  if (lat) {
+    switch (lat_tile_n(m, n)) {
+      case 6: return launch_gemm_lat<6, SKM>(a_q, a_s, b_q, b_s, b_scale_bn, c, f32, m, n, k, st);
+      case 4: return launch_gemm_lat<4, SKM>(a_q, a_s, b_q, b_s, b_scale_bn, c, f32, m, n, k, st);
+      case 3: return launch_gemm_lat<3, SKM>(a_q, a_s, b_q, b_s, b_scale_bn, c, f32, m, n, k, st);
+      default: return launch_gemm_lat<2, SKM>(a_q, a_s, b_q, b_s, b_scale_bn, c, f32, m, n, k, st);
+    }
+  }
   if (big) {
     if (b_scale_bn == 1)
       return f32 ? launch_gemm_256<1, true, SKM>(a_q, a_s, b_q, b_s, c, m, n, k, st)
@@ -803,8 +1180,10 @@ int launch_gemm_fp8(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, co
   // 256 x 256 tiles once they fill the chip (>= 128 workgroups), else 128 x 128
   const bool fits32 = (uint64_t)M * (uint64_t)K < (1ull << 31) && (uint64_t)N * (uint64_t)K < (1ull << 31);
   const bool big = fits32 && ((M + 255) / 256) * ((N + 255) / 256) >= 128;
-  return skm ? launch_gemm_fp8_layout<true>(a_q, a_s, b_q, b_s, b_scale_bn, c, f32, m, n, k, big, st)
-             : launch_gemm_fp8_layout<false>(a_q, a_s, b_q, b_s, b_scale_bn, c, f32, m, n, k, big, st);
+  // below that, the short-K ring kernel (32-bit buffer offsets, as the 256 kernel)
+  const bool lat = fits32 && !big && lat_kernel_enabled();
+  return skm ? launch_gemm_fp8_layout<true>(a_q, a_s, b_q, b_s, b_scale_bn, c, f32, m, n, k, big, lat, st)
+             : launch_gemm_fp8_layout<false>(a_q, a_s, b_q, b_s, b_scale_bn, c, f32, m, n, k, big, lat, st);
 }
 
 // ---------------------------------------------------------------------------
