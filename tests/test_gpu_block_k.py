@@ -90,6 +90,26 @@ def test_quantize_transposed_bit_exact(dev, block_k):
     assert same_scales(s.cpu().numpy(), so)
 
 
+@pytest.mark.parametrize("block_k,R,C,transpose", [(512, 5, 1024, False), (64, 37, 1536, False), (16, 3, 2000, False),
+                                                   (1024, 2048, 72, True), (512, 1024, 136, True),
+                                                   (16, 96, 1000, True), (256, 512, 64, True)])
+def test_quantize_wide_blocks_and_ragged_tiles_bit_exact(dev, block_k, R, C, transpose):
+    """The wave-cooperative quantizers at their limits: rows with 64 lanes per
+    block (512) and chunk counts that end mid-workgroup; columns with the
+    largest LDS tile (1024 rows), a last tile of 8 / 40 columns, and one
+    exactly 64 wide."""
+    rng = np.random.default_rng(block_k * 7 + R + C)
+    x = _specials_bf16(ob.randn_bf16(rng, (R, C)))
+    if transpose:
+        x[:, 5] = 0                                          # an all-zero column block
+        x[7, 9] = 0x7F80                                     # +inf inside a column block
+    q, s = fp8.quantize_fp8(to_dev(x, dev), block_k, transpose=transpose)
+    xf = ob.bf16_to_f32(x)
+    qo, so = fp8_ref.quantize_fp8(np.ascontiguousarray(xf.T) if transpose else xf, block_k)
+    np.testing.assert_array_equal(u8(q), qo)
+    assert same_scales(s.cpu().numpy(), so)
+
+
 def _gemm(qa, sa, qb, sb, dev, bn=1, out=torch.bfloat16):
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
     return fp8.scaled_matmul(t(qa), t(sa), t(qb), t(sb), b_scale_bn=bn, out_dtype=out)

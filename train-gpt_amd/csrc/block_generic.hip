@@ -12,9 +12,13 @@
 // chain in k order (which rounds once the block's products span more than
 // f32's 24 bits) and adds it as acc = fma(P, sa * sb, acc) in block order
 // (fp8.py:70-76), in f32 on the VALU.
-// They are correct for every block size, not tuned: one thread per block in
-// the quantizers (16-byte loads / stores where bk % 16 == 0), a 64 x 64
-// LDS-tiled VALU GEMM.
+// The quantizers: for bf16 x with bk % 16 == 0 one lane per 16-byte chunk
+// (rows, bk <= 512) and LDS-transposed tiles (columns, bk <= 1024); otherwise
+// one thread per block.  The GEMM for sizes the tuned kernels cannot take
+// (block sizes not a multiple or divisor of 128) is a 64 x 64 LDS-tiled VALU
+// GEMM.
+#include <mutex>
+
 #include "tg_device.h"
 #include "tg_host.h"
 
@@ -32,6 +36,14 @@ __device__ __forceinline__ uint8_t gb_quant1(float x, float s, bool finite_scale
 
 __device__ __forceinline__ bool gb_finite(float s) { return (__float_as_uint(s) & 0x7F800000u) != 0x7F800000u; }
 
+// Index of scale copy t of block b of output row r (srep copies per block):
+// row-major (r, b * srep + t), or K-block-major (b * srep + t, r) with skm,
+// the layout of the tuned GEMM's _km entry points.
+__device__ __forceinline__ int64_t gb_sidx(bool skm, int64_t r, int64_t b, int t, int64_t nrows, int64_t nb,
+                                           int srep) {
+  return skm ? (b * srep + t) * nrows + r : (r * nb + b) * srep + t;
+}
+
 // one thread per (row, block): q (rows, cols * pf), s (rows, cols / bk * srep).
 // Two layouts for the tuned GEMM: each block's scale written srep times
 // (srep = bk / 128: 128-wide blocks that share their scale), or each block's
@@ -40,7 +52,7 @@ __device__ __forceinline__ bool gb_finite(float s) { return (__float_as_uint(s) 
 template <bool F32_IN>
 __global__ __launch_bounds__(256) void quant_rows_gb_kernel(const void* __restrict__ x, int64_t rows,
                                                             int64_t cols, int bk, uint8_t* __restrict__ q,
-                                                            float* __restrict__ s, int srep, int pf) {
+                                                            float* __restrict__ s, int srep, int pf, bool skm) {
   const int64_t nb = cols / bk;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= rows * nb) return;
@@ -49,7 +61,7 @@ __global__ __launch_bounds__(256) void quant_rows_gb_kernel(const void* __restri
   uint32_t m = 0;
   for (int k = 0; k < bk; ++k) m = max(m, __float_as_uint(gb_load(x, base + k, F32_IN)) & 0x7FFFFFFFu);
   const float sc = block_scale(m);
-  for (int t = 0; t < srep; ++t) s[i * srep + t] = sc;
+  for (int t = 0; t < srep; ++t) s[gb_sidx(skm, r, b, t, rows, nb, srep)] = sc;
   const bool fin = gb_finite(sc);
   uint8_t* qo = q + base * pf;
   for (int k = 0; k < bk; ++k) qo[k] = gb_quant1(gb_load(x, base + k, F32_IN), sc, fin);
@@ -73,7 +85,7 @@ __device__ __forceinline__ uint32_t bf16_amax2(uint32_t w) {
 // and stores (a thread's block is contiguous in x and in q).
 __global__ __launch_bounds__(256) void quant_rows_gb16_kernel(const uint16_t* __restrict__ x, int64_t rows,
                                                               int64_t cols, int bk, uint8_t* __restrict__ q,
-                                                              float* __restrict__ s, int srep, int pf) {
+                                                              float* __restrict__ s, int srep, int pf, bool skm) {
   const int64_t nb = cols / bk;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= rows * nb) return;
@@ -86,7 +98,7 @@ __global__ __launch_bounds__(256) void quant_rows_gb16_kernel(const uint16_t* __
     m = max(max(max(m, bf16_amax2(v.x)), bf16_amax2(v.y)), max(bf16_amax2(v.z), bf16_amax2(v.w)));
   }
   const float sc = block_scale(m);
-  for (int t = 0; t < srep; ++t) s[i * srep + t] = sc;
+  for (int t = 0; t < srep; ++t) s[gb_sidx(skm, r, b, t, rows, nb, srep)] = sc;
   const bool fin = gb_finite(sc);
   uint4* qo = reinterpret_cast<uint4*>(q + base * pf);
   for (int k = 0; k < bk / 16; ++k) {
@@ -103,7 +115,7 @@ __global__ __launch_bounds__(256) void quant_rows_gb16_kernel(const uint16_t* __
 template <bool VEC, bool F32_IN>
 __global__ __launch_bounds__(256) void quant_cols_gb_kernel(const void* __restrict__ x, int64_t R, int64_t C,
                                                             int bk, uint8_t* __restrict__ qt,
-                                                            float* __restrict__ st, int srep, int pf) {
+                                                            float* __restrict__ st, int srep, int pf, bool skm) {
   const int64_t nb = R / bk;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= nb * C) return;
@@ -113,7 +125,7 @@ __global__ __launch_bounds__(256) void quant_cols_gb_kernel(const void* __restri
   uint32_t m = 0;
   for (int k = 0; k < bk; ++k) m = max(m, __float_as_uint(xf(k)) & 0x7FFFFFFFu);
   const float sc = block_scale(m);
-  for (int t = 0; t < srep; ++t) st[(c * nb + b) * srep + t] = sc;
+  for (int t = 0; t < srep; ++t) st[gb_sidx(skm, c, b, t, C, nb, srep)] = sc;
   const bool fin = gb_finite(sc);
   uint8_t* qo = qt + (c * R + r0) * pf;
   if (VEC) {   // bk % 16 == 0, q_t 16-byte aligned: a thread's bytes in 16-byte stores
@@ -130,6 +142,94 @@ __global__ __launch_bounds__(256) void quant_cols_gb_kernel(const void* __restri
   }
   for (int k = 0; k < bk; ++k) qo[k] = gb_quant1(xf(k), sc, fin);
   for (int k = bk; k < bk * pf; ++k) qo[k] = 0;
+}
+
+// Wave-cooperative forms of the two quantizers for bf16 x and bk % 16 == 0,
+// with the bytes and scales of the one-thread-per-block kernels above (same
+// scale and quotient functions).
+//
+// Rows, bk <= 512: one 16-byte chunk (8 elements) per lane; the L = bk / 8
+// lanes of a block are an aligned lane group (a block's first chunk index is
+// a multiple of L, since cols % bk == 0), which reduces the block's amax by
+// xor shuffles.  Each lane stores its 8 bytes, and the zeros of its column
+// of the block's 128-byte slot when pf > 1.
+template <int L>
+__global__ __launch_bounds__(256) void quant_rows_gbw_kernel(const uint16_t* __restrict__ x, int64_t nchunks,
+                                                             int64_t cols, int bk, uint8_t* __restrict__ q,
+                                                             float* __restrict__ s, int srep, int pf, bool skm) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const bool in = i < nchunks;                       // whole lane groups are in or out
+  const uint4 v = in ? *reinterpret_cast<const uint4*>(x + i * 8) : make_uint4(0u, 0u, 0u, 0u);
+  uint32_t m = max(max(bf16_amax2(v.x), bf16_amax2(v.y)), max(bf16_amax2(v.z), bf16_amax2(v.w)));
+#pragma unroll
+  for (int o = L / 2; o >= 1; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o));
+  if (!in) return;
+  const float sc = block_scale(m);
+  const int64_t e = i * 8, r = e / cols, col = e - r * cols, b = col / bk, within = col - b * bk;
+  if (within == 0)
+    for (int t = 0; t < srep; ++t) s[gb_sidx(skm, r, b, t, nchunks * 8 / cols, cols / bk, srep)] = sc;
+  const bool fin = gb_finite(sc);
+  uint8_t* qo = q + (r * cols + b * bk) * pf + within;
+  *reinterpret_cast<uint2*>(qo) = make_uint2(gb_quant4_bf16(v.x, v.y, sc, fin), gb_quant4_bf16(v.z, v.w, sc, fin));
+  for (int j = 1; j < pf; ++j) *reinterpret_cast<uint2*>(qo + j * bk) = make_uint2(0u, 0u);
+}
+
+// Columns (x.T along R), bk <= 1024: a workgroup takes one row block (bk rows)
+// x 64 columns.  It copies the tile to LDS with coalesced 16-byte loads (row
+// pitch 144 B) and keeps per-thread column maxima, reduces them to the 64
+// column scales, then each lane quantizes its column's bytes 16 rows at a time
+// from LDS and stores them as 16-byte pieces of q_t's row.
+constexpr int kGbtPitch = 64 * 2 + 16;
+__global__ __launch_bounds__(256) void quant_cols_gbt_kernel(const uint16_t* __restrict__ x, int64_t R, int64_t C,
+                                                             int bk, uint8_t* __restrict__ qt,
+                                                             float* __restrict__ st, int srep, int pf, bool skm) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t gbt_lds[];
+  uint32_t* pam = reinterpret_cast<uint32_t*>(gbt_lds + (size_t)bk * kGbtPitch);   // [32][64] partial maxima
+  __shared__ float scol[64];
+  const int tid = threadIdx.x, ch = tid & 7, rg = tid >> 3;
+  const int64_t c0 = (int64_t)blockIdx.x * 64, r0 = (int64_t)blockIdx.y * bk;
+  const bool cin = c0 + ch * 8 < C;                   // C % 8 == 0: a chunk is in or out
+  uint32_t m[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+  for (int r = rg; r < bk; r += 32) {
+    const uint4 v = cin ? *reinterpret_cast<const uint4*>(x + (r0 + r) * C + c0 + ch * 8) : make_uint4(0u, 0u, 0u, 0u);
+    *reinterpret_cast<uint4*>(gbt_lds + r * kGbtPitch + ch * 16) = v;
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      m[2 * k] = max(m[2 * k], (w[k] << 16) & 0x7FFFFFFFu);
+      m[2 * k + 1] = max(m[2 * k + 1], w[k] & 0x7FFF0000u);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) pam[rg * 64 + ch * 8 + k] = m[k];
+  __syncthreads();
+  const int64_t nb = R / bk, b = blockIdx.y;
+  if (tid < 64) {
+    uint32_t a = 0u;
+    for (int g = 0; g < 32; ++g) a = max(a, pam[g * 64 + tid]);
+    const float sc = block_scale(a);
+    scol[tid] = sc;
+    if (c0 + tid < C)
+      for (int t = 0; t < srep; ++t) st[gb_sidx(skm, c0 + tid, b, t, C, nb, srep)] = sc;
+  }
+  __syncthreads();
+  const int lane = tid & 63, wv = tid >> 6;
+  const int64_t c = c0 + lane;
+  if (c >= C) return;
+  const float sc = scol[lane];
+  const bool fin = gb_finite(sc);
+  uint8_t* qo = qt + (c * R + r0) * pf;
+  for (int p = wv; p < bk / 16; p += 4) {
+    float f[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      f[k] = __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(gbt_lds + (p * 16 + k) * kGbtPitch +
+                                                                          lane * 2) << 16);
+    *reinterpret_cast<uint4*>(qo + p * 16) =
+        make_uint4(gb_quant4(f[0], f[1], f[2], f[3], sc, fin), gb_quant4(f[4], f[5], f[6], f[7], sc, fin),
+                   gb_quant4(f[8], f[9], f[10], f[11], sc, fin), gb_quant4(f[12], f[13], f[14], f[15], sc, fin));
+  }
+  for (int p = bk / 16 + wv; p < bk * pf / 16; p += 4) *reinterpret_cast<uint4*>(qo + p * 16) = make_uint4(0u, 0u, 0u, 0u);
 }
 
 // C (M, N) = sum over K blocks b of (A_b . B_b^T) * sa[m][b] * sb[n / bn][b];
@@ -222,31 +322,69 @@ __global__ __launch_bounds__(256) void gemm_gb_kernel(const uint8_t* __restrict_
 static unsigned gb_grid(int64_t threads) { return (unsigned)((threads + 255) / 256); }
 
 int launch_quant_rows_gb(const void* x, int x_dtype, int64_t rows, int64_t cols, int bk, uint8_t* q, float* s,
-                         hipStream_t st, int srep, int pf) {
+                         hipStream_t st, int srep, int pf, bool skm) {
   const int64_t n = rows * (cols / bk);
   if (n == 0) return TG_OK;
   if (n / 256 >= 0x7FFFFFFF) return einval("quantize_rows: too many blocks");
   const bool vec = bk % 16 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 15) == 0;
-  if (x_dtype != TG_DTYPE_F32 && vec)
+  if (x_dtype != TG_DTYPE_F32 && vec && bk <= 512 && (bk & (bk - 1)) == 0) {
+    const int64_t nchunks = rows * cols / 8;
+    if (nchunks / 256 >= 0x7FFFFFFF) return einval("quantize_rows: too many blocks");
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(gb_grid(nchunks)), dim3(256), 0, st, reinterpret_cast<const uint16_t*>(x),
+                         nchunks, cols, bk, q, s, srep, pf, skm);
+    };
+    switch (bk) {
+      case 16: go(quant_rows_gbw_kernel<2>); break;
+      case 32: go(quant_rows_gbw_kernel<4>); break;
+      case 64: go(quant_rows_gbw_kernel<8>); break;
+      case 128: go(quant_rows_gbw_kernel<16>); break;
+      case 256: go(quant_rows_gbw_kernel<32>); break;
+      default: go(quant_rows_gbw_kernel<64>); break;
+    }
+  } else if (x_dtype != TG_DTYPE_F32 && vec)
     hipLaunchKernelGGL(quant_rows_gb16_kernel, dim3(gb_grid(n)), dim3(256), 0, st,
-                       reinterpret_cast<const uint16_t*>(x), rows, cols, bk, q, s, srep, pf);
+                       reinterpret_cast<const uint16_t*>(x), rows, cols, bk, q, s, srep, pf, skm);
   else if (x_dtype == TG_DTYPE_F32)
     hipLaunchKernelGGL(quant_rows_gb_kernel<true>, dim3(gb_grid(n)), dim3(256), 0, st, x, rows, cols, bk, q, s,
-                       srep, pf);
+                       srep, pf, skm);
   else
     hipLaunchKernelGGL(quant_rows_gb_kernel<false>, dim3(gb_grid(n)), dim3(256), 0, st, x, rows, cols, bk, q, s,
-                       srep, pf);
+                       srep, pf, skm);
   return check_launch("quantize_rows (block_k != 128)");
 }
 
 int launch_quant_cols_gb(const void* x, bool x_f32, int64_t rows, int64_t cols, int bk, uint8_t* q_t,
-                         float* s_t, hipStream_t st, int srep, int pf) {
+                         float* s_t, hipStream_t st, int srep, int pf, bool skm) {
   const int64_t n = (rows / bk) * cols;
   if (n == 0) return TG_OK;
   if (n / 256 >= 0x7FFFFFFF) return einval("quantize_cols: too many blocks");
   const bool vec = bk % 16 == 0 && ((uintptr_t)q_t & 15) == 0;
+  if (!x_f32 && vec && bk <= 1024 && cols % 8 == 0 && ((uintptr_t)x & 15) == 0 && (cols + 63) / 64 <= 0x7FFFFFFF &&
+      rows / bk <= 65535) {
+    const size_t lds = (size_t)bk * kGbtPitch + 32 * 64 * 4;
+    // the dynamic-LDS limit is a per-device function attribute: set once per
+    // device, for the largest tile (bk = 1024)
+    constexpr int kMaxDev = 64;
+    static std::once_flag once[kMaxDev];
+    static hipError_t attr_rc[kMaxDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) dev = 0;
+    std::call_once(once[dev], [&] {
+      attr_rc[dev] = hipFuncSetAttribute(reinterpret_cast<const void*>(quant_cols_gbt_kernel),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)((size_t)1024 * kGbtPitch + 32 * 64 * 4));
+    });
+    if (attr_rc[dev] != hipSuccess) {
+      set_error("quantize_cols (set LDS size): %s", hipGetErrorString(attr_rc[dev]));
+      return TG_EHIP;
+    }
+    hipLaunchKernelGGL(quant_cols_gbt_kernel, dim3((unsigned)((cols + 63) / 64), (unsigned)(rows / bk)), dim3(256),
+                       lds, st, reinterpret_cast<const uint16_t*>(x), rows, cols, bk, q_t, s_t, srep, pf, skm);
+    return check_launch("quantize_cols (general, transposed tile)");
+  }
   auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(gb_grid(n)), dim3(256), 0, st, x, rows, cols, bk, q_t, s_t, srep, pf);
+    hipLaunchKernelGGL(kern, dim3(gb_grid(n)), dim3(256), 0, st, x, rows, cols, bk, q_t, s_t, srep, pf, skm);
   };
   if (x_f32) {
     if (vec) go(quant_cols_gb_kernel<true, true>); else go(quant_cols_gb_kernel<false, true>);

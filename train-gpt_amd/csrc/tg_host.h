@@ -71,15 +71,16 @@ int launch_quant_dual_pair(const void* x0, int64_t rows0, int64_t cols0, uint8_t
 int launch_gemm_fp8(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s,
                     int b_scale_bn, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
                     hipStream_t st, bool skm = false);
-// The general path for block_k != 128 (block_generic.hip): row-major scales,
-// any block_k >= 1 dividing the contracted extent.
+// The general path for block_k != 128 (block_generic.hip): row-major scales
+// (K-block-major with skm), any block_k >= 1 dividing the contracted extent.
 // For the tuned GEMM: srep = bk / 128 writes each block's scale srep times;
 // pf = 128 / bk puts each block at the start of a zero-filled 128-byte slot
 // (q rows of cols * pf bytes).
+// skm: scales K-block-major ((block, slot) x rows, the _km GEMMs' layout).
 int launch_quant_rows_gb(const void* x, int x_dtype, int64_t rows, int64_t cols, int bk, uint8_t* q, float* s,
-                         hipStream_t st, int srep = 1, int pf = 1);
+                         hipStream_t st, int srep = 1, int pf = 1, bool skm = false);
 int launch_quant_cols_gb(const void* x, bool x_f32, int64_t rows, int64_t cols, int bk, uint8_t* q_t,
-                         float* s_t, hipStream_t st, int srep = 1, int pf = 1);
+                         float* s_t, hipStream_t st, int srep = 1, int pf = 1, bool skm = false);
 int launch_gemm_gb(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s, int bn, void* c,
                    int c_dtype, int64_t M, int64_t N, int64_t K, int bk, hipStream_t st);
 
