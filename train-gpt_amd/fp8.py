@@ -38,9 +38,10 @@ BACKWARD_MODE = "fp8"
 
 # block_k = 128 runs the tuned kernels (one scale block per pair of FP8 MFMA K
 # steps); any other block size dividing K runs the library's general
-# block-size kernels (correct for every block size, not tuned).  The fused
-# paths that exist only for 128 (the one-read dual quantizers, the kept FP8
-# residuals, relu^2 quantization) are taken only at 128.
+# block-size quantizers, then the tuned GEMM for multiples and divisors (>= 16)
+# of 128 and a VALU GEMM for the rest.  The fused paths that exist only for
+# 128 (the one-read dual quantizers, the kept FP8 residuals, relu^2
+# quantization) are taken only at 128.
 TUNED_BLOCK_K = 128
 
 
