@@ -216,9 +216,15 @@ def test_quantize_deterministic(dev):
     assert torch.equal(q1.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(s1, s2)
 
 
-def test_weight_128x128(dev):
-    rng = np.random.default_rng(4)
-    w = ob.randn_bf16(rng, (512, 300), std=0.02)
+@pytest.mark.parametrize("K,N", [(512, 300), (256, 384)])
+def test_weight_128x128(dev, K, N):
+    """Both load paths of the tile quantizer: element loads (N % 8 != 0) and
+    16-byte loads, with a NaN tile, an inf tile and an all-zero tile."""
+    rng = np.random.default_rng(4 + N)
+    w = ob.randn_bf16(rng, (K, N), std=0.02)
+    w[3, 5] = 0x7FC0                         # NaN in tile (0, 0)
+    w[130, 200] = 0xFF80                     # -inf in tile (1, 1)
+    w[128:256, 256:] = 0                     # tile (1, 2): all zero (scale floor)
     wq, ws, bn = fp8.quantize_weight(to_dev(w, dev), layout="128x128")
     assert bn == 128
     qo, so = fp8_ref.quantize_weight_128x128(np.ascontiguousarray(ob.bf16_to_f32(w).T))

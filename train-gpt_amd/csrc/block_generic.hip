@@ -77,9 +77,6 @@ __device__ __forceinline__ uint32_t gb_quant4(float a, float b, float c, float d
 __device__ __forceinline__ uint32_t gb_quant4_bf16(uint32_t lo, uint32_t hi, float s, bool fin) {
   return gb_quant4(bf16lo(lo), bf16hi(lo), bf16lo(hi), bf16hi(hi), s, fin);
 }
-__device__ __forceinline__ uint32_t bf16_amax2(uint32_t w) {
-  return max((w << 16) & 0x7FFFFFFFu, w & 0x7FFF0000u);
-}
 
 // The same for bf16 x, bk % 16 == 0, x and q 16-byte aligned: 16-byte loads
 // and stores (a thread's block is contiguous in x and in q).

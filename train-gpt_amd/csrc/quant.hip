@@ -274,18 +274,38 @@ int launch_quant_rows_cols(const void* a, int64_t M, int64_t K, uint8_t* qa, flo
 
 // ---------------------------------------------------------------------------
 // 128x128-tile weight quantization (offline weight preparation for the GEMV).
-// One workgroup per tile: pass 1 finds the tile amax, pass 2 writes w.T bytes.
+// One workgroup per tile: the tile (128 rows of K x 128 columns of N, bf16)
+// is copied to LDS with 16-byte loads while each thread keeps its maximum;
+// the tile amax gives the scale; then thread (column c, half h) quantizes
+// rows 64h .. 64h+63 of column c from LDS (a wave reads 64 consecutive
+// columns of one row, 128 B) and stores them as 4 x 16 bytes of w.T's row c.
 // ---------------------------------------------------------------------------
+constexpr int kW128Pitch = 128 * 2 + 16;
 __global__ __launch_bounds__(256) void quant_w128_kernel(const uint16_t* __restrict__ w, int64_t K,
                                                          int64_t N, uint8_t* __restrict__ wq,
-                                                         float* __restrict__ ws) {
+                                                         float* __restrict__ ws, int vec) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[128 * kW128Pitch];
   __shared__ uint32_t red[4];
   const int tid = threadIdx.x;
   const int64_t k0 = (int64_t)blockIdx.y * 128, n0 = (int64_t)blockIdx.x * 128;
+  const int ch = tid & 15, rr = tid >> 4;          // 16-byte chunk of a row, first row
+  const int64_t nc = n0 + ch * 8;
   uint32_t m = 0;
-  for (int e = tid; e < 128 * 128; e += 256) {
-    const int64_t k = k0 + (e >> 7), n = n0 + (e & 127);
-    if (n < N) m = max(m, ((uint32_t)w[k * N + n] << 16) & 0x7FFFFFFFu);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = rr + 16 * i;
+    const uint16_t* src = w + (k0 + r) * N + nc;
+    uint4 v;
+    if (vec && nc + 8 <= N) {
+      v = *reinterpret_cast<const uint4*>(src);
+    } else {                                       // N % 8 != 0, unaligned w, or the tile's ragged edge
+      uint32_t e[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) e[j] = nc + j < N ? (uint32_t)src[j] : 0u;
+      v = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+    }
+    *reinterpret_cast<uint4*>(tile + r * kW128Pitch + ch * 16) = v;
+    m = max(m, max(max(bf16_amax2(v.x), bf16_amax2(v.y)), max(bf16_amax2(v.z), bf16_amax2(v.w))));
   }
   for (int o = 32; o >= 1; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
   if ((tid & 63) == 0) red[tid >> 6] = m;
@@ -294,8 +314,8 @@ __global__ __launch_bounds__(256) void quant_w128_kernel(const uint16_t* __restr
   const float sc = block_scale_bf16(m);
   if (tid == 0) ws[blockIdx.x * (K >> 7) + blockIdx.y] = sc;
   Divider d(sc);
-  const int nl = tid >> 1, half = tid & 1;
-  const int64_t n = n0 + nl;
+  const int c = tid & 127, half = tid >> 7;
+  const int64_t n = n0 + c;
   if (n >= N) return;
   uint32_t out[16];
 #pragma unroll
@@ -303,7 +323,8 @@ __global__ __launch_bounds__(256) void quant_w128_kernel(const uint16_t* __restr
     float f[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      f[r] = __uint_as_float(((uint32_t)w[(k0 + half * 64 + 4 * i + r) * N + n]) << 16);
+      f[r] = __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(
+                                 tile + (half * 64 + 4 * i + r) * kW128Pitch + c * 2) << 16);
     if (d.fast)
       out[i] = e4m3x4(d.div(f[0]), d.div(f[1]), d.div(f[2]), d.div(f[3]));
     else
@@ -458,8 +479,9 @@ extern "C" int tg_quantize_weight_128x128(const void* w, int64_t K, int64_t N, u
   if (!w || !w_q || !w_s) return einval("quantize_weight_128x128: null pointer");
   if (!aligned(w_q, 16)) return einval("quantize_weight_128x128: w_q must be 16-byte aligned");
   dim3 grid((unsigned)((N + 127) / 128), (unsigned)(K / 128));
+  const int vec = N % 8 == 0 && aligned(w, 16);
   hipLaunchKernelGGL(quant_w128_kernel, grid, dim3(256), 0, as_stream(stream),
-                     reinterpret_cast<const uint16_t*>(w), K, N, w_q, w_s);
+                     reinterpret_cast<const uint16_t*>(w), K, N, w_q, w_s, vec);
   return check_launch("quant_w128");
 }
 

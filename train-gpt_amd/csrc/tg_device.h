@@ -116,6 +116,11 @@ __device__ __forceinline__ float block_scale_bf16(uint32_t amax_bits) {
   return (s < kScaleFloor) ? kScaleFloor : s;
 }
 
+// |x| bits (as f32 bits) of the larger-magnitude of the two bf16 values in w.
+__device__ __forceinline__ uint32_t bf16_amax2(uint32_t w) {
+  return max((w << 16) & 0x7FFFFFFFu, w & 0x7FFF0000u);
+}
+
 struct Divider {
   float s, y;
   bool fast;
