@@ -249,7 +249,8 @@ int tg_rms_norm_bwd_ex(const void* x, int x_dtype, const void* scale, int scale_
  * reference re-quantizes W every call at fp8.py:68):
  * out[m, n] = sum_kb x_s[m, kb] * w_s[n / w_scale_bn, kb] * sum_k x_q[m, k] * w_q[n, k]
  * x_q (M, K), x_s (M, K/128); w_q (N, K), w_s as b_s of tg_gemm_fp8_nt;
- * out (M, N) bf16.  Intended for M <= 64. */
+ * out (M, N) bf16.  M <= 64; 33-64 rows run tg_gemm_fp8_nt's kernel (one pass
+ * over W instead of two 32-row passes). */
 int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* w_q, const float* w_s,
                 int w_scale_bn, void* out, int64_t M, int64_t N, int64_t K, int block_k,
                 void* stream);
