@@ -50,8 +50,10 @@ __device__ __forceinline__ v4f mfma_bf16_16x16x32(const uint4& a, const uint4& b
 // the compiler's wait analysis merges paths at the loop header and drains
 // every outstanding copy there).  The barrier is a bare s_barrier (a fence
 // would wait for every outstanding copy).
-// LDS rows are 64 B, 16-byte chunk c of row r at c ^ ((r >> 2) & 3): the 16
-// rows of a fragment read fall in different banks.  Tiles are computed as
+// LDS rows are 64 B, 16-byte chunk c of row r at c ^ ((r >> 1) & 3): the
+// fragment reads (16 rows x 4 chunks per instruction) then run without bank
+// conflicts on gfx950 (measured: c ^ ((r >> 2) & 3) doubled every read's
+// LDS cycles).  Tiles are computed as
 // B . A^T so that a lane holds one output row and four consecutive columns
 // (8-byte bf16 pieces for the epilogue).
 // ---------------------------------------------------------------------------
@@ -250,14 +252,14 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_nt_q4_kernel(const __bf16* _
   c.rb = make_rsrc(B, (uint32_t)N * rowb);
   c.row16 = 16u * rowb;
   // DMA lane L lands at byte 16 L of its 1 KiB slot: row slot + L / 4,
-  // physical chunk L % 4, which holds logical chunk (L % 4) ^ ((L >> 4) & 3)
+  // physical chunk L % 4, which holds logical chunk (L % 4) ^ ((L >> 3) & 3)
   const int lrow = c.wave * 64 + (lane >> 2);   // loader waves 0-3
-  const uint32_t lch = (uint32_t)((lane & 3) ^ ((lane >> 4) & 3)) * 16u;
+  const uint32_t lch = (uint32_t)((lane & 3) ^ ((lane >> 3) & 3)) * 16u;
   c.voa = (uint32_t)(m0 + lrow) * rowb + lch;
   c.vob = (uint32_t)(n0 + lrow) * rowb + lch;
   // fragment: lane (fr, fg) reads logical chunk fg (k 8fg .. 8fg+7) of row
-  // (wave tile row) + 16 t + fr, at physical chunk fg ^ ((fr >> 2) & 3)
-  const uint32_t ch = (uint32_t)(fg ^ ((fr >> 2) & 3)) * 16u;
+  // (wave tile row) + 16 t + fr, at physical chunk fg ^ ((fr >> 1) & 3)
+  const uint32_t ch = (uint32_t)(fg ^ ((fr >> 1) & 3)) * 16u;
   c.fa = (uint32_t)(wm * 64 + fr) * 64u + ch;
   c.fb = (uint32_t)(wn * 128 + fr) * 64u + ch;
 
