@@ -11,6 +11,19 @@
 // quant_cols_kernel), quantize them and store 128 contiguous bytes per
 // column.  The bytes and scales equal those of the two separate kernels.
 //
+// LDS banks (gfx950, measured with SQ_LDS_BANK_CONFLICT): a 32-bit access
+// serves 32 lanes at a time over 32 banks of 4 bytes; a 128-bit read serves
+// 16 lanes at a time over 64 banks.  Both swizzles below leave every LDS
+// instruction of the kernel free of bank conflicts:
+//  - raw tile: 32-bit word w of row r sits at r * 68 + (w ^ (8 * ((r >> 3) & 1))).
+//    The column reads take rows 4j + const for the four lanes j of a quad,
+//    and a pitch of 68 words alone puts j and j + 2 on the same banks; the
+//    xor moves rows 8-15 of every 16 by 8 banks.  The 16-byte row stores
+//    only permute whole chunks within the row.
+//  - transposed bytes: column n is 128 bytes at n * 32 words, its 16-byte
+//    chunk c at position c ^ ((n >> 1) & 7), so that the 8 column pairs a
+//    half-wave writes at once (one word each) land in 8 distinct chunks.
+//
 // ROWS = false gives the column quantization alone (tg_quantize_cols for
 // 16-byte-aligned rows); GUARD handles a last tile narrower than 128 columns.
 //
@@ -64,6 +77,9 @@ struct DualJobs {
   int nblk0;   // tiles of job 0; gridDim.x - nblk0 are job 1's
 };
 
+// Word offset of 16-byte chunk c of transposed column n (128 bytes per column).
+__device__ __forceinline__ int dual_tq_at(int n, int c) { return n * 32 + 4 * (c ^ ((n >> 1) & 7)); }
+
 // IO: the probe's variant.  Every load, LDS access and store of the product
 // kernel stays (same addresses, same order, same widths); the values stored
 // are bit mixes of the loaded words instead of e4m3 bytes and scales, and
@@ -72,7 +88,7 @@ struct DualJobs {
 template <bool ROWS, bool GUARD, bool IO = false, bool IO_SCALES = true>
 __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
   // the raw tile (row pitch 272 B); once every column is in registers the
-  // same memory stages the transposed bytes (column pitch 144 B)
+  // same memory stages the transposed bytes (column pitch 128 B)
   __shared__ uint32_t tile[128 * 68];
   __shared__ float sgather[2][128];   // skm: the tile's row and column scales
   uint32_t* tq = tile;
@@ -128,7 +144,7 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
         else s[(r0 + row) * (cols >> 7) + tx] = sc;
       }
     }
-    if (do_cols) *reinterpret_cast<uint4*>(&tile[row * 68 + ch * 4]) = v[u];
+    if (do_cols) *reinterpret_cast<uint4*>(&tile[row * 68 + ((ch * 4) ^ (8 * ((row >> 3) & 1)))]) = v[u];
   }
   const bool rows_gathered = kScales && do_rows && skm;
   if (!do_cols && !rows_gathered) return;
@@ -139,6 +155,7 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
   // columns: quad (tid >> 2) owns the column pair 2c, 2c + 1 (one 32-bit LDS
   // word per row); lane j of the quad holds rows 16i + 4j + r
   const int j = tid & 3, cp = tid >> 2;
+  const int cpw = cp ^ (8 * (j >> 1));   // the pair's word in rows 16i + 4j + r
   auto put_scale = [&](float sc, int n) {
     if (kScales && j == 0 && (!GUARD || c0 + n < cols)) {
       if (skm) sgather[1][n] = sc;
@@ -150,12 +167,12 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) wd[i * 4 + r] = tile[(16 * i + 4 * j + r) * 68 + cp];
+      for (int r = 0; r < 4; ++r) wd[i * 4 + r] = tile[(16 * i + 4 * j + r) * 68 + cpw];
     __syncthreads();   // every lane has read its columns: the tile becomes tq
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      tq[(2 * cp) * 36 + 4 * i + j] = wd[4 * i] ^ wd[4 * i + 1];
-      tq[(2 * cp + 1) * 36 + 4 * i + j] = wd[4 * i + 2] ^ wd[4 * i + 3];
+      tq[dual_tq_at(2 * cp, i) + j] = wd[4 * i] ^ wd[4 * i + 1];
+      tq[dual_tq_at(2 * cp + 1, i) + j] = wd[4 * i + 2] ^ wd[4 * i + 3];
     }
     put_scale(__uint_as_float(wd[0]), 2 * cp);
     put_scale(__uint_as_float(wd[1]), 2 * cp + 1);
@@ -165,7 +182,7 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const uint32_t w = tile[(16 * i + 4 * j + r) * 68 + cp];
+        const uint32_t w = tile[(16 * i + 4 * j + r) * 68 + cpw];
         f0[i * 4 + r] = __uint_as_float(w << 16);
         f1[i * 4 + r] = __uint_as_float(w & 0xFFFF0000u);
       }
@@ -190,7 +207,7 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
               (e4m3_nonfinite_scale(f[4 * i + 2], sc) << 16) |
               (e4m3_nonfinite_scale(f[4 * i + 3], sc) << 24);
         }
-        tq[n * 36 + 4 * i + j] = w;
+        tq[dual_tq_at(n, i) + j] = w;
       }
       put_scale(sc, n);
     };
@@ -208,7 +225,7 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
   for (int p = 0; p < 4; ++p) {
     const int n = (tid >> 3) + 32 * p, k = tid & 7;
     if (GUARD && c0 + n >= cols) continue;
-    const uint4 val = *reinterpret_cast<const uint4*>(&tq[n * 36 + 4 * k]);
+    const uint4 val = *reinterpret_cast<const uint4*>(&tq[dual_tq_at(n, k)]);
     *(reinterpret_cast<uint4*>(qt + (c0 + n) * rows + r0) + k) = val;
   }
   if (kScales && skm && tid >= 128 && (!GUARD || c0 + tid - 128 < cols))
