@@ -92,7 +92,30 @@ def build_probe(verbose: bool = False) -> str:
 
 
 FFI_SRC = os.path.join(CSRC, "ffi", "tg_xla_ffi.cc")
+FFI_CORE = os.path.join(CSRC, "ffi", "tg_ffi_core.h")
+FFI_CORE_SHIM = os.path.join(CSRC, "ffi", "tg_ffi_core_shim.cc")
 FFI_LIB = os.path.join(HERE, "libtg_xla_ffi.so")
+FFI_CORE_LIB = os.path.join(HERE, "libtg_ffi_core.so")
+CXX = os.environ.get("CXX", "g++")
+
+
+def build_ffi_core(verbose: bool = False) -> str:
+    """Compile the XLA FFI handlers' logic (csrc/ffi/tg_ffi_core.h) with its C-ABI
+    shim into libtg_ffi_core.so, linked against libtg_fp8.so.  Host code only
+    (the C ABI takes streams as void*), so the host compiler builds it; it needs
+    no jaxlib.  Test tooling: the tests run the handlers' checks, dispatch and
+    workspace handling through it; nothing in the package loads it."""
+    root = os.path.dirname(HERE)
+    tmp = FFI_CORE_LIB + ".tmp"
+    cmd = [CXX, "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-I", os.path.join(root, "include"),
+           FFI_CORE_SHIM, "-L", HERE, "-ltg_fp8", "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"FFI core shim failed to build:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, FFI_CORE_LIB)
+    if verbose:
+        print(f"built {FFI_CORE_LIB}")
+    return FFI_CORE_LIB
 
 
 def build_xla_ffi(verbose: bool = False):
@@ -123,5 +146,6 @@ def build_xla_ffi(verbose: bool = False):
 if __name__ == "__main__":
     build_library(verbose=True)
     build_probe(verbose=True)
+    build_ffi_core(verbose=True)
     build_xla_ffi(verbose=True)
     sys.exit(0)
