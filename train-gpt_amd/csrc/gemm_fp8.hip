@@ -53,8 +53,6 @@ __device__ __forceinline__ v8i as_v8i(const u32x4_t& lo, const u32x4_t& hi) {
   return r;
 }
 
-// Cache-policy operand of the raw buffer loads: nt (streaming, read once).
-constexpr int kAuxNT = 2;
 
 // SKM: scales K-block-major (see gemm_fp8_nt_256_kernel).
 template <int TM, int TN, int BNS, bool OUT_F32, bool SKM>

@@ -29,6 +29,8 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 }
 
 constexpr int kBufferWord3 = 0x00020000;   // gfx9 raw buffer: 32-bit data format
+// Cache-policy operand of the raw buffer loads: nt (streaming, read once).
+constexpr int kAuxNT = 2;
 
 // LDS row swizzle of the 256-tile kernels: 16-byte chunk c of row r is stored
 // at chunk position c ^ swz(r).  (r >> 1) & 7 spreads the 16 rows one

@@ -16,6 +16,7 @@
 // scales are written once.
 #include <type_traits>
 
+#include "gemm_tile.h"
 #include "row_ops.h"
 #include "tg_device.h"
 #include "tg_host.h"
@@ -153,7 +154,8 @@ static int launch_rmsnorm(const void* x, const void* gamma, void* y, uint8_t* q,
 // order and the workgroup writes one partial row (slice-major, see
 // kNormBwdSlice), which rmsnorm_bwd_reduce_sm adds up in a fixed order.
 // Both orders are fixed, so dscale is the same on every run.
-// GREG: gamma in registers (J <= 4); PF: prefetch the next row (J <= 4).
+// GREG: gamma in registers (J <= 4); PF: two rows' loads in flight per wave
+// (J <= 4).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float (&f)[8]) {
   f[0] = bf16lo(v.x); f[1] = bf16hi(v.x); f[2] = bf16lo(v.y); f[3] = bf16hi(v.y);
@@ -183,7 +185,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint4* __restric
                                                           float eps) {
   constexpr bool GREG = J <= 4, PF = J <= 4;
   extern __shared__ float colsum[];   // nch * 8 floats
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t wave0 = (int64_t)blockIdx.x * 4 + wave;
   const int64_t wstride = (int64_t)gridDim.x * 4;
 
@@ -202,27 +204,8 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint4* __restric
 #pragma unroll
     for (int e = 0; e < 8; ++e) dg[j][e] = 0.0f;
 
-  uint4 nx[J], nd[J];
-  auto load_row = [&](int64_t row) {
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int c = lane + 64 * j;
-      nx[j] = (FULL || c < nch) ? ldg_stream(x + row * nch + c) : make_uint4(0, 0, 0, 0);
-      nd[j] = (FULL || c < nch) ? ldg_stream(dy + row * nch + c) : make_uint4(0, 0, 0, 0);
-    }
-  };
-
-  if (PF && wave0 < rows) load_row(wave0);
-  for (int64_t row = wave0; row < rows; row += wstride) {
-    if (!PF) load_row(row);
-    float xf[J][8], d[J][8];
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      unpack_bf16x8(nx[j], xf[j]);
-      unpack_bf16x8(nd[j], d[j]);
-    }
-    if (PF && row + wstride < rows) load_row(row + wstride);
-
+  // the row's rnorm and mean(gs * normed) from its unpacked registers
+  auto row_stats = [&](const float (&xf)[J][8], const float (&d)[J][8], float& rn, float& dot) {
     double sq = 0.0;
     float gx = 0.0f;   // this lane's part of sum(gs * x)
 #pragma unroll
@@ -239,26 +222,108 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint4* __restric
     sq = wave_sum_f64(sq);
     const double gxs = wave_sum_f64((double)gx);
     const float var = (float)sq / dimf;
-    const float rn = (float)(1.0 / __builtin_sqrt((double)(var + eps)));
-    const float dot = rn * ((float)gxs / dimf);
+    rn = (float)(1.0 / __builtin_sqrt((double)(var + eps)));
+    dot = rn * ((float)gxs / dimf);
+  };
+  // dx chunk j of the row (bf16 x 8), and the row's dscale terms when it is real
+  auto row_out = [&](int j, const float (&xf)[J][8], const float (&d)[J][8], float rn, float dot, bool real) {
+    float gl[8];
+    if (!GREG) gamma_chunk(j, gl);
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float gm = GREG ? greg[GREG ? j : 0][e] : gl[e];
+      const float nrm = xf[j][e] * rn;
+      o[e] = rn * (d[j][e] * gm - nrm * dot);
+      const float t = __builtin_fmaf(d[j][e], nrm, dg[j][e]);
+      dg[j][e] = real ? t : dg[j][e];
+    }
+    u32x4_t ov;
+    ov.x = pack_bf16x2(o[0], o[1]); ov.y = pack_bf16x2(o[2], o[3]);
+    ov.z = pack_bf16x2(o[4], o[5]); ov.w = pack_bf16x2(o[6], o[7]);
+    return ov;
+  };
+  // Row loads and stores are raw buffer accesses over the row's own bytes:
+  // lanes past the row's end, and every lane of a row past the last, read
+  // zero and write nothing, without a memory access.
+  auto row_rsrc = [&](const uint4* base, int64_t row) {
+    const bool in = row < rows;
+    return make_rsrc(base + (in ? row : 0) * nch, in ? (uint32_t)nch * 16u : 0u);
+  };
 
+  if constexpr (PF) {
+    // Two rows' loads in flight per wave, and each row's dx held in registers
+    // and stored one row later, after the wait for the next row's loads: every
+    // access is unconditional (rows past the end are phantoms that touch no
+    // memory and add nothing to dscale), so the compiler's waits are for the
+    // loads consumed and never for the stores.  With the prefetch behind a
+    // branch it waited at the loop head for every outstanding access, the
+    // previous row's stores included.
+    u32x4_t bx[2][J], bd[2][J], pend[J];
+    int64_t pend_row = rows;   // none yet: its stores are dropped
+    auto load_slot = [&](auto slot, int64_t row) {
+      constexpr int S = decltype(slot)::value;
+      const __amdgpu_buffer_rsrc_t rx = row_rsrc(x, row), rd = row_rsrc(dy, row);
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int c = lane + 64 * j;
-      float gl[8];
-      if (!GREG) gamma_chunk(j, gl);
-      float o[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float gm = GREG ? greg[GREG ? j : 0][e] : gl[e];
-        const float nrm = xf[j][e] * rn;
-        o[e] = rn * (d[j][e] * gm - nrm * dot);
-        dg[j][e] = __builtin_fmaf(d[j][e], nrm, dg[j][e]);
+      for (int j = 0; j < J; ++j) {
+        const uint32_t off = (uint32_t)(lane + 64 * j) * 16u;
+        bx[S][j] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, kAuxNT);
+        bd[S][j] = __builtin_amdgcn_raw_buffer_load_b128(rd, off, 0, kAuxNT);
       }
-      uint4 ov;
-      ov.x = pack_bf16x2(o[0], o[1]); ov.y = pack_bf16x2(o[2], o[3]);
-      ov.z = pack_bf16x2(o[4], o[5]); ov.w = pack_bf16x2(o[6], o[7]);
-      if (FULL || c < nch) stg_stream(dx + row * nch + c, ov);
+    };
+    auto store_pend = [&]() {
+      const __amdgpu_buffer_rsrc_t ro = row_rsrc(dx, pend_row);
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        __builtin_amdgcn_raw_buffer_store_b128(pend[j], ro, (uint32_t)(lane + 64 * j) * 16u, 0, kAuxNT);
+    };
+    auto step = [&](auto slot, int64_t row) {
+      constexpr int S = decltype(slot)::value;
+      float xf[J][8], d[J][8];
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        unpack_bf16x8(make_uint4(bx[S][j].x, bx[S][j].y, bx[S][j].z, bx[S][j].w), xf[j]);
+        unpack_bf16x8(make_uint4(bd[S][j].x, bd[S][j].y, bd[S][j].z, bd[S][j].w), d[j]);
+      }
+      store_pend();
+      load_slot(slot, row + 2 * wstride);
+      // keep the accesses here: the scheduler otherwise sinks the prefetch
+      // below the next row's arithmetic, to the end of the loop
+      __builtin_amdgcn_sched_barrier(0);
+      float rn, dot;
+      row_stats(xf, d, rn, dot);
+#pragma unroll
+      for (int j = 0; j < J; ++j) pend[j] = row_out(j, xf, d, rn, dot, row < rows);
+      pend_row = row;
+    };
+    load_slot(std::integral_constant<int, 0>{}, wave0);
+    __builtin_amdgcn_sched_barrier(0);   // the first row's loads strictly before the second's
+    load_slot(std::integral_constant<int, 1>{}, wave0 + wstride);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int64_t row = wave0; row < rows; row += 2 * wstride) {
+      step(std::integral_constant<int, 0>{}, row);
+      step(std::integral_constant<int, 1>{}, row + wstride);
+    }
+    store_pend();
+  } else {
+    for (int64_t row = wave0; row < rows; row += wstride) {
+      const __amdgpu_buffer_rsrc_t rx = row_rsrc(x, row), rd = row_rsrc(dy, row);
+      float xf[J][8], d[J][8];
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const uint32_t off = (uint32_t)(lane + 64 * j) * 16u;
+        const u32x4_t vx = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, kAuxNT);
+        const u32x4_t vd = __builtin_amdgcn_raw_buffer_load_b128(rd, off, 0, kAuxNT);
+        unpack_bf16x8(make_uint4(vx.x, vx.y, vx.z, vx.w), xf[j]);
+        unpack_bf16x8(make_uint4(vd.x, vd.y, vd.z, vd.w), d[j]);
+      }
+      float rn, dot;
+      row_stats(xf, d, rn, dot);
+      const __amdgpu_buffer_rsrc_t ro = row_rsrc(dx, row);
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        __builtin_amdgcn_raw_buffer_store_b128(row_out(j, xf, d, rn, dot, true), ro, (uint32_t)(lane + 64 * j) * 16u,
+                                               0, kAuxNT);
     }
   }
 
