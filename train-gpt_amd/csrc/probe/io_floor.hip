@@ -13,6 +13,9 @@
 // mode 1: read x, write y                      (a bf16 copy)
 // mode 2: read x, write y, q and the scales    (config 2's mix)
 // mode 3: write y, q and the scales, read nothing
+#include <type_traits>
+
+#include "../gemm_tile.h"
 #include "../tg_device.h"
 #include "../tg_host.h"
 
@@ -84,6 +87,110 @@ extern "C" int tg_probe_io_floor(int mode, const void* x, void* y, void* q, floa
     default: hipLaunchKernelGGL(io_floor_kernel<3>, g, b, 0, st, X, Y, Q, s, rows); break;
   }
   return check_launch("io_floor");
+}
+
+// The same rows, pipelined: each wave keeps two rows' loads in flight and
+// stores a row's y / q / scales one row later, after the wait for the next
+// row's loads; every access is an unconditional raw buffer access over the
+// row's own bytes (a row past the end, and a lane that stores no scale, touch
+// no memory), so the compiler's waits are for the loads consumed, never for
+// stores issued in the same step.  (io_floor_kernel's prefetch and stores sit
+// behind branches, and its wait for the prefetched row also waits for the
+// current row's stores: VMEM operations retire from vmcnt in issue order.)
+namespace tg {
+
+template <int MODE>
+__global__ __launch_bounds__(256) void io_pipe_kernel(const uint4* __restrict__ x, uint4* __restrict__ y,
+                                                      uint2* __restrict__ q, float* __restrict__ s,
+                                                      int64_t rows) {
+  constexpr int J = 4, NCH = 256;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave0 = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t wstride = (int64_t)gridDim.x * 4;
+  auto rsrc_of = [&](const void* base, int64_t row, uint32_t row_bytes) {
+    const bool in = row < rows;
+    return make_rsrc(static_cast<const uint8_t*>(base) + (in ? row : 0) * row_bytes, in ? row_bytes : 0u);
+  };
+  u32x4_t buf[2][J], pend[J];
+  int64_t pend_row = rows;   // none yet: its stores are dropped
+  auto load_slot = [&](auto slot, int64_t row) {
+    constexpr int S = decltype(slot)::value;
+    const __amdgpu_buffer_rsrc_t rx = rsrc_of(x, row, NCH * 16);
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      buf[S][j] = MODE == 3 ? u32x4_t{(uint32_t)row, (uint32_t)lane, (uint32_t)j, 0u}
+                            : __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(lane + 64 * j) * 16u, 0, kAuxNT);
+  };
+  auto store_pend = [&]() {
+    if (MODE == 0) {
+      uint32_t acc = 0;
+#pragma unroll
+      for (int j = 0; j < J; ++j) acc ^= pend[j].x ^ pend[j].y ^ pend[j].z ^ pend[j].w;
+      const __amdgpu_buffer_rsrc_t rs = rsrc_of(s, pend_row, 4);
+      __builtin_amdgcn_raw_buffer_store_b32(acc, rs, lane == 0 ? 0u : 0x80000000u, 0, 0);
+      return;
+    }
+    const __amdgpu_buffer_rsrc_t ry = rsrc_of(y, pend_row, NCH * 16);
+    const __amdgpu_buffer_rsrc_t rq = rsrc_of(q, pend_row, NCH * 8);
+    const __amdgpu_buffer_rsrc_t rs = rsrc_of(s, pend_row, NCH / 16 * 4);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t c = (uint32_t)(lane + 64 * j);
+      __builtin_amdgcn_raw_buffer_store_b128(pend[j], ry, c * 16u, 0, kAuxNT);
+      if (MODE >= 2) {
+        const u32x2_t qv = {pend[j].x ^ pend[j].z, pend[j].y ^ pend[j].w};
+        __builtin_amdgcn_raw_buffer_store_b64(qv, rq, c * 8u, 0, kAuxNT);
+        __builtin_amdgcn_raw_buffer_store_b32(pend[j].x, rs, (lane & 15) == 0 ? (c >> 4) * 4u : 0x80000000u, 0, 0);
+      }
+    }
+  };
+  auto step = [&](auto slot, int64_t row) {
+    constexpr int S = decltype(slot)::value;
+    u32x4_t cur[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) cur[j] = buf[S][j];
+    store_pend();
+    load_slot(slot, row + 2 * wstride);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < J; ++j) pend[j] = cur[j];
+    pend_row = row;
+  };
+  load_slot(std::integral_constant<int, 0>{}, wave0);
+  __builtin_amdgcn_sched_barrier(0);
+  load_slot(std::integral_constant<int, 1>{}, wave0 + wstride);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int64_t row = wave0; row < rows; row += 2 * wstride) {
+    step(std::integral_constant<int, 0>{}, row);
+    step(std::integral_constant<int, 1>{}, row + wstride);
+  }
+  store_pend();
+}
+
+}  // namespace tg
+
+// io_floor_kernel's modes and grid, on io_pipe_kernel.
+extern "C" int tg_probe_io_pipe(int mode, const void* x, void* y, void* q, float* s, int64_t rows,
+                                int rows_per_wave, void* stream) {
+  using namespace tg;
+  if (mode < 0 || mode > 3 || rows <= 0 || rows_per_wave <= 0) return einval("tg_probe_io_pipe: bad arguments");
+  if ((mode != 3 && !x) || (mode != 0 && !y) || (mode >= 2 && !q) || !s)
+    return einval("tg_probe_io_pipe: null pointer");
+  int64_t grid = (rows + 4 * rows_per_wave - 1) / (4 * rows_per_wave);
+  if (grid < 512) grid = (rows + 3) / 4 < 512 ? (rows + 3) / 4 : 512;
+  if (grid > 16384) grid = 16384;
+  auto st = static_cast<hipStream_t>(stream);
+  auto X = reinterpret_cast<const uint4*>(x);
+  auto Y = reinterpret_cast<uint4*>(y);
+  auto Q = reinterpret_cast<uint2*>(q);
+  const dim3 g((unsigned)grid), b(256);
+  switch (mode) {
+    case 0: hipLaunchKernelGGL(io_pipe_kernel<0>, g, b, 0, st, X, Y, Q, s, rows); break;
+    case 1: hipLaunchKernelGGL(io_pipe_kernel<1>, g, b, 0, st, X, Y, Q, s, rows); break;
+    case 2: hipLaunchKernelGGL(io_pipe_kernel<2>, g, b, 0, st, X, Y, Q, s, rows); break;
+    default: hipLaunchKernelGGL(io_pipe_kernel<3>, g, b, 0, st, X, Y, Q, s, rows); break;
+  }
+  return check_launch("io_pipe");
 }
 
 // A different access pattern for the same bytes: no rows at all.  x is a
