@@ -113,6 +113,8 @@ __global__ __launch_bounds__(256) void io_pipe_kernel(const uint4* __restrict__ 
   };
   u32x4_t buf[2][J], pend[J];
   int64_t pend_row = rows;   // none yet: its stores are dropped
+#pragma unroll
+  for (int j = 0; j < J; ++j) pend[j] = u32x4_t{0u, 0u, 0u, 0u};
   auto load_slot = [&](auto slot, int64_t row) {
     constexpr int S = decltype(slot)::value;
     const __amdgpu_buffer_rsrc_t rx = rsrc_of(x, row, NCH * 16);

@@ -261,6 +261,8 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint4* __restric
     // previous row's stores included.
     u32x4_t bx[2][J], bd[2][J], pend[J];
     int64_t pend_row = rows;   // none yet: its stores are dropped
+#pragma unroll
+    for (int j = 0; j < J; ++j) pend[j] = u32x4_t{0u, 0u, 0u, 0u};
     auto load_slot = [&](auto slot, int64_t row) {
       constexpr int S = decltype(slot)::value;
       const __amdgpu_buffer_rsrc_t rx = row_rsrc(x, row), rd = row_rsrc(dy, row);
