@@ -693,11 +693,33 @@ def bench_norm_bwd(dev, iters):
                                     L.ptr(dgamma), C2_ROWS, C2_D, 1e-6, L.ptr(ws), wsb, st))
     us = _mean_launch_us(launch, iters)
     gbps = C2_BWD_BYTES / (us * 1e-6) / 1e9
-    return {"workload": "rms_norm backward (kernels.py:104-118), x/dy bf16 [8,1024,2048]",
-            "us_per_call": round(us, 3), "bytes_per_call": C2_BWD_BYTES,
-            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
-                         "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                         "traffic": measured_traffic().get("rmsnorm_bwd")}}
+    out = {"workload": "rms_norm backward (kernels.py:104-118), x/dy bf16 [8,1024,2048]",
+           "us_per_call": round(us, 3), "bytes_per_call": C2_BWD_BYTES,
+           "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                        "traffic": measured_traffic().get("rmsnorm_bwd")}}
+    # the row kernel's I/O with no arithmetic (libtg_probe.so's io_bwd_kernel,
+    # same row walk), on the product's grid (256) and larger ones
+    import ctypes
+    import build as tg_build
+    if os.path.exists(tg_build.PROBE_LIB):
+        probe = ctypes.CDLL(tg_build.PROBE_LIB)
+        probe.tg_probe_io_bwd.restype = ctypes.c_int
+        probe.tg_probe_io_bwd.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                                                  ctypes.c_void_p]
+        part = torch.empty(4096 * C2_D, dtype=torch.float32, device=dev)
+        floor = {}
+        for grid, depth in ((256, 2), (512, 2), (1024, 2), (2048, 2), (256, 3), (256, 4), (512, 3)):
+            def pl(i, grid=grid, depth=depth):
+                k = i % nsets
+                L.check(probe.tg_probe_io_bwd(L.ptr(xs[k]), L.ptr(dys[k]), L.ptr(dxs[k]), L.ptr(part), C2_ROWS,
+                                              grid, depth, st))
+            pus = _mean_launch_us(pl, iters)
+            byts = 3 * C2_ROWS * C2_D * 2 + grid * C2_D * 4
+            floor[f"grid_{grid}_rows_in_flight_{depth}"] = {"us_per_launch": round(pus, 3), "bytes_per_launch": byts,
+                                                            "GB/s": round(byts / (pus * 1e-6) / 1e9, 1)}
+        out["row_kernel_io_floor"] = floor
+    return out
 
 
 def bench_gemv(dev, iters):

@@ -195,6 +195,108 @@ extern "C" int tg_probe_io_pipe(int mode, const void* x, void* y, void* q, float
   return check_launch("io_pipe");
 }
 
+// The norm backward's traffic (rmsnorm_bwd_kernel<4, true> at dim 2048, the
+// kernel behind tg_rms_norm_bwd): x and dy rows read, dx rows written, with
+// that kernel's pipelined row walk (two rows' loads in flight per wave, each
+// row's dx stored one row later, unconditional raw buffer accesses) and one
+// 2048-float partial row per workgroup at the end; dx is a bit mix of x and
+// dy, no arithmetic.  bench.py --only norm_bwd times it on the product's grid
+// (one workgroup per CU) and on larger ones, and with 3 or 4 rows in flight.
+namespace tg {
+
+template <int PD>
+__global__ __launch_bounds__(256) void io_bwd_kernel(const uint4* __restrict__ x, const uint4* __restrict__ dy,
+                                                     uint4* __restrict__ dx, float* __restrict__ partial,
+                                                     int64_t rows) {
+  constexpr int J = 4, NCH = 256;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave0 = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t wstride = (int64_t)gridDim.x * 4;
+  auto rsrc_of = [&](const uint4* base, int64_t row) {
+    const bool in = row < rows;
+    return make_rsrc(base + (in ? row : 0) * NCH, in ? (uint32_t)NCH * 16u : 0u);
+  };
+  u32x4_t bx[PD][J], bd[PD][J], pend[J];
+  int64_t pend_row = rows;   // none yet: its stores are dropped
+#pragma unroll
+  for (int j = 0; j < J; ++j) pend[j] = u32x4_t{0u, 0u, 0u, 0u};
+  uint32_t mix = 0;
+  auto load_slot = [&](auto slot, int64_t row) {
+    constexpr int S = decltype(slot)::value;
+    const __amdgpu_buffer_rsrc_t rx = rsrc_of(x, row), rd = rsrc_of(dy, row);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t off = (uint32_t)(lane + 64 * j) * 16u;
+      bx[S][j] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, kAuxNT);
+      bd[S][j] = __builtin_amdgcn_raw_buffer_load_b128(rd, off, 0, kAuxNT);
+    }
+  };
+  auto store_pend = [&]() {
+    const __amdgpu_buffer_rsrc_t ro = rsrc_of(dx, pend_row);
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      __builtin_amdgcn_raw_buffer_store_b128(pend[j], ro, (uint32_t)(lane + 64 * j) * 16u, 0, kAuxNT);
+  };
+  auto step = [&](auto slot, int64_t row) {
+    constexpr int S = decltype(slot)::value;
+    u32x4_t cur[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) cur[j] = bx[S][j] ^ bd[S][j];
+    store_pend();
+    load_slot(slot, row + PD * wstride);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      pend[j] = cur[j];
+      mix ^= cur[j].x;
+    }
+    pend_row = row;
+  };
+  load_slot(std::integral_constant<int, 0>{}, wave0);
+  __builtin_amdgcn_sched_barrier(0);
+  load_slot(std::integral_constant<int, 1>{}, wave0 + wstride);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (PD > 2) {
+    load_slot(std::integral_constant<int, 2 % PD>{}, wave0 + 2 * wstride);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if constexpr (PD > 3) {
+    load_slot(std::integral_constant<int, 3 % PD>{}, wave0 + 3 * wstride);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int64_t row = wave0; row < rows; row += PD * wstride) {
+    step(std::integral_constant<int, 0>{}, row);
+    step(std::integral_constant<int, 1>{}, row + wstride);
+    if constexpr (PD > 2) step(std::integral_constant<int, 2 % PD>{}, row + 2 * wstride);
+    if constexpr (PD > 3) step(std::integral_constant<int, 3 % PD>{}, row + 3 * wstride);
+  }
+  store_pend();
+  // the workgroup's partial row (2048 floats, as the product writes its dscale partials)
+  for (int i = threadIdx.x; i < NCH * 8; i += 256)
+    partial[(int64_t)blockIdx.x * NCH * 8 + i] = __uint_as_float(mix ^ (uint32_t)i);
+}
+
+}  // namespace tg
+
+// rows x 2048 bf16 x and dy, dx written; partial holds grid x 2048 floats;
+// depth 2, 3 or 4 rows' loads in flight per wave (the product keeps 2).
+extern "C" int tg_probe_io_bwd(const void* x, const void* dy, void* dx, float* partial, int64_t rows, int grid,
+                               int depth, void* stream) {
+  using namespace tg;
+  if (rows <= 0 || grid <= 0 || grid > 65535 || depth < 2 || depth > 4)
+    return einval("tg_probe_io_bwd: bad arguments");
+  if (!x || !dy || !dx || !partial) return einval("tg_probe_io_bwd: null pointer");
+  auto st = static_cast<hipStream_t>(stream);
+  auto X = reinterpret_cast<const uint4*>(x);
+  auto DY = reinterpret_cast<const uint4*>(dy);
+  auto DX = reinterpret_cast<uint4*>(dx);
+  const dim3 g((unsigned)grid), b(256);
+  if (depth == 2) hipLaunchKernelGGL(io_bwd_kernel<2>, g, b, 0, st, X, DY, DX, partial, rows);
+  else if (depth == 3) hipLaunchKernelGGL(io_bwd_kernel<3>, g, b, 0, st, X, DY, DX, partial, rows);
+  else hipLaunchKernelGGL(io_bwd_kernel<4>, g, b, 0, st, X, DY, DX, partial, rows);
+  return check_launch("io_bwd");
+}
+
 // A different access pattern for the same bytes: no rows at all.  x is a
 // stream of 16-byte units (8 bf16); unit i is read once (non-temporal) and
 // gives a 16-byte y store, an 8-byte q store and, every 16th unit, one 4-byte
