@@ -650,6 +650,45 @@ def bench_gemv_floor(dev, iters):
         out["shapes"].append(row)
         del ws, wsc
         torch.cuda.empty_cache()
+    # C5 (14336 x 4096, 128 x 128 scales) on the staged GEMV: the product at 8
+    # and 32 rows beside gemv_staged_kernel, its weight stream with no MFMAs,
+    # x fragments or reduction (weight only, and with the 8-row x copy)
+    probe.tg_probe_gemv_staged.restype = ctypes.c_int
+    probe.tg_probe_gemv_staged.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int64,
+                                           ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                           ctypes.c_int, ctypes.c_void_p]
+    N, K = C5_N, C5_K
+    nset = int(800e6 // (N * K)) + 1
+    ws = [torch.randint(0, 126, (N, K), generator=g, device=dev, dtype=torch.uint8) for _ in range(nset)]
+    wsc = [torch.rand((N + 127) // 128, K // 128, generator=g, device=dev) * 1e-2 for _ in range(nset)]
+    groups = (N + 7) // 8
+    grid = max(min(cus, groups), (groups + 7) // 8)
+    sink = torch.empty(grid * 512, dtype=torch.int32, device=dev)
+    st = L.stream_of(sink)
+    wbytes = N * K
+    c5 = {"weight": "C5", "N": N, "K": K, "weight_bytes": wbytes, "grid": grid}
+
+    def rate5(us):
+        return {"us_per_launch": round(us, 3), "weight_GB/s": round(wbytes / (us * 1e-6) / 1e9, 1)}
+    xq8 = torch.randint(0, 126, (8, K), generator=g, device=dev, dtype=torch.uint8)
+    for _ in range(2):   # the second pass is reported (first touches of the copies run slower)
+        for label, xb in (("staged_loads", 0), ("staged_loads_with_x_copy_8_rows", 8 * K)):
+            def launch(i, xb=xb):
+                L.check(probe.tg_probe_gemv_staged(L.ptr(ws[i % nset]), L.ptr(wsc[i % nset]), 128, N, K,
+                                                   L.ptr(xq8), xb, L.ptr(sink), grid, st))
+            c5[label] = rate5(_mean_launch_us(launch, iters))
+        for M in (8, 32):
+            xq = torch.randint(0, 126, (M, K), generator=g, device=dev, dtype=torch.uint8)
+            xs = torch.rand(M, K // 128, generator=g, device=dev)
+            o = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+
+            def gemv(i, xq=xq, xs=xs, o=o, M=M):
+                L.check(lib.tg_gemv_fp8(L.ptr(xq), L.ptr(xs), L.ptr(ws[i % nset]), L.ptr(wsc[i % nset]), 128,
+                                        L.ptr(o), M, N, K, 128, st))
+            c5[f"tg_gemv_fp8_M{M}"] = rate5(_mean_launch_us(gemv, iters))
+    out["c5_staged"] = c5
+    del ws, wsc
+    torch.cuda.empty_cache()
     return out
 
 
