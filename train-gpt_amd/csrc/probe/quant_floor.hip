@@ -33,9 +33,10 @@ extern "C" int tg_probe_quant_floor(int mode, const void* x0, int64_t rows0, int
   }
   auto st = static_cast<hipStream_t>(stream);
   if (mode == 0)
-    hipLaunchKernelGGL((quant_dual_kernel<true, false, true, true>), dim3((unsigned)total), dim3(256), 0, st, jobs);
+    hipLaunchKernelGGL((quant_dual_kernel<true, false, true, true>), dim3((unsigned)total), dim3(kDualThreads), 0,
+                       st, jobs);
   else
-    hipLaunchKernelGGL((quant_dual_kernel<true, false, true, false>), dim3((unsigned)total), dim3(256), 0, st,
-                       jobs);
+    hipLaunchKernelGGL((quant_dual_kernel<true, false, true, false>), dim3((unsigned)total), dim3(kDualThreads), 0,
+                       st, jobs);
   return check_launch("probe_quant_floor");
 }

@@ -208,9 +208,9 @@ int launch_quant_cols(const void* x, int64_t rows, int64_t cols, uint8_t* q_t, f
     jobs.nblk0 = jobs.job[0].gx * jobs.job[0].gy;
     const dim3 grid((unsigned)jobs.nblk0);
     if (cols % 128 == 0)
-      hipLaunchKernelGGL((quant_dual_kernel<false, false>), grid, dim3(256), 0, st, jobs);
+      hipLaunchKernelGGL((quant_dual_kernel<false, false>), grid, dim3(kDualThreads), 0, st, jobs);
     else
-      hipLaunchKernelGGL((quant_dual_kernel<false, true>), grid, dim3(256), 0, st, jobs);
+      hipLaunchKernelGGL((quant_dual_kernel<false, true>), grid, dim3(kDualThreads), 0, st, jobs);
     return check_launch("quant_cols");
   }
   // rows not 16-byte aligned: the element-load kernel
@@ -227,8 +227,8 @@ int launch_quant_dual(const void* x, int64_t rows, int64_t cols, uint8_t* q, flo
   DualJobs jobs{};
   TG_TRY(dual_job(jobs.job[0], "quantize_dual", x, rows, cols, q, s, q_t, s_t, true, skm));
   jobs.nblk0 = jobs.job[0].gx * jobs.job[0].gy;
-  hipLaunchKernelGGL((quant_dual_kernel<true, false>), dim3((unsigned)jobs.nblk0), dim3(256), 0, st,
-                     jobs);
+  hipLaunchKernelGGL((quant_dual_kernel<true, false>), dim3((unsigned)jobs.nblk0), dim3(kDualThreads), 0,
+                     st, jobs);
   return check_launch("quant_dual");
 }
 
@@ -248,7 +248,7 @@ int launch_quant_dual_pair(const void* x0, int64_t rows0, int64_t cols0, uint8_t
                   jobs.nblk0 % 8 == 0, skm));
   const int64_t total = (int64_t)jobs.nblk0 + (int64_t)jobs.job[1].gx * jobs.job[1].gy;
   if (total > kDualMaxTiles) return einval("quantize_dual_pair: too many 128 x 128 tiles");
-  hipLaunchKernelGGL((quant_dual_kernel<true, false>), dim3((unsigned)total), dim3(256), 0, st, jobs);
+  hipLaunchKernelGGL((quant_dual_kernel<true, false>), dim3((unsigned)total), dim3(kDualThreads), 0, st, jobs);
   return check_launch("quant_dual_pair");
 }
 
@@ -268,7 +268,7 @@ int launch_quant_rows_cols(const void* a, int64_t M, int64_t K, uint8_t* qa, flo
   jobs.job[1].part = 2;
   const int64_t total = (int64_t)jobs.nblk0 + (int64_t)jobs.job[1].gx * jobs.job[1].gy;
   if (total > kDualMaxTiles) return einval("quantize_rows_cols: too many 128 x 128 tiles");
-  hipLaunchKernelGGL((quant_dual_kernel<true, false>), dim3((unsigned)total), dim3(256), 0, st, jobs);
+  hipLaunchKernelGGL((quant_dual_kernel<true, false>), dim3((unsigned)total), dim3(kDualThreads), 0, st, jobs);
   return check_launch("quant_rows_cols");
 }
 

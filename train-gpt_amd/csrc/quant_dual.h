@@ -5,24 +5,28 @@
 // kernel with its arithmetic taken out (IO = true) so that the I/O floor of
 // this exact access pattern can be timed.
 //
-// Tile = 128 x 128 bf16.  Lanes 16r .. 16r+15 of a wave hold one 128-element
-// row block (as in quant_rows_kernel), quantize it and keep the raw tile in
-// LDS (row pitch 272 B); then quads of lanes own whole columns (as in
-// quant_cols_kernel), quantize them and store 128 contiguous bytes per
-// column.  The bytes and scales equal those of the two separate kernels.
+// Tile = 128 x 128 bf16, one workgroup of kDualThreads = 512 threads.  Lanes
+// 16r .. 16r+15 of a wave hold one 128-element row block (as in
+// quant_rows_kernel; 4 row blocks per lane), quantize it and keep the raw tile
+// in LDS (row pitch 272 B); then groups of 8 lanes own column pairs (16 rows
+// per lane), quantize them and store 128 contiguous bytes per column.  The
+// bytes and scales equal those of the two separate kernels.  Eight waves per
+// tile rather than four halve each wave's arithmetic, which is what the last
+// workgroups of a launch (and a launch of one round, such as C1's) wait for.
 //
 // LDS banks (gfx950, measured with SQ_LDS_BANK_CONFLICT): a 32-bit access
 // serves 32 lanes at a time over 32 banks of 4 bytes; a 128-bit read serves
-// 16 lanes at a time over 64 banks.  Both swizzles below leave every LDS
-// instruction of the kernel free of bank conflicts:
-//  - raw tile: 32-bit word w of row r sits at r * 68 + (w ^ (8 * ((r >> 3) & 1))).
-//    The column reads take rows 4j + const for the four lanes j of a quad,
-//    and a pitch of 68 words alone puts j and j + 2 on the same banks; the
-//    xor moves rows 8-15 of every 16 by 8 banks.  The 16-byte row stores
-//    only permute whole chunks within the row.
+// 16 lanes at a time over 64 banks, the quads {0, 3, 5, 6} or {1, 2, 4, 7} of
+// a half-wave.  Both swizzles below leave every LDS instruction of the kernel
+// free of bank conflicts:
+//  - raw tile: 32-bit word w of row r sits at r * 68 + (w ^ (4 * ((r >> 3) & 3))).
+//    The column reads take rows 4j + const for the eight lanes j of a group,
+//    and a pitch of 68 words alone puts j, j + 2, j + 4 and j + 6 on the same
+//    banks; the xor moves them 4 words apart.  The 16-byte row stores only
+//    permute chunks within aligned groups of four.
 //  - transposed bytes: column n is 128 bytes at n * 32 words, its 16-byte
-//    chunk c at position c ^ ((n >> 1) & 7), so that the 8 column pairs a
-//    half-wave writes at once (one word each) land in 8 distinct chunks.
+//    chunk c at position c ^ (2 * ((n >> 1) & 3)), so that the words the four
+//    column pairs of a half-wave write at once land on distinct banks.
 //
 // ROWS = false gives the column quantization alone (tg_quantize_cols for
 // 16-byte-aligned rows); GUARD handles a last tile narrower than 128 columns.
@@ -77,8 +81,18 @@ struct DualJobs {
   int nblk0;   // tiles of job 0; gridDim.x - nblk0 are job 1's
 };
 
+constexpr int kDualThreads = 512;
+
 // Word offset of 16-byte chunk c of transposed column n (128 bytes per column).
-__device__ __forceinline__ int dual_tq_at(int n, int c) { return n * 32 + 4 * (c ^ ((n >> 1) & 7)); }
+__device__ __forceinline__ int dual_tq_at(int n, int c) { return n * 32 + 4 * (c ^ (2 * ((n >> 1) & 3))); }
+
+// max over the 8 lanes of a DPP half-row (all lanes receive the result)
+__device__ __forceinline__ uint32_t oct_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));    // quad_perm [1,0,3,2]
+  v = max(v, dpp_u32<0x4E>(v));    // quad_perm [2,3,0,1]
+  v = max(v, dpp_u32<0x141>(v));   // row_half_mirror
+  return v;
+}
 
 // IO: the probe's variant.  Every load, LDS access and store of the product
 // kernel stays (same addresses, same order, same widths); the values stored
@@ -86,7 +100,7 @@ __device__ __forceinline__ int dual_tq_at(int n, int c) { return n * 32 + 4 * (c
 // the amax reductions and divides are gone.  IO_SCALES = false also drops
 // the scale stores.
 template <bool ROWS, bool GUARD, bool IO = false, bool IO_SCALES = true>
-__global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
+__global__ __launch_bounds__(kDualThreads) void quant_dual_kernel(DualJobs jobs) {
   // the raw tile (row pitch 272 B); once every column is in registers the
   // same memory stages the transposed bytes (column pitch 128 B)
   __shared__ uint32_t tile[128 * 68];
@@ -120,13 +134,13 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
   const bool ch_ok = !GUARD || (c0 >> 3) + ch < cchunks;
   // the job's parts (workgroup-uniform)
   const bool do_rows = ROWS && J.part != 2, do_cols = J.part != 1;
-  uint4 v[8];
+  uint4 v[4];
 #pragma unroll
-  for (int u = 0; u < 8; ++u)
-    v[u] = ch_ok ? ldg_stream(x + (r0 + rr + 16 * u) * cchunks + (c0 >> 3) + ch) : make_uint4(0, 0, 0, 0);
+  for (int u = 0; u < 4; ++u)
+    v[u] = ch_ok ? ldg_stream(x + (r0 + rr + 32 * u) * cchunks + (c0 >> 3) + ch) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int row = rr + 16 * u;
+  for (int u = 0; u < 4; ++u) {
+    const int row = rr + 32 * u;
     if (do_rows) {
       float sc;
       if constexpr (IO) {
@@ -144,7 +158,7 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
         else s[(r0 + row) * (cols >> 7) + tx] = sc;
       }
     }
-    if (do_cols) *reinterpret_cast<uint4*>(&tile[row * 68 + ((ch * 4) ^ (8 * ((row >> 3) & 1)))]) = v[u];
+    if (do_cols) *reinterpret_cast<uint4*>(&tile[row * 68 + ((ch * 4) ^ (4 * ((row >> 3) & 3)))]) = v[u];
   }
   const bool rows_gathered = kScales && do_rows && skm;
   if (!do_cols && !rows_gathered) return;
@@ -152,62 +166,65 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
   if (rows_gathered && tid < 128) s[(int64_t)tx * rows + r0 + tid] = sgather[0][tid];
   if (!do_cols) return;
 
-  // columns: quad (tid >> 2) owns the column pair 2c, 2c + 1 (one 32-bit LDS
-  // word per row); lane j of the quad holds rows 16i + 4j + r
-  const int j = tid & 3, cp = tid >> 2;
-  const int cpw = cp ^ (8 * (j >> 1));   // the pair's word in rows 16i + 4j + r
+  // columns: the 8 lanes tid >> 3 own the column pair 2c, 2c + 1 (one 32-bit
+  // LDS word per row); lane j of the group holds rows 32t + 4j + r, i.e. the
+  // 4-row words g = 8t + j of each column
+  const int j = tid & 7, cp = tid >> 3;
+  const int cpw = cp ^ (4 * ((j >> 1) & 3));   // the pair's word in rows 32t + 4j + r
   auto put_scale = [&](float sc, int n) {
     if (kScales && j == 0 && (!GUARD || c0 + n < cols)) {
       if (skm) sgather[1][n] = sc;
       else st[(c0 + n) * (rows >> 7) + ty] = sc;
     }
   };
+  // word g = 8t + j of column n: chunk (g >> 2) = 2t + (j >> 2), word j & 3 of it
+  const int jc = j >> 2, jw = j & 3;
   if constexpr (IO) {
-    uint32_t wd[32];
+    uint32_t wd[16];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) wd[i * 4 + r] = tile[(16 * i + 4 * j + r) * 68 + cpw];
+      for (int r = 0; r < 4; ++r) wd[t * 4 + r] = tile[(32 * t + 4 * j + r) * 68 + cpw];
     __syncthreads();   // every lane has read its columns: the tile becomes tq
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      tq[dual_tq_at(2 * cp, i) + j] = wd[4 * i] ^ wd[4 * i + 1];
-      tq[dual_tq_at(2 * cp + 1, i) + j] = wd[4 * i + 2] ^ wd[4 * i + 3];
+    for (int t = 0; t < 4; ++t) {
+      tq[dual_tq_at(2 * cp, 2 * t + jc) + jw] = wd[4 * t] ^ wd[4 * t + 1];
+      tq[dual_tq_at(2 * cp + 1, 2 * t + jc) + jw] = wd[4 * t + 2] ^ wd[4 * t + 3];
     }
     put_scale(__uint_as_float(wd[0]), 2 * cp);
     put_scale(__uint_as_float(wd[1]), 2 * cp + 1);
   } else {
-    float f0[32], f1[32];
+    float f0[16], f1[16];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const uint32_t w = tile[(16 * i + 4 * j + r) * 68 + cpw];
-        f0[i * 4 + r] = __uint_as_float(w << 16);
-        f1[i * 4 + r] = __uint_as_float(w & 0xFFFF0000u);
+        const uint32_t w = tile[(32 * t + 4 * j + r) * 68 + cpw];
+        f0[t * 4 + r] = __uint_as_float(w << 16);
+        f1[t * 4 + r] = __uint_as_float(w & 0xFFFF0000u);
       }
     uint32_t m0 = 0, m1 = 0;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < 16; ++i) {
       m0 = max(m0, __float_as_uint(f0[i]) & 0x7FFFFFFFu);
       m1 = max(m1, __float_as_uint(f1[i]) & 0x7FFFFFFFu);
     }
-    const float sc0 = block_scale_bf16(quad_max_u32(m0));
-    const float sc1 = block_scale_bf16(quad_max_u32(m1));
+    const float sc0 = block_scale_bf16(oct_max_u32(m0));
+    const float sc1 = block_scale_bf16(oct_max_u32(m1));
     __syncthreads();   // every lane has read its columns: the tile becomes tq
-    auto col_words = [&](const float (&f)[32], float sc, int n) {
+    auto col_words = [&](const float (&f)[16], float sc, int n) {
       Divider d(sc);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int t = 0; t < 4; ++t) {
         uint32_t w;
         if (d.fast) {
-          w = e4m3x4(d.div(f[4 * i]), d.div(f[4 * i + 1]), d.div(f[4 * i + 2]), d.div(f[4 * i + 3]));
+          w = e4m3x4(d.div(f[4 * t]), d.div(f[4 * t + 1]), d.div(f[4 * t + 2]), d.div(f[4 * t + 3]));
         } else {
-          w = e4m3_nonfinite_scale(f[4 * i], sc) | (e4m3_nonfinite_scale(f[4 * i + 1], sc) << 8) |
-              (e4m3_nonfinite_scale(f[4 * i + 2], sc) << 16) |
-              (e4m3_nonfinite_scale(f[4 * i + 3], sc) << 24);
+          w = e4m3_nonfinite_scale(f[4 * t], sc) | (e4m3_nonfinite_scale(f[4 * t + 1], sc) << 8) |
+              (e4m3_nonfinite_scale(f[4 * t + 2], sc) << 16) |
+              (e4m3_nonfinite_scale(f[4 * t + 3], sc) << 24);
         }
-        tq[dual_tq_at(n, i) + j] = w;
+        tq[dual_tq_at(n, 2 * t + jc) + jw] = w;
       }
       put_scale(sc, n);
     };
@@ -222,13 +239,13 @@ __global__ __launch_bounds__(256) void quant_dual_kernel(DualJobs jobs) {
   // Infinity Cache they came back from HBM with each dY.T panel read by one
   // XCD only, which left dW ~15% slower than dX inside the C3 step.
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int n = (tid >> 3) + 32 * p, k = tid & 7;
+  for (int p = 0; p < 2; ++p) {
+    const int n = (tid >> 3) + 64 * p, k = tid & 7;
     if (GUARD && c0 + n >= cols) continue;
     const uint4 val = *reinterpret_cast<const uint4*>(&tq[dual_tq_at(n, k)]);
     *(reinterpret_cast<uint4*>(qt + (c0 + n) * rows + r0) + k) = val;
   }
-  if (kScales && skm && tid >= 128 && (!GUARD || c0 + tid - 128 < cols))
+  if (kScales && skm && tid >= 128 && tid < 256 && (!GUARD || c0 + tid - 128 < cols))
     st[(int64_t)ty * cols + c0 + tid - 128] = sgather[1][tid - 128];
 }
 
