@@ -158,7 +158,10 @@ size_t tg_block_scaled_matmul_bwd_workspace(int64_t M, int64_t N, int64_t K, int
  *   db (K, N) = fwd(a.T, g):  a.T and g.T quantized along M
  * a: (M, K), b: (K, N), g: (M, N), all bf16; da, db bf16.  block_k any
  * divisor of K; M and N multiples of block_k (a caller pads a ragged last
- * block with zeros, which change neither amax nor any product). */
+ * block with zeros, which change neither amax nor any product).  M == 0 or
+ * N == 0: the gradient that sums over the empty extent is written as zeros
+ * (db with M == 0, da with N == 0); only an empty gradient's pointer may be
+ * null, and a, b, g, workspace are not read. */
 int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, const void* g, void* da,
                                    void* db, int64_t M, int64_t N, int64_t K, int block_k,
                                    void* workspace, size_t workspace_bytes, void* stream);

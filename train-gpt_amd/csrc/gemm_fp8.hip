@@ -2260,7 +2260,13 @@ extern "C" int tg_block_scaled_matmul_bwd_fp8(const void* a, const void* b, cons
   TG_TRY(check_gemm_args("block_scaled_matmul_bwd_fp8", M, N, K, block_k, 1, true));
   if (M % block_k || N % block_k)
     return einval("block_scaled_matmul_bwd_fp8: M and N must be multiples of block_k");
-  if (M == 0 || N == 0) return TG_OK;
+  if (M == 0 || N == 0) {
+    // an empty M or N: the gradient that sums over it is zero (db = a.T @ g
+    // over M = 0, da = g @ b.T over N = 0), the other one is empty
+    if ((M * K && !da) || (K * N && !db)) return einval("block_scaled_matmul_bwd_fp8: null pointer");
+    TG_TRY(launch_fill_zero_bf16(da, M * K, as_stream(stream)));
+    return launch_fill_zero_bf16(db, K * N, as_stream(stream));
+  }
   if (!a || !b || !g || !da || !db || !workspace) return einval("block_scaled_matmul_bwd_fp8: null pointer");
   if (workspace_bytes < tg_block_scaled_matmul_bwd_workspace(M, N, K, block_k))
     return einval("block_scaled_matmul_bwd_fp8: workspace too small");

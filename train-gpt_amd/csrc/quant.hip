@@ -474,8 +474,10 @@ extern "C" int tg_quantize_cols(const void* x, int x_dtype, int64_t rows, int64_
 
 extern "C" int tg_quantize_weight_128x128(const void* w, int64_t K, int64_t N, uint8_t* w_q,
                                           float* w_s, void* stream) {
-  if (K <= 0 || N <= 0 || K % 128) return einval("quantize_weight_128x128: K must be a positive multiple of 128");
+  if (K <= 0 || K % 128) return einval("quantize_weight_128x128: K must be a positive multiple of 128");
+  if (N < 0) return einval("quantize_weight_128x128: bad shape");
   if (K / 128 > 65535) return einval("quantize_weight_128x128: K too large");
+  if (N == 0) return TG_OK;
   if (!w || !w_q || !w_s) return einval("quantize_weight_128x128: null pointer");
   if (!aligned(w_q, 16)) return einval("quantize_weight_128x128: w_q must be 16-byte aligned");
   dim3 grid((unsigned)((N + 127) / 128), (unsigned)(K / 128));

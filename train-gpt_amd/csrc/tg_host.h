@@ -83,6 +83,9 @@ int launch_quant_cols_gb(const void* x, bool x_f32, int64_t rows, int64_t cols, 
                          float* s_t, hipStream_t st, int srep = 1, int pf = 1, bool skm = false);
 int launch_gemm_gb(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, const float* b_s, int bn, void* c,
                    int c_dtype, int64_t M, int64_t N, int64_t K, int bk, hipStream_t st);
+// n bf16 zeros at p by a fill kernel (no hipMemsetAsync: the callers may be
+// captured into a graph); n == 0 launches nothing (gemm_bf16.hip).
+int launch_fill_zero_bf16(void* p, int64_t n, hipStream_t st);
 
 }  // namespace tg
 
