@@ -166,3 +166,58 @@ def test_rms_norm_any_dtype_and_width(dev, x_dt, g_dt, D):
         np.testing.assert_array_equal(y.cpu().numpy().view(np.uint16), want.astype(np.float16).view(np.uint16))
     else:
         np.testing.assert_array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def _non_finite_rows(D):
+    """Rows of bf16 x that take the norm's special cases (kernels.py:30-33 op by op):
+    one +inf / -inf (var = inf, r = 0: finite elements -> 0, the inf one -> NaN),
+    one NaN (the whole row NaN), values whose f32 squares overflow (var = inf),
+    values near the bf16 maximum, all zeros (r = rsqrt(eps)), bf16 subnormals,
+    and an ordinary row between them."""
+    rng = np.random.default_rng(D)
+    x = rng.standard_normal((9, D)).astype(np.float32)
+    x[1, 3] = np.inf
+    x[2, D // 2] = np.nan
+    x[3, D - 1] = -np.inf
+    x[4] *= np.float32(1e30)
+    x[5, :] = np.float32(3.0e38) * np.sign(x[5])
+    x[6, :] = 0.0
+    x[7] *= np.float32(1e-39)                          # bf16 subnormals (min normal ~1.18e-38)
+    with np.errstate(over="ignore"):
+        xb = ob.f32_to_bf16(x)
+    g = ob.f32_to_bf16((1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32))
+    return xb, g
+
+
+def _same_bf16(got_bits, ref_bits):
+    """Bit equality, any NaN equal to any NaN (the NaN payload is the hardware's)."""
+    gn = (got_bits & 0x7F80) == 0x7F80
+    gn &= (got_bits & 0x7F) != 0
+    rn = (ref_bits & 0x7F80) == 0x7F80
+    rn &= (ref_bits & 0x7F) != 0
+    assert np.array_equal(gn, rn)
+    np.testing.assert_array_equal(got_bits[~gn], ref_bits[~rn])
+
+
+@pytest.mark.parametrize("D", [256, 2048, 6000])
+def test_rms_norm_non_finite_rows(dev, D):
+    x, g = _non_finite_rows(D)
+    y = kernels.rms_norm(to_dev(x, dev), to_dev(g, dev), 1e-6)
+    yo = norm_ref.rms_norm_pure(x, g, 1e-6)
+    assert np.isnan(ob.bf16_to_f32(yo[1])).sum() == 1 and np.all(np.isnan(ob.bf16_to_f32(yo[2])))
+    _same_bf16(bf16_bits(y), yo)
+
+
+@pytest.mark.parametrize("D", [256, 2048])
+def test_rms_norm_fp8_non_finite_rows(dev, D):
+    """The fused quantizer on those rows: a block holding a NaN has a NaN scale
+    and NaN bytes (fp8.py:39-47 on the NaN y), the rest as the oracle."""
+    x, g = _non_finite_rows(D)
+    y, q, s = kernels.rms_norm_fp8(to_dev(x, dev), to_dev(g, dev), 1e-6)
+    yo, qo, so = norm_ref.rms_norm_fp8(x, g, 1e-6)
+    _same_bf16(bf16_bits(y), yo)
+    qg = u8(q)
+    nan_g, nan_o = (qg & 0x7F) == 0x7F, (qo & 0x7F) == 0x7F
+    assert np.array_equal(nan_g, nan_o)
+    np.testing.assert_array_equal(qg[~nan_g], qo[~nan_o])
+    assert same_scales(s.cpu().numpy(), so)
