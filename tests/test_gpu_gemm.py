@@ -379,3 +379,32 @@ def test_fp8_backward_mode_switch_after_forward_raises(dev):
             y.sum().backward()
     finally:
         fp8.BACKWARD_MODE = old
+
+
+def test_composite_forward_non_finite_operands(dev):
+    """NaN / +-inf in a and b through tg_block_scaled_matmul (fp8.py:50-78):
+    a NaN element gives its block a NaN scale, an infinite one an infinite
+    scale and a NaN byte (inf / inf), so exactly the rows of a and the columns
+    of b that hold one come out NaN (the oracle's float64 product); every
+    other output stays within the usual bar, and the operand bytes and scales
+    the forward quantizes are bit-exact."""
+    rng = np.random.default_rng(7)
+    M, K, N = 256, 384, 320
+    a = ob.randn_bf16(rng, (M, K))
+    b = ob.randn_bf16(rng, (K, N), std=0.02)
+    a[3, 10] = 0x7FC0                               # NaN in row 3, K block 0
+    a[7, 200] = 0x7F80                              # +inf in row 7, K block 1
+    b[5, 9] = 0xFF80                                # -inf in column 9, K block 0
+    with np.errstate(invalid="ignore", over="ignore"):
+        _, ref, (qa, sa), (qb, sb) = fp8_ref.fp8_forward(a, b)
+    y = fp8.block_scaled_matmul(to_dev(a, dev), to_dev(b, dev)).float().cpu().numpy()
+    nan_ref = np.isnan(ref)
+    assert nan_ref.sum() == 2 * N + M - 2          # rows 3 and 7, column 9
+    np.testing.assert_array_equal(np.isnan(y), nan_ref)
+    assert maxabs_rel(y[~nan_ref], ref[~nan_ref]) <= TOL
+    qx, sx = fp8.quantize_fp8(to_dev(a, dev))
+    np.testing.assert_array_equal(u8(qx), qa)
+    assert same_scales(sx.cpu().numpy(), sa)
+    qw, sw = fp8.quantize_fp8(to_dev(b, dev), transpose=True)
+    np.testing.assert_array_equal(u8(qw), qb)
+    assert same_scales(sw.cpu().numpy(), sb)
