@@ -112,3 +112,45 @@ def test_rms_norm_bwd_any_dtype_and_width(dev, x_dt, g_dt, D):
     gt.grad = None
     kernels.rms_norm(xt, gt, 1e-6).backward(torch.from_numpy(dy).to(dev).to(out_dt))
     assert torch.equal(gt.grad, first)
+
+
+def _nan_class_match(got, ref):
+    g = got.float().cpu().numpy() if isinstance(got, torch.Tensor) else np.asarray(got)
+    np.testing.assert_array_equal(np.isnan(g), np.isnan(ref))
+    m = ~np.isnan(ref)
+    return g[m], ref[m]
+
+
+@pytest.mark.parametrize("D", [256, 2048, 6000])
+def test_rms_norm_bwd_infinite_rows(dev, D):
+    """kernels.py:104-118 on rows holding +inf / -inf (rnorm = 0, normed NaN at the
+    inf and 0 elsewhere, so the mean and the row's dx are NaN, and dscale is NaN
+    in those columns only) and an all-zero row (rnorm = rsqrt(eps), dx = rnorm * gs);
+    the other rows and columns as in the finite case."""
+    rng = np.random.default_rng(D + 1)
+    x, g, dy = _inputs(rng, (12, D))
+    x[2, 5] = 0x7F80
+    x[6, D - 3] = 0xFF80
+    x[9, :] = 0
+    with np.errstate(invalid="ignore", over="ignore"):
+        rdx, rdg = norm_ref.rms_norm_vjp(x, g, 1e-6, dy)
+    assert np.all(np.isnan(rdx[2])) and np.isnan(rdg).sum() == 2
+    dx, dg = _bwd(x, g, dy, 1e-6, dev)
+    a, b = _nan_class_match(dx, rdx)
+    assert maxabs_rel(a, b) <= TOL
+    a, b = _nan_class_match(dg, rdg)
+    assert maxabs_rel(a, b) <= TOL
+
+
+def test_rms_norm_bwd_nan_row(dev):
+    """A NaN in x: that row's dx and every dscale entry are NaN (it enters every
+    column's sum through normed); the other rows' dx unchanged."""
+    rng = np.random.default_rng(3)
+    x, g, dy = _inputs(rng, (8, 512))
+    x[4, 100] = 0x7FC0
+    with np.errstate(invalid="ignore"):
+        rdx, rdg = norm_ref.rms_norm_vjp(x, g, 1e-6, dy)
+    dx, dg = _bwd(x, g, dy, 1e-6, dev)
+    a, b = _nan_class_match(dx, rdx)
+    assert np.all(np.isnan(rdx[4])) and maxabs_rel(a, b) <= TOL
+    assert torch.all(torch.isnan(dg))
