@@ -1259,6 +1259,10 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
   static_assert(PRO == PRO_X || (XLDS && MT == 1), "the norm prologue takes at most 16 rows");
   // rows of x held in LDS: 16 for the norm prologue, 8 for the copy
   constexpr int XROWS = PRO == PRO_XCOPY ? 8 : 16;
+  // 17..32 rows from x_q: x loaded as whole K-block rows and permuted into
+  // fragments in the wave (half the cache lines per load; at 9..16 rows, one
+  // x tile per K block, it measured no faster)
+  constexpr bool XROW8 = PRO == PRO_X && MT == 2;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 15, fg = lane >> 4;
@@ -1310,6 +1314,34 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
     const uint32_t soff = (rv && lane < 32 && b < nkb) ? ((uint32_t)srow * (uint32_t)nkb + (uint32_t)b) * 4u
                                                        : sbytes;
     wsr[SL] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, soff, 0, 0));
+  };
+
+  // XROW8: the x rows of a chunk -> MFMA fragments, within the wave (the
+  // loads below take whole 128-byte K-block rows, 8 rows per load): lane
+  // (fr, fg) takes chunks fg and 4 + fg of row fr, held by lane (fr % 8) * 8 +
+  // chunk of the load of rows 0..7 (fr < 8) or of rows 8..15.  Run once the
+  // chunk's first stages' loads are issued, so their round trip covers it.
+  auto x_fragments = [&]() {
+    const int s0 = ((fr & 7) * 8 + fg) * 4, s1 = s0 + 16;
+    const bool lo = fr < 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const u32x4_t a = xr[i][mt][0], b = xr[i][mt][1];
+        u32x4_t x0, x1;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t a0 = (uint32_t)__builtin_amdgcn_ds_bpermute(s0, (int)a[d]);
+          const uint32_t b0 = (uint32_t)__builtin_amdgcn_ds_bpermute(s0, (int)b[d]);
+          const uint32_t a1 = (uint32_t)__builtin_amdgcn_ds_bpermute(s1, (int)a[d]);
+          const uint32_t b1 = (uint32_t)__builtin_amdgcn_ds_bpermute(s1, (int)b[d]);
+          x0[d] = lo ? a0 : b0;
+          x1[d] = lo ? a1 : b1;
+        }
+        xr[i][mt][0] = x0;
+        xr[i][mt][1] = x1;
+      }
   };
 
   // stage (c, G): registers -> LDS buffer SL = G % NS, start the loads of stage
@@ -1468,9 +1500,24 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
           xr[i][mt][1] = ok ? *reinterpret_cast<const u32x4_t*>(px + 64) : z;
           sxr[i][mt] = ok ? gemv_xs[m * nkb + kb] : 0.0f;
         } else {
-          const uint32_t xo = ok ? (uint32_t)m * (uint32_t)K + (uint32_t)kb * 128u + fg * 16u : xbytes;
-          xr[i][mt][0] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
-          xr[i][mt][1] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? xo + 64u : xbytes, 0, 0);
+          if constexpr (XROW8) {
+            // whole 128-byte K-block rows, 8 rows per load (one cache line
+            // each, against 16 rows' 64-byte halves for a fragment-shaped
+            // load): lane (r8, c8) takes 16-byte chunk c8 of rows mt*16 + r8
+            // and mt*16 + 8 + r8; x_fragments moves them into the fragment
+            // layout
+            const int r8 = lane >> 3, c8 = lane & 7;
+            const int m1 = mt * 16 + r8, m2 = m1 + 8;
+            const uint32_t kofs = (uint32_t)kb * 128u + c8 * 16u;
+            xr[i][mt][0] = __builtin_amdgcn_raw_buffer_load_b128(
+                rx, m1 < M && kb < nkb ? (uint32_t)m1 * (uint32_t)K + kofs : xbytes, 0, 0);
+            xr[i][mt][1] = __builtin_amdgcn_raw_buffer_load_b128(
+                rx, m2 < M && kb < nkb ? (uint32_t)m2 * (uint32_t)K + kofs : xbytes, 0, 0);
+          } else {
+            const uint32_t xo = ok ? (uint32_t)m * (uint32_t)K + (uint32_t)kb * 128u + fg * 16u : xbytes;
+            xr[i][mt][0] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+            xr[i][mt][1] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? xo + 64u : xbytes, 0, 0);
+          }
           const uint32_t so = ok ? ((uint32_t)m * (uint32_t)nkb + (uint32_t)kb) * 4u : xsbytes;
           sxr[i][mt] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxs, so, 0, 0));
         }
@@ -1481,6 +1528,7 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
       load_w(IntC<1>{}, c, 1);
       if constexpr (NS > 2) load_w(IntC<2 % NS>{}, c, 2);
     }
+    if constexpr (XROW8) x_fragments();
     // every path to stage G runs stages 0 .. G-1 first (early exits only), so
     // the compiler's count of the loads in flight at stage G is exact
     do {
