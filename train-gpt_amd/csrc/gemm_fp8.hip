@@ -1551,19 +1551,23 @@ __global__ __launch_bounds__(512) void gemv_fp8_kernel(const uint8_t* __restrict
     __syncthreads();                      // the next chunk rewrites the stage buffers
   }
 
-  // wave-ordered sum of the partial tiles through LDS (stage memory reused), one
-  // pass per x-row tile: lane (fr, fg) of pair tile P holds rows
-  // 8(2P + fg / 2) + 4(fg % 2) .. +3, so each wave stores its 4 pair tiles (32
-  // KiB for the workgroup), and wave g then adds group g's partials of the 8
-  // waves in wave order
-  v4f* red = reinterpret_cast<v4f*>(gemv_lds0);   // [NW][4][64]
+  // wave-ordered sum of the partial tiles through LDS (stage memory reused):
+  // lane (fr, fg) of pair tile P holds rows 8(2P + fg / 2) + 4(fg % 2) .. +3,
+  // so each wave stores its 4 pair tiles of every x-row tile (32 KiB per tile
+  // for the workgroup, tile mt in stage buffer mt), and after one barrier wave
+  // g adds group g's partials of the 8 waves in wave order
+  static_assert(MT <= 2 && NW * (kGemvGroups / 2) * 64 * sizeof(v4f) <= kGemvStage, "partials fit a stage buffer");
   const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    if (mt > 0) __syncthreads();          // the previous pass has read red
+    v4f* red = reinterpret_cast<v4f*>(mt == 0 ? gemv_lds0 : gemv_lds1);   // [NW][4][64]
 #pragma unroll
     for (int pp = 0; pp < kGemvGroups / 2; ++pp) red[(wave * (kGemvGroups / 2) + pp) * 64 + lane] = acc[pp][mt];
-    __syncthreads();
+  }
+  __syncthreads();
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const v4f* red = reinterpret_cast<const v4f*>(mt == 0 ? gemv_lds0 : gemv_lds1);
     const int g = wave;
     const int m = mt * 16 + fr, lr = 8 * g + 4 * fg;
     const int src = (g & 1) * 32 + lane;  // the lane of pair tile g / 2 holding these rows
