@@ -92,6 +92,62 @@ def init_params(cfg: Config, device, seed: int = 0):
     return p
 
 
+_LAYER_KEYS = ("norm1", "wq", "wk", "wv", "wo", "norm2", "w_up", "w_down")
+
+
+def config_from_reference(c) -> Config:
+    """Config from the reference's config object or a dict of its fields
+    (config.py:6-27, as stored under "config" in a checkpoint payload,
+    train_modal.py:402-407); dtype, use_remat and use_pallas_norm do not apply."""
+    get = (lambda k: c[k]) if isinstance(c, dict) else (lambda k: getattr(c, k))
+    kw = {}
+    for f in Config.__dataclass_fields__:
+        try:
+            kw[f] = get(f)
+        except (KeyError, AttributeError):
+            pass
+    return Config(**kw)
+
+
+def _to_bf16(a, device) -> torch.Tensor:
+    """One parameter leaf as a bf16 tensor on device: a torch tensor, or a numpy
+    array in any float dtype, bfloat16 (2-byte, e.g. ml_dtypes' bfloat16 from a
+    checkpoint of jax arrays) taken bit for bit, f16 / f32 / f64 rounded to bf16."""
+    if isinstance(a, torch.Tensor):
+        return a.detach().to(device=device, dtype=torch.bfloat16)
+    a = np.asarray(a)
+    if a.dtype.name == "bfloat16" and a.dtype.itemsize == 2:
+        t = torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)
+        return t.to(device)
+    if a.dtype.kind != "f":
+        raise TypeError(f"parameter of dtype {a.dtype} is not a float array")
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(device).to(torch.bfloat16)
+
+
+def params_from_reference(tree, device) -> dict:
+    """The reference's parameter tree (model.py:19-54, e.g. the "params" of a
+    checkpoint payload, train_modal.py:402-407, after the caller has loaded it)
+    as this module's parameters: bf16 tensors on device, "layers" a list of
+    per-layer dicts.  The reference stacks the layers' leaves along a leading
+    n_layers axis (jax.vmap of init_layer, model.py:44); a list of per-layer
+    dicts is taken as it is."""
+    layers = tree["layers"]
+    if isinstance(layers, dict):
+        missing = [k for k in _LAYER_KEYS if k not in layers]
+        if missing:
+            raise KeyError(f"layers is missing {missing}")
+        n = len(layers["norm1"])
+        for k in _LAYER_KEYS:
+            if len(layers[k]) != n:
+                raise ValueError(f"layers[{k!r}] stacks {len(layers[k])} layers, norm1 stacks {n}")
+        layers = [{k: layers[k][i] for k in _LAYER_KEYS} for i in range(n)]
+    out = {k: _to_bf16(tree[k], device) for k in ("embed", "pos", "final_norm")}
+    if "unembed" in tree:
+        out["unembed"] = _to_bf16(tree["unembed"], device)
+    out["layers"] = [{k: _to_bf16(lp[k], device) for k in _LAYER_KEYS} for lp in layers]
+    return out
+
+
 def _check_fp8_dims(cfg: Config):
     h = cfg.n_heads * cfg.head_dim
     for name, k in (("d_model", cfg.d_model), ("n_heads*head_dim", h), ("d_ff", cfg.d_ff)):
@@ -133,6 +189,9 @@ def decode_attention(qkv: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
 class FP8Decoder:
     """The reference model (model.py) with kept FP8 weights and a KV cache.
 
+    params: this module's layout (init_params) or the reference's tree with
+    the layers stacked (model.py:19-54, e.g. a checkpoint's "params"), whose
+    numpy leaves go to the current GPU (params_from_reference).
     layout: scale layout of the kept weights, "128x128" (one scale per
     128x128 tile, the baseline's decode config) or "128x1" (per column, the
     bytes and scales fp8.py:68 computes on every call).
@@ -156,6 +215,10 @@ class FP8Decoder:
     def __init__(self, params, cfg: Config, layout: str = "128x128", max_batch: int = 1,
                  decode_attn: str = "hip", exact_gemv: bool = None, fused: bool = None):
         _check_fp8_dims(cfg)
+        if isinstance(params["layers"], dict) or not isinstance(params["embed"], torch.Tensor):
+            dev = (params["embed"].device if isinstance(params["embed"], torch.Tensor)
+                   else torch.device("cuda", torch.cuda.current_device()))
+            params = params_from_reference(params, dev)
         if decode_attn not in ("hip", "sdpa"):
             raise ValueError("decode_attn must be 'hip' or 'sdpa'")
         self.decode_attn = decode_attn
