@@ -296,3 +296,32 @@ def test_fused_gemv_errors(dev):
         xr = torch.zeros((rows, 256), dtype=torch.bfloat16, device=dev)
         with pytest.raises(ValueError, match="must not overlap"):
             qw2.matmul_rms_norm(xr, g2, 1e-6, delta=torch.zeros_like(xr), xout=xr)
+
+
+@pytest.mark.parametrize("layout", ["128x1", "128x128"])
+@pytest.mark.parametrize("M,exact,N", [(1, False, 12288), (1, True, 12288), (8, True, 12288), (8, True, 2048),
+                                       (24, True, 12288), (32, True, 12288), (32, True, 2048)])
+def test_gemv_non_finite_operands(dev, layout, M, exact, N):
+    """NaN / inf through every GEMV kernel (VALU, x-copy MFMA, direct, 17-32
+    rows from x_q): an inf in W makes its scale block's scale inf, so the
+    outputs of its 128x1 column, or of its whole 128-row tile with 128x128
+    scales (0 x inf), are NaN; a NaN in x makes its row NaN; exactly where the
+    float64 oracle has them, the rest within the usual bar."""
+    K = 1024
+    rng = np.random.default_rng(M + N)
+    w = ob.randn_bf16(rng, (K, N), std=0.02)
+    w[5, 700] = 0x7F80                               # +inf: W.T row 700, K block 0
+    x = ob.randn_bf16(rng, (M, K))
+    nan_rows = 1 if M > 1 else 0                     # (with one row a NaN leaves nothing finite)
+    if nan_rows:
+        x[M - 1, 300] = 0x7FC0                       # NaN in the last row, K block 2
+    wq, ws, bn = fp8.quantize_weight(to_dev(w, dev), layout=layout)
+    out = fp8.fp8_gemv(to_dev(x, dev), wq, ws, w_scale_bn=bn, exact=exact).float().cpu().numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        qx, sx = fp8_ref.quantize_fp8(ob.bf16_to_f32(x))
+        ref = fp8_ref.gemv_prequant(qx, sx, u8(wq), ws.cpu().numpy(), bn)
+    nan_ref = np.isnan(ref)
+    cols = 1 if layout == "128x1" else 128
+    assert nan_ref.sum() == (M - nan_rows) * cols + nan_rows * N
+    np.testing.assert_array_equal(np.isnan(out), nan_ref)
+    assert maxabs_rel(out[~nan_ref], ref[~nan_ref]) <= 1e-2
