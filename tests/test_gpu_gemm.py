@@ -408,3 +408,29 @@ def test_composite_forward_non_finite_operands(dev):
     qw, sw = fp8.quantize_fp8(to_dev(b, dev), transpose=True)
     np.testing.assert_array_equal(u8(qw), qb)
     assert same_scales(sw.cpu().numpy(), sb)
+
+
+def test_fp8_backward_non_finite_operands(dev):
+    """NaN / +-inf through the FP8 backward (dX = fwd(g, b.T), dW = fwd(a.T, g)):
+    a NaN in g poisons its row of dX and its column of dW, an inf in a its row
+    of dW (the K index), an inf in b its column of dX; exactly where the float64
+    oracle has NaN, the rest within the bar."""
+    rng = np.random.default_rng(11)
+    M, N, K = 256, 384, 256
+    a_u = ob.randn_bf16(rng, (M, K))
+    b_u = ob.randn_bf16(rng, (K, N), std=0.02)
+    g_u = ob.randn_bf16(rng, (M, N), std=1e-3)
+    g_u[3, 10] = 0x7FC0                             # NaN: dX row 3, dW column 10
+    a_u[7, 200] = 0x7F80                            # +inf: dW row 200
+    b_u[5, 9] = 0xFF80                              # -inf: dX column 5
+    a = to_dev(a_u, dev).requires_grad_(True)
+    b = to_dev(b_u, dev).requires_grad_(True)
+    fp8.block_scaled_matmul(a, b).backward(to_dev(g_u, dev))
+    with np.errstate(invalid="ignore", over="ignore"):
+        dx_ref, dw_ref, _ = fp8_ref.fp8_backward_fp8(a_u, b_u, g_u)
+    assert np.isnan(dx_ref).sum() == K + M - 1 and np.isnan(dw_ref).sum() == N + K - 1
+    for got, ref in ((a.grad, dx_ref), (b.grad, dw_ref)):
+        g = got.float().cpu().numpy()
+        np.testing.assert_array_equal(np.isnan(g), np.isnan(ref))
+        m = ~np.isnan(ref)
+        assert maxabs_rel(g[m], ref[m]) <= TOL
