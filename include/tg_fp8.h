@@ -290,6 +290,21 @@ int tg_rms_norm_fp8_gemv(const void* x, const void* delta, const void* gamma, fl
 int tg_relu2_fp8_gemv(const void* u, const uint8_t* w_q, const float* w_s, int w_scale_bn, void* out,
                       int64_t M, int64_t N, int64_t K, void* stream);
 
+/* The residual adds of model.py:75-76 (x = x + attn(...), x = x + mlp(...))
+ * fused into the decode GEMV that produces their term (no reference
+ * counterpart; one or two rows): out (M, N) = bf16(resid + bf16(h @ W^T)),
+ * h from x_q / x_s as tg_gemv_fp8_rowdot or from relu(u)^2 as
+ * tg_relu2_fp8_gemv; the same bits as that entry point followed by the bf16
+ * tensor add (f32 sum of the two bf16 values, rounded once).  resid (M, N)
+ * bf16, 2-byte aligned; out may be resid itself (the residual stream updated
+ * in place), any other overlap is refused.  M <= 2, K <= 16384.  The norm that
+ * follows then needs no add of its own (tg_rms_norm_fp8_gemv, delta == NULL). */
+int tg_gemv_fp8_rowdot_add(const uint8_t* x_q, const float* x_s, const uint8_t* w_q, const float* w_s,
+                           int w_scale_bn, const void* resid, void* out, int64_t M, int64_t N, int64_t K,
+                           int block_k, void* stream);
+int tg_relu2_fp8_gemv_add(const void* u, const uint8_t* w_q, const float* w_s, int w_scale_bn,
+                          const void* resid, void* out, int64_t M, int64_t N, int64_t K, void* stream);
+
 /* Quantize W.T into the pre-quantized weight format with one scale per
  * 128x128 tile (w_scale_bn == 128).  w: (K, N) bf16; w_q (N, K); w_s (ceil(N/128), K/128). */
 int tg_quantize_weight_128x128(const void* w, int64_t K, int64_t N, uint8_t* w_q, float* w_s,

@@ -72,6 +72,10 @@ CASES = {
                              (N, N, N, 1e-6, N, N, N, 1, N, 0, 16, 256, N)),
     "tg_relu2_fp8_gemv": ((N, N, N, 1, N, 1, 16, 256, N), (N, N, N, 1, N, -1, 16, 256, N),
                           (N, N, N, 1, N, 0, 16, 256, N)),
+    "tg_gemv_fp8_rowdot_add": ((N, N, N, N, 1, N, N, 1, 16, 256, 128, N), (N, N, N, N, 1, N, N, -1, 16, 256, 128, N),
+                               (N, N, N, N, 1, N, N, 0, 16, 256, 128, N)),
+    "tg_relu2_fp8_gemv_add": ((N, N, N, 1, N, N, 1, 16, 256, N), (N, N, N, 1, N, N, -1, 16, 256, N),
+                              (N, N, N, 1, N, N, 0, 16, 256, N)),
     "tg_quantize_weight_128x128": ((N, 256, 16, N, N, N), (N, 256, -16, N, N, N), (N, 256, 0, N, N, N)),
     "tg_decode_attention": ((N, N, N, N, N, N, N, 1, 2, 16, 128, 0.1, N), (N, N, N, N, N, N, N, -1, 2, 16, 128, 0.1, N),
                             (N, N, N, N, N, N, N, 0, 2, 16, 128, 0.1, N)),

@@ -325,3 +325,46 @@ def test_gemv_non_finite_operands(dev, layout, M, exact, N):
     assert nan_ref.sum() == (M - nan_rows) * cols + nan_rows * N
     np.testing.assert_array_equal(np.isnan(out), nan_ref)
     assert maxabs_rel(out[~nan_ref], ref[~nan_ref]) <= 1e-2
+
+
+# ------------------------------------------------- residual adds in the GEMV store
+# tg_gemv_fp8_rowdot_add / tg_relu2_fp8_gemv_add: out = bf16(resid + the plain
+# entry point's output), the bf16 tensor add (torch's bf16 + rounds the f32 sum
+# once, as model.py:75-76's jax adds do); out may be resid itself.
+RESID_ADD = [(1, 1, 128), (2, 77, 640), (1, 2304, 2304), (2, 2304, 2304), (1, 2304, 9216), (2, 513, 16384),
+             (1, 14336, 4096)]
+
+
+@pytest.mark.parametrize("layout", ["128x1", "128x128"])
+@pytest.mark.parametrize("M,N,K", RESID_ADD)
+def test_gemv_residual_add_same_bits(dev, M, N, K, layout):
+    rng = np.random.default_rng(M * 131 + N + K)
+    resid = to_dev(_bf16_rows(rng, M, N), dev)
+    w = to_dev(ob.randn_bf16(rng, (K, N), std=0.02), dev)
+    qw = fp8.QuantizedWeight.from_weight(w, layout)
+    # projection of already-quantized rows (the o projection of a decode step)
+    q, s = fp8.quantize_fp8(to_dev(_bf16_rows(rng, M, K), dev))
+    want = resid + qw.matmul_prequant(q, s)
+    got = qw.matmul_prequant_add(q, s, resid)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    inplace = resid.clone()
+    qw.matmul_prequant_add(q, s, inplace, out=inplace)
+    assert torch.equal(inplace.view(torch.int16), want.view(torch.int16))
+    # relu^2 of u, then the projection (the down projection)
+    u = to_dev(_bf16_rows(rng, M, K), dev)
+    want = resid + qw.matmul_relu2(u)
+    got = qw.matmul_relu2_add(u, resid)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    inplace = resid.clone()
+    qw.matmul_relu2_add(u, inplace, out=inplace)
+    assert torch.equal(inplace.view(torch.int16), want.view(torch.int16))
+
+
+def test_gemv_residual_add_refuses_partial_overlap(dev):
+    rng = np.random.default_rng(3)
+    qw = fp8.QuantizedWeight.from_weight(to_dev(ob.randn_bf16(rng, (256, 64), std=0.02), dev), "128x128")
+    q, s = fp8.quantize_fp8(to_dev(_bf16_rows(rng, 1, 256), dev))
+    buf = torch.zeros(130, dtype=torch.bfloat16, device=dev)
+    resid, out = buf[:64].view(1, 64), buf[2:66].view(1, 64)
+    with pytest.raises(ValueError, match="out must be resid itself or not overlap it"):
+        qw.matmul_prequant_add(q, s, resid, out=out)

@@ -50,6 +50,8 @@ SIGNATURES = {
     "tg_gemv_fp8_rowdot": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _i64, _i64, _i64, _int, _vp]),
     "tg_rms_norm_fp8_gemv": (_int, [_vp, _vp, _vp, _f32, _vp, _vp, _vp, _int, _vp, _i64, _i64, _i64, _vp]),
     "tg_relu2_fp8_gemv": (_int, [_vp, _vp, _vp, _int, _vp, _i64, _i64, _i64, _vp]),
+    "tg_gemv_fp8_rowdot_add": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
+    "tg_relu2_fp8_gemv_add": (_int, [_vp, _vp, _vp, _int, _vp, _vp, _i64, _i64, _i64, _vp]),
     "tg_quantize_weight_128x128": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "tg_gemm_bf16_nt": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "tg_pack_bf16": (_int, [_vp, _int, _i64, _i64, _int, _vp, _i64, _vp]),

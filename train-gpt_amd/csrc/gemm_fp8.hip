@@ -1862,6 +1862,7 @@ struct RowdotIn {
   const uint4* delta;     // PRO_NORM_ADD: (M, K) bf16
   const uint4* gamma;     // PRO_NORM*: (K,) bf16
   uint4* xout;            // PRO_NORM_ADD: (M, K) bf16 residual sum (workgroup 0 stores it)
+  const __bf16* resid;    // RES: (M, N) bf16 residual; out = bf16(resid + bf16(dot))
   float eps;
 };
 
@@ -1909,7 +1910,7 @@ __device__ __forceinline__ void rowdot_compute(const RowdotUnit& U, const uint8_
 // (4 for PRO_X; 8 for the computing prologues, whose bf16 row loads every
 // workgroup repeats: 8 waves measured best of 4, 8 and 16 at the decode
 // shapes).
-template <int NX, int PRO, int XL, int J, int WPG>
+template <int NX, int PRO, int XL, int J, int WPG, bool RES>
 __global__ __launch_bounds__(64 * WPG) void gemv_rowdot_kernel(RowdotIn in, const uint8_t* __restrict__ WQ,
                                                           const float* __restrict__ WS, int bns,
                                                           __bf16* __restrict__ out, int N, int K,
@@ -2066,7 +2067,15 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rowdot_kernel(RowdotIn in, cons
       const int r = gw + ((jr & ~63) + lane) * nw;
       if (lane <= (jr & 63)) {
 #pragma unroll
-        for (int m = 0; m < NX; ++m) out[(int64_t)m * N + r] = (__bf16)res[m];
+        for (int m = 0; m < NX; ++m) {
+          const int64_t o = (int64_t)m * N + r;
+          if constexpr (RES) {   // the bf16 tensor add: f32 sum of the two bf16 values, rounded once
+            const float sum = (float)in.resid[o] + (float)(__bf16)res[m];
+            out[o] = __builtin_bit_cast(__bf16, (uint16_t)(pack_bf16x2(sum, 0.0f) & 0xFFFFu));
+          } else {
+            out[o] = (__bf16)res[m];
+          }
+        }
       }
     }
   };
@@ -2585,7 +2594,7 @@ extern "C" int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* 
   return launch_gemm_fp8(x_q, x_s, w_q, w_s, w_scale_bn, out, TG_DTYPE_BF16, M, N, K, st, false);
 }
 
-template <int NX, int PRO, int XL, int J, int WPG = 4>
+template <int NX, int PRO, int XL, int J, int WPG = 4, bool RES = false>
 static void launch_rowdot_k(const RowdotIn& in, const uint8_t* w_q, const float* w_s, int bns, __bf16* o,
                             int n, int k, int sx_off, size_t lds, hipStream_t st) {
   // persistent waves, one wave per weight row at a time: as many workgroups
@@ -2594,7 +2603,7 @@ static void launch_rowdot_k(const RowdotIn& in, const uint8_t* w_q, const float*
   // slot (a function-local static: its initializer runs once, thread-safely)
   static const int occ_regs = [] {
     int v = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_rowdot_kernel<NX, PRO, XL, J, WPG>, 64 * WPG, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_rowdot_kernel<NX, PRO, XL, J, WPG, RES>, 64 * WPG, 0) !=
             hipSuccess || v <= 0)
       v = 16 / WPG;
     return v;
@@ -2604,23 +2613,23 @@ static void launch_rowdot_k(const RowdotIn& in, const uint8_t* w_q, const float*
   const int by_lds = (int)((160 * 1024) / (lds > 0 ? lds : 1));
   if (by_lds < per_cu) per_cu = by_lds < 1 ? 1 : by_lds;
   const int64_t wgs = ((int64_t)n + WPG - 1) / WPG, cap = (int64_t)per_cu * device_cus();
-  hipLaunchKernelGGL((gemv_rowdot_kernel<NX, PRO, XL, J, WPG>), dim3((unsigned)(wgs < cap ? wgs : cap)),
+  hipLaunchKernelGGL((gemv_rowdot_kernel<NX, PRO, XL, J, WPG, RES>), dim3((unsigned)(wgs < cap ? wgs : cap)),
                      dim3(64 * WPG), lds, st, in, w_q, w_s, bns, o, n, k, sx_off);
 }
 
 // PRO_X: XL 4 KiB pieces of x; PRO_RELU2: XL 16-byte chunks of u per thread;
 // PRO_NORM*: J chunks of the norm row per lane.
-template <int NX, int PRO>
+template <int NX, int PRO, bool RES = false>
 static int launch_rowdot(const RowdotIn& in, const uint8_t* w_q, const float* w_s, int bns, __bf16* o,
                          int n, int k, hipStream_t st) {
   if constexpr (PRO == PRO_X) {
     const int need = (NX * k + 4095) / 4096;
     const int sx_off = (need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8) * 4096;
     const size_t lds = (size_t)sx_off + 1024;
-    if (need <= 1) launch_rowdot_k<NX, PRO, 1, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-    else if (need <= 2) launch_rowdot_k<NX, PRO, 2, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-    else if (need <= 4) launch_rowdot_k<NX, PRO, 4, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-    else launch_rowdot_k<NX, PRO, 8, 1>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+    if (need <= 1) launch_rowdot_k<NX, PRO, 1, 1, 4, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+    else if (need <= 2) launch_rowdot_k<NX, PRO, 2, 1, 4, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+    else if (need <= 4) launch_rowdot_k<NX, PRO, 4, 1, 4, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+    else launch_rowdot_k<NX, PRO, 8, 1, 4, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
   } else {
     const int sx_off = NX * k;   // a multiple of 128
     // x bytes, x scales; for the norm prologues also the bf16 residual sums and r
@@ -2631,18 +2640,18 @@ static int launch_rowdot(const RowdotIn& in, const uint8_t* w_q, const float* w_
     constexpr int W = kRowdotProWaves;
     if constexpr (PRO == PRO_RELU2) {
       const int need = (NX * k / 8 + 64 * W - 1) / (64 * W);   // 16-byte chunks of u per thread
-      if (need <= 1) launch_rowdot_k<NX, PRO, 1, 1, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (need <= 2) launch_rowdot_k<NX, PRO, 2, 1, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (need <= 4) launch_rowdot_k<NX, PRO, 4, 1, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (need <= 8) launch_rowdot_k<NX, PRO, 8, 1, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else launch_rowdot_k<NX, PRO, 16, 1, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      if (need <= 1) launch_rowdot_k<NX, PRO, 1, 1, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (need <= 2) launch_rowdot_k<NX, PRO, 2, 1, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (need <= 4) launch_rowdot_k<NX, PRO, 4, 1, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (need <= 8) launch_rowdot_k<NX, PRO, 8, 1, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else launch_rowdot_k<NX, PRO, 16, 1, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
     } else {
       const int jneed = (k / 8 + 63) / 64;
-      if (jneed <= 1) launch_rowdot_k<NX, PRO, 1, 1, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (jneed <= 2) launch_rowdot_k<NX, PRO, 1, 2, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (jneed <= 4) launch_rowdot_k<NX, PRO, 1, 4, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (jneed <= 5) launch_rowdot_k<NX, PRO, 1, 5, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else launch_rowdot_k<NX, PRO, 1, 8, W>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      if (jneed <= 1) launch_rowdot_k<NX, PRO, 1, 1, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (jneed <= 2) launch_rowdot_k<NX, PRO, 1, 2, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (jneed <= 4) launch_rowdot_k<NX, PRO, 1, 4, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (jneed <= 5) launch_rowdot_k<NX, PRO, 1, 5, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else launch_rowdot_k<NX, PRO, 1, 8, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
     }
   }
   return TG_OK;
@@ -2775,4 +2784,59 @@ extern "C" int tg_relu2_fp8_gemv(const void* u, const uint8_t* w_q, const float*
   if (M == 1) TG_TRY((launch_rowdot<1, PRO_RELU2>(in, w_q, w_s, w_scale_bn, o, (int)N, (int)K, st)));
   else TG_TRY((launch_rowdot<2, PRO_RELU2>(in, w_q, w_s, w_scale_bn, o, (int)N, (int)K, st)));
   return check_launch("relu2_fp8_gemv");
+}
+
+// The residual adds of model.py:75-76 fused into the GEMV that produces their
+// term (1-2 rows, the VALU GEMV): out (M, N) = bf16(resid + bf16(x . W^T)),
+// the bf16 tensor add of the plain entry point's output.  out may be resid
+// itself (each element is read and written by one lane); any other overlap
+// is refused.
+static int rowdot_add_checks(const char* who, const void* resid, const void* out, int64_t M, int64_t N) {
+  char msg[160];
+  const char* what = nullptr;
+  if (!resid) what = "null pointer";
+  else if (!aligned(resid, 2)) what = "resid must be 2-byte aligned";
+  else if (out != resid && ranges_overlap(out, resid, (size_t)M * (size_t)N * 2))
+    what = "out must be resid itself or not overlap it";
+  if (!what) return TG_OK;
+  snprintf(msg, sizeof(msg), "%s: %s", who, what);
+  return einval(msg);
+}
+
+extern "C" int tg_gemv_fp8_rowdot_add(const uint8_t* x_q, const float* x_s, const uint8_t* w_q,
+                                      const float* w_s, int w_scale_bn, const void* resid, void* out,
+                                      int64_t M, int64_t N, int64_t K, int block_k, void* stream) {
+  if (block_k != 128) return einval("block_k must be 128");
+  TG_TRY(rowdot_common_checks("gemv_fp8_rowdot_add", M, N, K, w_scale_bn, w_q, w_s, out, kRowdotMaxK));
+  if (M == 0 || N == 0) return TG_OK;
+  if (!x_q || !x_s) return einval("gemv_fp8_rowdot_add: null pointer");
+  if (!aligned(x_q, 16)) return einval("gemv_fp8_rowdot_add: operands must be 16-byte aligned");
+  TG_TRY(rowdot_add_checks("gemv_fp8_rowdot_add", resid, out, M, N));
+  RowdotIn in{};
+  in.xq = x_q;
+  in.xs = x_s;
+  in.resid = reinterpret_cast<const __bf16*>(resid);
+  auto o = reinterpret_cast<__bf16*>(out);
+  hipStream_t st = as_stream(stream);
+  if (M == 1) TG_TRY((launch_rowdot<1, PRO_X, true>(in, w_q, w_s, w_scale_bn, o, (int)N, (int)K, st)));
+  else TG_TRY((launch_rowdot<2, PRO_X, true>(in, w_q, w_s, w_scale_bn, o, (int)N, (int)K, st)));
+  return check_launch("gemv_fp8_rowdot_add");
+}
+
+extern "C" int tg_relu2_fp8_gemv_add(const void* u, const uint8_t* w_q, const float* w_s, int w_scale_bn,
+                                     const void* resid, void* out, int64_t M, int64_t N, int64_t K,
+                                     void* stream) {
+  TG_TRY(rowdot_common_checks("relu2_fp8_gemv_add", M, N, K, w_scale_bn, w_q, w_s, out, kRowdotMaxK));
+  if (M == 0 || N == 0) return TG_OK;
+  if (!u) return einval("relu2_fp8_gemv_add: null pointer");
+  if (!aligned(u, 16)) return einval("relu2_fp8_gemv_add: u must be 16-byte aligned");
+  TG_TRY(rowdot_add_checks("relu2_fp8_gemv_add", resid, out, M, N));
+  RowdotIn in{};
+  in.x = reinterpret_cast<const uint4*>(u);
+  in.resid = reinterpret_cast<const __bf16*>(resid);
+  auto o = reinterpret_cast<__bf16*>(out);
+  hipStream_t st = as_stream(stream);
+  if (M == 1) TG_TRY((launch_rowdot<1, PRO_RELU2, true>(in, w_q, w_s, w_scale_bn, o, (int)N, (int)K, st)));
+  else TG_TRY((launch_rowdot<2, PRO_RELU2, true>(in, w_q, w_s, w_scale_bn, o, (int)N, (int)K, st)));
+  return check_launch("relu2_fp8_gemv_add");
 }

@@ -353,13 +353,32 @@ class FP8Decoder:
 
     def _step_dev_fused(self, tok: torch.Tensor, t: torch.Tensor, B: int) -> torch.Tensor:
         """_step_dev with each norm / relu^2 quantization inside the GEMV that
-        consumes it.  The residual stream alternates between two buffers
-        (a fused kernel reads one while its workgroup 0 writes the other)."""
+        consumes it.  At 1-2 rows the residual adds (model.py:75-76) run in the
+        stores of the o and down projections, on the residual stream in place,
+        so the norms after them have no add of their own; at 3-16 rows the
+        norm GEMV adds, and the residual stream alternates between two
+        buffers (a fused kernel reads one while its workgroup 0 writes the
+        other).  The same bits either way."""
         cfg = self.cfg
         H, eps = cfg.n_heads, cfg.rms_eps
         xa = self.embed[tok] + self.pos.index_select(0, t)                # (B, d)
-        xb = torch.empty_like(xa)
         qkv = self.layers[0]["wqkv"].matmul_rms_norm(xa, self.layers[0]["norm1"], eps)   # model.py:61-64
+        if B <= 2:
+            for li, lp in enumerate(self.layers):
+                if self.decode_attn == "hip":
+                    o_q, o_s, _ = decode_attention(qkv, self.k_cache[li], self.v_cache[li], t, H)
+                else:
+                    o_q, o_s = fp8.quantize_fp8(self._sdpa_step(li, qkv, int(t.item())))
+                lp["wo"].matmul_prequant_add(o_q, o_s, xa, out=xa)          # x += o wo (model.py:68, 75)
+                u = lp["w_up"].matmul_rms_norm(xa, lp["norm2"], eps)        # model.py:71, 75
+                lp["w_down"].matmul_relu2_add(u, xa, out=xa)                # x += relu(u)^2 w_down (72, 76)
+                last = li + 1 == len(self.layers)
+                nxt = self.final_norm if last else self.layers[li + 1]["norm1"]
+                w = self.unembed if last else self.layers[li + 1]["wqkv"]
+                qkv = w.matmul_rms_norm(xa, nxt, eps)
+            logits = qkv.float()
+            return cfg.logit_cap * torch.tanh(logits / cfg.logit_cap)       # model.py:97
+        xb = torch.empty_like(xa)
         for li, lp in enumerate(self.layers):
             if self.decode_attn == "hip":
                 o_q, o_s, _ = decode_attention(qkv, self.k_cache[li], self.v_cache[li], t, H)
@@ -368,10 +387,7 @@ class FP8Decoder:
                 a = lp["wo"].matmul(self._sdpa_step(li, qkv, int(t.item())))
             # x = x + a (model.py:75), norm2, w_up (model.py:71-72)
             u = lp["w_up"].matmul_rms_norm(xa, lp["norm2"], eps, delta=a, xout=xb)
-            if B <= 2:
-                m = lp["w_down"].matmul_relu2(u)                            # model.py:72-73
-            else:
-                m = lp["w_down"].matmul_prequant(*fp8.quantize_relu2(u))
+            m = lp["w_down"].matmul_prequant(*fp8.quantize_relu2(u))        # model.py:72-73
             # x = x + m (model.py:76), then the next layer's norm1 and q|k|v, or
             # the final norm and the unembedding (model.py:93-96)
             last = li + 1 == len(self.layers)

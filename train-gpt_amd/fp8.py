@@ -702,6 +702,52 @@ class QuantizedWeight:
                                             self.bn, _L.ptr(out), u.shape[0], N, K, _L.stream_of(u)))
         return out
 
+    def _check_resid(self, x, resid, out, who):
+        M, N = x.shape[0], self.shape[1]
+        if resid.shape != (M, N) or resid.dtype != torch.bfloat16 or not resid.is_contiguous():
+            raise ValueError(f"{who}: resid must be a contiguous bf16 ({M}, {N}) tensor")
+        if out is None:
+            return torch.empty_like(resid)
+        if out.shape != resid.shape or out.dtype != torch.bfloat16 or not out.is_contiguous():
+            raise ValueError(f"{who}: out must be a contiguous bf16 tensor of resid's shape")
+        return out
+
+    def matmul_prequant_add(self, x_q: torch.Tensor, x_s: torch.Tensor, resid: torch.Tensor,
+                            out: torch.Tensor = None) -> torch.Tensor:
+        """The residual add of model.py:75-76 fused into the GEMV of its term, 1-2
+        rows: out = bf16(resid + matmul_prequant(x_q, x_s)) (tg_gemv_fp8_rowdot_add,
+        the same bits as the bf16 tensor add after the VALU GEMV).  out may be
+        resid itself (in place); by default a new tensor."""
+        M, K = x_q.shape
+        if K != self.shape[0]:
+            raise ValueError(f"contracted-dim mismatch: a K={K}, b K={self.shape[0]}")
+        if not 1 <= M <= 2 or K > ROWDOT_MAX_K:
+            raise ValueError(f"matmul_prequant_add: 1-2 rows with K <= {ROWDOT_MAX_K}")
+        out = self._check_resid(x_q, resid, out, "matmul_prequant_add")
+        _L.require_gpu(x_q, self.q)
+        xq = x_q.view(torch.uint8).contiguous()
+        xs = x_s.contiguous().float()
+        _L.check(_L.lib().tg_gemv_fp8_rowdot_add(
+            _L.ptr(xq), _L.ptr(xs), _L.ptr(self.q.view(torch.uint8)), _L.ptr(self.scales), self.bn,
+            _L.ptr(resid), _L.ptr(out), M, self.shape[1], K, self.block_k, _L.stream_of(xq)))
+        return out
+
+    def matmul_relu2_add(self, u: torch.Tensor, resid: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
+        """out = bf16(resid + matmul_relu2(u)) for 1-2 rows (tg_relu2_fp8_gemv_add):
+        model.py:72-76's MLP down projection and residual add in one launch, the
+        same bits as matmul_relu2 followed by the bf16 tensor add.  out may be
+        resid itself."""
+        K, N = self.shape
+        if u.dim() != 2 or u.shape[1] != K or u.dtype != torch.bfloat16 or not 1 <= u.shape[0] <= 2:
+            raise ValueError(f"matmul_relu2_add: u must be bf16 (1 or 2, {K})")
+        out = self._check_resid(u, resid, out, "matmul_relu2_add")
+        _L.require_gpu(u, self.q)
+        u = u.contiguous()
+        _L.check(_L.lib().tg_relu2_fp8_gemv_add(_L.ptr(u), _L.ptr(self.q.view(torch.uint8)), _L.ptr(self.scales),
+                                                self.bn, _L.ptr(resid), _L.ptr(out), u.shape[0], N, K,
+                                                _L.stream_of(u)))
+        return out
+
     def state_dict(self):
         return {"q": self.q, "scales": self.scales}
 
