@@ -137,8 +137,9 @@ int tg_block_scaled_matmul(const void* a, const void* b, void* out, int64_t M, i
  * allocate (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  No counterpart in the reference.  The quantized
  * operands live in a static device array of TG_NOALLOC_SCRATCH_BYTES (each
- * device the library runs on holds it until the process ends), whose address
- * is resolved once per device; the call allocates nothing.  Shapes whose
+ * device this entry point has run on holds it from that first call until the
+ * process ends), whose address is resolved once per device; the call
+ * allocates nothing.  Shapes whose
  * workspace (tg_block_scaled_matmul_workspace) exceeds it return TG_EINVAL;
  * C3's forward (8192 x 2048 x 8192) needs 34.6 MB.  Output bits equal
  * tg_block_scaled_matmul's.  All calls on one device share the array: calls

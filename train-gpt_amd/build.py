@@ -17,7 +17,7 @@ LIB = os.path.join(HERE, "libtg_fp8.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["quant.hip", "rmsnorm.hip", "gemm_fp8.hip", "gemm_bf16.hip", "attention.hip",
-           "xent.hip", "block_generic.hip"]
+           "xent.hip", "block_generic.hip", "noalloc.hip"]
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 (plain f32 VALU only).
 # -ffp-contract=off: every multiply/add in the numeric contract stays a single

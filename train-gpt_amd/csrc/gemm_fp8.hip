@@ -2122,8 +2122,8 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rowdot_kernel(RowdotIn in, cons
 using namespace tg;
 
 // any_block: the entry has the general path for block_k != 128 (block_generic.hip)
-static int check_gemm_args(const char* who, int64_t M, int64_t N, int64_t K, int block_k, int bns,
-                           bool any_block = false) {
+int tg::check_gemm_args(const char* who, int64_t M, int64_t N, int64_t K, int block_k, int bns,
+                        bool any_block) {
   if (any_block ? block_k <= 0 : block_k != 128)
     return einval(any_block ? "block_k must be positive" : "block_k must be 128");
   if (M < 0 || N < 0 || K <= 0) return einval("bad GEMM shape");
@@ -2184,8 +2184,8 @@ extern "C" size_t tg_block_scaled_matmul_workspace(int64_t M, int64_t N, int64_t
 }
 
 // The forward composite's kernels on a workspace the caller has checked.
-static int block_scaled_matmul_on(const void* a, const void* b, void* out, int64_t M, int64_t N,
-                                  int64_t K, void* workspace, hipStream_t st) {
+int tg::block_scaled_matmul_on(const void* a, const void* b, void* out, int64_t M, int64_t N,
+                               int64_t K, void* workspace, hipStream_t st) {
   const int64_t nkb = K / 128;
   uint8_t* p = reinterpret_cast<uint8_t*>(workspace);
   uint8_t* qa = p;                 p += align256((size_t)M * K);
@@ -2249,60 +2249,6 @@ extern "C" int tg_block_scaled_matmul(const void* a, const void* b, void* out, i
   if (!aligned(workspace, 256) || !aligned(a, 16) || !aligned(b, 16))
     return einval("block_scaled_matmul: a, b must be 16-byte and workspace 256-byte aligned");
   return block_scaled_matmul_on(a, b, out, M, N, K, workspace, as_stream(stream));
-}
-
-// Static workspace of tg_block_scaled_matmul_noalloc: every device the
-// library runs on holds its own copy from module load until the process
-// ends.  The array's name is a host-side handle, not a device address: host
-// code only uses the per-device address hipGetSymbolAddress returns.
-constexpr size_t kScratchBytes = TG_NOALLOC_SCRATCH_BYTES;
-static __device__ __align__(256) uint8_t scratch[kScratchBytes];
-
-// scratch's address on the current device, resolved once per device (with
-// that device current) and kept; null with the error set if it fails.
-static uint8_t* scratch_on_current_device() {
-  constexpr int kMaxDev = 64;
-  static std::once_flag once[kMaxDev];
-  static uint8_t* addr[kMaxDev];
-  static hipError_t rc[kMaxDev];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
-    set_error("block_scaled_matmul_noalloc: no usable current device");
-    return nullptr;
-  }
-  std::call_once(once[dev], [dev] {
-    void* p = nullptr;
-    rc[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    addr[dev] = rc[dev] == hipSuccess ? reinterpret_cast<uint8_t*>(p) : nullptr;
-  });
-  if (rc[dev] != hipSuccess || !addr[dev]) {
-    set_error("block_scaled_matmul_noalloc: hipGetSymbolAddress(scratch) failed: %s",
-              hipGetErrorString(rc[dev]));
-    return nullptr;
-  }
-  return addr[dev];
-}
-
-extern "C" int tg_block_scaled_matmul_noalloc(const void* a, const void* b, void* out, int64_t M,
-                                              int64_t N, int64_t K, int block_k, void* stream) {
-  TG_TRY(check_gemm_args("block_scaled_matmul_noalloc", M, N, K, block_k, 1));
-  if (M == 0 || N == 0) return TG_OK;
-  if (!a || !b || !out) return einval("block_scaled_matmul_noalloc: null pointer");
-  if (!aligned(a, 16) || !aligned(b, 16))
-    return einval("block_scaled_matmul_noalloc: a, b must be 16-byte aligned");
-  const size_t need = tg_block_scaled_matmul_workspace(M, N, K, block_k);
-  if (need > kScratchBytes) {
-    set_error("invalid argument: block_scaled_matmul_noalloc: M=%lld N=%lld K=%lld needs %zu bytes of "
-              "workspace, more than the %zu-byte static scratch (use tg_block_scaled_matmul with a "
-              "caller workspace)",
-              (long long)M, (long long)N, (long long)K, need, kScratchBytes);
-    return TG_EINVAL;
-  }
-  uint8_t* ws = scratch_on_current_device();
-  if (!ws) return TG_EHIP;
-  // every byte the GEMM reads is written by the two quantizers first, so the
-  // previous call's contents never leak into this one
-  return block_scaled_matmul_on(a, b, out, M, N, K, ws, as_stream(stream));
 }
 
 extern "C" size_t tg_block_scaled_matmul_bwd_workspace(int64_t M, int64_t N, int64_t K, int block_k) {

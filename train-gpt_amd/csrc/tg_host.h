@@ -86,6 +86,15 @@ int launch_gemm_gb(const uint8_t* a_q, const float* a_s, const uint8_t* b_q, con
 // n bf16 zeros at p by a fill kernel (no hipMemsetAsync: the callers may be
 // captured into a graph); n == 0 launches nothing (gemm_bf16.hip).
 int launch_fill_zero_bf16(void* p, int64_t n, hipStream_t st);
+// The GEMM entry points' shape and block checks (gemm_fp8.hip); any_block:
+// the entry has the general path for block_k != 128.
+int check_gemm_args(const char* who, int64_t M, int64_t N, int64_t K, int block_k, int bns,
+                    bool any_block = false);
+// tg_block_scaled_matmul's kernels (the two quantizers, then the GEMM) on a
+// workspace of tg_block_scaled_matmul_workspace(M, N, K, 128) bytes the caller
+// has checked (gemm_fp8.hip).
+int block_scaled_matmul_on(const void* a, const void* b, void* out, int64_t M, int64_t N, int64_t K,
+                           void* workspace, hipStream_t st);
 
 }  // namespace tg
 
