@@ -1809,9 +1809,12 @@ __global__ __launch_bounds__(512) void gemv_direct_kernel(const uint8_t* __restr
 // W).  With M <= 2 the MFMA kernel above spends its time moving each weight
 // row through LDS so that 8 rows can feed one 16-row MFMA fragment; here each
 // wave streams whole weight rows and takes the dot products itself.
-//   * A unit is 4 KiB of one weight row: four 1 KiB loads (16 bytes per lane)
-//     and the four W scales of those lanes.  A wave owns rows gw, gw + nw, ...
-//     (nw = waves in the grid), walked unit by unit with two units in flight.
+//   * A unit is NQ KiB of one weight row: NQ 1 KiB loads (16 bytes per lane)
+//     and the NQ W scales of those lanes; NQ = 3 when the row is a multiple of
+//     3 KiB or shorter (the decode widths 2304 and 9216: 2.25 of 4 KiB-unit
+//     pieces, or a last unit of 1 KiB, would be loaded and computed for
+//     nothing), else 4.  A wave owns rows gw, gw + nw, ... (nw = waves in the
+//     grid), walked unit by unit with two units in flight.
 //   * Per 16-byte piece: 16 e4m3 x 16 e4m3 products (v_cvt_pk_f32_fp8, f32
 //     fma chain) into the block partial, scaled by w_s * x_s of its 128-wide
 //     block; at a row's end a 64-lane butterfly, and the row's sum is parked
@@ -1872,14 +1875,15 @@ struct RowdotUnit {
 };
 
 // unit (row, g): 1 KiB pieces 4g .. 4g+3 of weight row `row`
+template <int NQ>
 __device__ __forceinline__ void rowdot_load(RowdotUnit& U, const __amdgpu_buffer_rsrc_t& rw,
                                             const __amdgpu_buffer_rsrc_t& rs, int row, int g, int K,
                                             int nkb, int bns, int lane) {
   const uint32_t rbase = (uint32_t)row * (uint32_t)K;
   const uint32_t sbase = (uint32_t)(bns == 1 ? row : row >> 7) * (uint32_t)nkb;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const uint32_t k = (uint32_t)(g * 4 + q) * 1024u + lane * 16u;
+  for (int q = 0; q < NQ; ++q) {
+    const uint32_t k = (uint32_t)(g * NQ + q) * 1024u + lane * 16u;
     const bool ok = k < (uint32_t)K;
     U.w[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, rbase + (ok ? k : 0u), 0, kAuxNT);
     U.s[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
@@ -1887,12 +1891,12 @@ __device__ __forceinline__ void rowdot_load(RowdotUnit& U, const __amdgpu_buffer
   }
 }
 
-template <int NX>
+template <int NX, int NQ>
 __device__ __forceinline__ void rowdot_compute(const RowdotUnit& U, const uint8_t* xl, const float* sxs,
                                                int g, int K, int nkb, int lane, float (&acc)[NX]) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const uint32_t k = (uint32_t)(g * 4 + q) * 1024u + lane * 16u;
+  for (int q = 0; q < NQ; ++q) {
+    const uint32_t k = (uint32_t)(g * NQ + q) * 1024u + lane * 16u;
     const bool ok = k < (uint32_t)K;
     const uint32_t kk = ok ? k : 0u;
 #pragma unroll
@@ -1910,7 +1914,7 @@ __device__ __forceinline__ void rowdot_compute(const RowdotUnit& U, const uint8_
 // (4 for PRO_X; 8 for the computing prologues, whose bf16 row loads every
 // workgroup repeats: 8 waves measured best of 4, 8 and 16 at the decode
 // shapes).
-template <int NX, int PRO, int XL, int J, int WPG, bool RES>
+template <int NX, int PRO, int XL, int J, int WPG, bool RES, int NQ>
 __global__ __launch_bounds__(64 * WPG) void gemv_rowdot_kernel(RowdotIn in, const uint8_t* __restrict__ WQ,
                                                           const float* __restrict__ WS, int bns,
                                                           __bf16* __restrict__ out, int N, int K,
@@ -1927,7 +1931,7 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rowdot_kernel(RowdotIn in, cons
   const int srows = bns == 1 ? N : (N + 127) >> 7;
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(WS, (uint32_t)srows * (uint32_t)nkb * 4u);
   const int nw = gridDim.x * WPG, gw = blockIdx.x * WPG + wave;
-  const int G = (K + 4095) >> 12;                      // units per row
+  const int G = (K + NQ * 1024 - 1) / (NQ * 1024);     // units per row
   const int nrows = gw < N ? (N - 1 - gw) / nw + 1 : 0;
   const int nu = nrows * G;
 
@@ -1987,7 +1991,7 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rowdot_kernel(RowdotIn in, cons
   // order, so the prologue's arithmetic can start before these arrive) ----
   __builtin_amdgcn_sched_barrier(0);
   RowdotUnit A, B;
-  rowdot_load(A, rw, rs, gw < N ? gw : N - 1, 0, K, nkb, bns, lane);
+  rowdot_load<NQ>(A, rw, rs, gw < N ? gw : N - 1, 0, K, nkb, bns, lane);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- prologue arithmetic -> LDS ----
@@ -2091,13 +2095,13 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rowdot_kernel(RowdotIn in, cons
   for (int it = 0; it < pairs; ++it) {
     int row1 = row, g1 = g, j1 = j;
     next(row1, g1, j1);
-    rowdot_load(B, rw, rs, row1, g1, K, nkb, bns, lane);
-    rowdot_compute<NX>(A, xl, sxs, g, K, nkb, lane, acc);
+    rowdot_load<NQ>(B, rw, rs, row1, g1, K, nkb, bns, lane);
+    rowdot_compute<NX, NQ>(A, xl, sxs, g, K, nkb, lane, acc);
     if (g == G - 1) finish(j);
     int row2 = row1, g2 = g1, j2 = j1;
     next(row2, g2, j2);
-    rowdot_load(A, rw, rs, row2, g2, K, nkb, bns, lane);
-    rowdot_compute<NX>(B, xl, sxs, g1, K, nkb, lane, acc);
+    rowdot_load<NQ>(A, rw, rs, row2, g2, K, nkb, bns, lane);
+    rowdot_compute<NX, NQ>(B, xl, sxs, g1, K, nkb, lane, acc);
     if (g1 == G - 1) finish(j1);
     row = row2;
     g = g2;
@@ -2106,13 +2110,13 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rowdot_kernel(RowdotIn in, cons
   if ((nu & 1) == 0) {
     int row1 = row, g1 = g, j1 = j;
     next(row1, g1, j1);
-    rowdot_load(B, rw, rs, row1, g1, K, nkb, bns, lane);
-    rowdot_compute<NX>(A, xl, sxs, g, K, nkb, lane, acc);
+    rowdot_load<NQ>(B, rw, rs, row1, g1, K, nkb, bns, lane);
+    rowdot_compute<NX, NQ>(A, xl, sxs, g, K, nkb, lane, acc);
     if (g == G - 1) finish(j);
-    rowdot_compute<NX>(B, xl, sxs, g1, K, nkb, lane, acc);
+    rowdot_compute<NX, NQ>(B, xl, sxs, g1, K, nkb, lane, acc);
     finish(j1);
   } else {
-    rowdot_compute<NX>(A, xl, sxs, g, K, nkb, lane, acc);
+    rowdot_compute<NX, NQ>(A, xl, sxs, g, K, nkb, lane, acc);
     finish(j);
   }
 }
@@ -2540,7 +2544,7 @@ extern "C" int tg_gemv_fp8(const uint8_t* x_q, const float* x_s, const uint8_t* 
   return launch_gemm_fp8(x_q, x_s, w_q, w_s, w_scale_bn, out, TG_DTYPE_BF16, M, N, K, st, false);
 }
 
-template <int NX, int PRO, int XL, int J, int WPG = 4, bool RES = false>
+template <int NX, int PRO, int XL, int J, int WPG = 4, bool RES = false, int NQ = 4>
 static void launch_rowdot_k(const RowdotIn& in, const uint8_t* w_q, const float* w_s, int bns, __bf16* o,
                             int n, int k, int sx_off, size_t lds, hipStream_t st) {
   // persistent waves, one wave per weight row at a time: as many workgroups
@@ -2549,7 +2553,7 @@ static void launch_rowdot_k(const RowdotIn& in, const uint8_t* w_q, const float*
   // slot (a function-local static: its initializer runs once, thread-safely)
   static const int occ_regs = [] {
     int v = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_rowdot_kernel<NX, PRO, XL, J, WPG, RES>, 64 * WPG, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemv_rowdot_kernel<NX, PRO, XL, J, WPG, RES, NQ>, 64 * WPG, 0) !=
             hipSuccess || v <= 0)
       v = 16 / WPG;
     return v;
@@ -2559,23 +2563,23 @@ static void launch_rowdot_k(const RowdotIn& in, const uint8_t* w_q, const float*
   const int by_lds = (int)((160 * 1024) / (lds > 0 ? lds : 1));
   if (by_lds < per_cu) per_cu = by_lds < 1 ? 1 : by_lds;
   const int64_t wgs = ((int64_t)n + WPG - 1) / WPG, cap = (int64_t)per_cu * device_cus();
-  hipLaunchKernelGGL((gemv_rowdot_kernel<NX, PRO, XL, J, WPG, RES>), dim3((unsigned)(wgs < cap ? wgs : cap)),
+  hipLaunchKernelGGL((gemv_rowdot_kernel<NX, PRO, XL, J, WPG, RES, NQ>), dim3((unsigned)(wgs < cap ? wgs : cap)),
                      dim3(64 * WPG), lds, st, in, w_q, w_s, bns, o, n, k, sx_off);
 }
 
 // PRO_X: XL 4 KiB pieces of x; PRO_RELU2: XL 16-byte chunks of u per thread;
 // PRO_NORM*: J chunks of the norm row per lane.
-template <int NX, int PRO, bool RES = false>
-static int launch_rowdot(const RowdotIn& in, const uint8_t* w_q, const float* w_s, int bns, __bf16* o,
+template <int NX, int PRO, bool RES, int NQ>
+static int launch_rowdot_q(const RowdotIn& in, const uint8_t* w_q, const float* w_s, int bns, __bf16* o,
                          int n, int k, hipStream_t st) {
   if constexpr (PRO == PRO_X) {
     const int need = (NX * k + 4095) / 4096;
     const int sx_off = (need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8) * 4096;
     const size_t lds = (size_t)sx_off + 1024;
-    if (need <= 1) launch_rowdot_k<NX, PRO, 1, 1, 4, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-    else if (need <= 2) launch_rowdot_k<NX, PRO, 2, 1, 4, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-    else if (need <= 4) launch_rowdot_k<NX, PRO, 4, 1, 4, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-    else launch_rowdot_k<NX, PRO, 8, 1, 4, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+    if (need <= 1) launch_rowdot_k<NX, PRO, 1, 1, 4, RES, NQ>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+    else if (need <= 2) launch_rowdot_k<NX, PRO, 2, 1, 4, RES, NQ>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+    else if (need <= 4) launch_rowdot_k<NX, PRO, 4, 1, 4, RES, NQ>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+    else launch_rowdot_k<NX, PRO, 8, 1, 4, RES, NQ>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
   } else {
     const int sx_off = NX * k;   // a multiple of 128
     // x bytes, x scales; for the norm prologues also the bf16 residual sums and r
@@ -2586,21 +2590,29 @@ static int launch_rowdot(const RowdotIn& in, const uint8_t* w_q, const float* w_
     constexpr int W = kRowdotProWaves;
     if constexpr (PRO == PRO_RELU2) {
       const int need = (NX * k / 8 + 64 * W - 1) / (64 * W);   // 16-byte chunks of u per thread
-      if (need <= 1) launch_rowdot_k<NX, PRO, 1, 1, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (need <= 2) launch_rowdot_k<NX, PRO, 2, 1, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (need <= 4) launch_rowdot_k<NX, PRO, 4, 1, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (need <= 8) launch_rowdot_k<NX, PRO, 8, 1, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else launch_rowdot_k<NX, PRO, 16, 1, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      if (need <= 1) launch_rowdot_k<NX, PRO, 1, 1, W, RES, NQ>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (need <= 2) launch_rowdot_k<NX, PRO, 2, 1, W, RES, NQ>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (need <= 4) launch_rowdot_k<NX, PRO, 4, 1, W, RES, NQ>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (need <= 8) launch_rowdot_k<NX, PRO, 8, 1, W, RES, NQ>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else launch_rowdot_k<NX, PRO, 16, 1, W, RES, NQ>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
     } else {
       const int jneed = (k / 8 + 63) / 64;
-      if (jneed <= 1) launch_rowdot_k<NX, PRO, 1, 1, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (jneed <= 2) launch_rowdot_k<NX, PRO, 1, 2, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (jneed <= 4) launch_rowdot_k<NX, PRO, 1, 4, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else if (jneed <= 5) launch_rowdot_k<NX, PRO, 1, 5, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
-      else launch_rowdot_k<NX, PRO, 1, 8, W, RES>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      if (jneed <= 1) launch_rowdot_k<NX, PRO, 1, 1, W, RES, NQ>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (jneed <= 2) launch_rowdot_k<NX, PRO, 1, 2, W, RES, NQ>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (jneed <= 4) launch_rowdot_k<NX, PRO, 1, 4, W, RES, NQ>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else if (jneed <= 5) launch_rowdot_k<NX, PRO, 1, 5, W, RES, NQ>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
+      else launch_rowdot_k<NX, PRO, 1, 8, W, RES, NQ>(in, w_q, w_s, bns, o, n, k, sx_off, lds, st);
     }
   }
   return TG_OK;
+}
+
+// Units of 3 KiB when the rows are a multiple of 3 KiB or shorter, else 4 KiB.
+template <int NX, int PRO, bool RES = false>
+static int launch_rowdot(const RowdotIn& in, const uint8_t* w_q, const float* w_s, int bns, __bf16* o,
+                         int n, int k, hipStream_t st) {
+  if (k % 3072 == 0 || k <= 3072) return launch_rowdot_q<NX, PRO, RES, 3>(in, w_q, w_s, bns, o, n, k, st);
+  return launch_rowdot_q<NX, PRO, RES, 4>(in, w_q, w_s, bns, o, n, k, st);
 }
 
 static int rowdot_common_checks(const char* who, int64_t M, int64_t N, int64_t K, int w_scale_bn,
