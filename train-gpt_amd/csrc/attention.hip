@@ -105,8 +105,14 @@ __global__ __launch_bounds__(kAttnWaves * 64) void decode_attention_kernel(
   // not used, rows past S read zero (the buffers span this head's S rows)
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc + cbase, (uint32_t)S * kAttnDh * 2u);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + cbase, (uint32_t)S * kAttnDh * 2u);
+  // this head's q, k, v are read before t (they do not depend on it): the
+  // first key group's arithmetic then waits for one round trip, not for t's
+  // and then q's
   KvGroup A, B;
   kv_load(A, rk, rv, 0, wave, kr, dl);
+  const uint4 qw = *reinterpret_cast<const uint4*>(row + h * kAttnDh + dl * 8);
+  const uint4 knew = *reinterpret_cast<const uint4*>(row + hd + h * kAttnDh + dl * 8);
+  const uint4 vnew = *reinterpret_cast<const uint4*>(row + 2 * hd + h * kAttnDh + dl * 8);
   const int64_t t = *tpos;
   if (t < 0 || t >= S) {                   // position outside the cache: touch nothing
     if (threadIdx.x == 0) os[(int64_t)b * H + h] = __builtin_nanf("");
@@ -114,13 +120,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void decode_attention_kernel(
   }
 
   float qf[8];
-  {
-    const uint4 w = *reinterpret_cast<const uint4*>(row + h * kAttnDh + dl * 8);
-    qf[0] = bf16lo(w.x); qf[1] = bf16hi(w.x); qf[2] = bf16lo(w.y); qf[3] = bf16hi(w.y);
-    qf[4] = bf16lo(w.z); qf[5] = bf16hi(w.z); qf[6] = bf16lo(w.w); qf[7] = bf16hi(w.w);
-  }
-  const uint4 knew = *reinterpret_cast<const uint4*>(row + hd + h * kAttnDh + dl * 8);
-  const uint4 vnew = *reinterpret_cast<const uint4*>(row + 2 * hd + h * kAttnDh + dl * 8);
+  qf[0] = bf16lo(qw.x); qf[1] = bf16hi(qw.x); qf[2] = bf16lo(qw.y); qf[3] = bf16hi(qw.y);
+  qf[4] = bf16lo(qw.z); qf[5] = bf16hi(qw.z); qf[6] = bf16lo(qw.w); qf[7] = bf16hi(qw.w);
   if (wave == 0 && kr == 0) {                           // append k, v at position t
     *reinterpret_cast<uint4*>(kc + cbase + t * kAttnDh + dl * 8) = knew;
     *reinterpret_cast<uint4*>(vc + cbase + t * kAttnDh + dl * 8) = vnew;
