@@ -344,6 +344,13 @@ int tg_decode_attention(const void* qkv, void* k_cache, void* v_cache, const int
                         uint8_t* o_q, float* o_s, void* o, int64_t B, int64_t H, int64_t S,
                         int64_t head_dim, float scale, void* stream);
 
+/* The logit cap of model.py:97 on bf16 logits: out (n,) f32 = cap * tanh(l / cap)
+ * with torch's arithmetic for `cap * torch.tanh(l.float() / cap)` (l times the
+ * f32 reciprocal of cap, the device tanhf, one f32 multiply), the same bits in
+ * one launch.  For the decode step's unembedding rows (the reference applies
+ * the cap inside model.forward, generate.py:166-171).  cap finite and > 0. */
+int tg_logit_cap(const void* logits, float* out, int64_t n, float cap, void* stream);
+
 /* Logit cap + cross entropy, forward: for each row r of the bf16 logits
  * (rows, vocab) and target t = targets[r],
  *   z = cap * tanh(l / cap)   (f32; model.py:96-97 with config.logit_cap)

@@ -381,9 +381,32 @@ __global__ __launch_bounds__(kXentThreads) __attribute__((amdgpu_waves_per_eu(6)
   }
 }
 
+// z = cap * tanh(l * inv_cap), f32, from bf16 logits l: model.py:97 on the
+// decode step's unembedding rows, with torch's arithmetic for
+// `cap * torch.tanh(l.float() / cap)` (a division by a scalar is a multiply by
+// its f32 reciprocal, then the device tanhf and one f32 multiply), so the
+// same bits in one launch instead of four
+__global__ __launch_bounds__(256) void logit_cap_kernel(const uint16_t* __restrict__ l, float* __restrict__ z,
+                                                        int64_t n, float cap, float inv_cap) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) z[i] = cap * tanhf(bf16lo(l[i]) * inv_cap);
+}
+
 }  // namespace tg
 
 using namespace tg;
+
+extern "C" int tg_logit_cap(const void* logits, float* out, int64_t n, float cap, void* stream) {
+  if (n < 0) return einval("logit_cap: n must be >= 0");
+  if (!(cap > 0.0f) || cap == __builtin_inff()) return einval("logit_cap: cap must be finite and > 0");
+  if (n == 0) return TG_OK;
+  if (!logits || !out) return einval("logit_cap: null pointer");
+  if ((n + 255) / 256 > 0x7FFFFFFF) return einval("logit_cap: n too large");
+  const float inv_cap = 1.0f / cap;   // the f32 reciprocal torch multiplies by
+  hipLaunchKernelGGL(logit_cap_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const uint16_t*>(logits), out, n, cap, inv_cap);
+  return check_launch("logit_cap");
+}
 
 static int xent_check(const void* logits, const int64_t* tgt, int64_t rows, int64_t vocab, float cap) {
   if (rows < 0 || vocab <= 0) return einval("logit_cap_xent: rows must be >= 0 and vocab > 0");

@@ -162,6 +162,23 @@ def _attention(q, k, v, causal: bool):
         return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
 
 
+# the decode steps of decode_attn "hip" apply the logit cap in one HIP kernel
+# (tg_logit_cap, the same bits as torch's four kernels)
+HIP_LOGIT_CAP = True
+
+
+def logit_cap(logits: torch.Tensor, cap: float) -> torch.Tensor:
+    """model.py:97 on bf16 logits: f32 cap * tanh(logits / cap), one HIP kernel
+    (tg_logit_cap) with the bits of `cap * torch.tanh(logits.float() / cap)`."""
+    if logits.dtype != torch.bfloat16:
+        raise ValueError("logit_cap: logits must be bf16")
+    _L.require_gpu(logits)
+    x = logits.contiguous()
+    out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    _L.check(_L.lib().tg_logit_cap(_L.ptr(x), _L.ptr(out), x.numel(), float(cap), _L.stream_of(x)))
+    return out
+
+
 def decode_attention(qkv: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                      t: torch.Tensor, n_heads: int, want_bf16: bool = False):
     """The HIP decode attention (tg_decode_attention): appends k, v of qkv
@@ -348,8 +365,10 @@ class FP8Decoder:
             # x = x + m (model.py:76) fused with the next norm (norm1 or final_norm)
             nxt = self.layers[li + 1]["norm1"] if li + 1 < len(self.layers) else self.final_norm
             x, h_q, h_s, _ = kernels.add_rms_norm_fp8(x, m, nxt, cfg.rms_eps, inplace=True)
-        logits = self.unembed.matmul_prequant(h_q, h_s, self.exact_gemv).float()            # model.py:96
-        return cfg.logit_cap * torch.tanh(logits / cfg.logit_cap)           # model.py:97
+        logits = self.unembed.matmul_prequant(h_q, h_s, self.exact_gemv)                    # model.py:96
+        if HIP_LOGIT_CAP and self.decode_attn == "hip":
+            return logit_cap(logits, cfg.logit_cap)                                          # model.py:97
+        return cfg.logit_cap * torch.tanh(logits.float() / cfg.logit_cap)  # model.py:97
 
     def _step_dev_fused(self, tok: torch.Tensor, t: torch.Tensor, B: int) -> torch.Tensor:
         """_step_dev with each norm / relu^2 quantization inside the GEMV that
@@ -376,8 +395,9 @@ class FP8Decoder:
                 nxt = self.final_norm if last else self.layers[li + 1]["norm1"]
                 w = self.unembed if last else self.layers[li + 1]["wqkv"]
                 qkv = w.matmul_rms_norm(xa, nxt, eps)
-            logits = qkv.float()
-            return cfg.logit_cap * torch.tanh(logits / cfg.logit_cap)       # model.py:97
+            if HIP_LOGIT_CAP and self.decode_attn == "hip":
+                return logit_cap(qkv, cfg.logit_cap)                          # model.py:97
+            return cfg.logit_cap * torch.tanh(qkv.float() / cfg.logit_cap)  # model.py:97
         xb = torch.empty_like(xa)
         for li, lp in enumerate(self.layers):
             if self.decode_attn == "hip":
@@ -394,8 +414,9 @@ class FP8Decoder:
             nxt = self.final_norm if last else self.layers[li + 1]["norm1"]
             w = self.unembed if last else self.layers[li + 1]["wqkv"]
             qkv = w.matmul_rms_norm(xb, nxt, eps, delta=m, xout=xa)
-        logits = qkv.float()
-        return cfg.logit_cap * torch.tanh(logits / cfg.logit_cap)           # model.py:97
+        if HIP_LOGIT_CAP and self.decode_attn == "hip":
+            return logit_cap(qkv, cfg.logit_cap)                              # model.py:97
+        return cfg.logit_cap * torch.tanh(qkv.float() / cfg.logit_cap)      # model.py:97
 
     def _sdpa_step(self, li: int, qkv: torch.Tensor, t: int) -> torch.Tensor:
         """decode_attn="sdpa": append k, v at t, torch attention over 0 .. t."""
