@@ -351,6 +351,15 @@ int tg_decode_attention(const void* qkv, void* k_cache, void* v_cache, const int
  * the cap inside model.forward, generate.py:166-171).  cap finite and > 0. */
 int tg_logit_cap(const void* logits, float* out, int64_t n, float cap, void* stream);
 
+/* The decode step's input rows, model.py:89-90 for one token per sequence:
+ * out[b] (d) bf16 = bf16(embed[tok[b]] + pos[t]) (the f32 sum of the two bf16
+ * values, rounded once: torch's bf16 add), with tok (B,) and t (1,) int64 in
+ * device memory (a captured graph serves every token).  embed (V, d) and pos
+ * (P, d) bf16, d a multiple of 8.  A token or position outside its table
+ * reads a zero row (no fault; torch's indexing would assert). */
+int tg_decode_embed(const void* embed, const void* pos, const int64_t* tok, const int64_t* t, void* out,
+                    int64_t B, int64_t V, int64_t P, int64_t d, void* stream);
+
 /* Logit cap + cross entropy, forward: for each row r of the bf16 logits
  * (rows, vocab) and target t = targets[r],
  *   z = cap * tanh(l / cap)   (f32; model.py:96-97 with config.logit_cap)

@@ -79,6 +79,8 @@ CASES = {
     "tg_quantize_weight_128x128": ((N, 256, 16, N, N, N), (N, 256, -16, N, N, N), (N, 256, 0, N, N, N)),
     "tg_decode_attention": ((N, N, N, N, N, N, N, 1, 2, 16, 128, 0.1, N), (N, N, N, N, N, N, N, -1, 2, 16, 128, 0.1, N),
                             (N, N, N, N, N, N, N, 0, 2, 16, 128, 0.1, N)),
+    "tg_decode_embed": ((N, N, N, N, N, 1, 512, 64, 256, N), (N, N, N, N, N, -1, 512, 64, 256, N),
+                        (N, N, N, N, N, 0, 512, 64, 256, N)),
     "tg_logit_cap": ((N, N, 50257, 15.0, N), (N, N, -1, 15.0, N), (N, N, 0, 15.0, N)),
     "tg_logit_cap_xent_fwd": ((N, N, 4, 256, 15.0, N, N, N), (N, N, -4, 256, 15.0, N, N, N),
                               (N, N, 0, 256, 15.0, N, N, N)),

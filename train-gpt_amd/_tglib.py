@@ -64,6 +64,7 @@ SIGNATURES = {
     "tg_decode_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                    ctypes.c_float, _vp]),
     "tg_logit_cap": (_int, [_vp, _vp, _i64, _f32, _vp]),
+    "tg_decode_embed": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "tg_logit_cap_xent_fwd": (_int, [_vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp]),
     "tg_logit_cap_xent_bwd": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _i64, _i64, _f32, _vp, _vp]),
     "tg_selftest_fp8_cvt": (_int, [_vp, _vp]),

@@ -199,9 +199,55 @@ __global__ __launch_bounds__(kAttnWaves * 64) void decode_attention_kernel(
   if (dl == 0) os[(int64_t)b * H + h] = sc;
 }
 
+// The decode step's input rows (model.py:89-90 for one token per sequence):
+// out[b] = bf16(embed[tok[b]] + pos[t]), the f32 sum of the two bf16 values
+// rounded once (torch's bf16 add).  The rows are read through buffer
+// descriptors of the two tables, so a token or position outside them reads a
+// zero row and touches no other memory.  One workgroup per sequence, 16-byte
+// chunks (d % 8 == 0).
+__global__ __launch_bounds__(256) void decode_embed_kernel(const uint16_t* __restrict__ embed,
+                                                           const uint16_t* __restrict__ pos,
+                                                           const int64_t* __restrict__ tok,
+                                                           const int64_t* __restrict__ tpos,
+                                                           uint16_t* __restrict__ out, int64_t V, int64_t P, int d) {
+  const int b = blockIdx.x;
+  const int64_t tk = tok[b], t = *tpos;
+  const uint32_t rowb = (uint32_t)d * 2u;
+  const __amdgpu_buffer_rsrc_t re = make_rsrc(embed, (uint32_t)V * rowb);
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(pos, (uint32_t)P * rowb);
+  const uint32_t eo = tk >= 0 && tk < V ? (uint32_t)tk * rowb : (uint32_t)V * rowb;   // past the end: zeros
+  const uint32_t po = t >= 0 && t < P ? (uint32_t)t * rowb : (uint32_t)P * rowb;
+  for (int c = threadIdx.x; c < d / 8; c += 256) {
+    const u32x4_t e = __builtin_amdgcn_raw_buffer_load_b128(re, eo + (uint32_t)c * 16u, 0, 0);
+    const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(rp, po + (uint32_t)c * 16u, 0, 0);
+    const uint32_t ew[4] = {e.x, e.y, e.z, e.w}, pw[4] = {q.x, q.y, q.z, q.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = pack_bf16x2(bf16lo(ew[i]) + bf16lo(pw[i]), bf16hi(ew[i]) + bf16hi(pw[i]));
+    *reinterpret_cast<uint4*>(out + (int64_t)b * d + c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 }  // namespace tg
 
 using namespace tg;
+
+extern "C" int tg_decode_embed(const void* embed, const void* pos, const int64_t* tok, const int64_t* t,
+                               void* out, int64_t B, int64_t V, int64_t P, int64_t d, void* stream) {
+  if (B < 0 || V <= 0 || P <= 0 || d <= 0 || d % 8) return einval("decode_embed: bad shape (d a multiple of 8)");
+  if (B == 0) return TG_OK;
+  if (B > 0x7FFFFFFF || (uint64_t)V * (uint64_t)d * 2u >= (1ull << 32) ||
+      (uint64_t)P * (uint64_t)d * 2u >= (1ull << 32))
+    return einval("decode_embed: tables too large for 32-bit buffer offsets");
+  if (!embed || !pos || !tok || !t || !out) return einval("decode_embed: null pointer");
+  if (!aligned(embed, 16) || !aligned(pos, 16) || !aligned(out, 16))
+    return einval("decode_embed: embed, pos and out must be 16-byte aligned");
+  hipLaunchKernelGGL(decode_embed_kernel, dim3((unsigned)B), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const uint16_t*>(embed), reinterpret_cast<const uint16_t*>(pos), tok, t,
+                     reinterpret_cast<uint16_t*>(out), V, P, (int)d);
+  return check_launch("decode_embed");
+}
 
 extern "C" int tg_decode_attention(const void* qkv, void* k_cache, void* v_cache, const int64_t* t,
                                    uint8_t* o_q, float* o_s, void* o, int64_t B, int64_t H,

@@ -162,9 +162,28 @@ def _attention(q, k, v, causal: bool):
         return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
 
 
-# the decode steps of decode_attn "hip" apply the logit cap in one HIP kernel
-# (tg_logit_cap, the same bits as torch's four kernels)
+# the decode steps of decode_attn "hip" form their input rows and apply the
+# logit cap in one HIP kernel each (tg_decode_embed, tg_logit_cap: the same
+# bits as torch's three and four kernels)
 HIP_LOGIT_CAP = True
+
+
+def decode_embed(embed: torch.Tensor, pos: torch.Tensor, tok: torch.Tensor, t: torch.Tensor) -> torch.Tensor:
+    """The step's input rows embed[tok] + pos[t] (model.py:89-90), bf16, in one
+    HIP kernel (tg_decode_embed, the bits of torch's index, index_select and
+    add).  A token or position outside its table reads a zero row."""
+    if embed.dtype != torch.bfloat16 or pos.dtype != torch.bfloat16 or embed.shape[1] != pos.shape[1]:
+        raise ValueError("decode_embed: embed (V, d) and pos (P, d) must be bf16 with one d")
+    if tok.dim() != 1 or t.dtype != torch.int64 or t.numel() != 1:
+        raise ValueError("decode_embed: tok must be (B,) and t a one-element int64 tensor")
+    _L.require_gpu(embed, pos, t)
+    # an int64 device tok (the captured step's) is used as it is: no copy, no launch
+    tk = tok.to(device=embed.device, dtype=torch.int64).contiguous()
+    e, p = embed.contiguous(), pos.contiguous()
+    out = torch.empty((tk.shape[0], e.shape[1]), dtype=torch.bfloat16, device=e.device)
+    _L.check(_L.lib().tg_decode_embed(_L.ptr(e), _L.ptr(p), _L.ptr(tk), _L.ptr(t), _L.ptr(out), tk.shape[0],
+                                      e.shape[0], p.shape[0], e.shape[1], _L.stream_of(e)))
+    return out
 
 
 def logit_cap(logits: torch.Tensor, cap: float) -> torch.Tensor:
@@ -349,7 +368,10 @@ class FP8Decoder:
             return self._step_dev_fused(tok, t, B)
         cfg = self.cfg
         H = cfg.n_heads
-        x = self.embed[tok] + self.pos.index_select(0, t)                 # (B, d)
+        if HIP_LOGIT_CAP and self.decode_attn == "hip":
+            x = decode_embed(self.embed, self.pos, tok, t)                 # (B, d), model.py:89-90
+        else:
+            x = self.embed[tok] + self.pos.index_select(0, t)
         _, h_q, h_s = kernels.rms_norm_fp8(x, self.layers[0]["norm1"], cfg.rms_eps)
         for li, lp in enumerate(self.layers):
             qkv = lp["wqkv"].matmul_prequant(h_q, h_s, self.exact_gemv)                      # (B, 3 H Dh)
@@ -380,7 +402,10 @@ class FP8Decoder:
         other).  The same bits either way."""
         cfg = self.cfg
         H, eps = cfg.n_heads, cfg.rms_eps
-        xa = self.embed[tok] + self.pos.index_select(0, t)                # (B, d)
+        if HIP_LOGIT_CAP and self.decode_attn == "hip":
+            xa = decode_embed(self.embed, self.pos, tok, t)                 # (B, d), model.py:89-90
+        else:
+            xa = self.embed[tok] + self.pos.index_select(0, t)
         qkv = self.layers[0]["wqkv"].matmul_rms_norm(xa, self.layers[0]["norm1"], eps)   # model.py:61-64
         if B <= 2:
             for li, lp in enumerate(self.layers):
